@@ -1,0 +1,230 @@
+"""Benchmark of the Q4_K / Q6_K matmul hot path on one MI355X.
+
+Workload (Llama-3.1-8B FFN decode at batch 1): one step =
+fused Q4_K gate+up+SwiGLU GEMV (2 x 14336x4096) followed by the Q6_K
+ffn_down GEMV (4096x14336) on its output.  `value` is the algorithmic HBM
+bytes of one step divided by the measured step time (GB/s).  Weights are
+seeded synthetic GGUF blocks generated in device memory; several distinct
+weight copies are cycled so each step streams from HBM, not from the 256 MB
+Infinity Cache.
+
+The prefill GEMM is reported as an extra object
+("prefill_gemm": TFLOP/s at M = 64..512) beside the headline line.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+K_FFN, N_FFN = 4096, 14336
+Q4K_BYTES, Q6K_BYTES = 144, 210
+# algorithmic bytes: N*(K/256)*B + 4K (x) + 4N (y)
+GATE_UP_BYTES = 2 * N_FFN * (K_FFN // 256) * Q4K_BYTES + 4 * K_FFN + 4 * N_FFN      # 66,134,016
+DOWN_BYTES = K_FFN * (N_FFN // 256) * Q6K_BYTES + 4 * N_FFN + 4 * K_FFN            # 48,242,688
+STEP_BYTES = GATE_UP_BYTES + DOWN_BYTES
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def bench_decode(lib, torch, steps, warmup):
+    from rocmforge_amd import synth
+
+    dev = torch.device("cuda:0")
+    set_bytes = 2 * N_FFN * (K_FFN // 256) * Q4K_BYTES + K_FFN * (N_FFN // 256) * Q6K_BYTES
+    copies = max(2, -(-4 * MALL_BYTES // set_bytes))          # >= 4x the Infinity Cache
+    sets = []
+    for c in range(copies):
+        wg = synth.torch_weights("q4_k", N_FFN, K_FFN, seed=3 * c + 1, device=dev)
+        wu = synth.torch_weights("q4_k", N_FFN, K_FFN, seed=3 * c + 2, device=dev)
+        wd = synth.torch_weights("q6_k", K_FFN, N_FFN, seed=3 * c + 3, device=dev)
+        sets.append((wg, wu, wd))
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn(K_FFN, device=dev, generator=g)
+    h = torch.empty(N_FFN, device=dev)
+    y = torch.empty(K_FFN, device=dev)
+    stream = torch.cuda.current_stream()
+    st = ctypes.c_void_p(stream.cuda_stream)
+    gu = lib.gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch
+    dn = lib.gemv_q6_k_f32_launch
+
+    def step(i, ev=None):
+        wg, wu, wd = sets[i % copies]
+        if ev is not None:
+            ev[0].record(stream)
+        rc = gu(vp(wg), vp(wu), vp(x), vp(h), K_FFN, N_FFN, st)
+        if ev is not None:
+            ev[1].record(stream)
+        rc |= dn(vp(wd), vp(h), vp(y), N_FFN, K_FFN, st)
+        if ev is not None:
+            ev[2].record(stream)
+        if rc:
+            raise RuntimeError(f"launch failed: hipError {rc}")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # per-kernel durations with HIP events on the launch stream (separate pass
+    # so the headline timing carries no event overhead)
+    nev = min(steps, 500)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev)]
+    torch.cuda.synchronize()
+    for i in range(nev):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    gu_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / nev
+    dn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / nev
+    return {
+        "wall": wall, "copies": copies, "gate_up_ms": gu_ms, "down_ms": dn_ms,
+        "x": x, "h": h, "y": y,
+    }
+
+
+def bench_gemm(lib, torch):
+    """Prefill GEMM TFLOP/s at Llama-3.1-8B FFN shapes, M = 64..512."""
+    from rocmforge_amd import synth
+
+    if not hasattr(lib, "wmma_gemm_q4_k_launch"):
+        return None
+    dev = torch.device("cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    shapes = [("q4_k", N_FFN, K_FFN, lib.wmma_gemm_q4_k_launch), ("q6_k", K_FFN, N_FFN, lib.wmma_gemm_q6_k_launch)]
+    for fmt, n, k, fn in shapes:
+        wsets = [synth.torch_weights(fmt, n, k, seed=50 + c, device=dev) for c in range(6)]
+        for m in (64, 128, 256, 512):
+            a = torch.randn(m, k, device=dev).to(torch.bfloat16).float()
+            d = torch.empty(m, n, device=dev)
+            for i in range(5):
+                fn(vp(a), vp(wsets[i % 6]), vp(d), m, n, k, st)
+            iters = 50
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(iters):
+                rc = fn(vp(a), vp(wsets[i % 6]), vp(d), m, n, k, st)
+                if rc:
+                    raise RuntimeError(f"gemm launch failed {rc}")
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000 / iters
+            tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            res[f"{fmt}_{n}x{k}_M{m}"] = {"us": round(us, 2), "tflops": round(tflops, 1),
+                                          "frac_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+    return res
+
+
+def cpu_baseline(seconds):
+    """The reference CPU algorithm (C port in oracle/) on the same workload:
+    Q4_K x Q8_K AVX2 gate/up on all host threads + silu_fuse, then the scalar
+    Q6_K ffn_down on ONE thread (the reference's rayon split is over batch
+    rows, so a single-token Q6_K GEMV is single-threaded)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from rocmforge_amd import synth
+
+    threads = min(16, os.cpu_count() or 1)
+    wg = synth.q4_k_weights(N_FFN, K_FFN, seed=1)
+    wu = synth.q4_k_weights(N_FFN, K_FFN, seed=2)
+    wd = synth.q6_k_weights(K_FFN, N_FFN, seed=3)
+    x = synth.activations(K_FFN, seed=0)
+    O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads)        # warm
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        h = O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads)
+        O.cpu_gemv_q6k(wd, np.ascontiguousarray(h), K_FFN, N_FFN, 1)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {
+        "value": round(STEP_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{n} full steps (gate+up {N_FFN}x{K_FFN} Q4_K on {threads} threads + Q6_K down "
+                  f"{K_FFN}x{N_FFN} on 1 thread), {dt * 1e3:.1f} ms/step",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(the sharding design is described in DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    import rocmforge_amd
+    lib = rocmforge_amd.load()
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU (cuda:0)")
+
+    r = bench_decode(lib, torch, args.steps, args.warmup)
+    ms = r["wall"] * 1e3 / args.steps
+    value = STEP_BYTES / (ms * 1e-3) / 1e9
+    gu_gbs = GATE_UP_BYTES / (r["gate_up_ms"] * 1e-3) / 1e9
+    dn_gbs = DOWN_BYTES / (r["down_ms"] * 1e-3) / 1e9
+    out = {
+        "metric": "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s at Llama-3.1-8B shapes",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights; int8 dot + fp32",
+        "data": "synthetic (seeded GGUF Q4_K/Q6_K blocks, x ~ N(0,1))",
+        "config": {"workload": "BASELINE config 1: Llama-3.1-8B FFN decode, batch 1: fused Q4_K gate+up+SwiGLU "
+                               "2x14336x4096 then Q6_K ffn_down 4096x14336",
+                   "bytes_per_step": STEP_BYTES, "weight_copies_cycled": r["copies"],
+                   "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "kernel": "rf_q4k_q8_gemv_kernel<gate_up>",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(r["gate_up_ms"] * 1e3, 3), "bytes_per_launch": GATE_UP_BYTES},
+        "kernels": {"gate_up_us": round(r["gate_up_ms"] * 1e3, 3), "gate_up_gbs": round(gu_gbs, 1),
+                    "q6k_down_us": round(r["down_ms"] * 1e3, 3), "q6k_down_gbs": round(dn_gbs, 1)},
+    }
+    if not args.no_gemm:
+        out["prefill_gemm"] = bench_gemm(lib, torch)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

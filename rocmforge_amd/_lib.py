@@ -1,0 +1,57 @@
+"""ctypes binding of librocmforge_cdna4.so (the C ABI in include/rocmforge_cdna4.h).
+
+The library is the product: nothing here falls back to another
+implementation.  If the shared object is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "librocmforge_cdna4.so"
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+# name -> argtypes (all return hipError_t as int)
+SIGNATURES = {
+    "gemv_q4_k_f32_q8_inline_launch": [_vp, _vp, _vp, _i, _i, _vp],
+    "gemv_q4_k_f32_q8_inline_residual_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
+    "gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
+    "gemv_q4_k_f32_launch": [_vp, _vp, _vp, _i, _i, _vp],
+    "gemv_q4_k_f32_residual_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
+    "gemv_gate_up_swiglu_q4_k_f32_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
+    "gemv_q6_k_f32_launch": [_vp, _vp, _vp, _i, _i, _vp],
+    "wmma_gemm_q4_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "wmma_gemm_q6_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],
+    "rf_q4_k_q8_int_dots_launch": [_vp, _vp, _vp, _i, _i, _vp],
+}
+
+_LIB = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise LibraryMissing if it was never built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise LibraryMissing(
+            f"{LIB_PATH} not found: build it with `python -m rocmforge_amd.build` "
+            "(there is no fallback implementation)")
+    lib = ctypes.CDLL(os.fspath(LIB_PATH), mode=ctypes.RTLD_LOCAL)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.rf_library_version.restype = ctypes.c_char_p
+    _LIB = lib
+    return lib

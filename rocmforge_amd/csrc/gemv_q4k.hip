@@ -1,0 +1,429 @@
+// gemv_q4k.hip -- Q4_K decode GEMVs for CDNA4 (gfx950, wave64).
+//
+// Drop-in for hip_kernels/quant/q4_k_q8_inline.hip (Q8_0-inline family) and
+// hip_kernels/quant/q4_k_gemv.hip (FP32-activation family): same extern "C"
+// symbols, argument meaning (n_rows = K = input length, ncols_dst = N =
+// output rows) and error returns.
+//
+// Design (MI355X-first, not a port of the wave32 kernels):
+//  * 256-thread workgroups = 4 wave64s.  Each wave owns R output rows at a
+//    time; inside a row the 64 lanes split 16 consecutive super-blocks four
+//    ways (lane = 4*s + p: super-block s, nibble pair p).  One row step
+//    therefore reads 16 x 144 B = 2304 contiguous bytes per row with
+//    16-byte loads, instead of one lane per 144-byte block.
+//  * The activation vector is quantised to Q8_0 once per workgroup into LDS
+//    (qs contiguous, scales and per-block int sums separate) while the
+//    first weight loads are already in flight.
+//  * Integer dots use v_dot4_i32_i8 (4 nibble x int8 products per op); the
+//    fp32 sub-block combine is the reference expression, so the only
+//    difference to the reference is the fp32 summation order.
+//  * Workgroups stride over row groups; the grid is capped at a multiple of
+//    the CU count so a large N re-uses each workgroup's quantised vector.
+#include "qk_common.h"
+
+namespace rf {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerWg = kThreads / kWave;
+constexpr int kSbPerStep = 16;  // super-blocks per wave row step
+
+enum Q4Mode { kPlain = 0, kResidual = 1, kGateUp = 2 };
+
+// Q8-inline LDS rule of the reference launchers (q4_k_q8_inline.hip:374-378):
+// (K/32) * 34 bytes <= 32 KB.  Kept so callers see identical validation.
+static inline bool q8_inline_fits(int K) { return (size_t)(K / 32) * 34 <= 32768; }
+
+static inline size_t q8_lds_bytes(int K) { return (size_t)K + (size_t)(K / 32) * 8; }
+
+__device__ __forceinline__ Q8Lds q8_lds_carve(uint8_t* smem, int K) {
+    Q8Lds l;
+    l.qs = reinterpret_cast<int8_t*>(smem);
+    l.xd = reinterpret_cast<float*>(smem + K);
+    l.qsum = reinterpret_cast<int*>(smem + K + 4 * (K / 32));
+    return l;
+}
+
+// One row step of one matrix for one lane: the unit's two sub-blocks
+// against the Q8 slab.
+__device__ __forceinline__ float q4k_q8_unit_dot(const Q4KUnit& u, int p, const u32x4 xlo[2], const u32x4 xhi[2],
+                                                 float xd0, float xd1, int qs0, int qs1, float acc) {
+    int dlo, dhi;
+    q4k_int_dots(u, xlo, xhi, &dlo, &dhi);
+    const float d = half_bits_to_float(u.hdr.x);
+    const float dmin = half_bits_to_float(u.hdr.x >> 16);
+    int sc0, m0, sc1, m1;
+    q4k_scale_min_pair(u.hdr.y, u.hdr.z, u.hdr.w, p, &sc0, &m0, &sc1, &m1);
+    acc = q4k_q8_combine(acc, xd0, d, dmin, sc0, m0, dlo, qs0);
+    acc = q4k_q8_combine(acc, xd1, d, dmin, sc1, m1, dhi, qs1);
+    return acc;
+}
+
+template <int M, int R>
+__device__ __forceinline__ void q4k_load_step(Q4KUnit (&u)[M][R], const uint8_t* w0, const uint8_t* w1,
+                                              size_t row_bytes, int row0, int N, int sbc, int p) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, N - 1);
+        const size_t off = (size_t)row * row_bytes + (size_t)sbc * kQ4KBytes;
+        u[0][r] = q4k_load_unit(w0 + off, p);
+        if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
+    }
+}
+
+template <int MODE, int R>
+__global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
+                                                                   const uint8_t* __restrict__ w1,
+                                                                   const float* __restrict__ x,
+                                                                   const float* residual, float* y, int K, int N) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Q8Lds q8 = q8_lds_carve(smem, K);
+    constexpr int M = (MODE == kGateUp) ? 2 : 1;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int s = lane >> 2;
+    const int p = lane & 3;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ4KBytes;
+    const int rows_per_iter = gridDim.x * kWavesPerWg * R;
+
+    // Software pipeline over (row group, 16-super-block step): the loads of
+    // step i+1 are in flight while step i is computed.  The first step's
+    // loads are issued before the activation quantisation, which hides the
+    // quantisation behind HBM latency.
+    int row0 = (blockIdx.x * kWavesPerWg + wave) * R;
+    int sb0 = 0;
+    Q4KUnit cur[M][R];
+    if (row0 < N) q4k_load_step<M, R>(cur, w0, w1, row_bytes, row0, N, min(s, nsb - 1), p);
+
+    q8_0_quantize_to_lds(x, K, q8);
+    __syncthreads();
+
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    while (row0 < N) {
+        int nrow0 = row0, nsb0 = sb0 + kSbPerStep;
+        if (nsb0 >= nsb) {
+            nsb0 = 0;
+            nrow0 += rows_per_iter;
+        }
+        Q4KUnit nxt[M][R];
+        if (nrow0 < N) q4k_load_step<M, R>(nxt, w0, w1, row_bytes, nrow0, N, min(nsb0 + s, nsb - 1), p);
+
+        const int sb = sb0 + s;
+        const bool live = sb < nsb;
+        const int sbc = live ? sb : nsb - 1;
+        // Q8 slab for this lane: 64 int8 at element sb*256 + 64p.
+        const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + sbc * kQK + 64 * p);
+        const u32x4 xlo[2] = {xs[0], xs[1]};
+        const u32x4 xhi[2] = {xs[2], xs[3]};
+        const int b0 = sbc * 8 + 2 * p;
+        const float xd0 = q8.xd[b0], xd1 = q8.xd[b0 + 1];
+        const int qs0 = q8.qsum[b0], qs1 = q8.qsum[b0 + 1];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float a = q4k_q8_unit_dot(cur[m][r], p, xlo, xhi, xd0, xd1, qs0, qs1, acc[m][r]);
+                acc[m][r] = live ? a : acc[m][r];
+            }
+
+        if (nsb0 == 0) {  // row group finished: reduce and write
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float g = wave_sum(acc[0][r]);
+                const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
+                const int row = row0 + r;
+                if (lane == r && row < N) {
+                    if (MODE == kPlain) {
+                        y[row] = g;
+                    } else if (MODE == kResidual) {
+                        y[row] = g + residual[row];
+                    } else {
+                        y[row] = g / (1.0f + expf(-g)) * v;
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[m][r] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) cur[m][r] = nxt[m][r];
+        row0 = nrow0;
+        sb0 = nsb0;
+    }
+}
+
+// ── FP32-activation family (q4_k_gemv.hip) ───────────────────────────────
+// value = d*sc*nib - dmin*m (fp32, q4_k_gemv.hip:60-71), times x from LDS.
+// Same lane tiling as the Q8 kernel; x is staged in LDS as fp32 when it
+// fits (K*4 <= 64 KB), otherwise read through L2 directly.
+template <bool LDS>
+__device__ __forceinline__ float q4k_f32_unit_dot(const Q4KUnit& u, int p, const float* xb, float acc) {
+    const float d = half_bits_to_float(u.hdr.x);
+    const float dmin = half_bits_to_float(u.hdr.x >> 16);
+    int sc0, m0, sc1, m1;
+    q4k_scale_min_pair(u.hdr.y, u.hdr.z, u.hdr.w, p, &sc0, &m0, &sc1, &m1);
+    const float ds0 = d * (float)sc0, dm0 = dmin * (float)m0;
+    const float ds1 = d * (float)sc1, dm1 = dmin * (float)m1;
+    const uint32_t w[8] = {u.qa.x, u.qa.y, u.qa.z, u.qa.w, u.qb.x, u.qb.y, u.qb.z, u.qb.w};
+    const float4* xl = reinterpret_cast<const float4*>(xb);
+    const float4* xh = reinterpret_cast<const float4*>(xb + 32);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const float4 a = xl[t];
+        const float4 b = xh[t];
+        const uint32_t v = w[t];
+        acc += (ds0 * (float)((v >> 0) & 15) - dm0) * a.x;
+        acc += (ds0 * (float)((v >> 8) & 15) - dm0) * a.y;
+        acc += (ds0 * (float)((v >> 16) & 15) - dm0) * a.z;
+        acc += (ds0 * (float)((v >> 24) & 15) - dm0) * a.w;
+        acc += (ds1 * (float)((v >> 4) & 15) - dm1) * b.x;
+        acc += (ds1 * (float)((v >> 12) & 15) - dm1) * b.y;
+        acc += (ds1 * (float)((v >> 20) & 15) - dm1) * b.z;
+        acc += (ds1 * (float)((v >> 28) & 15) - dm1) * b.w;
+    }
+    return acc;
+}
+
+template <int MODE, int R, bool LDS>
+__global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t* __restrict__ w0,
+                                                                    const uint8_t* __restrict__ w1,
+                                                                    const float* __restrict__ x,
+                                                                    const float* residual, float* y, int K, int N) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* xs = reinterpret_cast<float*>(smem);
+    constexpr int M = (MODE == kGateUp) ? 2 : 1;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int s = lane >> 2;
+    const int p = lane & 3;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ4KBytes;
+    const int rows_per_iter = gridDim.x * kWavesPerWg * R;
+
+    if (LDS) {
+        for (int i = threadIdx.x * 4; i < K; i += kThreads * 4)
+            *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+        __syncthreads();
+    }
+    const float* xv = LDS ? xs : x;
+
+    for (int row0 = (blockIdx.x * kWavesPerWg + wave) * R; row0 < N; row0 += rows_per_iter) {
+        float acc[M][R];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        for (int sb0 = 0; sb0 < nsb; sb0 += kSbPerStep) {
+            const int sb = sb0 + s;
+            if (sb < nsb) {
+                const float* xb = xv + sb * kQK + 64 * p;
+                Q4KUnit u[M][R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int row = min(row0 + r, N - 1);
+                    u[0][r] = q4k_load_unit(w0 + (size_t)row * row_bytes + (size_t)sb * kQ4KBytes, p);
+                    if (MODE == kGateUp)
+                        u[M - 1][r] = q4k_load_unit(w1 + (size_t)row * row_bytes + (size_t)sb * kQ4KBytes, p);
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[m][r] = q4k_f32_unit_dot<LDS>(u[m][r], p, xb, acc[m][r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float g = wave_sum(acc[0][r]);
+            const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
+            const int row = row0 + r;
+            if (lane == r && row < N) {
+                if (MODE == kPlain) y[row] = g;
+                else if (MODE == kResidual) y[row] = g + residual[row];
+                else y[row] = g / (1.0f + expf(-g)) * v;
+            }
+        }
+    }
+}
+
+// ── launch helpers ────────────────────────────────────────────────────────
+static inline int gemv_grid(int N, int rows_per_wg) {
+    const int groups = (N + rows_per_wg - 1) / rows_per_wg;
+    const int cap = device_cu_count() * 8;
+    return groups < cap ? groups : cap;
+}
+
+template <int MODE>
+static hipError_t launch_q8(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
+                            hipStream_t st) {
+    constexpr int R = (MODE == kGateUp) ? 2 : 4;
+    const int grid = gemv_grid(N, kWavesPerWg * R);
+    hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, R>), dim3(grid), dim3(kThreads), q8_lds_bytes(K), st,
+                       static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), x, res, y, K, N);
+    return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t launch_f32(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
+                             hipStream_t st) {
+    constexpr int R = (MODE == kGateUp) ? 2 : 4;
+    const int grid = gemv_grid(N, kWavesPerWg * R);
+    const size_t lds = (size_t)K * sizeof(float);
+    if (lds <= 65536) {
+        hipLaunchKernelGGL((rf_q4k_f32_gemv_kernel<MODE, R, true>), dim3(grid), dim3(kThreads), lds, st,
+                           static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), x, res, y, K, N);
+    } else {
+        hipLaunchKernelGGL((rf_q4k_f32_gemv_kernel<MODE, R, false>), dim3(grid), dim3(kThreads), 0, st,
+                           static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), x, res, y, K, N);
+    }
+    return hipGetLastError();
+}
+
+// ── debug / parity entry points (same device code as the GEMV) ───────────
+__global__ __launch_bounds__(kThreads) void rf_q8_0_quantize_kernel(const float* __restrict__ x, int K,
+                                                                     uint16_t* __restrict__ d_out,
+                                                                     int8_t* __restrict__ qs_out,
+                                                                     int* __restrict__ sum_out) {
+    const int lane32 = threadIdx.x & 31;
+    const int b = (blockIdx.x * kThreads + threadIdx.x) >> 5;
+    if (b >= (K >> 5)) return;  // whole half-waves exit together
+    float d;
+    int8_t q;
+    int s;
+    uint16_t dbits;
+    q8_0_quantize_block(x[b * 32 + lane32], lane32, &d, &q, &s, &dbits);
+    qs_out[b * 32 + lane32] = q;
+    if (lane32 == 0) {
+        d_out[b] = dbits;
+        sum_out[b] = s;
+    }
+}
+
+// int_dot[row*(K/32) + sub-block] for every row and sub-block, computed
+// with the GEMV's own load/unpack/dot path.
+__global__ __launch_bounds__(kThreads) void rf_q4k_q8_partials_kernel(const uint8_t* __restrict__ w,
+                                                                       const float* __restrict__ x,
+                                                                       int* __restrict__ int_dot, int K, int N) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Q8Lds q8 = q8_lds_carve(smem, K);
+    q8_0_quantize_to_lds(x, K, q8);
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int s = lane >> 2, p = lane & 3;
+    const int nsb = K / kQK;
+    for (int row = blockIdx.x * kWavesPerWg + wave; row < N; row += gridDim.x * kWavesPerWg) {
+        for (int sb0 = 0; sb0 < nsb; sb0 += kSbPerStep) {
+            const int sb = sb0 + s;
+            if (sb < nsb) {
+                const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + sb * kQK + 64 * p);
+                u32x4 xlo[2] = {xs[0], xs[1]};
+                u32x4 xhi[2] = {xs[2], xs[3]};
+                Q4KUnit u = q4k_load_unit(w + ((size_t)row * nsb + sb) * kQ4KBytes, p);
+                int dlo, dhi;
+                q4k_int_dots(u, xlo, xhi, &dlo, &dhi);
+                int_dot[(size_t)row * (K / 32) + sb * 8 + 2 * p] = dlo;
+                int_dot[(size_t)row * (K / 32) + sb * 8 + 2 * p + 1] = dhi;
+            }
+        }
+    }
+}
+
+}  // namespace rf
+
+using namespace rf;
+
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shape/pointer validation of the reference launchers
+// (q4_k_q8_inline.hip:388-390, 413-415, 438-443; q4_k_gemv.hip:489-493,
+// 525-526, 556-557).  Additionally the weights must be 16-byte aligned: the
+// kernels stream them with 16-byte loads (GGUF tensors are uploaded into
+// their own hipMalloc buffers, which are 256-byte aligned).
+extern "C" hipError_t gemv_q4_k_f32_q8_inline_launch(const void* weights_q4_k, const float* input, float* output,
+                                                     int n_rows, int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    return launch_q8<kPlain>(weights_q4_k, nullptr, input, nullptr, output, n_rows, ncols_dst, stream);
+}
+
+extern "C" hipError_t gemv_q4_k_f32_q8_inline_residual_launch(const void* weights_q4_k, const float* input,
+                                                              const float* residual, float* output, int n_rows,
+                                                              int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || residual == nullptr) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    return launch_q8<kResidual>(weights_q4_k, nullptr, input, residual, output, n_rows, ncols_dst, stream);
+}
+
+extern "C" hipError_t gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch(const void* weights_gate_q4_k,
+                                                                    const void* weights_up_q4_k, const float* input,
+                                                                    float* swiglu_out, int n_rows, int ncols_dst,
+                                                                    hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (weights_gate_q4_k == nullptr || weights_up_q4_k == nullptr) return hipErrorInvalidValue;
+    if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!aligned16(weights_gate_q4_k) || !aligned16(weights_up_q4_k)) return hipErrorInvalidValue;
+    return launch_q8<kGateUp>(weights_gate_q4_k, weights_up_q4_k, input, nullptr, swiglu_out, n_rows, ncols_dst,
+                              stream);
+}
+
+extern "C" hipError_t gemv_q4_k_f32_launch(const void* weights_q4_k, const float* input, float* output, int n_rows,
+                                           int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    return launch_f32<kPlain>(weights_q4_k, nullptr, input, nullptr, output, n_rows, ncols_dst, stream);
+}
+
+extern "C" hipError_t gemv_q4_k_f32_residual_launch(const void* weights_q4_k, const float* input,
+                                                    const float* residual, float* output, int n_rows, int ncols_dst,
+                                                    hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || residual == nullptr) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    return launch_f32<kResidual>(weights_q4_k, nullptr, input, residual, output, n_rows, ncols_dst, stream);
+}
+
+extern "C" hipError_t gemv_gate_up_swiglu_q4_k_f32_launch(const void* weights_gate_q4_k, const void* weights_up_q4_k,
+                                                          const float* input, float* swiglu_out, int n_rows,
+                                                          int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (weights_gate_q4_k == nullptr || weights_up_q4_k == nullptr) return hipErrorInvalidValue;
+    if (!aligned16(weights_gate_q4_k) || !aligned16(weights_up_q4_k)) return hipErrorInvalidValue;
+    return launch_f32<kGateUp>(weights_gate_q4_k, weights_up_q4_k, input, nullptr, swiglu_out, n_rows, ncols_dst,
+                               stream);
+}
+
+// Parity probes: Q8_0 blocks (fp16 bits, int8, int sum) and the per
+// sub-block integer dots exactly as the Q8-inline GEMV forms them.
+extern "C" hipError_t rf_q8_0_quantize_launch(const float* input, uint16_t* d_out, int8_t* qs_out, int* sum_out,
+                                              int n, hipStream_t stream) {
+    if (n <= 0 || (n % 32) != 0 || !input || !d_out || !qs_out || !sum_out) return hipErrorInvalidValue;
+    const int grid = (n / 32 + 7) / 8;
+    hipLaunchKernelGGL(rf_q8_0_quantize_kernel, dim3(grid), dim3(kThreads), 0, stream, input, n, d_out, qs_out,
+                       sum_out);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t rf_q4_k_q8_int_dots_launch(const void* weights_q4_k, const float* input, int* int_dot,
+                                                 int n_rows, int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!weights_q4_k || !input || !int_dot || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    const int grid = gemv_grid(ncols_dst, kWavesPerWg);
+    hipLaunchKernelGGL(rf_q4k_q8_partials_kernel, dim3(grid), dim3(kThreads), q8_lds_bytes(n_rows), stream,
+                       static_cast<const uint8_t*>(weights_q4_k), input, int_dot, n_rows, ncols_dst);
+    return hipGetLastError();
+}

@@ -1,0 +1,183 @@
+// qk_common.h -- device-side building blocks shared by the CDNA4 (gfx950)
+// Q4_K / Q6_K GEMV and GEMM kernels.
+//
+// GGUF block layouts (kept byte-identical to ROCmForge, which uploads raw
+// GGUF bytes: src/gpu/weights.rs:415-419):
+//   Q4_K  144 B / 256 weights: half d @0, half dmin @2, 12 B packed 6-bit
+//         scales/mins @4, 128 B nibbles @16 (pair-interleaved: byte 32k+i
+//         holds element 64k+i in its low nibble, 64k+32+i in its high one).
+//   Q6_K  210 B / 256 weights: ql[128] @0, qh[64] @128, int8 scales[16]
+//         @192, half d @208.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rf {
+
+constexpr int kQK = 256;          // weights per super-block
+constexpr int kQ4KBytes = 144;
+constexpr int kQ6KBytes = 210;
+constexpr int kWave = 64;         // CDNA wavefront
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 16-byte load with only 2-byte alignment promised.  gfx950 runs with the
+// unaligned access mode that ROCm enables, and the backend lowers this to a
+// single global_load_dwordx4.
+struct __attribute__((packed, aligned(2))) Un16 { u32x4 v; };
+struct __attribute__((packed, aligned(2))) Un8 { u32x2 v; };
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+    return reinterpret_cast<const Un16*>(p)->v;
+}
+__device__ __forceinline__ u32x2 ld8(const uint8_t* p) {
+    return reinterpret_cast<const Un8*>(p)->v;
+}
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    __half_raw r;
+    r.x = (unsigned short)(bits & 0xFFFFu);
+    return __half2float(__half(r));
+}
+
+// Sum over the 64 lanes of a wave (butterfly: every lane ends with the sum).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Q4_K (scale, min) for sub-blocks 2p and 2p+1, from the three scale words
+// (s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11]).
+// Same bit layout as ggml get_scale_min_k4 (q4_k_q8_inline.hip:49-59):
+//   j<4 : sc = s[j]&63,                     m = s[j+4]&63
+//   j>=4: sc = (s[j+4]&15) | (s[j-4]>>6)<<4, m = (s[j+4]>>4) | (s[j]>>6)<<4
+// With j' = j&3 both cases read byte j' of s0/s1/s2, so the lane-variable
+// index turns into shifts and one select instead of a dynamic byte array.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int p,
+                                                   int* sc0, int* m0, int* sc1, int* m1) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int jj = (2 * p + h) & 3;
+        const uint32_t sh = 8u * (uint32_t)jj;
+        const int by = (int)((s0 >> sh) & 0xFFu);
+        const int bz = (int)((s1 >> sh) & 0xFFu);
+        const int bw = (int)((s2 >> sh) & 0xFFu);
+        const bool lo = p < 2;
+        const int sc = lo ? (by & 63) : ((bw & 15) | ((by >> 6) << 4));
+        const int mn = lo ? (bz & 63) : ((bw >> 4) | ((bz >> 6) << 4));
+        if (h == 0) { *sc0 = sc; *m0 = mn; } else { *sc1 = sc; *m1 = mn; }
+    }
+}
+
+// ── Q8_0 activation quantisation into LDS ────────────────────────────────
+// Semantics restated from q4_k_q8_inline.hip:141-161 (bit-exact):
+//   amax = max|x| over 32; scale = fmaxf(amax/127, 1e-30); d = half(scale);
+//   inv = 1/float(d); q = (int8) trunc(fminf(fmaxf(x*inv, -127), 127)).
+// Layout chosen for wave64 consumers: qs[K] int8 contiguous, xd[K/32] as
+// float(d), qsum[K/32] = sum of the 32 int8 (exact int; computed once per
+// block here instead of once per row as the reference does).
+// Each half-wave (32 lanes) owns one 32-element block per step.
+struct Q8Lds {
+    int8_t* qs;
+    float* xd;
+    int* qsum;
+};
+
+__device__ __forceinline__ void q8_0_quantize_block(float v, int lane32, float* d_out, int8_t* q_out,
+                                                    int* sum_out, uint16_t* dbits_out) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+    const float scale = fmaxf(amax / 127.0f, 1e-30f);
+    const __half dh = __float2half(scale);
+    const float sf = __half2float(dh);
+    const float inv = 1.0f / sf;
+    const float qf = fminf(fmaxf(v * inv, -127.0f), 127.0f);
+    const int q = (int)qf;  // truncation toward zero, |qf| <= 127
+    int s = q;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+    *d_out = sf;
+    *q_out = (int8_t)q;
+    *sum_out = s;
+    *dbits_out = __half_as_ushort(dh);
+    (void)lane32;
+}
+
+// Whole-vector quantisation by a 256-thread workgroup (8 half-waves).
+__device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x, int K, Q8Lds lds) {
+    const int tid = threadIdx.x;
+    const int lane32 = tid & 31;
+    const int nblk = K >> 5;
+
+    for (int b = tid >> 5; b < nblk; b += (int)(blockDim.x >> 5)) {
+        const float v = x[b * 32 + lane32];
+        float d;
+        int8_t q;
+        int s;
+        uint16_t dbits;
+        q8_0_quantize_block(v, lane32, &d, &q, &s, &dbits);
+        lds.qs[b * 32 + lane32] = q;
+        if (lane32 == 0) {
+            lds.xd[b] = d;
+            lds.qsum[b] = s;
+        }
+    }
+}
+
+// ── Q4_K × Q8_0 per-lane work unit ───────────────────────────────────────
+// A lane owns nibble pair p (bytes 32p..32p+31 of qs) of one super-block:
+// sub-blocks 2p (low nibbles) and 2p+1 (high nibbles), 64 weights.  Four
+// lanes cover a super-block; a wave covers 16 super-blocks per row step.
+struct Q4KUnit {
+    u32x4 hdr;      // d | dmin<<16, scales[0..11]
+    u32x4 qa, qb;   // qs bytes 32p .. 32p+31
+};
+
+__device__ __forceinline__ Q4KUnit q4k_load_unit(const uint8_t* blk, int p) {
+    Q4KUnit u;
+    u.hdr = *reinterpret_cast<const u32x4*>(blk);
+    const u32x4* q = reinterpret_cast<const u32x4*>(blk + 16 + 32 * p);
+    u.qa = q[0];
+    u.qb = q[1];
+    return u;
+}
+
+// Integer dots of the lane's 64 nibbles against the matching Q8 bytes
+// (x8lo = 32 int8 of sub-block 2p, x8hi = 32 int8 of sub-block 2p+1).
+// Exact restatement of q4_k_q8_inline.hip:68-95 (int_dot = Σ nib*q8),
+// four products per v_dot4_i32_i8 (nibbles 0..15 are non-negative int8).
+__device__ __forceinline__ void q4k_int_dots(const Q4KUnit& u, const u32x4 x8lo[2], const u32x4 x8hi[2],
+                                             int* dot_lo, int* dot_hi) {
+    int lo = 0, hi = 0;
+    const uint32_t w[8] = {u.qa.x, u.qa.y, u.qa.z, u.qa.w, u.qb.x, u.qb.y, u.qb.z, u.qb.w};
+    const uint32_t a[8] = {x8lo[0].x, x8lo[0].y, x8lo[0].z, x8lo[0].w, x8lo[1].x, x8lo[1].y, x8lo[1].z, x8lo[1].w};
+    const uint32_t b[8] = {x8hi[0].x, x8hi[0].y, x8hi[0].z, x8hi[0].w, x8hi[1].x, x8hi[1].y, x8hi[1].z, x8hi[1].w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        lo = __builtin_amdgcn_sdot4((int)(w[t] & 0x0F0F0F0Fu), (int)a[t], lo, false);
+        hi = __builtin_amdgcn_sdot4((int)((w[t] >> 4) & 0x0F0F0F0Fu), (int)b[t], hi, false);
+    }
+    *dot_lo = lo;
+    *dot_hi = hi;
+}
+
+// Sub-block combine, the reference's fp32 expression
+// (q4_k_q8_inline.hip:119-122):
+//   acc += x_scale * (d*sc*int_dot - dmin*m*q8_sum)
+__device__ __forceinline__ float q4k_q8_combine(float acc, float xd, float d, float dmin, int sc, int mn,
+                                                int dot, int qsum) {
+    return acc + xd * (d * (float)sc * (float)dot - dmin * (float)mn * (float)qsum);
+}
+
+// Device CU count, cached per device (host side).
+int device_cu_count();
+
+}  // namespace rf

@@ -1,0 +1,179 @@
+"""GPU parity of the decode GEMVs, through the C ABI.
+
+Bars:
+  * Q8_0 activation blocks and per-sub-block int32 dots: bit-exact against the
+    oracle (oracle/qk_oracle.c, itself pinned in tests/test_oracle.py).
+  * fp32 outputs against the oracle's float64 value of the same integer
+    partials: TOLERANCE below, checked normwise and per element.
+  * Where the reference's own kernels were built (oracle/_ref), the same
+    inputs through them agree to the same tolerance.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from rocmforge_amd import synth
+from tests import gpu_util as G
+
+pytestmark = pytest.mark.gpu
+
+# rel = max|y - y_ref| / max|y_ref| <= 1e-5, and per element
+# |y - y_ref| <= 1e-6 * max|y_ref| + 1e-5 * |y_ref|  (fp32 accumulation order
+# differs from the float64 oracle; the absolute term is scaled by the output
+# magnitude because the outputs are O(10) for these weight distributions)
+REL_TOL = 1e-5
+ELEM_TOL = 1.0
+
+SHAPES = [(256, 1), (256, 64), (512, 100), (4096, 4096), (1024, 6144 + 13), (14336, 96), (30720, 40)]
+
+
+def _check(y, ref, what):
+    rel, elem = G.gemv_error(y, ref)
+    print(f"{what}: rel={rel:.3e} elem={elem:.3f}", flush=True)
+    assert rel <= REL_TOL and elem <= ELEM_TOL, f"{what}: rel {rel:.3e} elem {elem:.3f}"
+
+
+@pytest.mark.parametrize("k", [256, 4096, 14336, 30720])
+def test_q8_0_quantize_bit_exact(rf, dev, k):
+    x = synth.activations(k, seed=k)
+    x[:32] = 0.0                      # all-zero block edge case
+    x[64:96] *= 1e-33                 # underflowing scale
+    dx = G.to_dev(x)
+    d = G.empty(k // 32, torch.int16)
+    q = G.empty(k, torch.int8)
+    s = G.empty(k // 32, torch.int32)
+    G.call(rf.rf_q8_0_quantize_launch, G.ptr(dx), G.ptr(d), G.ptr(q), G.ptr(s), k)
+    dref, qref = O.q8_0_quantize(x)
+    assert np.array_equal(G.host(d).view(np.uint16), dref)
+    assert np.array_equal(G.host(q), qref)
+    assert np.array_equal(G.host(s), qref.reshape(-1, 32).astype(np.int32).sum(axis=1))
+
+
+@pytest.mark.parametrize("k,n", [(256, 3), (4096, 64), (14336, 20)])
+def test_q4k_int_dots_bit_exact(rf, dev, k, n):
+    w = synth.q4_k_weights(n, k, seed=k + n)
+    x = synth.activations(k, seed=k - n)
+    dw, dx = G.to_dev(w), G.to_dev(x)
+    dots = G.empty(n * (k // 32), torch.int32)
+    G.call(rf.rf_q4_k_q8_int_dots_launch, G.ptr(dw), G.ptr(dx), G.ptr(dots), k, n)
+    _, xq = O.q8_0_quantize(x)
+    ref, _ = O.q4k_q8_partials(w, xq, k, n)
+    assert np.array_equal(G.host(dots).reshape(n, -1), ref)
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_q4k_q8_inline_gemv(rf, dev, k, n):
+    w = synth.q4_k_weights(n, k, seed=1000 + n)
+    x = synth.activations(k, seed=2000 + k)
+    dw, dx = G.to_dev(w), G.to_dev(x)
+    y = G.empty(n, torch.float32)
+    G.call(rf.gemv_q4_k_f32_q8_inline_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    _check(G.host(y), O.gemv_q4k_q8(w, x, k, n), f"q8 gemv {n}x{k}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (512, 77)])
+def test_q4k_q8_inline_residual_in_place(rf, dev, k, n):
+    w = synth.q4_k_weights(n, k, seed=7)
+    x = synth.activations(k, seed=8)
+    r = synth.activations(n, seed=9) * 10
+    dw, dx, dr = G.to_dev(w), G.to_dev(x), G.to_dev(r)
+    # output aliases residual (forward.rs in-place O-proj)
+    G.call(rf.gemv_q4_k_f32_q8_inline_residual_launch, G.ptr(dw), G.ptr(dx), G.ptr(dr), G.ptr(dr), k, n)
+    _check(G.host(dr), O.gemv_q4k_q8(w, x, k, n) + r.astype(np.float64), f"q8 residual {n}x{k}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 14336), (256, 50), (14336, 64)])
+def test_q4k_q8_gate_up_swiglu(rf, dev, k, n):
+    wg = synth.q4_k_weights(n, k, seed=11)
+    wu = synth.q4_k_weights(n, k, seed=12)
+    x = synth.activations(k, seed=13)
+    dg, du, dx = G.to_dev(wg), G.to_dev(wu), G.to_dev(x)
+    out = G.empty(n, torch.float32)
+    G.call(rf.gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch, G.ptr(dg), G.ptr(du), G.ptr(dx), G.ptr(out), k, n)
+    ref = O.swiglu(O.gemv_q4k_q8(wg, x, k, n), O.gemv_q4k_q8(wu, x, k, n))
+    _check(G.host(out), ref, f"gate_up {n}x{k}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (14336, 64), (512, 33), (40960, 8)])
+def test_q4k_fp32_family(rf, dev, k, n):
+    w = synth.q4_k_weights(n, k, seed=21)
+    w2 = synth.q4_k_weights(n, k, seed=22)
+    x = synth.activations(k, seed=23)
+    r = synth.activations(n, seed=24)
+    dw, dw2, dx, dr = G.to_dev(w), G.to_dev(w2), G.to_dev(x), G.to_dev(r)
+    y = G.empty(n, torch.float32)
+    ref = O.gemv_q4k_f32(w, x, k, n)
+    G.call(rf.gemv_q4_k_f32_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    _check(G.host(y), ref, f"f32 gemv {n}x{k}")
+    G.call(rf.gemv_q4_k_f32_residual_launch, G.ptr(dw), G.ptr(dx), G.ptr(dr), G.ptr(y), k, n)
+    _check(G.host(y), ref + r, f"f32 residual {n}x{k}")
+    G.call(rf.gemv_gate_up_swiglu_q4_k_f32_launch, G.ptr(dw), G.ptr(dw2), G.ptr(dx), G.ptr(y), k, n)
+    _check(G.host(y), O.swiglu(ref, O.gemv_q4k_f32(w2, x, k, n)), f"f32 gate_up {n}x{k}")
+
+
+@pytest.mark.parametrize("k,n", [(256, 1), (4096, 1024), (14336, 4096), (4096, 333), (768, 64), (40960, 16)])
+def test_q6k_gemv(rf, dev, k, n):
+    w = synth.q6_k_weights(n, k, seed=31 + n)
+    x = synth.activations(k, seed=32 + k)
+    dw, dx = G.to_dev(w), G.to_dev(x)
+    y = G.empty(n, torch.float32)
+    G.call(rf.gemv_q6_k_f32_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    _check(G.host(y), O.gemv_q6k(w, x, k, n), f"q6 gemv {n}x{k}")
+
+
+def test_q6k_unaligned_blocks(rf, dev):
+    # K = 768 gives 630-byte rows: blocks start at every even offset mod 16
+    k, n = 768, 40
+    w = synth.q6_k_weights(n, k, seed=5)
+    buf = np.zeros(w.size + 2, np.uint8)
+    buf[2:] = w.ravel()               # 2-byte aligned start
+    dbuf = G.to_dev(buf)
+    x = synth.activations(k, seed=6)
+    dx = G.to_dev(x)
+    y = G.empty(n, torch.float32)
+    G.call(rf.gemv_q6_k_f32_launch, ctypes.c_void_p(dbuf.data_ptr() + 2), G.ptr(dx), G.ptr(y), k, n)
+    _check(G.host(y), O.gemv_q6k(w, x, k, n), "q6 unaligned")
+
+
+# ---- the reference's own kernels (oracle/_ref), same inputs -------------------
+
+def _ref_lib():
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref not built (needs the reference tree at build time)")
+    lib = ctypes.CDLL(str(O.REF_LIB), mode=ctypes.RTLD_LOCAL)
+    return lib
+
+
+@pytest.mark.parametrize("fmt,k,n", [("q8", 4096, 4096), ("q8", 14336, 512), ("q6", 14336, 4096),
+                                     ("q6", 4096, 1024), ("f32", 4096, 512), ("gu", 4096, 14336)])
+def test_against_reference_kernels(rf, dev, fmt, k, n):
+    ref = _ref_lib()
+    gen = synth.q6_k_weights if fmt == "q6" else synth.q4_k_weights
+    w = gen(n, k, seed=99)
+    w2 = synth.q4_k_weights(n, k, seed=98)
+    x = synth.activations(k, seed=97)
+    dw, dw2, dx = G.to_dev(w), G.to_dev(w2), G.to_dev(x)
+    y_ours = G.empty(n, torch.float32)
+    y_ref = G.empty(n, torch.float32)
+    name = {"q8": "gemv_q4_k_f32_q8_inline_launch", "q6": "gemv_q6_k_f32_launch",
+            "f32": "gemv_q4_k_f32_launch", "gu": "gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch"}[fmt]
+    for lib, y in ((rf, y_ours), (ref, y_ref)):
+        fn = getattr(lib, name)
+        if fmt == "gu":
+            fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 2 + [ctypes.c_void_p]
+            G.call(fn, G.ptr(dw), G.ptr(dw2), G.ptr(dx), G.ptr(y), k, n)
+        else:
+            fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 2 + [ctypes.c_void_p]
+            G.call(fn, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    a, b = G.host(y_ours).astype(np.float64), G.host(y_ref).astype(np.float64)
+    rel = np.abs(a - b).max() / np.abs(b).max()
+    print(f"ours vs reference kernel {fmt} {n}x{k}: rel={rel:.3e}", flush=True)
+    assert rel <= 2 * REL_TOL
+    # and the reference kernel itself sits within the same bar of the oracle
+    oref = {"q8": lambda: O.gemv_q4k_q8(w, x, k, n), "q6": lambda: O.gemv_q6k(w, x, k, n),
+            "f32": lambda: O.gemv_q4k_f32(w, x, k, n),
+            "gu": lambda: O.swiglu(O.gemv_q4k_q8(w, x, k, n), O.gemv_q4k_q8(w2, x, k, n))}[fmt]()
+    _check(b, oref, f"reference kernel vs oracle {fmt}")
