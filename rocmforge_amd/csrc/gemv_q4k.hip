@@ -85,16 +85,18 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
-    const int rows_per_iter = gridDim.x * kWavesPerWg * R;
+    int row_begin, row_end;
+    wave_row_range(N, blockIdx.x * kWavesPerWg + wave, gridDim.x * kWavesPerWg, &row_begin, &row_end);
+    const int last = max(row_end - 1, 0);
 
-    // Software pipeline over (row group, 16-super-block step): the loads of
-    // step i+1 are in flight while step i is computed.  The first step's
-    // loads are issued before the activation quantisation, which hides the
-    // quantisation behind HBM latency.
-    int row0 = (blockIdx.x * kWavesPerWg + wave) * R;
+    // Software pipeline over (R-row group, 16-super-block step) of this
+    // wave's contiguous row range: the loads of step i+1 are in flight while
+    // step i is computed.  The first step's loads are issued before the
+    // activation quantisation, hiding it behind HBM latency.
+    int row0 = row_begin;
     int sb0 = 0;
     Q4KUnit cur[M][R];
-    if (row0 < N) q4k_load_step<M, R>(cur, w0, w1, row_bytes, row0, N, min(s, nsb - 1), p);
+    if (row0 < row_end) q4k_load_step<M, R>(cur, w0, w1, row_bytes, row0, last + 1, min(s, nsb - 1), p);
 
     q8_0_quantize_to_lds(x, K, q8);
     __syncthreads();
@@ -105,14 +107,14 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-    while (row0 < N) {
+    while (row0 < row_end) {
         int nrow0 = row0, nsb0 = sb0 + kSbPerStep;
         if (nsb0 >= nsb) {
             nsb0 = 0;
-            nrow0 += rows_per_iter;
+            nrow0 += R;
         }
         Q4KUnit nxt[M][R];
-        if (nrow0 < N) q4k_load_step<M, R>(nxt, w0, w1, row_bytes, nrow0, N, min(nsb0 + s, nsb - 1), p);
+        if (nrow0 < row_end) q4k_load_step<M, R>(nxt, w0, w1, row_bytes, nrow0, last + 1, min(nsb0 + s, nsb - 1), p);
 
         const int sb = sb0 + s;
         const bool live = sb < nsb;
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
                 const float g = wave_sum(acc[0][r]);
                 const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
                 const int row = row0 + r;
-                if (lane == r && row < N) {
+                if (lane == r && row < row_end) {
                     if (MODE == kPlain) {
                         y[row] = g;
                     } else if (MODE == kResidual) {
@@ -206,16 +208,16 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
-    const int rows_per_iter = gridDim.x * kWavesPerWg * R;
+    int row_begin, row_end;
+    wave_row_range(N, blockIdx.x * kWavesPerWg + wave, gridDim.x * kWavesPerWg, &row_begin, &row_end);
 
     if (LDS) {
-        for (int i = threadIdx.x * 4; i < K; i += kThreads * 4)
-            *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+        stage_f32_to_lds(x, K, xs);
         __syncthreads();
     }
     const float* xv = LDS ? xs : x;
 
-    for (int row0 = (blockIdx.x * kWavesPerWg + wave) * R; row0 < N; row0 += rows_per_iter) {
+    for (int row0 = row_begin; row0 < row_end; row0 += R) {
         float acc[M][R];
 #pragma unroll
         for (int m = 0; m < M; ++m)
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
                 Q4KUnit u[M][R];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const int row = min(row0 + r, N - 1);
+                    const int row = min(row0 + r, row_end - 1);
                     u[0][r] = q4k_load_unit(w0 + (size_t)row * row_bytes + (size_t)sb * kQ4KBytes, p);
                     if (MODE == kGateUp)
                         u[M - 1][r] = q4k_load_unit(w1 + (size_t)row * row_bytes + (size_t)sb * kQ4KBytes, p);
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
             const float g = wave_sum(acc[0][r]);
             const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
             const int row = row0 + r;
-            if (lane == r && row < N) {
+            if (lane == r && row < row_end) {
                 if (MODE == kPlain) y[row] = g;
                 else if (MODE == kResidual) y[row] = g + residual[row];
                 else y[row] = g / (1.0f + expf(-g)) * v;
@@ -254,17 +256,20 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
 }
 
 // ── launch helpers ────────────────────────────────────────────────────────
-static inline int gemv_grid(int N, int rows_per_wg) {
-    const int groups = (N + rows_per_wg - 1) / rows_per_wg;
-    const int cap = device_cu_count() * 8;
-    return groups < cap ? groups : cap;
+// Grid: a fixed number of workgroups per CU (every wave then streams an
+// equal contiguous share of the rows), fewer when N is too small to give each
+// wave at least `min_rows` rows.
+static inline int gemv_grid(int N, int min_rows) {
+    const int cap = device_cu_count() * gemv_wg_per_cu();
+    const int need = (N + kWavesPerWg * min_rows - 1) / (kWavesPerWg * min_rows);
+    return need < cap ? need : cap;
 }
 
 template <int MODE>
 static hipError_t launch_q8(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
                             hipStream_t st) {
     constexpr int R = (MODE == kGateUp) ? 2 : 4;
-    const int grid = gemv_grid(N, kWavesPerWg * R);
+    const int grid = gemv_grid(N, 1);
     hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, R>), dim3(grid), dim3(kThreads), q8_lds_bytes(K), st,
                        static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), x, res, y, K, N);
     return hipGetLastError();
@@ -274,7 +279,7 @@ template <int MODE>
 static hipError_t launch_f32(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
                              hipStream_t st) {
     constexpr int R = (MODE == kGateUp) ? 2 : 4;
-    const int grid = gemv_grid(N, kWavesPerWg * R);
+    const int grid = gemv_grid(N, 1);
     const size_t lds = (size_t)K * sizeof(float);
     if (lds <= 65536) {
         hipLaunchKernelGGL((rf_q4k_f32_gemv_kernel<MODE, R, true>), dim3(grid), dim3(kThreads), lds, st,
@@ -287,22 +292,23 @@ static hipError_t launch_f32(const void* w0, const void* w1, const float* x, con
 }
 
 // ── debug / parity entry points (same device code as the GEMV) ───────────
+// Each workgroup quantises a slice of kQuantSlice elements with the GEMV's
+// own LDS quantiser and copies the LDS image out.
+constexpr int kQuantSlice = 8192;
 __global__ __launch_bounds__(kThreads) void rf_q8_0_quantize_kernel(const float* __restrict__ x, int K,
                                                                      uint16_t* __restrict__ d_out,
                                                                      int8_t* __restrict__ qs_out,
                                                                      int* __restrict__ sum_out) {
-    const int lane32 = threadIdx.x & 31;
-    const int b = (blockIdx.x * kThreads + threadIdx.x) >> 5;
-    if (b >= (K >> 5)) return;  // whole half-waves exit together
-    float d;
-    int8_t q;
-    int s;
-    uint16_t dbits;
-    q8_0_quantize_block(x[b * 32 + lane32], lane32, &d, &q, &s, &dbits);
-    qs_out[b * 32 + lane32] = q;
-    if (lane32 == 0) {
-        d_out[b] = dbits;
-        sum_out[b] = s;
+    __shared__ __align__(16) uint8_t smem[kQuantSlice + kQuantSlice / 4];
+    const int base = blockIdx.x * kQuantSlice;
+    const int len = min(kQuantSlice, K - base);
+    const Q8Lds q8 = q8_lds_carve(smem, len);
+    q8_0_quantize_to_lds(x + base, len, q8);
+    __syncthreads();
+    for (int i = threadIdx.x; i < len; i += kThreads) qs_out[base + i] = q8.qs[i];
+    for (int b = threadIdx.x; b < len / 32; b += kThreads) {
+        d_out[base / 32 + b] = __half_as_ushort(__float2half(q8.xd[b]));
+        sum_out[base / 32 + b] = q8.qsum[b];
     }
 }
 
@@ -412,7 +418,7 @@ extern "C" hipError_t gemv_gate_up_swiglu_q4_k_f32_launch(const void* weights_ga
 extern "C" hipError_t rf_q8_0_quantize_launch(const float* input, uint16_t* d_out, int8_t* qs_out, int* sum_out,
                                               int n, hipStream_t stream) {
     if (n <= 0 || (n % 32) != 0 || !input || !d_out || !qs_out || !sum_out) return hipErrorInvalidValue;
-    const int grid = (n / 32 + 7) / 8;
+    const int grid = (n + kQuantSlice - 1) / kQuantSlice;
     hipLaunchKernelGGL(rf_q8_0_quantize_kernel, dim3(grid), dim3(kThreads), 0, stream, input, n, d_out, qs_out,
                        sum_out);
     return hipGetLastError();
@@ -422,7 +428,7 @@ extern "C" hipError_t rf_q4_k_q8_int_dots_launch(const void* weights_q4_k, const
                                                  int n_rows, int ncols_dst, hipStream_t stream) {
     if (n_rows <= 0 || ncols_dst <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows)) return hipErrorInvalidValue;
     if (!weights_q4_k || !input || !int_dot || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
-    const int grid = gemv_grid(ncols_dst, kWavesPerWg);
+    const int grid = gemv_grid(ncols_dst, 1);
     hipLaunchKernelGGL(rf_q4k_q8_partials_kernel, dim3(grid), dim3(kThreads), q8_lds_bytes(n_rows), stream,
                        static_cast<const uint8_t*>(weights_q4_k), input, int_dot, n_rows, ncols_dst);
     return hipGetLastError();

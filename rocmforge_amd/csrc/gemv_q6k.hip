@@ -94,23 +94,23 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ6KBytes;
-    const int rows_per_iter = gridDim.x * kQ6Waves * R;
+    int row_begin, row_end;
+    wave_row_range(N, blockIdx.x * kQ6Waves + wave, gridDim.x * kQ6Waves, &row_begin, &row_end);
 
-    int row0 = (blockIdx.x * kQ6Waves + wave) * R;
+    int row0 = row_begin;
     int sb0 = 0;
     Q6Unit cur[R];
     auto load_step = [&](Q6Unit(&u)[R], int r0, int sbc) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = min(r0 + r, N - 1);
+            const int row = min(r0 + r, row_end - 1);
             u[r] = q6k_load_unit(w + (size_t)row * row_bytes + (size_t)sbc * kQ6KBytes, p);
         }
     };
-    if (row0 < N) load_step(cur, row0, min(s, nsb - 1));
+    if (row0 < row_end) load_step(cur, row0, min(s, nsb - 1));
 
     if (LDS) {
-        for (int i = threadIdx.x * 4; i < K; i += kQ6Threads * 4)
-            *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+        stage_f32_to_lds(x, K, xs);
         __syncthreads();
     }
     const float* xv = LDS ? xs : x;
@@ -119,14 +119,14 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    while (row0 < N) {
+    while (row0 < row_end) {
         int nrow0 = row0, nsb0 = sb0 + kQ6SbPerStep;
         if (nsb0 >= nsb) {
             nsb0 = 0;
-            nrow0 += rows_per_iter;
+            nrow0 += R;
         }
         Q6Unit nxt[R];
-        if (nrow0 < N) load_step(nxt, nrow0, min(nsb0 + s, nsb - 1));
+        if (nrow0 < row_end) load_step(nxt, nrow0, min(nsb0 + s, nsb - 1));
 
         const int sb = sb0 + s;
         if (sb < nsb) {
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float g = wave_sum(acc[r]);
-                if (lane == r && row0 + r < N) y[row0 + r] = g;
+                if (lane == r && row0 + r < row_end) y[row0 + r] = g;
                 acc[r] = 0.0f;
             }
         }
@@ -160,10 +160,10 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
     if (n_rows % kQK != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
-    constexpr int R = 4;
-    const int groups = (ncols_dst + kQ6Waves * R - 1) / (kQ6Waves * R);
-    const int cap = device_cu_count() * 8;
-    const int grid = groups < cap ? groups : cap;
+    constexpr int R = 2;
+    const int need = (ncols_dst + kQ6Waves - 1) / kQ6Waves;
+    const int cap = device_cu_count() * gemv_wg_per_cu();
+    const int grid = need < cap ? need : cap;
     const size_t lds = (size_t)n_rows * sizeof(float);
     const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
     if (lds <= 65536) {

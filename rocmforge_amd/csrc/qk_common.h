@@ -90,46 +90,81 @@ struct Q8Lds {
     int* qsum;
 };
 
-__device__ __forceinline__ void q8_0_quantize_block(float v, int lane32, float* d_out, int8_t* q_out,
-                                                    int* sum_out, uint16_t* dbits_out) {
-    float amax = fabsf(v);
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-    const float scale = fmaxf(amax / 127.0f, 1e-30f);
-    const __half dh = __float2half(scale);
-    const float sf = __half2float(dh);
-    const float inv = 1.0f / sf;
-    const float qf = fminf(fmaxf(v * inv, -127.0f), 127.0f);
-    const int q = (int)qf;  // truncation toward zero, |qf| <= 127
-    int s = q;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
-    *d_out = sf;
-    *q_out = (int8_t)q;
-    *sum_out = s;
-    *dbits_out = __half_as_ushort(dh);
-    (void)lane32;
-}
-
-// Whole-vector quantisation by a 256-thread workgroup (8 half-waves).
+// Whole-vector quantisation by one workgroup.  Each thread quantises 8
+// consecutive elements (two float4 loads); four neighbouring lanes form one
+// 32-element block and combine amax / int sums with two xor-shuffles.  The
+// loads of up to four passes are issued before any is consumed, so the
+// quantisation costs about one L2 round trip per 4*8*blockDim elements.
 __device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x, int K, Q8Lds lds) {
-    const int tid = threadIdx.x;
-    const int lane32 = tid & 31;
-    const int nblk = K >> 5;
-
-    for (int b = tid >> 5; b < nblk; b += (int)(blockDim.x >> 5)) {
-        const float v = x[b * 32 + lane32];
-        float d;
-        int8_t q;
-        int s;
-        uint16_t dbits;
-        q8_0_quantize_block(v, lane32, &d, &q, &s, &dbits);
-        lds.qs[b * 32 + lane32] = q;
-        if (lane32 == 0) {
-            lds.xd[b] = d;
-            lds.qsum[b] = s;
+    const int per_pass = (int)blockDim.x * 8;
+    constexpr int kBatch = 4;
+    for (int base = 0; base < K; base += kBatch * per_pass) {
+        float4 v[kBatch][2];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int idx = base + u * per_pass + (int)threadIdx.x * 8;
+            const int src = idx < K ? idx : 0;   // out-of-range lanes re-read x[0..7], never stored
+            v[u][0] = *reinterpret_cast<const float4*>(x + src);
+            v[u][1] = *reinterpret_cast<const float4*>(x + src + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int idx = base + u * per_pass + (int)threadIdx.x * 8;
+            const float e[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
+                                v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(e[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+            const float scale = fmaxf(amax / 127.0f, 1e-30f);
+            const float sf = __half2float(__float2half(scale));
+            const float inv = 1.0f / sf;
+            uint32_t packed[2] = {0u, 0u};
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = (int)fminf(fmaxf(e[i] * inv, -127.0f), 127.0f);
+                s += q;
+                packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+            }
+            s += __shfl_xor(s, 1, kWave);
+            s += __shfl_xor(s, 2, kWave);
+            if (idx < K) {
+                *reinterpret_cast<u32x2*>(lds.qs + idx) = u32x2{packed[0], packed[1]};
+                if ((threadIdx.x & 3) == 0) {
+                    lds.xd[idx >> 5] = sf;
+                    lds.qsum[idx >> 5] = s;
+                }
+            }
         }
     }
+}
+
+// fp32 copy of x into LDS with the same batched-load structure.
+__device__ __forceinline__ void stage_f32_to_lds(const float* __restrict__ x, int K, float* xs) {
+    const int per_pass = (int)blockDim.x * 4;
+    constexpr int kBatch = 8;
+    for (int base = 0; base < K; base += kBatch * per_pass) {
+        float4 v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int idx = base + u * per_pass + (int)threadIdx.x * 4;
+            v[u] = *reinterpret_cast<const float4*>(x + (idx < K ? idx : 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int idx = base + u * per_pass + (int)threadIdx.x * 4;
+            if (idx < K) *reinterpret_cast<float4*>(xs + idx) = v[u];
+        }
+    }
+}
+
+// Contiguous output-row range of global wave `gw` out of `nw` (balanced to
+// within one row): each wave streams one contiguous stretch of the matrix.
+__device__ __forceinline__ void wave_row_range(int N, int gw, int nw, int* begin, int* end) {
+    *begin = (int)(((long long)N * gw) / nw);
+    *end = (int)(((long long)N * (gw + 1)) / nw);
 }
 
 // ── Q4_K × Q8_0 per-lane work unit ───────────────────────────────────────
@@ -179,5 +214,8 @@ __device__ __forceinline__ float q4k_q8_combine(float acc, float xd, float d, fl
 
 // Device CU count, cached per device (host side).
 int device_cu_count();
+// GEMV workgroups per CU (host side; default 2, RF_GEMV_WG_PER_CU overrides
+// it for tuning sweeps).
+int gemv_wg_per_cu();
 
 }  // namespace rf

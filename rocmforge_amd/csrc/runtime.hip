@@ -1,4 +1,6 @@
 // runtime.hip -- host-side helpers shared by the launchers.
+#include <stdlib.h>
+
 #include "qk_common.h"
 
 namespace rf {
@@ -15,6 +17,16 @@ int device_cu_count() {
         cached[dev] = n;
     }
     return cached[dev];
+}
+
+int gemv_wg_per_cu() {
+    static int v = 0;
+    if (v == 0) {
+        const char* e = getenv("RF_GEMV_WG_PER_CU");
+        int n = e ? atoi(e) : 0;
+        v = (n >= 1 && n <= 16) ? n : 2;
+    }
+    return v;
 }
 
 }  // namespace rf

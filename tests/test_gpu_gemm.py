@@ -1,0 +1,79 @@
+"""GPU parity of the prefill GEMMs (wmma_gemm_q4_k_launch / wmma_gemm_q6_k_launch)
+through the C ABI, against the oracle's float64 product of the fp16-rounded
+operands (the reference stages both operands through __float2half).
+
+Tolerance (BASELINE: 2e-3 relative): per element
+  |D - D_ref| <= 2e-3 * |D_ref| + 1e-5 * max|D_ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from rocmforge_amd import synth
+from tests import gpu_util as G
+from tests.test_oracle import _byte_level_q4k_block, _byte_level_q6k_block
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(rf, fmt, a, w, m, n, k):
+    da, dw = G.to_dev(a), G.to_dev(w)
+    d = G.empty(m * n, torch.float32)
+    fn = rf.wmma_gemm_q4_k_launch if fmt == "q4_k" else rf.wmma_gemm_q6_k_launch
+    G.call(fn, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
+    return G.host(d).reshape(m, n)
+
+
+def _check(got, ref, what):
+    scale = np.abs(ref).max()
+    err = np.abs(got.astype(np.float64) - ref)
+    worst = (err / (2e-3 * np.abs(ref) + 1e-5 * scale)).max()
+    print(f"{what}: max_abs={err.max():.3e} max|ref|={scale:.3e} worst={worst:.3f}", flush=True)
+    assert worst <= 1.0, what
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k"])
+def test_gemm_byte_level_identity(rf, dev, fmt):
+    # the reference's byte-level test (wmma_q4_k_correctness.rs:89-185,
+    # wmma_q6_k_correctness.rs:75-160): A = I (64 x 256), every W row the same
+    # hand-built block, so D[r, c] = dequant[r].
+    m, n, k = 64, 64, 256
+    blk = _byte_level_q4k_block() if fmt == "q4_k" else _byte_level_q6k_block()
+    w = np.tile(blk, (n, 1))
+    a = np.zeros((m, k), np.float32)
+    a[np.arange(m), np.arange(m)] = 1.0
+    got = _run(rf, fmt, a, w, m, n, k)
+    deq = O.dequant_f16(fmt, w, n, k)[0]
+    for c in range(n):
+        np.testing.assert_array_equal(got[:, c], deq[:m])
+
+
+@pytest.mark.parametrize("fmt,m,n,k", [
+    ("q4_k", 64, 64, 256), ("q4_k", 128, 192, 512), ("q4_k", 192, 128, 768), ("q4_k", 256, 256, 1024),
+    ("q6_k", 64, 64, 256), ("q6_k", 128, 320, 768), ("q6_k", 256, 128, 1024),
+])
+def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
+    a = synth.activations(k, seed=m + n, m=m)
+    w = synth.weights(fmt, n, k, seed=k)
+    _check(_run(rf, fmt, a, w, m, n, k), O.gemm(fmt, a, w, m, n, k), f"{fmt} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 14336, 4096), ("q6_k", 4096, 14336)])
+@pytest.mark.parametrize("m", [64, 512])
+def test_gemm_llama_ffn_shapes(rf, dev, fmt, n, k, m):
+    # BASELINE config 3 at full size; A is bf16-valued N(0,1)
+    a = torch.from_numpy(synth.activations(k, seed=7, m=m)).to(torch.bfloat16).float().numpy()
+    w = synth.weights(fmt, n, k, seed=8)
+    _check(_run(rf, fmt, a, w, m, n, k), O.gemm(fmt, a, w, m, n, k), f"{fmt} M={m} {n}x{k}")
+
+
+def test_gemm_zero_padded_rows(rf, dev):
+    # prefill buffers are padded to 64 rows with zeros (cache.rs:781-834)
+    m, n, k = 128, 128, 512
+    a = synth.activations(k, seed=3, m=m)
+    a[77:] = 0.0
+    w = synth.q4_k_weights(n, k, seed=4)
+    got = _run(rf, "q4_k", a, w, m, n, k)
+    assert np.all(got[77:] == 0.0)
+    _check(got, O.gemm("q4_k", a, w, m, n, k), "padded")
