@@ -19,7 +19,7 @@
 //    difference to the reference is the fp32 summation order.
 //  * Workgroups stride over row groups; the grid is capped at a multiple of
 //    the CU count so a large N re-uses each workgroup's quantised vector.
-#include "qk_common.h"
+#include "stream.h"
 
 namespace rf {
 
@@ -33,13 +33,13 @@ enum Q4Mode { kPlain = 0, kResidual = 1, kGateUp = 2 };
 // (K/32) * 34 bytes <= 32 KB.  Kept so callers see identical validation.
 static inline bool q8_inline_fits(int K) { return (size_t)(K / 32) * 34 <= 32768; }
 
-static inline size_t q8_lds_bytes(int K) { return (size_t)K + (size_t)(K / 32) * 8; }
+__host__ __device__ inline size_t q8_lds_bytes(int K) { return (size_t)q8_padded_bytes(K) + (size_t)(K / 32) * 8; }
 
 __device__ __forceinline__ Q8Lds q8_lds_carve(uint8_t* smem, int K) {
     Q8Lds l;
     l.qs = reinterpret_cast<int8_t*>(smem);
-    l.xd = reinterpret_cast<float*>(smem + K);
-    l.qsum = reinterpret_cast<int*>(smem + K + 4 * (K / 32));
+    l.xd = reinterpret_cast<float*>(smem + q8_padded_bytes(K));
+    l.qsum = reinterpret_cast<int*>(smem + q8_padded_bytes(K) + 4 * (K / 32));
     return l;
 }
 
@@ -80,47 +80,42 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
     const int s = lane >> 2;
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
+    const int nwaves = gridDim.x * kWavesPerWg;
     int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * kWavesPerWg + wave, gridDim.x * kWavesPerWg, &row_begin, &row_end);
+    wave_row_range(N, blockIdx.x * kWavesPerWg + wave, nwaves, &row_begin, &row_end);
     const int last = max(row_end - 1, 0);
 
-    // Software pipeline over (R-row group, 16-super-block step) of this
-    // wave's contiguous row range: the loads of step i+1 are in flight while
-    // step i is computed.  The first step's loads are issued before the
-    // activation quantisation, hiding it behind HBM latency.
-    int row0 = row_begin;
-    int sb0 = 0;
-    Q4KUnit cur[M][R];
-    if (row0 < row_end) q4k_load_step<M, R>(cur, w0, w1, row_bytes, row0, last + 1, min(s, nsb - 1), p);
-
-    q8_0_quantize_to_lds(x, K, q8);
-    __syncthreads();
-
+    // Software pipeline over the steps (R-row group x 16 super-blocks) of
+    // this wave's contiguous row range (register buffers below).
+    const int spr = (nsb + kSbPerStep - 1) / kSbPerStep;        // steps per row group
+    const int nsteps = ((row_end - row_begin + R - 1) / R) * spr;
+    auto load = [&](Q4KUnit (&u)[M][R], int i) {
+        const int row0 = row_begin + (i / spr) * R;
+        const int sb = (i % spr) * kSbPerStep + s;
+        q4k_load_step<M, R>(u, w0, w1, row_bytes, row0, last + 1, min(sb, nsb - 1), p);
+    };
     float acc[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-
-    while (row0 < row_end) {
-        int nrow0 = row0, nsb0 = sb0 + kSbPerStep;
-        if (nsb0 >= nsb) {
-            nsb0 = 0;
-            nrow0 += R;
-        }
-        Q4KUnit nxt[M][R];
-        if (nrow0 < row_end) q4k_load_step<M, R>(nxt, w0, w1, row_bytes, nrow0, last + 1, min(nsb0 + s, nsb - 1), p);
-
-        const int sb = sb0 + s;
+    // Row results are parked in this wave's LDS slots and written to HBM
+    // after the loop: no global store (or residual load) sits between the
+    // prefetch loads in the in-order memory counter.
+    const int max_rows = (N + nwaves - 1) / nwaves;
+    float* out_lds = reinterpret_cast<float*>(smem + q8_lds_bytes(K)) + wave * max_rows * M;
+    auto process = [&](const Q4KUnit (&u)[M][R], int i) {
+        const int row0 = row_begin + (i / spr) * R;
+        const int sb = (i % spr) * kSbPerStep + s;
         const bool live = sb < nsb;
         const int sbc = live ? sb : nsb - 1;
         // Q8 slab for this lane: 64 int8 at element sb*256 + 64p.
-        const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + sbc * kQK + 64 * p);
+        const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + q8_pad(sbc * kQK) + 64 * p);
         const u32x4 xlo[2] = {xs[0], xs[1]};
         const u32x4 xhi[2] = {xs[2], xs[3]};
         const int b0 = sbc * 8 + 2 * p;
@@ -130,35 +125,187 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float a = q4k_q8_unit_dot(cur[m][r], p, xlo, xhi, xd0, xd1, qs0, qs1, acc[m][r]);
+                const float a = q4k_q8_unit_dot(u[m][r], p, xlo, xhi, xd0, xd1, qs0, qs1, acc[m][r]);
                 acc[m][r] = live ? a : acc[m][r];
             }
-
-        if (nsb0 == 0) {  // row group finished: reduce and write
+        if ((i % spr) == spr - 1) {  // row group finished: reduce into the wave's LDS slots
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float g = wave_sum(acc[0][r]);
                 const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
-                const int row = row0 + r;
-                if (lane == r && row < row_end) {
-                    if (MODE == kPlain) {
-                        y[row] = g;
-                    } else if (MODE == kResidual) {
-                        y[row] = g + residual[row];
-                    } else {
-                        y[row] = g / (1.0f + expf(-g)) * v;
-                    }
+                const int j = row0 + r - row_begin;
+                if (lane == 0 && row0 + r < row_end) {
+                    out_lds[M * j] = g;
+                    if (M == 2) out_lds[M * j + 1] = v;
                 }
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[m][r] = 0.0f;
             }
         }
+    };
+
+    Q4KUnit ua[M][R], ub[M][R], uc[M][R];
+    // Three register buffers in rotation (loop unrolled by three): two steps
+    // are always in flight while one is computed, including during the
+    // activation staging.  Every load is unconditional (step index clamped;
+    // redundant reloads of the last step hit the cache) and the loop has a
+    // single exit at the latch, so the compiler's wait counting stays exact.
+    load(ua, 0);
+    load(ub, min(1, max(nsteps - 1, 0)));
+    q8_0_quantize_to_lds(x, K, q8);
+    __syncthreads();
+    int i = 0;
+    for (; i + 2 < nsteps; i += 3) {
+        load(uc, i + 2);
+        process(ua, i);
+        load(ua, min(i + 3, nsteps - 1));
+        process(ub, i + 1);
+        load(ub, min(i + 4, nsteps - 1));
+        process(uc, i + 2);
+    }
+    if (i < nsteps) process(ua, i);
+    if (i + 1 < nsteps) process(ub, i + 1);
+    for (int j = lane; j < row_end - row_begin; j += kWave) {
+        const int row = row_begin + j;
+        const float g = out_lds[M * j];
+        if (MODE == kPlain) {
+            y[row] = g;
+        } else if (MODE == kResidual) {
+            y[row] = g + residual[row];
+        } else {
+            y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
+        }
+    }
+}
+
+// ── LDS-streamed Q8-inline GEMV (main path) ──────────────────────────────
+// Same arithmetic as rf_q4k_q8_gemv_kernel; the weights travel HBM -> LDS
+// through each wave's S-stage ring (stream.h) instead of through registers:
+// every load instruction moves 1 KB of contiguous bytes, the prefetch depth
+// costs no VGPRs, and the lanes pick their 48-byte units out of LDS.
+template <int MODE, int R, int NW, int S>
+__global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_stream_kernel(const uint8_t* __restrict__ w0,
+                                                                         const uint8_t* __restrict__ w1,
+                                                                         const float* __restrict__ x,
+                                                                         const float* residual, float* y, int K,
+                                                                         int N) {
+    constexpr int M = (MODE == kGateUp) ? 2 : 1;
+    constexpr int NSEG = M * R;
+    using G = StepGeom<kQ4KBytes, NSEG>;
+    // The ring is its own LDS object, so alias analysis can tell the other
+    // LDS reads from the in-flight ring DMA.
+    __shared__ __align__(16) uint8_t ring_lds[NW * S * G::kStageBytes];
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Q8Lds q8 = q8_lds_carve(smem, K);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int s = lane >> 2;
+    const int p = lane & 3;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ4KBytes;
+    const int nwaves = gridDim.x * NW;
+    int row_begin, row_end;
+    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
+    const int max_rows = (N + nwaves - 1) / nwaves;
+    const size_t out_off = (q8_lds_bytes(K) + 15) & ~(size_t)15;
+    uint8_t* ring = ring_lds + (size_t)wave * S * G::kStageBytes;
+    float* out_lds = reinterpret_cast<float*>(smem + out_off) + wave * max_rows * M;
+
+    const int spr = (nsb + kSB - 1) / kSB;
+    const int nsteps = ((row_end - row_begin + R - 1) / R) * spr;
+    LaneChunks<kQ4KBytes, NSEG> lc;
+    lc.init(lane);
+    // issue(step i into ring slot `slot`): the tail re-issues the last step
+    // (clamped index) into the slot freed last iteration, never a live one.
+    auto issue = [&](int i, int slot) {
+        const int row0 = row_begin + (i / spr) * R;
+        const int sb0 = (i % spr) * kSB;
+        const uint8_t* segp[NSEG];
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int r = 0; r < R; ++r) cur[m][r] = nxt[m][r];
-        row0 = nrow0;
-        sb0 = nsb0;
+            for (int r = 0; r < R; ++r) {
+                const int row = max(min(row0 + r, row_end - 1), 0);   // waves without rows re-read row 0
+                segp[m * R + r] = (m == 0 ? w0 : w1) + (size_t)row * row_bytes + (size_t)sb0 * kQ4KBytes;
+            }
+        issue_step<kQ4KBytes, NSEG>(lc, segp, min(kSB, nsb - sb0) * (kQ4KBytes / 16),
+                                    ring + slot * G::kStageBytes);
+    };
+
+    // Prologue: the first S-1 weight stages and x are put in flight together
+    // (all by DMA); the quantisation reads x from LDS once everything has
+    // landed, so it costs one memory latency shared with the weight ramp-up.
+    // (The compiler's wait counting turns conservative once LDS DMA is
+    // pending, which rules out a separate register prefetch of x.)
+    float* xs = reinterpret_cast<float*>(smem + out_off + (((size_t)NW * max_rows * M * 4 + 15) & ~(size_t)15));
+#pragma unroll
+    for (int k = 0; k < S - 1; ++k) issue(max(min(k, nsteps - 1), 0), k);   // unconditional: exact counts
+    stage_f32_to_lds(x, K, xs);
+    wait_vmcnt<0>();
+    lds_barrier();
+    q8_quantize_from_lds(xs, K, q8);
+    lds_barrier();
+
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    for (int i = 0; i < nsteps; ++i) {
+        asm volatile("" ::: "memory");
+        issue(min(i + S - 1, nsteps - 1), (i + S - 1) % S);   // into the slot consumed last iteration
+        wait_vmcnt<(S - 1) * G::kNI>();      // step i has landed in LDS
+        const uint8_t* slot = ring + (i % S) * G::kStageBytes;
+        const int row0 = row_begin + (i / spr) * R;
+        const int sb = (i % spr) * kSB + s;
+        if (sb < nsb) {
+            // Q8 slab for this lane: 64 int8 at element sb*256 + 64p.
+            const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + q8_pad(sb * kQK) + 64 * p);
+            const u32x4 xlo[2] = {xs[0], xs[1]};
+            const u32x4 xhi[2] = {xs[2], xs[3]};
+            const int b0 = sb * 8 + 2 * p;
+            const float xd0 = q8.xd[b0], xd1 = q8.xd[b0 + 1];
+            const int qs0 = q8.qsum[b0], qs1 = q8.qsum[b0 + 1];
+            static_assert(NSEG == 2, "ring reads are grouped for two segments");
+            Q4KUnit u[M][R];
+            u32x4 o[6];
+            ring_read_q4x2(slot + s * kQ4KBytes, slot + kSB * kQ4KBytes + s * kQ4KBytes, p, o);
+            u[0][0] = Q4KUnit{o[0], o[1], o[2]};
+            u[M - 1][R - 1] = Q4KUnit{o[3], o[4], o[5]};   // segment 1: (m=1,r=0) or (m=0,r=1)
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    acc[m][r] = q4k_q8_unit_dot(u[m][r], p, xlo, xhi, xd0, xd1, qs0, qs1, acc[m][r]);
+        }
+        if ((i % spr) == spr - 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float g = wave_sum(acc[0][r]);
+                const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
+                const int j = row0 + r - row_begin;
+                if (lane == 0 && row0 + r < row_end) {
+                    out_lds[M * j] = g;
+                    if (M == 2) out_lds[M * j + 1] = v;
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[m][r] = 0.0f;
+            }
+        }
+    }
+    wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
+    for (int j = lane; j < row_end - row_begin; j += kWave) {
+        const int row = row_begin + j;
+        const float g = out_lds[M * j];
+        if (MODE == kPlain) {
+            y[row] = g;
+        } else if (MODE == kResidual) {
+            y[row] = g + residual[row];
+        } else {
+            y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
+        }
     }
 }
 
@@ -203,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
     float* xs = reinterpret_cast<float*>(smem);
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
     const int s = lane >> 2;
     const int p = lane & 3;
     const int nsb = K / kQK;
@@ -268,10 +415,45 @@ static inline int gemv_grid(int N, int min_rows) {
 template <int MODE>
 static hipError_t launch_q8(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
                             hipStream_t st) {
-    constexpr int R = (MODE == kGateUp) ? 2 : 4;
+    constexpr int M = (MODE == kGateUp) ? 2 : 1;
+    if (gemv_use_stream() && K <= 8192) {
+        constexpr int R = (MODE == kGateUp) ? 1 : 2;
+        constexpr int NW = 8, S = 3;
+        using G = StepGeom<kQ4KBytes, M * R>;
+        const int cap = device_cu_count() * gemv_wg_per_cu();
+        const int need = (N + NW - 1) / NW;
+        const int grid = need < cap ? need : cap;
+        const size_t out_off = (q8_lds_bytes(K) + 15) & ~(size_t)15;
+        const size_t max_rows = (N + (size_t)grid * NW - 1) / ((size_t)grid * NW);
+        const size_t lds = out_off + (((size_t)NW * max_rows * M * 4 + 15) & ~(size_t)15) + (size_t)K * 4;
+        if (lds + (size_t)NW * S * G::kStageBytes > 160 * 1024) return hipErrorInvalidValue;
+        auto kern = rf_q4k_q8_gemv_stream_kernel<MODE, R, NW, S>;
+        static bool attr = false;
+        if (!attr) {
+            // dynamic LDS may use what the static ring leaves of the 160 KB
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024 - NW * S * G::kStageBytes);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), lds, st, static_cast<const uint8_t*>(w0),
+                           static_cast<const uint8_t*>(w1), x, res, y, K, N);
+        return hipGetLastError();
+    }
     const int grid = gemv_grid(N, 1);
-    hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, R>), dim3(grid), dim3(kThreads), q8_lds_bytes(K), st,
-                       static_cast<const uint8_t*>(w0), static_cast<const uint8_t*>(w1), x, res, y, K, N);
+    const size_t out_bytes = (size_t)kWavesPerWg * ((N + grid * kWavesPerWg - 1) / (grid * kWavesPerWg)) * M * 4;
+    if (q8_lds_bytes(K) + out_bytes > 160 * 1024) return hipErrorInvalidValue;
+    const int r = gemv_rows_per_step();
+    const uint8_t* a = static_cast<const uint8_t*>(w0);
+    const uint8_t* b = static_cast<const uint8_t*>(w1);
+    const size_t lds = q8_lds_bytes(K) + out_bytes;
+    if (r == 1)
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
+    else if (r == 4 && MODE != kGateUp)
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
+    else
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
     return hipGetLastError();
 }
 
@@ -299,13 +481,13 @@ __global__ __launch_bounds__(kThreads) void rf_q8_0_quantize_kernel(const float*
                                                                      uint16_t* __restrict__ d_out,
                                                                      int8_t* __restrict__ qs_out,
                                                                      int* __restrict__ sum_out) {
-    __shared__ __align__(16) uint8_t smem[kQuantSlice + kQuantSlice / 4];
+    __shared__ __align__(16) uint8_t smem[q8_padded_bytes(kQuantSlice) + kQuantSlice / 4];
     const int base = blockIdx.x * kQuantSlice;
     const int len = min(kQuantSlice, K - base);
     const Q8Lds q8 = q8_lds_carve(smem, len);
     q8_0_quantize_to_lds(x + base, len, q8);
     __syncthreads();
-    for (int i = threadIdx.x; i < len; i += kThreads) qs_out[base + i] = q8.qs[i];
+    for (int i = threadIdx.x; i < len; i += kThreads) qs_out[base + i] = q8.qs[q8_pad(i)];
     for (int b = threadIdx.x; b < len / 32; b += kThreads) {
         d_out[base / 32 + b] = __half_as_ushort(__float2half(q8.xd[b]));
         sum_out[base / 32 + b] = q8.qsum[b];
@@ -322,14 +504,14 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_partials_kernel(const uint
     q8_0_quantize_to_lds(x, K, q8);
     __syncthreads();
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
     const int s = lane >> 2, p = lane & 3;
     const int nsb = K / kQK;
     for (int row = blockIdx.x * kWavesPerWg + wave; row < N; row += gridDim.x * kWavesPerWg) {
         for (int sb0 = 0; sb0 < nsb; sb0 += kSbPerStep) {
             const int sb = sb0 + s;
             if (sb < nsb) {
-                const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + sb * kQK + 64 * p);
+                const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + q8_pad(sb * kQK) + 64 * p);
                 u32x4 xlo[2] = {xs[0], xs[1]};
                 u32x4 xhi[2] = {xs[2], xs[3]};
                 Q4KUnit u = q4k_load_unit(w + ((size_t)row * nsb + sb) * kQ4KBytes, p);

@@ -14,7 +14,7 @@
 // reads its 16 B of low-ql, 16 B of high-ql and 16 B of qh with unaligned
 // 16-byte loads (blocks are only 2-byte aligned), 8 scale bytes and d, and
 // produces 64 products against x held in LDS.
-#include "qk_common.h"
+#include "stream.h"
 
 namespace rf {
 
@@ -25,7 +25,7 @@ constexpr int kQ6SbPerStep = 16;
 struct Q6Unit {
     u32x4 lo, hi, qh;  // ql[64n+16c..], ql[64n+32+16c..], qh[32n+16c..]
     u32x2 sc;          // scales[8n .. 8n+7]
-    uint32_t d;        // fp16 bits
+    uint32_t d;        // bytes 206..209: scales[14], scales[15], d (fp16 in the high half)
 };
 
 __device__ __forceinline__ Q6Unit q6k_load_unit(const uint8_t* blk, int p) {
@@ -35,28 +35,40 @@ __device__ __forceinline__ Q6Unit q6k_load_unit(const uint8_t* blk, int p) {
     u.hi = ld16(blk + 64 * n + 32 + 16 * c);
     u.qh = ld16(blk + 128 + 32 * n + 16 * c);
     u.sc = ld8(blk + 192 + 8 * n);
-    u.d = ld_u16(blk + 208);
+    // d is read as the high half of the in-block dword at 206 (a 16-bit load
+    // would be packed with its neighbour by the compiler, forcing an early
+    // wait on the prefetch)
+    u.d = ld4(blk + 206);
     return u;
 }
 
-// 16 products of one quarter: packed q6 bytes (4 dwords) against 16 x.
-__device__ __forceinline__ float q6_quarter(float acc, float s, const uint32_t q6[4], const float* xq) {
+// One 16-weight scale group: s * sum_i (q6_i - 32) * x_i, evaluated as
+// s * (sum_i q6_i * x_i - 32 * sum_i x_i) with sum_i x_i (xsum) precomputed
+// once per group of x.  The q6 bytes convert straight to float
+// (v_cvt_f32_ubyteN), so a weight costs a convert and an FMA.
+__device__ __forceinline__ float q6_group(float acc, float s, const uint32_t q6[4], const float* xq, float xsum) {
     const float4* xv = reinterpret_cast<const float4*>(xq);
+    float t = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const float4 a = xv[t];
-        const uint32_t v = q6[t];
-        acc += s * ((float)((v >> 0) & 0xFFu) - 32.0f) * a.x;
-        acc += s * ((float)((v >> 8) & 0xFFu) - 32.0f) * a.y;
-        acc += s * ((float)((v >> 16) & 0xFFu) - 32.0f) * a.z;
-        acc += s * ((float)((v >> 24) & 0xFFu) - 32.0f) * a.w;
+    for (int k = 0; k < 4; ++k) {
+        const float4 a = xv[k];
+        const uint32_t v = q6[k];
+        t += (float)((v >> 0) & 0xFFu) * a.x;
+        t += (float)((v >> 8) & 0xFFu) * a.y;
+        t += (float)((v >> 16) & 0xFFu) * a.z;
+        t += (float)((v >> 24) & 0xFFu) * a.w;
     }
-    return acc;
+    return acc + s * (t - 32.0f * xsum);
 }
 
-__device__ __forceinline__ float q6k_unit_dot(const Q6Unit& u, int p, const float* xblk, float acc) {
+// xblk: x of this super-block; in the padded LDS layout (x_pad) its second
+// half starts 132 floats in, otherwise 128 (HALF).  xsum16: sums of x over
+// the block's 16-element groups.
+template <int HALF>
+__device__ __forceinline__ float q6k_unit_dot(const Q6Unit& u, int p, const float* xblk, const float* xsum16,
+                                              float acc) {
     const int n = p >> 1, c = p & 1;
-    const float d = half_bits_to_float(u.d);
+    const float d = half_bits_to_float(u.d >> 16);
     // scale bytes 8n + 2q + c, q = 0..3: bytes c, c+2 of sc.x and of sc.y
     const uint32_t sh = 8u * (uint32_t)c;
     const float s0 = d * (float)(int8_t)((u.sc.x >> sh) & 0xFFu);
@@ -74,12 +86,28 @@ __device__ __forceinline__ float q6k_unit_dot(const Q6Unit& u, int p, const floa
         q2[t] = ((L[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> 4) & 0x03030303u) << 4);
         q3[t] = ((H[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> 6) & 0x03030303u) << 4);
     }
-    const float* xb = xblk + 128 * n + 16 * c;
-    acc = q6_quarter(acc, s0, q0, xb);
-    acc = q6_quarter(acc, s1, q1, xb + 32);
-    acc = q6_quarter(acc, s2, q2, xb + 64);
-    acc = q6_quarter(acc, s3, q3, xb + 96);
+    const int g = 8 * n + c;   // 16-element group of quarter 0 inside the block
+    const float* xb = xblk + HALF * n + 16 * c;
+    acc = q6_group(acc, s0, q0, xb, xsum16[g]);
+    acc = q6_group(acc, s1, q1, xb + 32, xsum16[g + 2]);
+    acc = q6_group(acc, s2, q2, xb + 64, xsum16[g + 4]);
+    acc = q6_group(acc, s3, q3, xb + 96, xsum16[g + 6]);
     return acc;
+}
+
+// Per-group sums of the staged x (after a barrier that published xs).
+template <bool PADDED>
+__device__ __forceinline__ void q6_xsum16(const float* xs, int K, float* xsum16) {
+    for (int g = threadIdx.x; g < K / 16; g += blockDim.x) {
+        const float4* v = reinterpret_cast<const float4*>(xs + (PADDED ? x_pad(16 * g) : 16 * g));
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 a = v[k];
+            t += a.x + a.y + a.z + a.w;
+        }
+        xsum16[g] = t;
+    }
 }
 
 template <int R, bool LDS>
@@ -89,64 +117,153 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
     extern __shared__ __align__(16) uint8_t smem[];
     float* xs = reinterpret_cast<float*>(smem);
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
     const int s = lane >> 2;
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ6KBytes;
+    const int nwaves = gridDim.x * kQ6Waves;
     int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * kQ6Waves + wave, gridDim.x * kQ6Waves, &row_begin, &row_end);
+    wave_row_range(N, blockIdx.x * kQ6Waves + wave, nwaves, &row_begin, &row_end);
 
-    int row0 = row_begin;
-    int sb0 = 0;
-    Q6Unit cur[R];
-    auto load_step = [&](Q6Unit(&u)[R], int r0, int sbc) {
+    // Register-buffer pipeline, as in the Q4_K kernel.
+    const int spr = (nsb + kQ6SbPerStep - 1) / kQ6SbPerStep;
+    const int nsteps = ((row_end - row_begin + R - 1) / R) * spr;
+    auto load = [&](Q6Unit (&u)[R], int i) {
+        const int row0 = row_begin + (i / spr) * R;
+        const int sbc = min((i % spr) * kQ6SbPerStep + s, nsb - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = min(r0 + r, row_end - 1);
+            const int row = max(min(row0 + r, row_end - 1), 0);   // waves without rows re-read row 0
             u[r] = q6k_load_unit(w + (size_t)row * row_bytes + (size_t)sbc * kQ6KBytes, p);
         }
     };
-    if (row0 < row_end) load_step(cur, row0, min(s, nsb - 1));
-
-    if (LDS) {
-        stage_f32_to_lds(x, K, xs);
-        __syncthreads();
-    }
-    const float* xv = LDS ? xs : x;
-
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    while (row0 < row_end) {
-        int nrow0 = row0, nsb0 = sb0 + kQ6SbPerStep;
-        if (nsb0 >= nsb) {
-            nsb0 = 0;
-            nrow0 += R;
-        }
-        Q6Unit nxt[R];
-        if (nrow0 < row_end) load_step(nxt, nrow0, min(nsb0 + s, nsb - 1));
-
-        const int sb = sb0 + s;
+    const float* xv = LDS ? xs : x;
+    // row results parked in LDS, written to HBM after the loop (no global
+    // store between the prefetch loads in the in-order memory counter)
+    // LDS: [x (padded, LDS mode only)] [x group sums (K/16)] [row results]
+    const int max_rows = (N + nwaves - 1) / nwaves;
+    float* xsum16 = reinterpret_cast<float*>(smem + (LDS ? (size_t)x_padded_floats(K) * 4 : 0));
+    float* out_lds = xsum16 + K / 16 + wave * max_rows;
+    auto process = [&](const Q6Unit (&u)[R], int i) {
+        const int row0 = row_begin + (i / spr) * R;
+        const int sb = (i % spr) * kQ6SbPerStep + s;
         if (sb < nsb) {
-            const float* xblk = xv + sb * kQK;
+            const float* xblk = xv + (LDS ? x_pad(sb * kQK) : sb * kQK);
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = q6k_unit_dot(cur[r], p, xblk, acc[r]);
+            for (int r = 0; r < R; ++r)
+                acc[r] = q6k_unit_dot<LDS ? 132 : 128>(u[r], p, xblk, xsum16 + sb * 16, acc[r]);
         }
-        if (nsb0 == 0) {
+        if ((i % spr) == spr - 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float g = wave_sum(acc[r]);
-                if (lane == r && row0 + r < row_end) y[row0 + r] = g;
+                if (lane == 0 && row0 + r < row_end) out_lds[row0 + r - row_begin] = g;
                 acc[r] = 0.0f;
             }
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) cur[r] = nxt[r];
-        row0 = nrow0;
-        sb0 = nsb0;
+    };
+
+    Q6Unit ua[R], ub[R], uc[R];
+    // Three register buffers in rotation (loop unrolled by three): two steps
+    // are always in flight while one is computed, including during the
+    // activation staging.  Every load is unconditional (step index clamped;
+    // redundant reloads of the last step hit the cache) and the loop has a
+    // single exit at the latch, so the compiler's wait counting stays exact.
+    load(ua, 0);
+    load(ub, min(1, max(nsteps - 1, 0)));
+    if (LDS) {
+        stage_f32_to_lds_regs(x, K, xs);
+        __syncthreads();
     }
+    q6_xsum16<LDS>(xv, K, xsum16);
+    __syncthreads();
+    int i = 0;
+    for (; i + 2 < nsteps; i += 3) {
+        load(uc, i + 2);
+        process(ua, i);
+        load(ua, min(i + 3, nsteps - 1));
+        process(ub, i + 1);
+        load(ub, min(i + 4, nsteps - 1));
+        process(uc, i + 2);
+    }
+    if (i < nsteps) process(ua, i);
+    if (i + 1 < nsteps) process(ub, i + 1);
+    for (int j = lane; j < row_end - row_begin; j += kWave) y[row_begin + j] = out_lds[j];
+}
+
+// ── LDS-streamed Q6_K GEMV (main path) ───────────────────────────────────
+// Weights travel HBM -> LDS through each wave's S-stage ring (stream.h); x
+// is staged in LDS as fp32.  A step covers 16 super-blocks (3360 B, 16-byte
+// aligned when the row is), so the path needs K/256 % 8 == 0, a 16-byte
+// aligned weight pointer and K <= KMAX; other layouts use
+// rf_q6k_gemv_kernel.  Both LDS buffers are static objects: the compiler
+// only separates LDS reads from in-flight LDS DMA for such objects (for
+// anything else it waits for all DMA), and a wave's row results are held in
+// lane registers (lane j keeps row begin+j, at most 64 rows per wave).
+template <int NW, int S, int KMAX>
+__global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_stream_kernel(const uint8_t* __restrict__ w,
+                                                                      const float* __restrict__ x,
+                                                                      float* __restrict__ y, int K, int N) {
+    using G = StepGeom<kQ6KBytes, 1>;
+    __shared__ __align__(16) uint8_t ring_lds[NW * S * G::kStageBytes];
+    __shared__ __align__(16) float xs[x_padded_floats(KMAX)];
+    __shared__ __align__(16) float xsum16[KMAX / 16];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int s = lane >> 2;
+    const int p = lane & 3;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ6KBytes;
+    const int nwaves = gridDim.x * NW;
+    int row_begin, row_end;
+    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
+    uint8_t* ring = ring_lds + (size_t)wave * S * G::kStageBytes;
+
+    const int spr = (nsb + kSB - 1) / kSB;
+    const int nsteps = (row_end - row_begin) * spr;
+    LaneChunks<kQ6KBytes, 1> lc;
+    lc.init(lane);
+    // issue(step i into ring slot `slot`): the tail re-issues the last step
+    // (clamped index) into the slot freed last iteration, never a live one.
+    auto issue = [&](int i, int slot) {
+        const int row = max(min(row_begin + i / spr, row_end - 1), 0);
+        const int sb0 = (i % spr) * kSB;
+        const uint8_t* segp[1] = {w + (size_t)row * row_bytes + (size_t)sb0 * kQ6KBytes};
+        issue_step<kQ6KBytes, 1>(lc, segp, min(kSB, nsb - sb0) * kQ6KBytes / 16, ring + slot * G::kStageBytes);
+    };
+
+#pragma unroll
+    for (int k = 0; k < S - 1; ++k) issue(max(min(k, nsteps - 1), 0), k);   // unconditional: exact counts
+    stage_f32_to_lds_regs(x, K, xs);   // padded layout (bank-conflict free reads)
+    wait_vmcnt<0>();
+    lds_barrier();
+    q6_xsum16<true>(xs, K, xsum16);
+    lds_barrier();
+
+    float acc = 0.0f, out = 0.0f;
+    for (int i = 0; i < nsteps; ++i) {
+        asm volatile("" ::: "memory");
+        issue(min(i + S - 1, nsteps - 1), (i + S - 1) % S);
+        wait_vmcnt<(S - 1) * G::kNI>();
+        const uint8_t* slot = ring + (i % S) * G::kStageBytes;
+        const int sb = (i % spr) * kSB + s;
+        if (sb < nsb) {
+            Q6Unit u;
+            ring_read_q6(slot + s * kQ6KBytes, p, u.lo, u.hi, u.qh, u.sc, u.d);
+            acc = q6k_unit_dot<132>(u, p, xs + x_pad(sb * kQK), xsum16 + sb * 16, acc);
+        }
+        if ((i % spr) == spr - 1) {
+            const float g = wave_sum(acc);
+            out = (lane == i / spr) ? g : out;
+            acc = 0.0f;
+        }
+    }
+    wait_vmcnt<0>();
+    if (lane < row_end - row_begin) y[row_begin + lane] = out;
 }
 
 }  // namespace rf
@@ -160,18 +277,50 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
     if (n_rows % kQK != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
-    constexpr int R = 2;
+    const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
+    const int nsb = n_rows / kQK;
+    if (gemv_use_stream() && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+        (reinterpret_cast<uintptr_t>(input) & 15u) == 0) {
+        constexpr int NW = 8, S = 3;
+        const int cap = device_cu_count() * gemv_wg_per_cu();
+        const int need = (ncols_dst + NW - 1) / NW;
+        const int grid = need < cap ? need : cap;
+        const size_t max_rows = (ncols_dst + (size_t)grid * NW - 1) / ((size_t)grid * NW);
+        if (max_rows <= (size_t)kWave && n_rows <= 14336) {
+            const void* kern = n_rows <= 4096 ? reinterpret_cast<const void*>(rf_q6k_gemv_stream_kernel<NW, S, 4096>)
+                                              : reinterpret_cast<const void*>(rf_q6k_gemv_stream_kernel<NW, S, 14336>);
+            if (n_rows <= 4096)
+                hipLaunchKernelGGL((rf_q6k_gemv_stream_kernel<NW, S, 4096>), dim3(grid), dim3(NW * 64), 0, stream, w,
+                                   input, output, n_rows, ncols_dst);
+            else
+                hipLaunchKernelGGL((rf_q6k_gemv_stream_kernel<NW, S, 14336>), dim3(grid), dim3(NW * 64), 0, stream, w,
+                                   input, output, n_rows, ncols_dst);
+            (void)kern;
+            return hipGetLastError();
+        }
+    }
     const int need = (ncols_dst + kQ6Waves - 1) / kQ6Waves;
     const int cap = device_cu_count() * gemv_wg_per_cu();
     const int grid = need < cap ? need : cap;
-    const size_t lds = (size_t)n_rows * sizeof(float);
-    const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
+    const size_t lds = (size_t)x_padded_floats(n_rows) * sizeof(float);
+    const size_t out_bytes = (size_t)kQ6Waves * ((ncols_dst + grid * kQ6Waves - 1) / (grid * kQ6Waves)) * 4 +
+                             (size_t)(n_rows / 16) * 4;   // + x group sums
+    if (out_bytes > 64 * 1024) return hipErrorInvalidValue;
+    const bool r2 = gemv_rows_per_step() >= 2;
     if (lds <= 65536) {
-        hipLaunchKernelGGL((rf_q6k_gemv_kernel<R, true>), dim3(grid), dim3(kQ6Threads), lds, stream, w, input, output,
-                           n_rows, ncols_dst);
+        if (r2)
+            hipLaunchKernelGGL((rf_q6k_gemv_kernel<2, true>), dim3(grid), dim3(kQ6Threads), lds + out_bytes, stream, w,
+                               input, output, n_rows, ncols_dst);
+        else
+            hipLaunchKernelGGL((rf_q6k_gemv_kernel<1, true>), dim3(grid), dim3(kQ6Threads), lds + out_bytes, stream, w,
+                               input, output, n_rows, ncols_dst);
     } else {
-        hipLaunchKernelGGL((rf_q6k_gemv_kernel<R, false>), dim3(grid), dim3(kQ6Threads), 0, stream, w, input, output,
-                           n_rows, ncols_dst);
+        if (r2)
+            hipLaunchKernelGGL((rf_q6k_gemv_kernel<2, false>), dim3(grid), dim3(kQ6Threads), out_bytes, stream, w,
+                               input, output, n_rows, ncols_dst);
+        else
+            hipLaunchKernelGGL((rf_q6k_gemv_kernel<1, false>), dim3(grid), dim3(kQ6Threads), out_bytes, stream, w,
+                               input, output, n_rows, ncols_dst);
     }
     return hipGetLastError();
 }

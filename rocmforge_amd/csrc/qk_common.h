@@ -29,12 +29,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // single global_load_dwordx4.
 struct __attribute__((packed, aligned(2))) Un16 { u32x4 v; };
 struct __attribute__((packed, aligned(2))) Un8 { u32x2 v; };
+struct __attribute__((packed, aligned(2))) Un4 { uint32_t v; };
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
     return reinterpret_cast<const Un16*>(p)->v;
 }
 __device__ __forceinline__ u32x2 ld8(const uint8_t* p) {
     return reinterpret_cast<const Un8*>(p)->v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
+    return reinterpret_cast<const Un4*>(p)->v;
 }
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);
@@ -46,11 +50,31 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
     return __half2float(__half(r));
 }
 
-// Sum over the 64 lanes of a wave (butterfly: every lane ends with the sum).
+// ── cross-lane helpers on DPP (VALU only; no LDS round trips) ───────────
+// dpp_ctrl encodings (GFX9): quad_perm(a,b,c,d) = a|b<<2|c<<4|d<<6,
+// row_ror:n = 0x120+n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+
+// Sum over the 64 lanes of a wave, returned to every lane: rows of 16 are
+// reduced with quad permutes and row rotates, rows are combined with
+// row_bcast into lane 63, which is read back as a scalar.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    v += dpp_f<kQuadXor1>(v);
+    v += dpp_f<kQuadXor2>(v);
+    v += dpp_f<0x124>(v);          // row_ror:4
+    v += dpp_f<0x128>(v);          // row_ror:8  -> every lane holds its row's sum
+    v += dpp_f<0x142, 0xA>(v);     // row_bcast:15 into rows 1, 3
+    v += dpp_f<0x143, 0xC>(v);     // row_bcast:31 into rows 2, 3 -> lane 63 holds the total
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Q4_K (scale, min) for sub-blocks 2p and 2p+1, from the three scale words
@@ -85,78 +109,146 @@ __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uin
 // block here instead of once per row as the reference does).
 // Each half-wave (32 lanes) owns one 32-element block per step.
 struct Q8Lds {
-    int8_t* qs;
+    int8_t* qs;   // padded: element e at byte q8_pad(e)
     float* xd;
     int* qsum;
 };
 
+// LDS padding against bank conflicts.  The GEMV lanes of one step read the
+// same offsets of 16 consecutive super-blocks; an unpadded layout (256 B of
+// Q8 / 1 KB of fp32 x per super-block) puts all of them in the same banks.
+// Q8 bytes: 16 extra bytes after every 256; fp32 x: 4 extra floats after
+// every 128 elements.
+__host__ __device__ constexpr int q8_pad(int e) { return e + 16 * (e >> 8); }
+__host__ __device__ constexpr int q8_padded_bytes(int K) { return K + 16 * (K >> 8); }
+__host__ __device__ constexpr int x_pad(int e) { return e + 4 * (e >> 7); }
+__host__ __device__ constexpr int x_padded_floats(int K) { return K + 4 * (K >> 7); }
+
 // Whole-vector quantisation by one workgroup.  Each thread quantises 8
 // consecutive elements (two float4 loads); four neighbouring lanes form one
-// 32-element block and combine amax / int sums with two xor-shuffles.  The
-// loads of up to four passes are issued before any is consumed, so the
-// quantisation costs about one L2 round trip per 4*8*blockDim elements.
-__device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x, int K, Q8Lds lds) {
+// 32-element block and combine amax / int sums with two xor-shuffles.
+// Loads are batched four passes at a time.  The first batch can be loaded
+// separately (q8_prefetch) so a caller can issue it ahead of its own weight
+// loads: the memory counter is in order, so loads issued first are waited
+// for first.
+struct X8Batch {
+    float4 v[4][2];
+};
+
+__device__ __forceinline__ void q8_load_batch(const float* __restrict__ x, int K, int base, X8Batch& b) {
     const int per_pass = (int)blockDim.x * 8;
-    constexpr int kBatch = 4;
-    for (int base = 0; base < K; base += kBatch * per_pass) {
-        float4 v[kBatch][2];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int idx = base + u * per_pass + (int)threadIdx.x * 8;
-            const int src = idx < K ? idx : 0;   // out-of-range lanes re-read x[0..7], never stored
-            v[u][0] = *reinterpret_cast<const float4*>(x + src);
-            v[u][1] = *reinterpret_cast<const float4*>(x + src + 4);
+    for (int u = 0; u < 4; ++u) {
+        const int idx = base + u * per_pass + (int)threadIdx.x * 8;
+        const int src = idx < K ? idx : 0;   // out-of-range lanes re-read x[0..7], never stored
+        b.v[u][0] = *reinterpret_cast<const float4*>(x + src);
+        b.v[u][1] = *reinterpret_cast<const float4*>(x + src + 4);
+    }
+}
+
+__device__ __forceinline__ void q8_quantize_batch(const X8Batch& b, int K, int base, Q8Lds lds) {
+    const int per_pass = (int)blockDim.x * 8;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int idx = base + u * per_pass + (int)threadIdx.x * 8;
+        const float e[8] = {b.v[u][0].x, b.v[u][0].y, b.v[u][0].z, b.v[u][0].w,
+                            b.v[u][1].x, b.v[u][1].y, b.v[u][1].z, b.v[u][1].w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(e[i]));
+        amax = fmaxf(amax, dpp_f<kQuadXor1>(amax));   // 4 lanes = one 32-element block
+        amax = fmaxf(amax, dpp_f<kQuadXor2>(amax));
+        const float scale = fmaxf(amax / 127.0f, 1e-30f);
+        const float sf = __half2float(__float2half(scale));
+        const float inv = 1.0f / sf;
+        uint32_t packed[2] = {0u, 0u};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = (int)fminf(fmaxf(e[i] * inv, -127.0f), 127.0f);
+            s += q;
+            packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
         }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int idx = base + u * per_pass + (int)threadIdx.x * 8;
-            const float e[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
-                                v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(e[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
-            const float scale = fmaxf(amax / 127.0f, 1e-30f);
-            const float sf = __half2float(__float2half(scale));
-            const float inv = 1.0f / sf;
-            uint32_t packed[2] = {0u, 0u};
-            int s = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int q = (int)fminf(fmaxf(e[i] * inv, -127.0f), 127.0f);
-                s += q;
-                packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
-            }
-            s += __shfl_xor(s, 1, kWave);
-            s += __shfl_xor(s, 2, kWave);
-            if (idx < K) {
-                *reinterpret_cast<u32x2*>(lds.qs + idx) = u32x2{packed[0], packed[1]};
-                if ((threadIdx.x & 3) == 0) {
-                    lds.xd[idx >> 5] = sf;
-                    lds.qsum[idx >> 5] = s;
-                }
+        s += dpp_i<kQuadXor1>(s);
+        s += dpp_i<kQuadXor2>(s);
+        if (idx < K) {
+            *reinterpret_cast<u32x2*>(lds.qs + q8_pad(idx)) = u32x2{packed[0], packed[1]};
+            if ((threadIdx.x & 3) == 0) {
+                lds.xd[idx >> 5] = sf;
+                lds.qsum[idx >> 5] = s;
             }
         }
     }
 }
 
-// fp32 copy of x into LDS with the same batched-load structure.
-__device__ __forceinline__ void stage_f32_to_lds(const float* __restrict__ x, int K, float* xs) {
-    const int per_pass = (int)blockDim.x * 4;
-    constexpr int kBatch = 8;
-    for (int base = 0; base < K; base += kBatch * per_pass) {
-        float4 v[kBatch];
+// Quantisation from an fp32 copy of x already in LDS (same arithmetic).
+__device__ __forceinline__ void q8_quantize_from_lds(const float* xs, int K, Q8Lds lds) {
+    const int per_pass = (int)blockDim.x * 8;
+    for (int base = 0; base < K; base += 4 * per_pass) {
+        X8Batch b;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < 4; ++u) {
+            const int idx = base + u * per_pass + (int)threadIdx.x * 8;
+            const int src = idx < K ? idx : 0;
+            b.v[u][0] = *reinterpret_cast<const float4*>(xs + src);
+            b.v[u][1] = *reinterpret_cast<const float4*>(xs + src + 4);
+        }
+        q8_quantize_batch(b, K, base, lds);
+    }
+}
+
+__device__ __forceinline__ void q8_prefetch(const float* __restrict__ x, int K, X8Batch& b0) {
+    q8_load_batch(x, K, 0, b0);
+}
+
+// Quantise all of x given the already loaded first batch.
+__device__ __forceinline__ void q8_quantize_finish(const float* __restrict__ x, int K, Q8Lds lds, const X8Batch& b0) {
+    const int batch = (int)blockDim.x * 8 * 4;
+    q8_quantize_batch(b0, K, 0, lds);
+    for (int base = batch; base < K; base += batch) {
+        X8Batch b;
+        q8_load_batch(x, K, base, b);
+        q8_quantize_batch(b, K, base, lds);
+    }
+}
+
+__device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x, int K, Q8Lds lds) {
+    X8Batch b0;
+    q8_prefetch(x, K, b0);
+    q8_quantize_finish(x, K, lds, b0);
+}
+
+// fp32 copy of x into LDS through registers (batched: eight float4 loads
+// in flight per thread).  Used where LDS reads of x must not look, to the
+// compiler, like reads of a region that LDS DMA may still be writing.
+__device__ __forceinline__ void stage_f32_to_lds_regs(const float* __restrict__ x, int K, float* xs) {
+    const int per_pass = (int)blockDim.x * 4;
+    for (int base = 0; base < K; base += 8 * per_pass) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
             const int idx = base + u * per_pass + (int)threadIdx.x * 4;
             v[u] = *reinterpret_cast<const float4*>(x + (idx < K ? idx : 0));
         }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < 8; ++u) {
             const int idx = base + u * per_pass + (int)threadIdx.x * 4;
-            if (idx < K) *reinterpret_cast<float4*>(xs + idx) = v[u];
+            if (idx < K) *reinterpret_cast<float4*>(xs + x_pad(idx)) = v[u];
         }
+    }
+}
+
+// fp32 copy of x into LDS with gfx950's direct HBM->LDS loads
+// (global_load_lds_dwordx4: each wave moves 1 KB per instruction without
+// staging registers, so every copy of the workgroup is in flight at once).
+// K*4 must be a multiple of 1 KB (K % 256 == 0) and xs must point to LDS.
+__device__ __forceinline__ void stage_f32_to_lds(const float* __restrict__ x, int K, float* xs) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = (int)blockDim.x / kWave;
+    for (int base = wave * 256; base < K; base += nw * 256) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(x + base + lane * 4),
+                                         (__attribute__((address_space(3))) void*)(xs + base), 16, 0, 0);
     }
 }
 
@@ -217,5 +309,11 @@ int device_cu_count();
 // GEMV workgroups per CU (host side; default 2, RF_GEMV_WG_PER_CU overrides
 // it for tuning sweeps).
 int gemv_wg_per_cu();
+// Whether the LDS-DMA streamed GEMV kernels are used (default no: the
+// register-pipelined kernels measure faster; RF_GEMV_STREAM=1 selects them).
+bool gemv_use_stream();
+// Rows per pipeline step of the register GEMV (default 1; RF_GEMV_R=2|4
+// for tuning sweeps).
+int gemv_rows_per_step();
 
 }  // namespace rf

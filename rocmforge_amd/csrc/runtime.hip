@@ -29,6 +29,25 @@ int gemv_wg_per_cu() {
     return v;
 }
 
+bool gemv_use_stream() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("RF_GEMV_STREAM");
+        v = (e && e[0] == '1') ? 1 : 0;
+    }
+    return v == 1;
+}
+
+int gemv_rows_per_step() {
+    static int v = 0;
+    if (v == 0) {
+        const char* e = getenv("RF_GEMV_R");
+        int n = e ? atoi(e) : 0;
+        v = (n == 1 || n == 2 || n == 4) ? n : 1;
+    }
+    return v;
+}
+
 }  // namespace rf
 
 // Library identification for loaders (the ctypes layer checks it).
