@@ -40,11 +40,13 @@ MALL_BYTES = 256 << 20
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run plain copies of known size (PMC traffic calibration)")
     return ap.parse_args()
 
 
@@ -90,26 +92,81 @@ def bench_decode(lib, torch, steps, warmup):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
 
-    # per-kernel durations with HIP events on the launch stream (separate pass
-    # so the headline timing carries no event overhead)
-    nev = min(steps, 500)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nev)]
-    torch.cuda.synchronize()
-    for i in range(nev):
-        step(i, evs[i])
-    torch.cuda.synchronize()
-    gu_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / nev
-    dn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / nev
+    # The decode step is launched the way a decode loop launches it: captured
+    # into a HIP graph and replayed.
+    # The launchers allocate nothing and never synchronise, so they capture.
+    def capture(fn_list):
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            with torch.cuda.graph(g, stream=cs):
+                cst = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for f in fn_list:
+                    f(cst)
+        torch.cuda.current_stream().wait_stream(cs)
+        torch.cuda.synchronize()
+        return g
+
+    def gu_call(c):
+        return lambda cst: gu(vp(sets[c][0]), vp(sets[c][1]), vp(x), vp(h), K_FFN, N_FFN, cst)
+
+    def dn_call(c):
+        return lambda cst: dn(vp(sets[c][2]), vp(h), vp(y), N_FFN, K_FFN, cst)
+
+    # one graph holds exactly K steps (weight copy i % copies at step i);
+    # two more hold K launches of each kernel alone, for per-kernel times
+    g_step = capture([f for i in range(steps) for f in (gu_call(i % copies), dn_call(i % copies))])
+    g_gu = capture([gu_call(i % copies) for i in range(steps)])
+    g_dn = capture([dn_call(i % copies) for i in range(steps)])
+
+    def timed(g):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps   # ms per step / per launch
+
+    timed(g_step)   # first replays upload the graphs; not timed
+    timed(g_gu)
+    timed(g_dn)
+    t0 = time.perf_counter()
+    step_ms = timed(g_step)   # the timed region: exactly K steps
+    wall = time.perf_counter() - t0
+    gu_ms = timed(g_gu)
+    dn_ms = timed(g_dn)
     return {
-        "wall": wall, "copies": copies, "gate_up_ms": gu_ms, "down_ms": dn_ms,
-        "x": x, "h": h, "y": y,
+        "wall": wall, "steps_run": steps, "step_ms": step_ms, "copies": copies,
+        "gate_up_ms": gu_ms, "down_ms": dn_ms, "x": x, "h": h, "y": y,
     }
+
+
+def calibrate_copy(torch, mbytes=256, reps=10):
+    """Plain device-to-device copies of a known size, run under rocprofv3
+    --pmc to scale FETCH_SIZE / WRITE_SIZE (each copy reads and writes
+    `mbytes` MiB)."""
+    n = (mbytes << 20) // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_per_copy": n * 4, "reps": reps}))
+
+
+def read_traffic():
+    """HBM bytes per gate+up launch from the committed rocprofv3 --pmc summary
+    (profiles/gemv_gate_up_llama8b_traffic.md, line 'traffic_bytes_per_launch:')."""
+    f = ROOT / "profiles" / "gemv_gate_up_llama8b_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip().replace(",", ""))
+    return None
 
 
 def bench_gemm(lib, torch):
@@ -189,9 +246,12 @@ def main():
     lib = rocmforge_amd.load()
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU (cuda:0)")
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
 
     r = bench_decode(lib, torch, args.steps, args.warmup)
-    ms = r["wall"] * 1e3 / args.steps
+    ms = r["step_ms"]
     value = STEP_BYTES / (ms * 1e-3) / 1e9
     gu_gbs = GATE_UP_BYTES / (r["gate_up_ms"] * 1e-3) / 1e9
     dn_gbs = DOWN_BYTES / (r["down_ms"] * 1e-3) / 1e9
@@ -200,7 +260,7 @@ def main():
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": r["steps_run"],
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
@@ -214,7 +274,7 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": "rf_q4k_q8_gemv_kernel<gate_up>",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "avg_launch_us": round(r["gate_up_ms"] * 1e3, 3), "bytes_per_launch": GATE_UP_BYTES},
         "kernels": {"gate_up_us": round(r["gate_up_ms"] * 1e3, 3), "gate_up_gbs": round(gu_gbs, 1),
                     "q6k_down_us": round(r["down_ms"] * 1e3, 3), "q6k_down_gbs": round(dn_gbs, 1)},
