@@ -21,6 +21,10 @@
 //    the CU count so a large N re-uses each workgroup's quantised vector.
 #include "stream.h"
 
+#ifndef RF_NB
+#define RF_NB 3   // register ring depth of the one-row-per-step GEMV (measured best)
+#endif
+
 namespace rf {
 
 constexpr int kThreads = 256;
@@ -70,8 +74,8 @@ __device__ __forceinline__ void q4k_load_step(Q4KUnit (&u)[M][R], const uint8_t*
     }
 }
 
-template <int MODE, int R>
-__global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
+template <int MODE, int R, int NW, int NB>
+__global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
                                                                    const uint8_t* __restrict__ w1,
                                                                    const float* __restrict__ x,
                                                                    const float* residual, float* y, int K, int N) {
@@ -85,9 +89,9 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
-    const int nwaves = gridDim.x * kWavesPerWg;
+    const int nwaves = gridDim.x * NW;
     int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * kWavesPerWg + wave, nwaves, &row_begin, &row_end);
+    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
     const int last = max(row_end - 1, 0);
 
     // Software pipeline over the steps (R-row group x 16 super-blocks) of
@@ -144,27 +148,16 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_q8_gemv_kernel(const uint8_t*
         }
     };
 
-    Q4KUnit ua[M][R], ub[M][R], uc[M][R];
-    // Three register buffers in rotation (loop unrolled by three): two steps
-    // are always in flight while one is computed, including during the
-    // activation staging.  Every load is unconditional (step index clamped;
-    // redundant reloads of the last step hit the cache) and the loop has a
-    // single exit at the latch, so the compiler's wait counting stays exact.
-    load(ua, 0);
-    load(ub, min(1, max(nsteps - 1, 0)));
-    q8_0_quantize_to_lds(x, K, q8);
-    __syncthreads();
-    int i = 0;
-    for (; i + 2 < nsteps; i += 3) {
-        load(uc, i + 2);
-        process(ua, i);
-        load(ua, min(i + 3, nsteps - 1));
-        process(ub, i + 1);
-        load(ub, min(i + 4, nsteps - 1));
-        process(uc, i + 2);
-    }
-    if (i < nsteps) process(ua, i);
-    if (i + 1 < nsteps) process(ub, i + 1);
+    struct Step {
+        Q4KUnit u[M][R];
+    };
+    Step ring[NB];
+    ring_pipeline<NB>(nsteps, ring, [&](Step& b, int i) { load(b.u, i); },
+                      [&](const Step& b, int i) { process(b.u, i); },
+                      [&]() {
+                          q8_0_quantize_to_lds(x, K, q8);
+                          __syncthreads();
+                      });
     for (int j = lane; j < row_end - row_begin; j += kWave) {
         const int row = row_begin + j;
         const float g = out_lds[M * j];
@@ -407,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
 // equal contiguous share of the rows), fewer when N is too small to give each
 // wave at least `min_rows` rows.
 static inline int gemv_grid(int N, int min_rows) {
-    const int cap = device_cu_count() * gemv_wg_per_cu();
+    const int cap = device_cu_count() * gemv_wg_per_cu(2);
     const int need = (N + kWavesPerWg * min_rows - 1) / (kWavesPerWg * min_rows);
     return need < cap ? need : cap;
 }
@@ -420,7 +413,7 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
         constexpr int R = (MODE == kGateUp) ? 1 : 2;
         constexpr int NW = 8, S = 3;
         using G = StepGeom<kQ4KBytes, M * R>;
-        const int cap = device_cu_count() * gemv_wg_per_cu();
+        const int cap = device_cu_count() * gemv_wg_per_cu(2);
         const int need = (N + NW - 1) / NW;
         const int grid = need < cap ? need : cap;
         const size_t out_off = (q8_lds_bytes(K) + 15) & ~(size_t)15;
@@ -441,19 +434,26 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
                            static_cast<const uint8_t*>(w1), x, res, y, K, N);
         return hipGetLastError();
     }
-    const int grid = gemv_grid(N, 1);
-    const size_t out_bytes = (size_t)kWavesPerWg * ((N + grid * kWavesPerWg - 1) / (grid * kWavesPerWg)) * M * 4;
-    if (q8_lds_bytes(K) + out_bytes > 160 * 1024) return hipErrorInvalidValue;
     const int r = gemv_rows_per_step();
+    const int nw = (r == 1) ? gemv_waves_per_wg(4) : 4;
+    const int cap = device_cu_count() * gemv_wg_per_cu(2);
+    const int need = (N + nw - 1) / nw;
+    const int grid = need < cap ? need : cap;
+    const size_t out_bytes = (size_t)nw * ((N + (size_t)grid * nw - 1) / ((size_t)grid * nw)) * M * 4;
+    if (q8_lds_bytes(K) + out_bytes > 160 * 1024) return hipErrorInvalidValue;
     const uint8_t* a = static_cast<const uint8_t*>(w0);
     const uint8_t* b = static_cast<const uint8_t*>(w1);
     const size_t lds = q8_lds_bytes(K) + out_bytes;
-    if (r == 1)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
+    if (r == 1 && nw == 16)
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 16, RF_NB>), dim3(grid), dim3(16 * 64), lds, st, a, b, x, res, y, K, N);
+    else if (r == 1 && nw == 8)
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 8, RF_NB>), dim3(grid), dim3(8 * 64), lds, st, a, b, x, res, y, K, N);
+    else if (r == 1)
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 4, RF_NB>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
     else if (r == 4 && MODE != kGateUp)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
     else
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2>), dim3(grid), dim3(kThreads), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
     return hipGetLastError();
 }
 

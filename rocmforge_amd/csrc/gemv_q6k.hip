@@ -16,10 +16,12 @@
 // produces 64 products against x held in LDS.
 #include "stream.h"
 
+#ifndef RF_Q6_NB
+#define RF_Q6_NB 3   // register ring depth of the one-row-per-step GEMV (measured best)
+#endif
+
 namespace rf {
 
-constexpr int kQ6Threads = 256;
-constexpr int kQ6Waves = kQ6Threads / kWave;
 constexpr int kQ6SbPerStep = 16;
 
 struct Q6Unit {
@@ -110,8 +112,8 @@ __device__ __forceinline__ void q6_xsum16(const float* xs, int K, float* xsum16)
     }
 }
 
-template <int R, bool LDS>
-__global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* __restrict__ w,
+template <int R, bool LDS, int NW, int NB>
+__global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_kernel(const uint8_t* __restrict__ w,
                                                                   const float* __restrict__ x, float* __restrict__ y,
                                                                   int K, int N) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -122,9 +124,9 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ6KBytes;
-    const int nwaves = gridDim.x * kQ6Waves;
+    const int nwaves = gridDim.x * NW;
     int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * kQ6Waves + wave, nwaves, &row_begin, &row_end);
+    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
 
     // Register-buffer pipeline, as in the Q4_K kernel.
     const int spr = (nsb + kQ6SbPerStep - 1) / kQ6SbPerStep;
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
     // store between the prefetch loads in the in-order memory counter)
     // LDS: [x (padded, LDS mode only)] [x group sums (K/16)] [row results]
     const int max_rows = (N + nwaves - 1) / nwaves;
-    float* xsum16 = reinterpret_cast<float*>(smem + (LDS ? (size_t)x_padded_floats(K) * 4 : 0));
+    float* xsum16 = reinterpret_cast<float*>(smem + (LDS ? (size_t)(x_padded_floats(K) + 4) * 4 : 0));
     float* out_lds = xsum16 + K / 16 + wave * max_rows;
     auto process = [&](const Q6Unit (&u)[R], int i) {
         const int row0 = row_begin + (i / spr) * R;
@@ -167,31 +169,20 @@ __global__ __launch_bounds__(kQ6Threads) void rf_q6k_gemv_kernel(const uint8_t* 
         }
     };
 
-    Q6Unit ua[R], ub[R], uc[R];
-    // Three register buffers in rotation (loop unrolled by three): two steps
-    // are always in flight while one is computed, including during the
-    // activation staging.  Every load is unconditional (step index clamped;
-    // redundant reloads of the last step hit the cache) and the loop has a
-    // single exit at the latch, so the compiler's wait counting stays exact.
-    load(ua, 0);
-    load(ub, min(1, max(nsteps - 1, 0)));
-    if (LDS) {
-        stage_f32_to_lds_regs(x, K, xs);
-        __syncthreads();
-    }
-    q6_xsum16<LDS>(xv, K, xsum16);
-    __syncthreads();
-    int i = 0;
-    for (; i + 2 < nsteps; i += 3) {
-        load(uc, i + 2);
-        process(ua, i);
-        load(ua, min(i + 3, nsteps - 1));
-        process(ub, i + 1);
-        load(ub, min(i + 4, nsteps - 1));
-        process(uc, i + 2);
-    }
-    if (i < nsteps) process(ua, i);
-    if (i + 1 < nsteps) process(ub, i + 1);
+    struct Step {
+        Q6Unit u[R];
+    };
+    Step ring[NB];
+    ring_pipeline<NB>(nsteps, ring, [&](Step& b, int i) { load(b.u, i); },
+                      [&](const Step& b, int i) { process(b.u, i); },
+                      [&]() {
+                          if (LDS) {
+                              stage_f32_to_lds_regs(x, K, xs);
+                              __syncthreads();
+                          }
+                          q6_xsum16<LDS>(xv, K, xsum16);
+                          __syncthreads();
+                      });
     for (int j = lane; j < row_end - row_begin; j += kWave) y[row_begin + j] = out_lds[j];
 }
 
@@ -210,7 +201,7 @@ __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_stream_kernel(const uint8
                                                                       float* __restrict__ y, int K, int N) {
     using G = StepGeom<kQ6KBytes, 1>;
     __shared__ __align__(16) uint8_t ring_lds[NW * S * G::kStageBytes];
-    __shared__ __align__(16) float xs[x_padded_floats(KMAX)];
+    __shared__ __align__(16) float xs[x_padded_floats(KMAX) + 4];
     __shared__ __align__(16) float xsum16[KMAX / 16];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -282,7 +273,7 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if (gemv_use_stream() && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
         (reinterpret_cast<uintptr_t>(input) & 15u) == 0) {
         constexpr int NW = 8, S = 3;
-        const int cap = device_cu_count() * gemv_wg_per_cu();
+        const int cap = device_cu_count() * gemv_wg_per_cu(1);
         const int need = (ncols_dst + NW - 1) / NW;
         const int grid = need < cap ? need : cap;
         const size_t max_rows = (ncols_dst + (size_t)grid * NW - 1) / ((size_t)grid * NW);
@@ -299,28 +290,29 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
             return hipGetLastError();
         }
     }
-    const int need = (ncols_dst + kQ6Waves - 1) / kQ6Waves;
-    const int cap = device_cu_count() * gemv_wg_per_cu();
+    const int r = gemv_rows_per_step();
+    const int nw = (r == 1) ? gemv_waves_per_wg(8) : 4;
+    const int need = (ncols_dst + nw - 1) / nw;
+    const int cap = device_cu_count() * gemv_wg_per_cu(nw == 8 ? 1 : 2);
     const int grid = need < cap ? need : cap;
-    const size_t lds = (size_t)x_padded_floats(n_rows) * sizeof(float);
-    const size_t out_bytes = (size_t)kQ6Waves * ((ncols_dst + grid * kQ6Waves - 1) / (grid * kQ6Waves)) * 4 +
+    const bool in_lds = (size_t)x_padded_floats(n_rows) * sizeof(float) <= 65536;
+    const size_t lds = in_lds ? (size_t)(x_padded_floats(n_rows) + 4) * sizeof(float) : 0;
+    const size_t out_bytes = (size_t)nw * ((ncols_dst + (size_t)grid * nw - 1) / ((size_t)grid * nw)) * 4 +
                              (size_t)(n_rows / 16) * 4;   // + x group sums
     if (out_bytes > 64 * 1024) return hipErrorInvalidValue;
-    const bool r2 = gemv_rows_per_step() >= 2;
-    if (lds <= 65536) {
-        if (r2)
-            hipLaunchKernelGGL((rf_q6k_gemv_kernel<2, true>), dim3(grid), dim3(kQ6Threads), lds + out_bytes, stream, w,
-                               input, output, n_rows, ncols_dst);
-        else
-            hipLaunchKernelGGL((rf_q6k_gemv_kernel<1, true>), dim3(grid), dim3(kQ6Threads), lds + out_bytes, stream, w,
-                               input, output, n_rows, ncols_dst);
+    const dim3 blk(nw * 64);
+#define RF_Q6_LAUNCH(RR, L, W) \
+    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, (RR == 1 ? RF_Q6_NB : 3)>), dim3(grid), blk, lds + out_bytes, stream, w, input, output, \
+                       n_rows, ncols_dst)
+    if (r >= 2) {
+        if (in_lds) RF_Q6_LAUNCH(2, true, 4); else RF_Q6_LAUNCH(2, false, 4);
+    } else if (nw == 16) {
+        if (in_lds) RF_Q6_LAUNCH(1, true, 16); else RF_Q6_LAUNCH(1, false, 16);
+    } else if (nw == 8) {
+        if (in_lds) RF_Q6_LAUNCH(1, true, 8); else RF_Q6_LAUNCH(1, false, 8);
     } else {
-        if (r2)
-            hipLaunchKernelGGL((rf_q6k_gemv_kernel<2, false>), dim3(grid), dim3(kQ6Threads), out_bytes, stream, w,
-                               input, output, n_rows, ncols_dst);
-        else
-            hipLaunchKernelGGL((rf_q6k_gemv_kernel<1, false>), dim3(grid), dim3(kQ6Threads), out_bytes, stream, w,
-                               input, output, n_rows, ncols_dst);
+        if (in_lds) RF_Q6_LAUNCH(1, true, 4); else RF_Q6_LAUNCH(1, false, 4);
     }
+#undef RF_Q6_LAUNCH
     return hipGetLastError();
 }

@@ -218,11 +218,14 @@ __device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x
     q8_quantize_finish(x, K, lds, b0);
 }
 
-// fp32 copy of x into LDS through registers (batched: eight float4 loads
-// in flight per thread).  Used where LDS reads of x must not look, to the
-// compiler, like reads of a region that LDS DMA may still be writing.
+// fp32 copy of x into LDS through registers, in the padded layout (x_pad):
+// eight float4 loads in flight per thread.  Stores are unconditional --
+// out-of-range lanes write the spare float4 at xs[x_padded_floats(K)] -- so
+// the compiler cannot sink each load into a store branch and serialise them.
+// xs must hold x_padded_floats(K) + 4 floats.
 __device__ __forceinline__ void stage_f32_to_lds_regs(const float* __restrict__ x, int K, float* xs) {
     const int per_pass = (int)blockDim.x * 4;
+    const int spare = x_padded_floats(K);
     for (int base = 0; base < K; base += 8 * per_pass) {
         float4 v[8];
 #pragma unroll
@@ -233,7 +236,7 @@ __device__ __forceinline__ void stage_f32_to_lds_regs(const float* __restrict__ 
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int idx = base + u * per_pass + (int)threadIdx.x * 4;
-            if (idx < K) *reinterpret_cast<float4*>(xs + x_pad(idx)) = v[u];
+            *reinterpret_cast<float4*>(xs + (idx < K ? x_pad(idx) : spare)) = v[u];
         }
     }
 }
@@ -250,6 +253,33 @@ __device__ __forceinline__ void stage_f32_to_lds(const float* __restrict__ x, in
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(x + base + lane * 4),
                                          (__attribute__((address_space(3))) void*)(xs + base), 16, 0, 0);
     }
+}
+
+// Register-ring software pipeline over `nsteps` steps with NB buffers: the
+// loads of NB-1 steps are in flight while one is computed.  The loop is
+// unrolled by NB so every buffer index is a compile-time constant (the
+// buffers live in registers and are never copied); every load is
+// unconditional (the step index is clamped, redundant reloads of the last
+// step hit the cache) and the loop has a single exit at its latch.  Those
+// three properties keep the compiler's in-order wait counting exact, so no
+// load is waited for before its own step.  `pre()` runs after the first
+// NB-1 steps have been issued (activation staging goes there).
+template <int NB, typename Buf, typename Load, typename Process, typename Pre>
+__device__ __forceinline__ void ring_pipeline(int nsteps, Buf (&buf)[NB], Load load, Process process, Pre pre) {
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j) load(buf[j], min(j, max(nsteps - 1, 0)));
+    pre();
+    int i = 0;
+    for (; i + NB - 1 < nsteps; i += NB) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            load(buf[(j + NB - 1) % NB], min(i + j + NB - 1, nsteps - 1));
+            process(buf[j], i + j);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j)
+        if (i + j < nsteps) process(buf[j], i + j);
 }
 
 // Contiguous output-row range of global wave `gw` out of `nw` (balanced to
@@ -306,14 +336,16 @@ __device__ __forceinline__ float q4k_q8_combine(float acc, float xd, float d, fl
 
 // Device CU count, cached per device (host side).
 int device_cu_count();
-// GEMV workgroups per CU (host side; default 2, RF_GEMV_WG_PER_CU overrides
-// it for tuning sweeps).
-int gemv_wg_per_cu();
+// GEMV workgroups per CU and waves per workgroup (host side).  Each kernel
+// family passes its measured-best default; RF_GEMV_WG_PER_CU / RF_GEMV_NW
+// override them for tuning sweeps.
+int gemv_wg_per_cu(int dflt);
 // Whether the LDS-DMA streamed GEMV kernels are used (default no: the
 // register-pipelined kernels measure faster; RF_GEMV_STREAM=1 selects them).
 bool gemv_use_stream();
 // Rows per pipeline step of the register GEMV (default 1; RF_GEMV_R=2|4
 // for tuning sweeps).
 int gemv_rows_per_step();
+int gemv_waves_per_wg(int dflt);
 
 }  // namespace rf

@@ -19,14 +19,14 @@ int device_cu_count() {
     return cached[dev];
 }
 
-int gemv_wg_per_cu() {
-    static int v = 0;
-    if (v == 0) {
+int gemv_wg_per_cu(int dflt) {
+    static int v = -1;
+    if (v < 0) {
         const char* e = getenv("RF_GEMV_WG_PER_CU");
         int n = e ? atoi(e) : 0;
-        v = (n >= 1 && n <= 16) ? n : 2;
+        v = (n >= 1 && n <= 16) ? n : 0;
     }
-    return v;
+    return v ? v : dflt;
 }
 
 bool gemv_use_stream() {
@@ -46,6 +46,16 @@ int gemv_rows_per_step() {
         v = (n == 1 || n == 2 || n == 4) ? n : 1;
     }
     return v;
+}
+
+int gemv_waves_per_wg(int dflt) {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("RF_GEMV_NW");
+        int n = e ? atoi(e) : 0;
+        v = (n == 4 || n == 8 || n == 16) ? n : 0;
+    }
+    return v ? v : dflt;
 }
 
 }  // namespace rf
