@@ -7,21 +7,29 @@
 // rounding is the reference's: A via __float2half (wmma_gemm_q4_k.hip:86),
 // W via __float2half of the fp32 dequant value (:137, q6: :148).
 //
-// Design (wave64 MFMA, not the gfx12 WMMA tiling):
-//  * Workgroup = 4 wave64s in a 2x2 grid over a BM x BN output tile; each
-//    wave owns a (BM/2) x (BN/2) sub-tile built from 32x32 blocks of
-//    v_mfma_f32_32x32x16_f16 (fp32 accumulators stay in registers).
-//  * K advances in chunks of 64 (= one Q4_K nibble pair / half of a Q6_K
-//    half-block).  Each chunk: A is read as fp32 and rounded to fp16, W is
-//    dequantised in registers (2 threads per weight row, 16 bytes of packed
-//    quants each) and both land in LDS as [row][k] fp16 with a padded row
-//    stride; the next chunk's global loads are in flight while the MFMAs of
-//    the current chunk run (register double buffering, two LDS buffers).
+// Two kernels:
+//  * rf_gemm_qk_v4_kernel (default when N % 256 == 0 and K % 512 == 0):
+//    512-thread workgroups over BM x 256 output tiles, A rounded to fp16
+//    once into LDS, W dequantised straight into MFMA B-operand registers,
+//    two waves per SIMD splitting each K chunk, optional split-K with float
+//    atomics when the tile count is below the CU count.  Its comment block
+//    below has the details.
+//  * rf_gemm_qk_kernel (any M % 64 == 0, N % 64 == 0, K % 256 == 0): the
+//    general fallback.  4 wave64s in a 2x2 grid over a BM x BN tile of 32x32
+//    blocks of v_mfma_f32_32x32x16_f16; each 64-wide K chunk of A (fp32 ->
+//    fp16) and of W (dequantised in registers, 2 threads per weight row)
+//    lands in LDS as [row][k] fp16 with a padded stride, double buffered.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "qk_common.h"
+#include "stream.h"
 
 namespace rf {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmThreads = 256;
@@ -261,9 +269,358 @@ __global__ __launch_bounds__(kGemmThreads) void rf_gemm_qk_kernel(const float* _
         }
 }
 
+// ── v4: 8 waves, two per SIMD; A through LDS, W dequantised per lane ──────
+// Workgroup = 512 threads = 8 wave64s.  Wave w owns output columns
+// [n0 + 64*(w&3), +64) (two 32-column MFMA blocks) for all BM = 32*FM rows
+// of the tile, and the K half kh = w>>2 of every 64-wide chunk: waves w and
+// w+4 (same SIMD) compute partial sums of the same outputs over disjoint k,
+// which are added through LDS at the end.  With two waves per SIMD one
+// wave's MFMAs run while the other dequantises or waits on memory.  Every
+// weight is dequantised exactly once per M tile, in the register of the lane
+// whose MFMA B operand needs it; A is rounded to fp16 once per tile into LDS.
+//
+// K order inside a chunk.  A dot product does not depend on the order of its
+// terms, so the MFMA k index may be any permutation of the chunk's physical k
+// as long as A and B use the same one.  Wave half kh, k16 step s2 (0..1),
+// lane half h = lane >> 5, slot e (0..7):
+//     physical k = 32*kh + 16*h + 8*s2 + e
+// so a lane's B operands for its half chunk come from ONE 16 B run of quant
+// bytes per row, and its A operand for step s2 is LDS row m, columns
+// [32kh + 16h + 8s2, +8).
+//   Q4_K chunk CQ (nibble pair CQ): k < 32 -> low nibble of qs byte 32CQ + k,
+//   k >= 32 -> high nibble of qs byte 32CQ + k - 32; both halves read qs bytes
+//   [32CQ + 16h, +16): byte j -> step j>>3, slot j&7, low nibble for kh = 0,
+//   high nibble for kh = 1.
+//   Q6_K chunk CQ (half nh = CQ>>1, t = CQ&1): quarter q = 2t + kh,
+//   l = k % 32 = 16h + j; ql byte 64nh + 32kh + l (high nibble iff t = 1),
+//   qh byte 32nh + l (bits 2q), scale sc[8nh + 2q + h] = byte (2kh + h) of
+//   scale word CQ (sc bytes [4CQ, 4CQ+4)).
+struct Q4Hdr {
+    u32x4 v;   // d, dmin, scales[12]
+};
+struct Q4Qs {
+    u32x4 q;   // qs bytes [32CQ + 16h, +16)
+};
+struct Q6Hdr {
+    uint32_t d;  // fp16 bits of d (bytes 208..209 in the low half)
+};
+struct Q6Qs {
+    u32x4 ql;      // ql [64nh + 32kh + 16h, +16)
+    u32x4 qh;      // qh [32nh + 16h, +16)
+    uint32_t sc;   // scales [4CQ, 4CQ+4)
+};
+
+__device__ __forceinline__ void put4(f16x8& dst, int half, float a, float b, float c, float d) {
+    dst[4 * half + 0] = (_Float16)a;
+    dst[4 * half + 1] = (_Float16)b;
+    dst[4 * half + 2] = (_Float16)c;
+    dst[4 * half + 3] = (_Float16)d;
+}
+__device__ __forceinline__ float byte_f(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFFu); }
+
+// Q4_K: B operands of one column for the wave's two k16 steps.  Nibbles are
+// converted with byte converts on masked words: low nibbles via
+// w & 0x0F0F0F0F, high nibbles via w & 0xF0F0F0F0 (= 16 * nibble) with the
+// scale divided by 16 -- a power of two, so (ds/16) * (16 n) == ds * n
+// exactly and the fp32 value ds*n - dm (and its fp16 rounding) is the
+// reference's.
+struct Q4Ops {
+    using Hdr = Q4Hdr;
+    using Qs = Q4Qs;
+    static constexpr int kBytes = kQ4KBytes;
+    static constexpr bool kHdrPerBlock = true;
+    static __device__ __forceinline__ Hdr hdr(const uint8_t* row, int sb) {
+        return Hdr{*reinterpret_cast<const u32x4*>(row + (size_t)sb * kQ4KBytes)};
+    }
+    template <int CQ>
+    static __device__ __forceinline__ Qs qs(const uint8_t* row, int sb, int h, int /*kh*/) {
+        return Qs{*reinterpret_cast<const u32x4*>(row + (size_t)sb * kQ4KBytes + 16 + 32 * CQ + 16 * h)};
+    }
+    template <int CQ>
+    static __device__ __forceinline__ void dequant(const Hdr& hd, const Qs& r, int h, int kh, f16x8 (&b)[2]) {
+        int sc0, m0, sc1, m1;
+        q4k_scale_min_pair(hd.v.y, hd.v.z, hd.v.w, CQ, &sc0, &m0, &sc1, &m1);
+        const float d = half_bits_to_float(hd.v.x), dmin = half_bits_to_float(hd.v.x >> 16);
+        const float ds = kh ? d * (float)sc1 * 0.0625f : d * (float)sc0;
+        const float dm = kh ? dmin * (float)m1 : dmin * (float)m0;
+        const uint32_t mask = kh ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        const uint32_t w[4] = {r.q.x & mask, r.q.y & mask, r.q.z & mask, r.q.w & mask};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)   // word j = bytes 4j..4j+3: step j>>1, slots 4*(j&1) + [0,4)
+            put4(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
+                 ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
+    }
+};
+
+// Q6_K: q = (ql nibble | qh bits << 4) in 0..63, value = s * (q - 32)
+// evaluated as s*q - 32s: s*q, 32s and their difference s*(q-32) are all
+// exact in fp32 (|s| has at most 19 significant bits, q at most 6), so the
+// fp32 value is the reference's d * sc * (q - 32).
+struct Q6Ops {
+    using Hdr = Q6Hdr;
+    using Qs = Q6Qs;
+    static constexpr int kBytes = kQ6KBytes;
+    static constexpr bool kHdrPerBlock = true;
+    static __device__ __forceinline__ Hdr hdr(const uint8_t* row, int sb) {
+        return Hdr{ld_u16(row + (size_t)sb * kQ6KBytes + 208)};
+    }
+    template <int CQ>
+    static __device__ __forceinline__ Qs qs(const uint8_t* row, int sb, int h, int kh) {
+        constexpr int nh = CQ >> 1;
+        const uint8_t* blk = row + (size_t)sb * kQ6KBytes;
+        return Qs{ld16(blk + 64 * nh + 32 * kh + 16 * h), ld16(blk + 128 + 32 * nh + 16 * h), ld4(blk + 192 + 4 * CQ)};
+    }
+    template <int CQ>
+    static __device__ __forceinline__ void dequant(const Hdr& hd, const Qs& r, int h, int kh, f16x8 (&b)[2]) {
+        constexpr int t = CQ & 1;
+        const float d = half_bits_to_float(hd.d);
+        const float s = d * (float)(int8_t)((r.sc >> (8 * (2 * kh + h))) & 0xFFu);
+        const float o = 32.0f * s;
+        constexpr uint32_t nsh = 4u * t;                   // low nibble for q < 2, high for q >= 2
+        const uint32_t qsh = 4u * t + 2u * (uint32_t)kh;   // qh shift 2q
+        const uint32_t L[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
+        const uint32_t QH[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t q = ((L[j] >> nsh) & 0x0F0F0F0Fu) | (((QH[j] >> qsh) & 0x03030303u) << 4);
+            put4(b[j >> 1], j & 1, s * byte_f(q, 0) - o, s * byte_f(q, 1) - o, s * byte_f(q, 2) - o,
+                 s * byte_f(q, 3) - o);
+        }
+    }
+};
+
+constexpr int kV4Threads = 512;
+constexpr int kV4LdsBytes = 65536;
+
+// Chunk pipeline (K advances 64 per chunk; this workgroup's chunks are
+// [c_begin, c_last], c_begin and the count multiples of 8):
+//   iteration c:  (1) A(c+1) registers -> fp16 -> LDS buffer (c+1)&1
+//                 (2) W(c) quant registers (+ super-block header) -> B operands
+//                 (3) issue global loads of A(c+3) and W(c+2) (+ the header of
+//                     the super-block W(c+2) starts, if it starts one)
+//                 (4) 2 k16 steps x FM x 2 MFMAs from LDS buffer c&1
+//                 (5) LDS-only barrier (outstanding global loads stay in flight)
+// A and W loads have two iterations to land.  Register sets are indexed by
+// chunk parity (A staging, quant bytes) and super-block parity (headers); the
+// loop is unrolled over 8 chunks so every index is static.  Loads past c_last
+// re-read the chunk four back (same position in its super-block).
+// SPLIT: the grid is tiles x splits; split s covers an equal run of chunks
+// and adds its partial tile into D (zeroed beforehand) with float atomics.
+template <typename T, int FM, bool SPLIT>
+__global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int tiles, int chunks_per_split) {
+    constexpr int BM = 32 * FM;
+    constexpr int BN = 256;
+    constexpr int A_F4 = BM * kKC / 4 / kV4Threads;   // float4 per thread per chunk
+    constexpr int A_BUF = BM * kLdsStride;             // halves per A buffer
+    static_assert(2 * A_BUF * 2 <= kV4LdsBytes, "A buffers");
+    static_assert(4 * (FM / 2) * 2 * 16 * 64 * 4 <= kV4LdsBytes, "reduction buffer");
+    __shared__ __align__(16) uint8_t lds[kV4LdsBytes];
+    _Float16* lds_a = reinterpret_cast<_Float16*>(lds);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 3, kh = wave >> 2;
+    const int h = lane >> 5;
+    const int tile = blockIdx.x % tiles;
+    const int split = blockIdx.x / tiles;
+    const int ntiles = N / BN;
+    const int m0 = (tile / ntiles) * BM;
+    const int n0 = (tile % ntiles) * BN + wn * 64;
+    const int c_begin = split * chunks_per_split;
+    const int c_last = c_begin + chunks_per_split - 1;
+    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
+    const uint8_t* wrow0 = W + (size_t)(n0 + (lane & 31)) * row_bytes;
+    const uint8_t* wrow1 = wrow0 + 32 * row_bytes;
+
+    // A staging, coalesced: float4 f = i*512 + tid of the BM x 64 chunk is
+    // row f/16, columns 4*(f%16) .. +3 (a wave instruction covers 4 rows).
+    const int a_row = tid >> 4;
+    const int a_col = 4 * (tid & 15);
+    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
+    float4 a_reg[2][A_F4];
+    typename T::Hdr hdr[2][2];   // [super-block parity][row]
+    typename T::Qs qsr[2][2];    // [chunk parity][row]
+
+    auto a_load = [&](float4 (&r)[A_F4], int c) {
+        const float* src = a_base + (size_t)min(c, c_last) * kKC;
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(32 * i) * K);
+    };
+    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
+        _Float16* dst = lds_a + buf * A_BUF + a_row * kLdsStride + a_col;
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) {
+            f16x4 hv;
+            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
+            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
+            *reinterpret_cast<f16x4*>(dst + 32 * i * kLdsStride) = hv;
+        }
+    };
+    // W(c) with c = c8 + J (J static, c8 a multiple of 8)
+    auto w_load = [&](auto jj, int c8) {
+        constexpr int J = decltype(jj)::value;
+        constexpr int JQ = J & 3;
+        int sb = c8 / 4 + (J >> 2);
+        if (c8 + J > c_last) --sb;
+        if constexpr (JQ == 0) {
+            hdr[(J >> 2) & 1][0] = T::hdr(wrow0, sb);
+            hdr[(J >> 2) & 1][1] = T::hdr(wrow1, sb);
+        }
+        qsr[J & 1][0] = T::template qs<JQ>(wrow0, sb, h, kh);
+        qsr[J & 1][1] = T::template qs<JQ>(wrow1, sb, h, kh);
+    };
+
+    f32x16 acc[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int frag = (lane & 31) * kLdsStride + 32 * kh + 16 * h;
+    // iteration I of the 8-chunk group starting at chunk c8
+    auto iteration = [&](auto it, int c8) {
+        constexpr int I = decltype(it)::value;
+        constexpr int P = I & 1;
+        const int c = c8 + I;
+        __builtin_amdgcn_sched_barrier(0);
+        a_store(a_reg[P ^ 1], P ^ 1);
+        f16x8 bq[2][2];
+        T::template dequant<I & 3>(hdr[(I >> 2) & 1][0], qsr[P][0], h, kh, bq[0]);
+        T::template dequant<I & 3>(hdr[(I >> 2) & 1][1], qsr[P][1], h, kh, bq[1]);
+        a_load(a_reg[P ^ 1], c + 3);
+        w_load(std::integral_constant<int, I + 2>{}, c8);
+        const _Float16* la = lds_a + P * A_BUF + frag;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            f16x8 af[FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride + 8 * s2);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bq[j][s2], acc[i][j], 0, 0, 0);
+        }
+        lds_barrier();
+    };
+
+    // prologue: A(c0) -> LDS 0; A(c0+1), A(c0+2), W(c0), W(c0+1) in flight
+    a_load(a_reg[0], c_begin);
+    w_load(std::integral_constant<int, 0>{}, c_begin);
+    a_load(a_reg[1], c_begin + 1);
+    w_load(std::integral_constant<int, 1>{}, c_begin);
+    a_store(a_reg[0], 0);
+    a_load(a_reg[0], c_begin + 2);
+    lds_barrier();
+
+    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
+        iteration(std::integral_constant<int, 0>{}, c8);
+        iteration(std::integral_constant<int, 1>{}, c8);
+        iteration(std::integral_constant<int, 2>{}, c8);
+        iteration(std::integral_constant<int, 3>{}, c8);
+        iteration(std::integral_constant<int, 4>{}, c8);
+        iteration(std::integral_constant<int, 5>{}, c8);
+        iteration(std::integral_constant<int, 6>{}, c8);
+        iteration(std::integral_constant<int, 7>{}, c8);
+    }
+
+    // Add the two K halves through LDS and store: round 0, the kh = 1 wave
+    // hands its rows i < FM/2 to its kh = 0 partner, which adds and stores
+    // them; round 1 the other way round for rows i >= FM/2.
+    float* red = reinterpret_cast<float*>(lds) + wn * (FM / 2) * 2 * 16 * 64 + lane;
+    auto store = [&](int i, int j, const f32x16& v) {
+        const int col = n0 + 32 * j + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if constexpr (SPLIT)
+                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
+            else
+                D[(size_t)row * N + col] = v[e];
+        }
+    };
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        const int giver = round == 0 ? 1 : 0;
+        if (kh == giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) red[((ii * 2 + j) * 16 + e) * 64] = acc[round * (FM / 2) + ii][j][e];
+        }
+        __syncthreads();
+        if (kh != giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f32x16 v = acc[round * (FM / 2) + ii][j];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] += red[((ii * 2 + j) * 16 + e) * 64];
+                    store(round * (FM / 2) + ii, j, v);
+                }
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void rf_fill_zero_kernel(float4* __restrict__ p, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// Split count: the largest S with S | (K/64)/8 (each split a whole number of
+// 8-chunk groups) and tiles * S <= CUs (one workgroup per CU; the kernel
+// runs one 512-thread workgroup per CU).  Measured on MI355X at the
+// Llama-3.1-8B FFN shapes this is the best split for M = 64 .. 512.
+static int gemm_splits(int tiles, int nchunks, int cus) {
+    const int groups = nchunks / 8;
+    int best = 1;
+    for (int s = 2; s <= groups && s <= 32; ++s)
+        if (groups % s == 0 && (long)tiles * s <= cus) best = s;
+    return best;
+}
+
+template <bool IS_Q6, int FM>
+static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st) {
+    using T = typename std::conditional<IS_Q6, Q6Ops, Q4Ops>::type;
+    const int tiles = (M / (32 * FM)) * (N / 256);
+    const int nchunks = K / kKC;
+    int s = gemm_splits(tiles, nchunks, device_cu_count());
+    if (const char* e = getenv("RF_GEMM_SPLIT")) {   // tuning override, must divide (K/64)/8
+        const int v = atoi(e);
+        if (v >= 1 && (nchunks / 8) % v == 0) s = v;
+    }
+    if (s > 1) {
+        const size_t n4 = (size_t)M * N / 4;
+        hipLaunchKernelGGL(rf_fill_zero_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 2048)), dim3(256), 0,
+                           st, reinterpret_cast<float4*>(D), n4);
+        hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D, M,
+                           N, K, tiles, nchunks / s);
+    } else {
+        hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M, N,
+                           K, tiles, nchunks);
+    }
+}
+
 template <bool IS_Q6>
 static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
+    if (N % 256 == 0 && K % 512 == 0 && gemm_use_v2()) {
+        if (M % 128 == 0)
+            launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
+        else
+            launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st);
+        return hipGetLastError();
+    }
     if (M % 128 == 0 && N % 128 == 0 && (size_t)(M / 128) * (N / 128) >= (size_t)device_cu_count()) {
         hipLaunchKernelGGL((rf_gemm_qk_kernel<IS_Q6, 128, 128>), dim3(N / 128, M / 128), dim3(kGemmThreads), 0, st,
                            A, w, D, M, N, K);

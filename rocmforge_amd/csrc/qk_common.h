@@ -347,5 +347,7 @@ bool gemv_use_stream();
 // for tuning sweeps).
 int gemv_rows_per_step();
 int gemv_waves_per_wg(int dflt);
+// GEMM kernel generation (RF_GEMM_V=1 selects the first-generation tiling).
+bool gemm_use_v2();
 
 }  // namespace rf

@@ -58,6 +58,15 @@ int gemv_waves_per_wg(int dflt) {
     return v ? v : dflt;
 }
 
+bool gemm_use_v2() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("RF_GEMM_V");
+        v = (e && e[0] == '1') ? 0 : 1;
+    }
+    return v == 1;
+}
+
 }  // namespace rf
 
 // Library identification for loaders (the ctypes layer checks it).
