@@ -572,6 +572,256 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* 
     }
 }
 
+// ── v5: v4 with the weights staged through an LDS ring ───────────────────
+// Per-lane weight loads (32 rows per instruction, 16 B each) saturate the
+// vector L1 long before the MFMAs do.  Here the workgroup loads each
+// super-block of its 256 weight rows with coalesced 16-byte loads (a wave
+// instruction covers 1 KB of consecutive pieces of ~8 rows: whole cache
+// lines), parks them in registers for two chunk iterations, writes them to
+// a ring of kStages LDS stages, and each lane reads its operand bytes from
+// LDS.  (Plain loads + ds_write rather than LDS DMA: a DMA mixed with the A
+// loads leaves the compiler unable to count outstanding loads, and it then
+// waits for all of them.)
+//   Stage layout: row r of the tile at r * kRS.  Q4_K: the 144-byte block
+//   (9 pieces).  Q6_K (blocks are only 2-byte aligned): the 16-byte aligned
+//   window of 14 pieces starting at floor16(block), then one padding piece
+//   (a second copy of piece 13) so that the row stride, 240 bytes, is
+//   bank-conflict free; block byte b sits at r * 240 + shift + b with
+//   shift = block offset mod 16 = 2 * (sb mod 8) (row starts are 16-byte
+//   aligned because K % 2048 == 0).
+//   Loads: every wave issues kNI 16-byte loads per super-block; instruction
+//   g = wave * kNI + t moves stage pieces [64 g, 64 g + 64) (lane-linear).
+//   The stage holds kGroups such groups; g >= kGroups repeats group
+//   g - kGroups (the same bytes to the same place).
+//   Schedule: the loads of super-block sb + kDepth are issued in the first
+//   chunk iteration of sb and written to LDS in its third; the slot they
+//   overwrite belonged to sb - 1, finished one barrier earlier.
+template <bool IS_Q6>
+struct RingGeom;
+template <>
+struct RingGeom<false> {
+    static constexpr int kRS = 144, kNPR = 9, kStages = 3, kGroups = 36, kNI = 5;
+};
+template <>
+struct RingGeom<true> {
+    static constexpr int kRS = 240, kNPR = 15, kStages = 2, kGroups = 60, kNI = 8;
+};
+
+template <typename T, bool IS_Q6, int FM, bool SPLIT>
+__global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v5_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int tiles, int chunks_per_split) {
+    using G = RingGeom<IS_Q6>;
+    constexpr int BM = 32 * FM;
+    constexpr int BN = 256;
+    constexpr int A_F4 = BM * kKC / 4 / kV4Threads;   // float4 per thread per chunk
+    constexpr int kStageBytes = BN * G::kRS;
+    constexpr int kDepth = G::kStages - 1;             // super-blocks staged ahead
+    static_assert(G::kGroups * 1024 == kStageBytes && 8 * G::kNI >= G::kGroups && 8 * G::kNI < 2 * G::kGroups,
+                  "load groups cover the stage");
+    static_assert(4 * (FM / 2) * 2 * 16 * 64 * 4 <= G::kStages * kStageBytes, "reduction buffer");
+    __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
+    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 3, kh = wave >> 2;
+    const int h = lane >> 5;
+    const int tile = blockIdx.x % tiles;
+    const int split = blockIdx.x / tiles;
+    const int ntiles = N / BN;
+    const int m0 = (tile / ntiles) * BM;
+    const int nt0 = (tile % ntiles) * BN;   // first weight row of the tile
+    const int n0 = nt0 + wn * 64;
+    const int c_begin = split * chunks_per_split;
+    const int c_last = c_begin + chunks_per_split - 1;
+    const int sb_begin = c_begin / 4, sb_last = c_last / 4;
+    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
+    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
+
+    // per-lane staging source offsets (relative to the tile's rows at
+    // super-block 0) and LDS destinations
+    uint32_t goff[G::kNI];
+    uint32_t gdst[G::kNI];
+#pragma unroll
+    for (int t = 0; t < G::kNI; ++t) {
+        int g = wave * G::kNI + t;
+        if (g >= G::kGroups) g -= G::kGroups;
+        const int pc = 64 * g + lane;
+        gdst[t] = 16u * (uint32_t)pc;
+        const int row = pc / G::kNPR;
+        int piece = pc % G::kNPR;
+        if (IS_Q6 && piece == 14) piece = 13;
+        goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
+    }
+    u32x4 wst[G::kNI];
+    auto w_gload = [&](int sb) {
+        sb = min(sb, sb_last);
+        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
+    };
+    auto w_lstore = [&](int slot) {
+        uint8_t* dst = w_ring + slot * kStageBytes;
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
+    };
+
+    const int a_row = tid >> 4;
+    const int a_col = 4 * (tid & 15);
+    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
+    float4 a_reg[2][A_F4];
+    auto a_load = [&](float4 (&r)[A_F4], int c) {
+        const float* src = a_base + (size_t)min(c, c_last) * kKC;
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(32 * i) * K);
+    };
+    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
+        _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) {
+            f16x4 hv;
+            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
+            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
+            *reinterpret_cast<f16x4*>(dst + 32 * i * kLdsStride) = hv;
+        }
+    };
+
+    f32x16 acc[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int frag = (lane & 31) * kLdsStride + 32 * kh + 16 * h;
+    const int row_lds0 = (wn * 64 + (lane & 31)) * G::kRS;
+    const int row_lds1 = row_lds0 + 32 * G::kRS;
+
+    // iteration I of the 8-chunk group starting at chunk c8 (super-blocks
+    // c8/4 and c8/4+1 in ring slots slot0, slot1; staging targets sd0, sd1)
+    auto iteration = [&](auto it, int c8, int slot0, int slot1, int sd0, int sd1) {
+        constexpr int I = decltype(it)::value;
+        constexpr int P = I & 1, CQ = I & 3;
+        const int c = c8 + I;
+        const int sb = c8 / 4 + (I >> 2);
+        const int slot = (I >> 2) ? slot1 : slot0;
+        __builtin_amdgcn_sched_barrier(0);
+        a_store(a_reg[P ^ 1], P ^ 1);
+        if constexpr (CQ == 2) w_lstore((I >> 2) ? sd1 : sd0);
+        typename T::Hdr hd[2];
+        typename T::Qs qs[2];
+        const uint8_t* st = w_ring + slot * kStageBytes;
+        if constexpr (IS_Q6) {
+            const int shift = 2 * (sb & 7);
+            constexpr int nh = CQ >> 1;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + shift;
+                qs[r].ql = ld16(rb + 64 * nh + 32 * kh + 16 * h);
+                qs[r].qh = ld16(rb + 128 + 32 * nh + 16 * h);
+                qs[r].sc = ld4(rb + 192 + 4 * CQ);
+                hd[r].d = ld_u16(rb + 208);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
+                hd[r].v = *reinterpret_cast<const u32x4*>(rb);
+                qs[r].q = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
+            }
+        }
+        f16x8 bq[2][2];
+        T::template dequant<CQ>(hd[0], qs[0], h, kh, bq[0]);
+        T::template dequant<CQ>(hd[1], qs[1], h, kh, bq[1]);
+        a_load(a_reg[P ^ 1], c + 3);
+        if constexpr (CQ == 0) w_gload(sb + kDepth);
+        const _Float16* la = lds_a[P] + frag;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            f16x8 af[FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride + 8 * s2);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bq[j][s2], acc[i][j], 0, 0, 0);
+        }
+        lds_barrier();
+    };
+
+    // prologue: super-blocks sb_begin .. sb_begin+kDepth-1 into slots 0..;
+    // A(c0) -> LDS 0; A(c0+1), A(c0+2) in flight
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        w_gload(sb_begin + d);
+        w_lstore(d);
+    }
+    a_load(a_reg[0], c_begin);
+    a_load(a_reg[1], c_begin + 1);
+    a_store(a_reg[0], 0);
+    a_load(a_reg[0], c_begin + 2);
+    lds_barrier();
+
+    int slot0 = 0;   // ring slot of super-block c8/4
+    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
+        const int slot1 = slot0 + 1 == G::kStages ? 0 : slot0 + 1;
+        const int sd0 = slot0 + kDepth >= G::kStages ? slot0 + kDepth - G::kStages : slot0 + kDepth;
+        const int sd1 = sd0 + 1 == G::kStages ? 0 : sd0 + 1;
+        iteration(std::integral_constant<int, 0>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 1>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 2>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 3>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 4>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 5>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 6>{}, c8, slot0, slot1, sd0, sd1);
+        iteration(std::integral_constant<int, 7>{}, c8, slot0, slot1, sd0, sd1);
+        slot0 = slot1 + 1 == G::kStages ? 0 : slot1 + 1;
+    }
+
+    float* red = reinterpret_cast<float*>(w_ring) + wn * (FM / 2) * 2 * 16 * 64 + lane;
+    auto store = [&](int i, int j, const f32x16& v) {
+        const int col = n0 + 32 * j + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if constexpr (SPLIT)
+                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
+            else
+                D[(size_t)row * N + col] = v[e];
+        }
+    };
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        const int giver = round == 0 ? 1 : 0;
+        if (kh == giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) red[((ii * 2 + j) * 16 + e) * 64] = acc[round * (FM / 2) + ii][j][e];
+        }
+        __syncthreads();
+        if (kh != giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f32x16 v = acc[round * (FM / 2) + ii][j];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] += red[((ii * 2 + j) * 16 + e) * 64];
+                    store(round * (FM / 2) + ii, j, v);
+                }
+        }
+        __syncthreads();
+    }
+}
+
 __global__ void rf_fill_zero_kernel(float4* __restrict__ p, size_t n4) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
         p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -599,22 +849,32 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
         const int v = atoi(e);
         if (v >= 1 && (nchunks / 8) % v == 0) s = v;
     }
+    // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
+    const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
     if (s > 1) {
         const size_t n4 = (size_t)M * N / 4;
         hipLaunchKernelGGL(rf_fill_zero_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 2048)), dim3(256), 0,
                            st, reinterpret_cast<float4*>(D), n4);
-        hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D, M,
-                           N, K, tiles, nchunks / s);
+        if (v5)
+            hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
+                               w, D, M, N, K, tiles, nchunks / s);
+        else
+            hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D,
+                               M, N, K, tiles, nchunks / s);
     } else {
-        hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M, N,
-                           K, tiles, nchunks);
+        if (v5)
+            hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
+                               D, M, N, K, tiles, nchunks);
+        else
+            hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M,
+                               N, K, tiles, nchunks);
     }
 }
 
 template <bool IS_Q6>
 static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    if (N % 256 == 0 && K % 512 == 0 && gemm_use_v2()) {
+    if (N % 256 == 0 && K % 512 == 0 && gemm_kernel_version() != 1) {
         if (M % 128 == 0)
             launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
         else

@@ -347,7 +347,9 @@ bool gemv_use_stream();
 // for tuning sweeps).
 int gemv_rows_per_step();
 int gemv_waves_per_wg(int dflt);
-// GEMM kernel generation (RF_GEMM_V=1 selects the first-generation tiling).
-bool gemm_use_v2();
+// GEMM kernel selection for tuning comparisons: RF_GEMM_V=1 forces the
+// general 2x2-wave kernel, =4 the register-weight kernel; default (0) picks
+// the weight-ring kernel where it applies.
+int gemm_kernel_version();
 
 }  // namespace rf

@@ -58,13 +58,14 @@ int gemv_waves_per_wg(int dflt) {
     return v ? v : dflt;
 }
 
-bool gemm_use_v2() {
+int gemm_kernel_version() {
     static int v = -1;
     if (v < 0) {
         const char* e = getenv("RF_GEMM_V");
-        v = (e && e[0] == '1') ? 0 : 1;
+        const int n = e ? atoi(e) : 0;
+        v = (n == 1 || n == 4) ? n : 0;
     }
-    return v == 1;
+    return v;
 }
 
 }  // namespace rf

@@ -33,14 +33,15 @@ def _check(got, ref, what):
     assert worst <= 1.0, what
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q6_k"])
-def test_gemm_byte_level_identity(rf, dev, fmt):
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 64, 256), ("q6_k", 64, 256),      # general kernel
+                                     ("q4_k", 256, 512), ("q6_k", 256, 2048)])  # weight-ring kernel
+def test_gemm_byte_level_identity(rf, dev, fmt, n, k):
     # the reference's byte-level test (wmma_q4_k_correctness.rs:89-185,
-    # wmma_q6_k_correctness.rs:75-160): A = I (64 x 256), every W row the same
-    # hand-built block, so D[r, c] = dequant[r].
-    m, n, k = 64, 64, 256
+    # wmma_q6_k_correctness.rs:75-160): A = I (64 x k), every W row the same
+    # hand-built block, so D[r, c] = dequant[r] bit for bit.
+    m = 64
     blk = _byte_level_q4k_block() if fmt == "q4_k" else _byte_level_q6k_block()
-    w = np.tile(blk, (n, 1))
+    w = np.tile(blk, (n, k // 256))
     a = np.zeros((m, k), np.float32)
     a[np.arange(m), np.arange(m)] = 1.0
     got = _run(rf, fmt, a, w, m, n, k)
@@ -56,6 +57,26 @@ def test_gemm_byte_level_identity(rf, dev, fmt):
 def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
     a = synth.activations(k, seed=m + n, m=m)
     w = synth.weights(fmt, n, k, seed=k)
+    _check(_run(rf, fmt, a, w, m, n, k), O.gemm(fmt, a, w, m, n, k), f"{fmt} {m}x{n}x{k}")
+
+
+# One case per launcher branch for N % 256 == 0, K % 512 == 0 (the tiled
+# kernels): tile height 128 (M % 128 == 0) or 64, split-K (tiles below the CU
+# count) or not, weight-ring kernel or (Q6_K with K % 2048 != 0) the
+# register-weight kernel.
+@pytest.mark.parametrize("fmt,m,n,k", [
+    ("q4_k", 64, 256, 512),      # ring, 64-row tiles, 1 split
+    ("q4_k", 192, 256, 1024),    # ring, 64-row tiles, 2 splits
+    ("q4_k", 128, 512, 2048),    # ring, 128-row tiles, 4 splits
+    ("q4_k", 2048, 8192, 512),   # ring, 128-row tiles, 256 tiles, no split
+    ("q6_k", 64, 256, 2048),     # ring, 64-row tiles, 4 splits
+    ("q6_k", 256, 512, 4096),    # ring, 128-row tiles, 8 splits
+    ("q6_k", 128, 256, 1536),    # register weights, 128-row tiles, 3 splits
+    ("q6_k", 64, 256, 512),      # register weights, 64-row tiles, 1 split
+])
+def test_gemm_tiled_kernel_branches(rf, dev, fmt, m, n, k):
+    a = synth.activations(k, seed=m + 3 * n, m=m)
+    w = synth.weights(fmt, n, k, seed=k + 1)
     _check(_run(rf, fmt, a, w, m, n, k), O.gemm(fmt, a, w, m, n, k), f"{fmt} {m}x{n}x{k}")
 
 
