@@ -62,18 +62,6 @@ __device__ __forceinline__ float q4k_q8_unit_dot(const Q4KUnit& u, int p, const 
     return acc;
 }
 
-template <int M, int R>
-__device__ __forceinline__ void q4k_load_step(Q4KUnit (&u)[M][R], const uint8_t* w0, const uint8_t* w1,
-                                              size_t row_bytes, int row0, int N, int sbc, int p) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, N - 1);
-        const size_t off = (size_t)row * row_bytes + (size_t)sbc * kQ4KBytes;
-        u[0][r] = q4k_load_unit(w0 + off, p);
-        if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
-    }
-}
-
 template <int MODE, int R, int NW, int NB>
 __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
                                                                    const uint8_t* __restrict__ w1,
@@ -90,18 +78,26 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
     const int nwaves = gridDim.x * NW;
-    int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
-    const int last = max(row_end - 1, 0);
+    // Rows are dealt out round-robin: global wave gw owns rows gw, gw+nwaves,
+    // ...  All waves of the grid then stream neighbouring rows at the same
+    // time, which keeps the open DRAM pages few (measured: an interleaved
+    // read of 64 MB runs ~12% faster than per-wave contiguous stretches).
+    const int gw = blockIdx.x * NW + wave;
+    const int rstride = nwaves, rfirst = gw;
+    const int nrows = gw < N ? (N - 1 - gw) / nwaves + 1 : 0;
+    const int max_rows = (N + nwaves - 1) / nwaves;
 
-    // Software pipeline over the steps (R-row group x 16 super-blocks) of
-    // this wave's contiguous row range (register buffers below).
     const int spr = (nsb + kSbPerStep - 1) / kSbPerStep;        // steps per row group
-    const int nsteps = ((row_end - row_begin + R - 1) / R) * spr;
+    const int nsteps = ((nrows + R - 1) / R) * spr;
+    auto row_of = [&](int j) { return nrows ? rfirst + min(j, nrows - 1) * rstride : 0; };
     auto load = [&](Q4KUnit (&u)[M][R], int i) {
-        const int row0 = row_begin + (i / spr) * R;
-        const int sb = (i % spr) * kSbPerStep + s;
-        q4k_load_step<M, R>(u, w0, w1, row_bytes, row0, last + 1, min(sb, nsb - 1), p);
+        const int sb = min((i % spr) * kSbPerStep + s, nsb - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t off = (size_t)row_of((i / spr) * R + r) * row_bytes + (size_t)sb * kQ4KBytes;
+            u[0][r] = q4k_load_unit(w0 + off, p);
+            if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
+        }
     };
     float acc[M][R];
 #pragma unroll
@@ -111,10 +107,9 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     // Row results are parked in this wave's LDS slots and written to HBM
     // after the loop: no global store (or residual load) sits between the
     // prefetch loads in the in-order memory counter.
-    const int max_rows = (N + nwaves - 1) / nwaves;
     float* out_lds = reinterpret_cast<float*>(smem + q8_lds_bytes(K)) + wave * max_rows * M;
     auto process = [&](const Q4KUnit (&u)[M][R], int i) {
-        const int row0 = row_begin + (i / spr) * R;
+        const int j0 = (i / spr) * R;
         const int sb = (i % spr) * kSbPerStep + s;
         const bool live = sb < nsb;
         const int sbc = live ? sb : nsb - 1;
@@ -137,8 +132,8 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
             for (int r = 0; r < R; ++r) {
                 const float g = wave_sum(acc[0][r]);
                 const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
-                const int j = row0 + r - row_begin;
-                if (lane == 0 && row0 + r < row_end) {
+                const int j = j0 + r;
+                if (lane == 0 && j < nrows) {
                     out_lds[M * j] = g;
                     if (M == 2) out_lds[M * j + 1] = v;
                 }
@@ -158,8 +153,8 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
                           q8_0_quantize_to_lds(x, K, q8);
                           __syncthreads();
                       });
-    for (int j = lane; j < row_end - row_begin; j += kWave) {
-        const int row = row_begin + j;
+    for (int j = lane; j < nrows; j += kWave) {
+        const int row = rfirst + j * rstride;
         const float g = out_lds[M * j];
         if (MODE == kPlain) {
             y[row] = g;

@@ -17,7 +17,7 @@
 #include "stream.h"
 
 #ifndef RF_Q6_NB
-#define RF_Q6_NB 3   // register ring depth of the one-row-per-step GEMV (measured best)
+#define RF_Q6_NB 3   // register ring depth (rows in flight + 1) of the K-split GEMV (measured best)
 #endif
 
 namespace rf {
@@ -257,6 +257,138 @@ __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_stream_kernel(const uint8
     if (lane < row_end - row_begin) y[row_begin + lane] = out;
 }
 
+
+// ── K-split Q6_K GEMV with x held in registers (main path) ───────────────
+// A workgroup has one wave per 8-super-block slice of K (NWK = nsb/8
+// rounded up, at most 8 waves: K <= 16384).  The 8 lanes p = 0..7 of a
+// super-block sb = 8w + l/8 read its bytes with three 16-byte loads each,
+// so every load instruction covers whole contiguous runs of the block:
+//   A: ql[16p .. 16p+16)              (all 128 B of ql across the 8 lanes)
+//   B: qh[32n + 16(p&1) .. +16)       (n = p>>2; lanes p, p^2 share it)
+//   C: bytes 192..207 (n = 0) or 194..209 (n = 1): the scales, and d in
+//      the top half of the last dword for n = 1 (ds_bpermute hands d to
+//      the n = 0 lanes).
+// Lane p then owns the 32 weights its ql bytes encode: ql-half n, bytes
+// b = 16(p&3) .. b+15, i.e. l = 16(p&1) + i of quarters hq and hq + 2
+// (hq = (p&3)>>1): elements 128n + 32q + l.  Its 32 x values and their two
+// 16-element sums are loaded into registers once, so the weight stream runs
+// with no LDS traffic and no barrier in front of it.  Every wave walks all
+// rows of its workgroup (rows g, g + grid, g + 2 grid, ...: the grid
+// streams neighbouring rows together), reduces its slice's partial over the
+// wave and parks it in LDS; the slices of a row are summed in fixed slice
+// order at the end.
+struct Q6Lane {
+    u32x4 ql, qh, sc;
+};
+
+__device__ __forceinline__ Q6Lane q6k_load_lane(const uint8_t* blk, int p) {
+    const int n = p >> 2;
+    Q6Lane u;
+    u.ql = ld16(blk + 16 * p);
+    u.qh = ld16(blk + 128 + 32 * n + 16 * (p & 1));
+    u.sc = ld16(blk + 192 + 2 * n);
+    return u;
+}
+
+// 16 weights of one scale group (four dwords of 6-bit values) against 16 x.
+__device__ __forceinline__ float q6_dot16(const uint32_t v[4], const float* xv) {
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        t += (float)(v[k] & 0xFFu) * xv[4 * k + 0];
+        t += (float)((v[k] >> 8) & 0xFFu) * xv[4 * k + 1];
+        t += (float)((v[k] >> 16) & 0xFFu) * xv[4 * k + 2];
+        t += (float)(v[k] >> 24) * xv[4 * k + 3];
+    }
+    return t;
+}
+
+template <int NB>
+__global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __restrict__ w,
+                                                                const float* __restrict__ x,
+                                                                float* __restrict__ y, int K, int N) {
+    extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK]
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwk = blockDim.x / kWave;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ6KBytes;
+    const int sb = 8 * wave + (lane >> 3);
+    const bool live = sb < nsb;
+    const int sbc = live ? sb : nsb - 1;
+    const int p = lane & 7;
+    const int n = p >> 2;
+    const int hq = (p & 3) >> 1;
+    const int is = p & 1;
+    const int g = blockIdx.x;
+    const int G = gridDim.x;
+    const int nrows = g < N ? (N - 1 - g) / G + 1 : 0;
+
+    // x of this lane: run r (quarter hq + 2r) at element sbc*256 + 128n + 32(hq+2r) + 16 is
+    float xr[2][16];
+    {
+        const float* xb = x + (size_t)sbc * kQK + 128 * n + 32 * hq + 16 * is;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = *reinterpret_cast<const float4*>(xb + 64 * r + 4 * k);
+                xr[r][4 * k + 0] = a.x; xr[r][4 * k + 1] = a.y; xr[r][4 * k + 2] = a.z; xr[r][4 * k + 3] = a.w;
+            }
+    }
+    float xs[2];
+    const uint8_t* wl = w + (size_t)sbc * kQ6KBytes;
+    auto load = [&](Q6Lane& u, int j) {
+        const int row = nrows ? g + min(j, nrows - 1) * G : 0;
+        u = q6k_load_lane(wl + (size_t)row * row_bytes, p);
+    };
+    // scale bytes j1 = 8n + 2hq + is (run 0) and j1 + 4 (run 1) inside C:
+    // n = 0: dwords 0 / 1, byte j1; n = 1 (C starts at byte 194): offset
+    // o1 = j1 - 2 = 6 + 2hq + is -> dword 1 or 2, and o1 + 4 -> dword 2 or 3.
+    const int o1 = n ? 6 + 2 * hq + is : 2 * hq + is;
+    const uint32_t ssh = 8u * (uint32_t)(o1 & 3);
+    const int dw1 = o1 >> 2;
+    const uint32_t qsh = 2u * (uint32_t)hq;       // qh bit pair of run 0 (run 1: +4)
+    const int dsrc = 4 * ((lane & ~7) | 4);       // lane holding d (n = 1 lane of the group)
+    auto process = [&](const Q6Lane& u, int j) {
+        const uint32_t dword3 = (uint32_t)__builtin_amdgcn_ds_bpermute(dsrc, (int)u.sc.w);
+        const float d = half_bits_to_float(dword3 >> 16);
+        const uint32_t w1 = dw1 == 0 ? u.sc.x : (dw1 == 1 ? u.sc.y : u.sc.z);
+        const uint32_t w2 = dw1 == 0 ? u.sc.y : (dw1 == 1 ? u.sc.z : u.sc.w);
+        const float s0 = d * (float)(int8_t)((w1 >> ssh) & 0xFFu);
+        const float s1 = d * (float)(int8_t)((w2 >> ssh) & 0xFFu);
+        const uint32_t L[4] = {u.ql.x, u.ql.y, u.ql.z, u.ql.w};
+        const uint32_t Q[4] = {u.qh.x, u.qh.y, u.qh.z, u.qh.w};
+        uint32_t v0[4], v1[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v0[t] = (L[t] & 0x0F0F0F0Fu) | (((Q[t] >> qsh) & 0x03030303u) << 4);
+            v1[t] = ((L[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> (qsh + 4)) & 0x03030303u) << 4);
+        }
+        float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
+        acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
+        const float tot = wave_sum(live ? acc : 0.0f);
+        if (lane == 0) part[j * nwk + wave] = tot;
+    };
+    Q6Lane ring[NB];
+    ring_pipeline<NB>(nrows, ring, load, process, [&]() {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t += xr[r][i];
+            xs[r] = t;
+        }
+    });
+    __syncthreads();
+    for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
+        float t = 0.0f;
+        for (int k = 0; k < nwk; ++k) t += part[j * nwk + k];
+        y[g + j * G] = t;
+    }
+}
+
+
 }  // namespace rf
 
 using namespace rf;
@@ -270,6 +402,17 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
     const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
     const int nsb = n_rows / kQK;
+    if (gemv_q6_variant() == 0 && nsb <= 64) {
+        const int nwk = (nsb + 7) / 8;
+        const int cap = device_cu_count() * gemv_wg_per_cu(1);
+        const int grid = ncols_dst < cap ? ncols_dst : cap;
+        const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
+        if (lds <= 64 * 1024) {
+            hipLaunchKernelGGL((rf_q6k_gemv_xreg_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
+                               output, n_rows, ncols_dst);
+            return hipGetLastError();
+        }
+    }
     if (gemv_use_stream() && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
         (reinterpret_cast<uintptr_t>(input) & 15u) == 0) {
         constexpr int NW = 8, S = 3;
@@ -302,7 +445,7 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if (out_bytes > 64 * 1024) return hipErrorInvalidValue;
     const dim3 blk(nw * 64);
 #define RF_Q6_LAUNCH(RR, L, W) \
-    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, (RR == 1 ? RF_Q6_NB : 3)>), dim3(grid), blk, lds + out_bytes, stream, w, input, output, \
+    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, 3>), dim3(grid), blk, lds + out_bytes, stream, w, input, output, \
                        n_rows, ncols_dst)
     if (r >= 2) {
         if (in_lds) RF_Q6_LAUNCH(2, true, 4); else RF_Q6_LAUNCH(2, false, 4);

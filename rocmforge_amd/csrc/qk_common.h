@@ -300,6 +300,8 @@ struct Q4KUnit {
 
 __device__ __forceinline__ Q4KUnit q4k_load_unit(const uint8_t* blk, int p) {
     Q4KUnit u;
+    // (plain loads: nontemporal ones were measured 28% slower here -- they
+    // stop the L1 from merging the three loads that share a line)
     u.hdr = *reinterpret_cast<const u32x4*>(blk);
     const u32x4* q = reinterpret_cast<const u32x4*>(blk + 16 + 32 * p);
     u.qa = q[0];
@@ -347,6 +349,8 @@ bool gemv_use_stream();
 // for tuning sweeps).
 int gemv_rows_per_step();
 int gemv_waves_per_wg(int dflt);
+// Q6_K GEMV kernel family (0 = K-split register kernel, 1 = row-step kernel).
+int gemv_q6_variant();
 // GEMM kernel selection for tuning comparisons: RF_GEMM_V=1 forces the
 // general 2x2-wave kernel, =4 the register-weight kernel; default (0) picks
 // the weight-ring kernel where it applies.

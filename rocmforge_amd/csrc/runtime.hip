@@ -58,6 +58,15 @@ int gemv_waves_per_wg(int dflt) {
     return v ? v : dflt;
 }
 
+int gemv_q6_variant() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("RF_Q6_V");
+        v = e ? atoi(e) : 0;
+    }
+    return v;
+}
+
 int gemm_kernel_version() {
     static int v = -1;
     if (v < 0) {
