@@ -26,6 +26,10 @@
 #include "qk_common.h"
 #include "stream.h"
 
+#ifndef RF_GEMM_VPM
+#define RF_GEMM_VPM 6   // VALU instructions scheduled after each MFMA
+#endif
+
 namespace rf {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -336,6 +340,20 @@ struct Q4Ops {
     static __device__ __forceinline__ Qs qs(const uint8_t* row, int sb, int h, int /*kh*/) {
         return Qs{*reinterpret_cast<const u32x4*>(row + (size_t)sb * kQ4KBytes + 16 + 32 * CQ + 16 * h)};
     }
+    template <int CQ, int KH>
+    static __device__ __forceinline__ void dequant_k(const Hdr& hd, const Qs& r, int /*h*/, f16x8 (&b)[2]) {
+        int sc0, m0, sc1, m1;
+        q4k_scale_min_pair(hd.v.y, hd.v.z, hd.v.w, CQ, &sc0, &m0, &sc1, &m1);
+        const float d = half_bits_to_float(hd.v.x), dmin = half_bits_to_float(hd.v.x >> 16);
+        const float ds = KH ? d * (float)sc1 * 0.0625f : d * (float)sc0;
+        const float dm = KH ? dmin * (float)m1 : dmin * (float)m0;
+        constexpr uint32_t mask = KH ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        const uint32_t w[4] = {r.q.x & mask, r.q.y & mask, r.q.z & mask, r.q.w & mask};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            put4(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
+                 ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
+    }
     template <int CQ>
     static __device__ __forceinline__ void dequant(const Hdr& hd, const Qs& r, int h, int kh, f16x8 (&b)[2]) {
         int sc0, m0, sc1, m1;
@@ -369,6 +387,10 @@ struct Q6Ops {
         constexpr int nh = CQ >> 1;
         const uint8_t* blk = row + (size_t)sb * kQ6KBytes;
         return Qs{ld16(blk + 64 * nh + 32 * kh + 16 * h), ld16(blk + 128 + 32 * nh + 16 * h), ld4(blk + 192 + 4 * CQ)};
+    }
+    template <int CQ, int KH>
+    static __device__ __forceinline__ void dequant_k(const Hdr& hd, const Qs& r, int h, f16x8 (&b)[2]) {
+        dequant<CQ>(hd, r, h, KH, b);
     }
     template <int CQ>
     static __device__ __forceinline__ void dequant(const Hdr& hd, const Qs& r, int h, int kh, f16x8 (&b)[2]) {
@@ -822,6 +844,615 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v5_kernel(const float* 
     }
 }
 
+template <typename T, bool IS_Q6, int FM, bool SPLIT>
+__global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v6_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int tiles, int chunks_per_split) {
+    using G = RingGeom<IS_Q6>;
+    constexpr int BM = 32 * FM;
+    constexpr int BN = 256;
+    constexpr int A_F4 = BM * kKC / 4 / kV4Threads;   // float4 per thread per chunk
+    constexpr int kStageBytes = BN * G::kRS;
+    constexpr int kDepth = G::kStages - 1;             // super-blocks staged ahead
+    static_assert(G::kGroups * 1024 == kStageBytes && 8 * G::kNI >= G::kGroups && 8 * G::kNI < 2 * G::kGroups,
+                  "load groups cover the stage");
+    static_assert(4 * (FM / 2) * 2 * 16 * 64 * 4 <= G::kStages * kStageBytes, "reduction buffer");
+    __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
+    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 3, kh = wave >> 2;
+    const int h = lane >> 5;
+    const int tile = blockIdx.x % tiles;
+    const int split = blockIdx.x / tiles;
+    const int ntiles = N / BN;
+    const int m0 = (tile / ntiles) * BM;
+    const int nt0 = (tile % ntiles) * BN;   // first weight row of the tile
+    const int n0 = nt0 + wn * 64;
+    const int c_begin = split * chunks_per_split;
+    const int c_last = c_begin + chunks_per_split - 1;
+    const int sb_begin = c_begin / 4, sb_last = c_last / 4;
+    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
+    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
+
+    // per-lane staging source offsets (relative to the tile's rows at
+    // super-block 0) and LDS destinations
+    uint32_t goff[G::kNI];
+    uint32_t gdst[G::kNI];
+#pragma unroll
+    for (int t = 0; t < G::kNI; ++t) {
+        int g = wave * G::kNI + t;
+        if (g >= G::kGroups) g -= G::kGroups;
+        const int pc = 64 * g + lane;
+        gdst[t] = 16u * (uint32_t)pc;
+        const int row = pc / G::kNPR;
+        int piece = pc % G::kNPR;
+        if (IS_Q6 && piece == 14) piece = 13;
+        goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
+    }
+    u32x4 wst[G::kNI];
+    auto w_gload = [&](int sb) {
+        sb = min(sb, sb_last);
+        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
+    };
+    auto w_lstore = [&](int slot) {
+        uint8_t* dst = w_ring + slot * kStageBytes;
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
+    };
+
+    const int a_row = tid >> 4;
+    const int a_col = 4 * (tid & 15);
+    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
+    float4 a_reg[2][A_F4];
+    auto a_load = [&](float4 (&r)[A_F4], int c) {
+        const float* src = a_base + (size_t)min(c, c_last) * kKC;
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(32 * i) * K);
+    };
+    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
+        _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) {
+            f16x4 hv;
+            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
+            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
+            *reinterpret_cast<f16x4*>(dst + 32 * i * kLdsStride) = hv;
+        }
+    };
+
+    f32x16 acc[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int frag = (lane & 31) * kLdsStride + 32 * kh + 16 * h;
+    const int row_lds0 = (wn * 64 + (lane & 31)) * G::kRS;
+    const int row_lds1 = row_lds0 + 32 * G::kRS;
+
+    // B operands are double buffered: iteration c runs the MFMAs of chunk c
+    // on bq[c & 1] while the lanes dequantise chunk c + 1 into
+    // bq[(c + 1) & 1]; the two streams are independent, and the scheduling
+    // hints below interleave them (one MFMA, then a few VALU operations), so
+    // the VALU work hides under the matrix core instead of running before it.
+    f16x8 bq[2][2][2];
+    // dequantise chunk with in-group index J (static) of super-block sb from
+    // ring slot `slot` into bq[J & 1]
+    auto w_dequant = [&](auto jj, auto khc, int sb, int slot) {
+        constexpr int J = decltype(jj)::value;
+        constexpr int KH = decltype(khc)::value;
+        constexpr int CQ = J & 3;
+        typename T::Hdr hd[2];
+        typename T::Qs qs[2];
+        const uint8_t* st = w_ring + slot * kStageBytes;
+        if constexpr (IS_Q6) {
+            const int shift = 2 * (sb & 7);
+            constexpr int nh = CQ >> 1;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + shift;
+                qs[r].ql = ld16(rb + 64 * nh + 32 * KH + 16 * h);
+                qs[r].qh = ld16(rb + 128 + 32 * nh + 16 * h);
+                qs[r].sc = ld4(rb + 192 + 4 * CQ);
+                hd[r].d = ld_u16(rb + 208);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
+                hd[r].v = *reinterpret_cast<const u32x4*>(rb);
+                qs[r].q = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
+            }
+        }
+        T::template dequant_k<CQ, KH>(hd[0], qs[0], h, bq[J & 1][0]);
+        T::template dequant_k<CQ, KH>(hd[1], qs[1], h, bq[J & 1][1]);
+    };
+
+    // iteration I of the 8-chunk group starting at chunk c8 (super-blocks
+    // c8/4 and c8/4+1 in ring slots slot0, slot1, the next group's first
+    // super-block in slot2; staging targets sd0, sd1)
+    auto iteration = [&](auto it, auto khc, int c8, int slot0, int slot1, int slot2, int sd0, int sd1) {
+        constexpr int I = decltype(it)::value;
+        constexpr int P = I & 1, CQ = I & 3;
+        const int c = c8 + I;
+        const int sb = c8 / 4 + (I >> 2);
+        __builtin_amdgcn_sched_barrier(0);
+        // A fragments of chunk c (LDS buffer c & 1)
+        const _Float16* la = lds_a[P] + frag;
+        f16x8 af[2][FM];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[s2][i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride + 8 * s2);
+        a_store(a_reg[P ^ 1], P ^ 1);
+        if constexpr (CQ == 2) w_lstore((I >> 2) ? sd1 : sd0);
+        // next chunk's B operands (the chunk after the group's last one is
+        // the first of the next group, in slot2; past c_last it is unused)
+        if constexpr (I == 7)
+            w_dequant(std::integral_constant<int, 0>{}, khc, sb + 1, slot2);
+        else
+            w_dequant(std::integral_constant<int, I + 1>{}, khc, c8 / 4 + ((I + 1) >> 2), ((I + 1) >> 2) ? slot1 : slot0);
+        a_load(a_reg[P ^ 1], c + 3);
+        if constexpr (CQ == 0) w_gload(sb + kDepth);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s2][i], bq[P][j][s2], acc[i][j], 0, 0, 0);
+        // scheduling: fragment reads first, then MFMAs interleaved with the
+        // dequantisation / conversion VALU work and the LDS / global traffic
+        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);   // DS reads (A fragments of the first k16 step)
+#pragma unroll
+        for (int k = 0; k < 2 * FM * 2; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // 1 DS read
+            __builtin_amdgcn_sched_group_barrier(0x002, RF_GEMM_VPM, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);    // 1 DS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // 1 VMEM read
+        }
+        lds_barrier();
+    };
+
+    // The K half of a wave is a template parameter of the main loop: with a
+    // runtime (wave-uniform) kh the compiler branches inside the
+    // dequantisation, which splits the loop body into several scheduling
+    // regions and defeats the MFMA / VALU interleave.
+    auto run = [&](auto khc) {
+    // prologue: super-blocks sb_begin .. sb_begin+kDepth-1 into slots 0..;
+    // A(c0) -> LDS 0; A(c0+1), A(c0+2) in flight
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        w_gload(sb_begin + d);
+        w_lstore(d);
+    }
+    a_load(a_reg[0], c_begin);
+    a_load(a_reg[1], c_begin + 1);
+    a_store(a_reg[0], 0);
+    a_load(a_reg[0], c_begin + 2);
+    lds_barrier();
+    w_dequant(std::integral_constant<int, 0>{}, khc, sb_begin, 0);
+
+    int slot0 = 0;   // ring slot of super-block c8/4
+    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
+        const int slot1 = slot0 + 1 == G::kStages ? 0 : slot0 + 1;
+        const int sd0 = slot0 + kDepth >= G::kStages ? slot0 + kDepth - G::kStages : slot0 + kDepth;
+        const int sd1 = sd0 + 1 == G::kStages ? 0 : sd0 + 1;
+        const int slot2 = slot1 + 1 == G::kStages ? 0 : slot1 + 1;
+        iteration(std::integral_constant<int, 0>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 1>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 2>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 3>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 4>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 5>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 6>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 7>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
+        slot0 = slot2;
+    }
+    };
+    if (kh)
+        run(std::integral_constant<int, 1>{});
+    else
+        run(std::integral_constant<int, 0>{});
+
+    float* red = reinterpret_cast<float*>(w_ring) + wn * (FM / 2) * 2 * 16 * 64 + lane;
+    auto store = [&](int i, int j, const f32x16& v) {
+        const int col = n0 + 32 * j + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if constexpr (SPLIT)
+                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
+            else
+                D[(size_t)row * N + col] = v[e];
+        }
+    };
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        const int giver = round == 0 ? 1 : 0;
+        if (kh == giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) red[((ii * 2 + j) * 16 + e) * 64] = acc[round * (FM / 2) + ii][j][e];
+        }
+        __syncthreads();
+        if (kh != giver) {
+#pragma unroll
+            for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f32x16 v = acc[round * (FM / 2) + ii][j];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] += red[((ii * 2 + j) * 16 + e) * 64];
+                    store(round * (FM / 2) + ii, j, v);
+                }
+        }
+        __syncthreads();
+    }
+}
+
+
+
+// Workgroups are dispatched round-robin over the XCDs (b -> XCD b % 8).
+// Returns the virtual index of workgroup b such that XCD x processes the
+// contiguous virtual range [start_x, start_x + count_x): a bijection of
+// [0, total).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+    const int x = b % kXcds, local = b / kXcds;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+    return start + local;
+}
+
+// ── v7: 4 waves (one per SIMD), full K chunk per wave, MFMA/VALU interleave
+// Workgroup = 256 threads over a BM x 256 tile (BM = 32 FM); wave w owns
+// output columns [n0 + 64 w, +64) for all BM rows and both K halves of every
+// chunk, so no cross-wave reduction is needed and each wave has the whole
+// register file of its SIMD (accumulators in AGPRs).  Weights stage through
+// the same LDS ring as v5; B operands are double buffered so chunk c + 1 is
+// dequantised while the MFMAs of chunk c run, with scheduling hints placing
+// a few VALU operations after every MFMA (the matrix core executes an MFMA
+// for many cycles while the SIMD issues the independent VALU work).
+constexpr int kV7Threads = 256;
+
+template <bool IS_Q6>
+struct RingGeom7;
+template <>
+struct RingGeom7<false> {
+    static constexpr int kRS = 144, kNPR = 9, kStages = 3, kGroups = 36, kNI = 9;
+};
+template <>
+struct RingGeom7<true> {
+    static constexpr int kRS = 240, kNPR = 15, kStages = 2, kGroups = 60, kNI = 15;
+};
+
+template <typename T, bool IS_Q6, int FM, bool SPLIT>
+__global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int tiles, int chunks_per_split) {
+    using G = RingGeom7<IS_Q6>;
+    constexpr int BM = 32 * FM;
+    constexpr int BN = 256;
+    constexpr int A_RPP = kV7Threads / 16;              // A rows per staging pass
+    constexpr int A_F4 = BM * kKC / 4 / kV7Threads;     // float4 per thread per chunk
+    constexpr int kStageBytes = BN * G::kRS;
+    constexpr int kDepth = G::kStages - 1;
+    static_assert(G::kGroups * 1024 == kStageBytes && 4 * G::kNI == G::kGroups, "load groups cover the stage");
+    __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
+    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD one
+    // contiguous run of the (M-major) tile order so the workgroups sharing an
+    // M tile -- the same rows of A -- share that XCD's L2.
+    const int vidx = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int splits = (int)gridDim.x / tiles;
+    const int tile = vidx / splits;
+    const int split = vidx % splits;
+    const int ntiles = N / BN;
+    const int m0 = (tile / ntiles) * BM;
+    const int nt0 = (tile % ntiles) * BN;
+    const int n0 = nt0 + wave * 64;
+    const int c_begin = split * chunks_per_split;
+    const int c_last = c_begin + chunks_per_split - 1;
+    const int sb_begin = c_begin / 4, sb_last = c_last / 4;
+    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
+    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
+
+    uint32_t goff[G::kNI];
+    uint32_t gdst[G::kNI];
+#pragma unroll
+    for (int t = 0; t < G::kNI; ++t) {
+        const int g = wave * G::kNI + t;
+        const int pc = 64 * g + lane;
+        gdst[t] = 16u * (uint32_t)pc;
+        const int row = pc / G::kNPR;
+        int piece = pc % G::kNPR;
+        if (IS_Q6 && piece == 14) piece = 13;
+        goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
+    }
+    u32x4 wst[G::kNI];
+    auto w_gload = [&](int sb) {
+        sb = min(sb, sb_last);
+        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
+    };
+    auto w_lstore = [&](int slot) {
+        uint8_t* dst = w_ring + slot * kStageBytes;
+#pragma unroll
+        for (int t = 0; t < G::kNI; ++t) *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
+    };
+
+    const int a_row = tid >> 4;
+    const int a_col = 4 * (tid & 15);
+    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
+    float4 a_reg[2][A_F4];
+    auto a_load = [&](float4 (&r)[A_F4], int c) {
+        const float* src = a_base + (size_t)min(c, c_last) * kKC;
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(A_RPP * i) * K);
+    };
+    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
+        _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
+#pragma unroll
+        for (int i = 0; i < A_F4; ++i) {
+            f16x4 hv;
+            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
+            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
+            *reinterpret_cast<f16x4*>(dst + A_RPP * i * kLdsStride) = hv;
+        }
+    };
+
+    f32x16 acc[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int frag = (lane & 31) * kLdsStride + 16 * h;
+    const int row_lds0 = (wave * 64 + (lane & 31)) * G::kRS;
+    const int row_lds1 = row_lds0 + 32 * G::kRS;
+
+    // bq[buffer][k half][column block][k16 step]
+    f16x8 bq[2][2][2][2];
+    // Raw operand bytes of chunk c + 1 for the lane's two weight rows, read
+    // from the ring at the start of iteration c, and the per-(row, k half)
+    // scale terms: Q4_K value = a * byte - b (a = d*sc, or d*sc/16 for the
+    // high-nibble half read as 16*nibble; b = dmin*m); Q6_K value = a * q - b
+    // (a = d*sc, b = 32a).
+    u32x4 wq[2][2];     // Q4: [row][0] = header, [1] = qs bytes; Q6: [row][0] = ql (kh 0), [1] = ql (kh 1)
+    u32x4 wqh[2];       // Q6: qh bytes per row
+    uint32_t wsc[2];    // Q6: scale word per row
+    uint32_t wd[2];     // Q6: d per row
+    float pa[2][2], pb[2][2];
+    auto w_read = [&](auto jj, int sb, int slot) {
+        constexpr int CQ = decltype(jj)::value & 3;
+        const uint8_t* st = w_ring + slot * kStageBytes;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            if constexpr (IS_Q6) {
+                constexpr int nh = CQ >> 1;
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + 2 * (sb & 7);
+                wq[r][0] = ld16(rb + 64 * nh + 16 * h);
+                wq[r][1] = ld16(rb + 64 * nh + 32 + 16 * h);
+                wqh[r] = ld16(rb + 128 + 32 * nh + 16 * h);
+                wsc[r] = ld4(rb + 192 + 4 * CQ);
+                wd[r] = ld_u16(rb + 208);
+            } else {
+                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
+                wq[r][0] = *reinterpret_cast<const u32x4*>(rb);
+                wq[r][1] = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
+            }
+        }
+    };
+    auto w_prep = [&](auto jj, int r) {
+        constexpr int CQ = decltype(jj)::value & 3;
+        if constexpr (IS_Q6) {
+            const float d = half_bits_to_float(wd[r]);
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                pa[r][kh] = d * (float)(int8_t)((wsc[r] >> (8 * (2 * kh + h))) & 0xFFu);
+                pb[r][kh] = 32.0f * pa[r][kh];
+            }
+        } else {
+            int sc0, m0, sc1, m1;
+            q4k_scale_min_pair(wq[r][0].y, wq[r][0].z, wq[r][0].w, CQ, &sc0, &m0, &sc1, &m1);
+            const float d = half_bits_to_float(wq[r][0].x), dmin = half_bits_to_float(wq[r][0].x >> 16);
+            pa[r][0] = d * (float)sc0;
+            pb[r][0] = dmin * (float)m0;
+            pa[r][1] = d * (float)sc1 * 0.0625f;
+            pb[r][1] = dmin * (float)m1;
+        }
+    };
+    // piece (r, kh, word j) of the dequantisation into bq[buf]: 4 weights
+    auto w_piece = [&](auto jj, int buf, int r, int kh, int j) {
+        constexpr int CQ = decltype(jj)::value & 3;
+        uint32_t q;
+        if constexpr (IS_Q6) {
+            constexpr uint32_t nsh = 4u * (CQ & 1);
+            const uint32_t qsh = 4u * (CQ & 1) + 2u * (uint32_t)kh;
+            q = ((wq[r][kh][j] >> nsh) & 0x0F0F0F0Fu) | (((wqh[r][j] >> qsh) & 0x03030303u) << 4);
+        } else {
+            q = wq[r][1][j] & (kh ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+        }
+        // opaque to the optimiser: otherwise it folds the mask into per-byte
+        // bit-field extracts and converts byte 0, two instructions per weight
+        // instead of one v_cvt_f32_ubyteN
+        asm("" : "+v"(q));
+        const float a = pa[r][kh], b = pb[r][kh];
+        put4(bq[buf][kh][r][j >> 1], j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b,
+             a * byte_f(q, 3) - b);
+    };
+    auto w_dequant_all = [&](auto jj, int buf) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            w_prep(jj, r);
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w_piece(jj, buf, r, kh, j);
+        }
+    };
+    auto a_store1 = [&](const float4& v, int buf, int i) {
+        f16x4 hv;
+        hv[0] = (_Float16)v.x; hv[1] = (_Float16)v.y;
+        hv[2] = (_Float16)v.z; hv[3] = (_Float16)v.w;
+        *reinterpret_cast<f16x4*>(&lds_a[buf][a_row * kLdsStride + a_col] + A_RPP * i * kLdsStride) = hv;
+    };
+
+    // Iteration I of the 8-chunk group at c8.  Hand-scheduled in 16 slots
+    // separated by scheduling fences: slot t = 4*step + i issues the MFMA
+    // pair (acc[i][0], acc[i][1]) of k16 step `step` (independent of the
+    // previous pair) and one slice of the side work -- a piece of the next
+    // chunk's dequantisation, one A float4 to LDS, one global load, one ring
+    // store -- so the VALU work runs while the matrix core executes.
+    auto iteration = [&](auto it, int c8, int slot0, int slot1, int slot2, int sd0, int sd1) {
+        constexpr int I = decltype(it)::value;
+        constexpr int P = I & 1, CQ = I & 3;
+        constexpr int IN = (I + 1) & 7;            // in-group index of chunk c + 1
+        using JN = std::integral_constant<int, IN>;
+        const int c = c8 + I;
+        const int sb = c8 / 4 + (I >> 2);
+        const int sbn = I == 7 ? sb + 1 : c8 / 4 + ((I + 1) >> 2);
+        const int slotn = I == 7 ? slot2 : (((I + 1) >> 2) ? slot1 : slot0);
+        const _Float16* la = lds_a[P] + frag;
+        __builtin_amdgcn_sched_barrier(0);
+        w_read(JN{}, sbn, slotn);
+        f16x8 af[2][FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+            const int kh = step >> 1, s2 = step & 1;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    // slot t: one MFMA, then ~7 VALU operations of side work
+                    // (the MFMA occupies the matrix core for 32 cycles, the
+                    // time the SIMD needs to issue about 8 VALU operations)
+                    const int t = (step * FM + i) * 2 + j;   // 0 .. 8*FM-1
+                    constexpr int NS = 8 * FM;
+                    if (i == 0 && j == 0 && step < 3) {
+                        const int nk = (step + 1) >> 1, ns = (step + 1) & 1;
+#pragma unroll
+                        for (int ii = 0; ii < FM; ++ii)
+                            af[(step + 1) & 1][ii] =
+                                *reinterpret_cast<const f16x8*>(la + 32 * ii * kLdsStride + 32 * nk + 8 * ns);
+                    }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[step & 1][i], bq[P][kh][j][s2], acc[i][j],
+                                                                       0, 0, 0);
+                    // dequantisation of chunk c + 1: prep row 0 at slot 0,
+                    // its 8 pieces at 1..8, prep row 1 at 9, pieces 10..17
+                    // (packed into 16 slots when FM = 2)
+                    if constexpr (NS >= 18) {
+                        if (t == 0) w_prep(JN{}, 0);
+                        if (t >= 1 && t <= 8) w_piece(JN{}, P ^ 1, 0, (t - 1) >> 2, (t - 1) & 3);
+                        if (t == 9) w_prep(JN{}, 1);
+                        if (t >= 10 && t <= 17) w_piece(JN{}, P ^ 1, 1, (t - 10) >> 2, (t - 10) & 3);
+                    } else if constexpr (NS < 18) {
+                        if (t == 0) {
+                            w_prep(JN{}, 0);
+                            w_prep(JN{}, 1);
+                        }
+                        if (t < 16) w_piece(JN{}, P ^ 1, t >> 3, (t >> 2) & 1, t & 3);
+                    }
+                    // A: store float4 k of chunk c + 1 at slot NS-14+k, reload
+                    // it (chunk c + 3) six slots later
+                    if (t >= NS - 14 && t < NS - 14 + A_F4) a_store1(a_reg[P ^ 1][t - (NS - 14)], P ^ 1, t - (NS - 14));
+                    if (t >= NS - 8 && t < NS - 8 + A_F4) {
+                        const int k = t - (NS - 8);
+                        a_reg[P ^ 1][k] = *reinterpret_cast<const float4*>(
+                            a_base + (size_t)min(c + 3, c_last) * kKC + (size_t)(A_RPP * k) * K);
+                    }
+                    if constexpr (CQ == 0) {
+                        if (t < G::kNI) {
+                            const int sbl = min(sb + kDepth, sb_last);
+                            const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sbl * kQ6KBytes) & ~(size_t)15)
+                                                                : (size_t)sbl * kQ4KBytes);
+                            wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
+                        }
+                    }
+                    if constexpr (CQ == 2) {
+                        if (t < G::kNI) {
+                            uint8_t* dst = w_ring + ((I >> 2) ? sd1 : sd0) * kStageBytes;
+                            *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
+        static_assert(8 * FM >= 16 && 8 * FM >= G::kNI && 8 * FM >= 14, "side work fits the slots");
+        lds_barrier();
+    };
+
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        w_gload(sb_begin + d);
+        w_lstore(d);
+    }
+    a_load(a_reg[0], c_begin);
+    a_load(a_reg[1], c_begin + 1);
+    a_store(a_reg[0], 0);
+    a_load(a_reg[0], c_begin + 2);
+    lds_barrier();
+    w_read(std::integral_constant<int, 0>{}, sb_begin, 0);
+    w_dequant_all(std::integral_constant<int, 0>{}, 0);
+
+    int slot0 = 0;
+    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
+        const int slot1 = slot0 + 1 == G::kStages ? 0 : slot0 + 1;
+        const int sd0 = slot0 + kDepth >= G::kStages ? slot0 + kDepth - G::kStages : slot0 + kDepth;
+        const int sd1 = sd0 + 1 == G::kStages ? 0 : sd0 + 1;
+        const int slot2 = slot1 + 1 == G::kStages ? 0 : slot1 + 1;
+        iteration(std::integral_constant<int, 0>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 1>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 2>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 3>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 4>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 5>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 6>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        iteration(std::integral_constant<int, 7>{}, c8, slot0, slot1, slot2, sd0, sd1);
+        slot0 = slot2;
+    }
+
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + 32 * j + (lane & 31);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if constexpr (SPLIT)
+                    unsafeAtomicAdd(&D[(size_t)row * N + col], acc[i][j][e]);
+                else
+                    D[(size_t)row * N + col] = acc[i][j][e];
+            }
+        }
+}
+
 __global__ void rf_fill_zero_kernel(float4* __restrict__ p, size_t n4) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
         p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -851,18 +1482,32 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     }
     // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
     const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
+    const bool v6 = v5 && gemm_kernel_version() == 6;
+    const bool v7 = v5 && gemm_kernel_version() == 0;
     if (s > 1) {
         const size_t n4 = (size_t)M * N / 4;
         hipLaunchKernelGGL(rf_fill_zero_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 2048)), dim3(256), 0,
                            st, reinterpret_cast<float4*>(D), n4);
-        if (v5)
+        if (v7)
+            hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
+                               w, D, M, N, K, tiles, nchunks / s);
+        else if (v6)
+            hipLaunchKernelGGL((rf_gemm_qk_v6_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
+                               w, D, M, N, K, tiles, nchunks / s);
+        else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
                                w, D, M, N, K, tiles, nchunks / s);
         else
             hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D,
                                M, N, K, tiles, nchunks / s);
     } else {
-        if (v5)
+        if (v7)
+            hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
+                               D, M, N, K, tiles, nchunks);
+        else if (v6)
+            hipLaunchKernelGGL((rf_gemm_qk_v6_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
+                               D, M, N, K, tiles, nchunks);
+        else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
                                D, M, N, K, tiles, nchunks);
         else
