@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--no-stream", action="store_true", help="skip the full decode weight stream leg (config 2)")
+    ap.add_argument("--stream-tokens", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain copies of known size (PMC traffic calibration)")
@@ -142,6 +144,79 @@ def bench_decode(lib, torch, steps, warmup):
         "wall": wall, "steps_run": steps, "step_ms": step_ms, "copies": copies,
         "gate_up_ms": gu_ms, "down_ms": dn_ms, "x": x, "h": h, "y": y,
     }
+
+
+# the full decode weight stream of a Llama-3.1-8B-shaped
+# stack at batch 1 -- per layer the QKV GEMV (Q4_K 6144x4096, Q8-inline), the
+# O projection with the residual add fused (Q4_K 4096x4096), the fused
+# gate+up+SwiGLU (2 x Q4_K 14336x4096) and ffn_down (Q6_K 4096x14336); then
+# the Q6_K lm_head (128256x4096).  Attention, norms and RoPE are not part of
+# the path: the O projection reads the first 4096 QKV outputs in their place.
+L_LAYERS, QKV_N, VOCAB = 32, 6144, 128256
+STREAM_WEIGHT_BYTES = (L_LAYERS * (QKV_N * (K_FFN // 256) * Q4K_BYTES + K_FFN * (K_FFN // 256) * Q4K_BYTES
+                                   + 2 * N_FFN * (K_FFN // 256) * Q4K_BYTES + K_FFN * (N_FFN // 256) * Q6K_BYTES)
+                       + VOCAB * (K_FFN // 256) * Q6K_BYTES)   # 4,841,250,816
+
+
+def bench_decode_stream(lib, torch, tokens):
+    from rocmforge_amd import synth
+
+    dev = torch.device("cuda:0")
+    layers = []
+    for l in range(L_LAYERS):
+        layers.append((synth.torch_weights("q4_k", QKV_N, K_FFN, seed=1000 + 5 * l, device=dev),
+                       synth.torch_weights("q4_k", K_FFN, K_FFN, seed=1001 + 5 * l, device=dev),
+                       synth.torch_weights("q4_k", N_FFN, K_FFN, seed=1002 + 5 * l, device=dev),
+                       synth.torch_weights("q4_k", N_FFN, K_FFN, seed=1003 + 5 * l, device=dev),
+                       synth.torch_weights("q6_k", K_FFN, N_FFN, seed=1004 + 5 * l, device=dev)))
+    lm_head = synth.torch_weights("q6_k", VOCAB, K_FFN, seed=999, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    x = torch.randn(K_FFN, device=dev, generator=g)
+    hidden = torch.randn(K_FFN, device=dev, generator=g)
+    qkv = torch.empty(QKV_N, device=dev)
+    ffn = torch.empty(N_FFN, device=dev)
+    logits = torch.empty(VOCAB, device=dev)
+
+    def token(st):
+        rc = 0
+        for wqkv, wo, wg, wu, wd in layers:
+            rc |= lib.gemv_q4_k_f32_q8_inline_launch(vp(wqkv), vp(x), vp(qkv), K_FFN, QKV_N, st)
+            rc |= lib.gemv_q4_k_f32_q8_inline_residual_launch(vp(wo), vp(qkv), vp(hidden), vp(hidden), K_FFN, K_FFN,
+                                                              st)
+            rc |= lib.gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch(vp(wg), vp(wu), vp(hidden), vp(ffn), K_FFN, N_FFN,
+                                                                    st)
+            rc |= lib.gemv_q6_k_f32_launch(vp(wd), vp(ffn), vp(x), N_FFN, K_FFN, st)
+        rc |= lib.gemv_q6_k_f32_launch(vp(lm_head), vp(x), vp(logits), K_FFN, VOCAB, st)
+        if rc:
+            raise RuntimeError(f"decode stream launch failed: hipError {rc}")
+
+    st0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    token(st0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(graph, stream=cs):
+            token(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(tokens):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / tokens
+    gbs = STREAM_WEIGHT_BYTES / (ms * 1e-3) / 1e9
+    return {"workload": "BASELINE config 2: 32 x (QKV 6144x4096 Q4_K, O 4096x4096 Q4_K + residual, "
+                        "gate+up 2x14336x4096 Q4_K, down 4096x14336 Q6_K) + lm_head 128256x4096 Q6_K, batch 1",
+            "launches_per_token": 4 * L_LAYERS + 1, "weight_bytes_per_token": STREAM_WEIGHT_BYTES,
+            "tokens": tokens, "ms_per_token": round(ms, 4), "gbs": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def calibrate_copy(torch, mbytes=256, reps=10):
@@ -281,6 +356,8 @@ def main():
     }
     if not args.no_gemm:
         out["prefill_gemm"] = bench_gemm(lib, torch)
+    if not args.no_stream:
+        out["decode_stream"] = bench_decode_stream(lib, torch, args.stream_tokens)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -23,6 +23,7 @@
 #define ROCMFORGE_CDNA4_H
 
 #include <hip/hip_runtime_api.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -79,6 +80,98 @@ hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, f
                                  hipStream_t stream);
 hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N, int K,
                                  hipStream_t stream);
+
+/* ---- Host dispatch (routing of the arms above) --------------------------
+ * C counterparts of ROCmForge's src/gpu/ops.rs routing for the Q4_K / Q6_K
+ * arms: which launcher a GGUF weight tensor goes to, in which order the
+ * paths are tried, and the shape checks made before any launch.  They call
+ * the launchers above and allocate nothing.
+ *
+ * Return value: RF_DISPATCH_OK (0) on success; a hipError_t (> 0) from the
+ * last launcher tried; or one of the negative codes below:
+ *   RF_DISPATCH_INVALID_LAYOUT   -- GpuError::InvalidWeightLayout
+ *                                   (validate_gemv_layout, ops.rs:82-105)
+ *   RF_DISPATCH_UNSUPPORTED_TYPE -- GpuError::UnsupportedWeightType
+ *   RF_DISPATCH_NOT_IN_LIBRARY   -- an arm the reference serves with a
+ *                                   kernel outside this library (Q4_0, Q4_1,
+ *                                   Q8_0, Q5_K, the scalar Q4_K GEMM, the
+ *                                   unfused gate/up path): the caller keeps
+ *                                   its own route for it.
+ * Runtime flags (read once, cached; rf_dispatch_refresh_flags re-reads
+ * them, as refresh_runtime_env_flags, safety.rs:123):
+ *   ROCMFORGE_GPU_SAFE_MODE (default off) disables both fast paths,
+ *   ROCMFORGE_ENABLE_EXPERIMENTAL_Q8_ACTIVATION_FASTPATH (default on),
+ *   ROCMFORGE_DISABLE_WMMA_PREFILL (default off).
+ * Values "1", "true", "yes", "on" (any case) enable a flag. */
+enum {
+    RF_GGML_F32 = 0, RF_GGML_F16 = 1, RF_GGML_Q4_0 = 2, RF_GGML_Q4_1 = 3, RF_GGML_Q5_0 = 6, RF_GGML_Q5_1 = 7,
+    RF_GGML_Q8_0 = 8, RF_GGML_Q2_K = 10, RF_GGML_Q3_K = 11, RF_GGML_Q4_K = 12, RF_GGML_Q5_K = 13, RF_GGML_Q6_K = 14
+};  /* GgmlType codes (src/loader/ggml_type.rs:6-19) */
+
+enum { RF_DISPATCH_OK = 0, RF_DISPATCH_INVALID_LAYOUT = -1001, RF_DISPATCH_UNSUPPORTED_TYPE = -1002,
+       RF_DISPATCH_NOT_IN_LIBRARY = -1003 };
+
+/* WeightMeta (src/gpu/weights.rs:29-40): GGUF type code and dims (innermost
+ * first); role 0 generic, 1 lm_head, 2 tied lm_head. */
+typedef struct rf_weight_meta {
+    int32_t wtype;
+    int32_t n_dims;
+    uint64_t dims[4];
+    int32_t role;
+} rf_weight_meta;
+
+/* gpu_dispatch_gemv_on_stream (ops.rs:484) + dispatch_gemv_impl (ops.rs:270):
+ * Q4_K -> Q8-inline GEMV when the fast path is on and (K/32)*34 <= 32 KB, on
+ * any error the fp32-activation GEMV; Q6_K -> gemv_q6_k_f32_launch. */
+int rf_gpu_dispatch_gemv(const void* weights, const rf_weight_meta* meta, const float* input, float* output,
+                         size_t out_dim, size_t in_dim, hipStream_t stream);
+
+/* gpu_dispatch_gemv_residual_on_stream (ops.rs:509, note the argument
+ * order: in_dim before out_dim).  *dispatched = 1 when a residual kernel ran
+ * (Q4_K: Q8-inline first, then fp32); 0 with RF_DISPATCH_OK for types
+ * without a residual kernel (the reference's Ok(false): GEMV + add). */
+int rf_gpu_dispatch_gemv_residual(const void* weights, const rf_weight_meta* meta, const float* input,
+                                  const float* residual, float* output, size_t in_dim, size_t out_dim,
+                                  hipStream_t stream, int* dispatched);
+
+/* The Q4_K arm of gpu_dispatch_fused_gate_up_with_scratch_on_stream
+ * (ops.rs:1316-1355): both layouts validated, Q8-inline fused kernel first,
+ * then the fp32 fused kernel. */
+int rf_gpu_dispatch_fused_gate_up(const void* w_gate, const rf_weight_meta* gate_meta, const void* w_up,
+                                  const rf_weight_meta* up_meta, const float* input, float* output, size_t ff_size,
+                                  size_t h, hipStream_t stream);
+
+/* gpu_dispatch_gemm (ops.rs:1591), null stream as in the reference:
+ * seq_len == 1 -> GEMV; Q4_K / Q6_K with out_dim % 64 == 0, in_dim % 256 == 0
+ * -> WMMA-equivalent GEMM at padded_m = round_up(seq_len, 64) (input and
+ * output must hold padded_m rows, the extra ones zero); on failure
+ * seq_len <= 8 -> one GEMV per row; Q6_K -> one Q6_K GEMV per row. */
+int rf_gpu_dispatch_gemm(const void* weights, const rf_weight_meta* meta, const float* input, float* output,
+                         size_t out_dim, size_t in_dim, size_t seq_len);
+
+/* Re-read the cached runtime flags. */
+void rf_dispatch_refresh_flags(void);
+
+/* The flag parser itself (1 = enabled), for tests. */
+int rf_dispatch_parse_env_flag(const char* value, int dflt);
+
+/* Launcher table used by the dispatch functions (default: this library's
+ * launchers).  Passing NULL restores the default.  Tests install recording
+ * stand-ins to check the routing without a GPU; not thread-safe against
+ * concurrent dispatch. */
+typedef struct rf_launchers {
+    hipError_t (*gemv_q4_k_q8_inline)(const void*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*gemv_q4_k_q8_inline_residual)(const void*, const float*, const float*, float*, int, int,
+                                               hipStream_t);
+    hipError_t (*gemv_gate_up_q4_k_q8_inline)(const void*, const void*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*gemv_q4_k_f32)(const void*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*gemv_q4_k_f32_residual)(const void*, const float*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*gemv_gate_up_q4_k_f32)(const void*, const void*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*gemv_q6_k_f32)(const void*, const float*, float*, int, int, hipStream_t);
+    hipError_t (*wmma_gemm_q4_k)(const float*, const void*, float*, int, int, int, hipStream_t);
+    hipError_t (*wmma_gemm_q6_k)(const float*, const void*, float*, int, int, int, hipStream_t);
+} rf_launchers;
+void rf_dispatch_set_launchers(const rf_launchers* table);
 
 /* ---- Parity probes (no reference counterpart) ---------------------------
  * Expose the intermediate integers of the Q8-inline path so tests can check

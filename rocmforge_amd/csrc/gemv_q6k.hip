@@ -404,7 +404,9 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     const int nsb = n_rows / kQK;
     if (gemv_q6_variant() == 0 && nsb <= 64) {
         const int nwk = (nsb + 7) / 8;
-        const int cap = device_cu_count() * gemv_wg_per_cu(1);
+        // about 8 waves per CU: short K (few slices per workgroup) gets
+        // several workgroups per CU
+        const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
         const int grid = ncols_dst < cap ? ncols_dst : cap;
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
         if (lds <= 64 * 1024) {

@@ -13,7 +13,7 @@ HIP_ERROR_INVALID_VALUE = 1
 
 def header_symbols():
     text = (ROOT / "include" / "rocmforge_cdna4.h").read_text()
-    return sorted(set(re.findall(r"^(?:hipError_t|const char\*)\s+(\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:hipError_t|const char\*|int|void)\s+(\w+)\(", text, re.M)))
 
 
 def test_header_declares_reference_launchers():
