@@ -146,11 +146,15 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     struct Step {
         Q4KUnit u[M][R];
     };
+    // x is loaded before the weight prefetch: loads complete in issue
+    // order, so the quantisation then waits only for x, not for the weights
+    X8Batch xb;
+    q8_prefetch(x, K, xb);
     Step ring[NB];
     ring_pipeline<NB>(nsteps, ring, [&](Step& b, int i) { load(b.u, i); },
                       [&](const Step& b, int i) { process(b.u, i); },
                       [&]() {
-                          q8_0_quantize_to_lds(x, K, q8);
+                          q8_quantize_finish(x, K, q8, xb);
                           __syncthreads();
                       });
     for (int j = lane; j < nrows; j += kWave) {

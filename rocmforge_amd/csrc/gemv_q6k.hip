@@ -389,6 +389,123 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __
 }
 
 
+// ── K-split Q6_K GEMV, lane-linear loads restaged through LDS (main path) ─
+// Same lane roles, x registers and reduction as rf_q6k_gemv_xreg_kernel,
+// but the weights are read the way the memory system streams best: a
+// wave's 1680-byte part of a row (8 super-blocks, 16-byte aligned when the
+// matrix is and K/256 % 8 == 0) arrives as two lane-linear dwordx4 loads
+// (lane L: bytes 16L and 16(64+L)), with two rows in flight.  Per row the
+// wave writes the 1680 bytes to its own 2 KB LDS stage and each lane reads
+// its ql / qh / scale bytes back (LDS accesses of one wave complete in
+// order, so no barrier is needed).  Measured on MI355X for the 4096x14336
+// ffn_down layout: pure reads with this pattern run at ~7.7 TB/s against
+// ~4 TB/s with per-lane 16-byte loads at 2-byte aligned block offsets.
+struct Q6Seg {
+    u32x4 a, b;
+};
+
+template <int NB>
+__global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __restrict__ w,
+                                                               const float* __restrict__ x,
+                                                               float* __restrict__ y, int K, int N) {
+    __shared__ __align__(16) uint8_t stage_lds[8 * 2048];
+    extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK]
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwk = blockDim.x / kWave;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ6KBytes;
+    const int blk = lane >> 3;
+    const int sb = 8 * wave + blk;
+    const int p = lane & 7;
+    const int n = p >> 2;
+    const int hq = (p & 3) >> 1;
+    const int is = p & 1;
+    const int g = blockIdx.x;
+    const int G = gridDim.x;
+    const int nrows = g < N ? (N - 1 - g) / G + 1 : 0;
+    uint8_t* stage = stage_lds + wave * 2048;
+
+    float xr[2][16];
+    {
+        const float* xb = x + (size_t)sb * kQK + 128 * n + 32 * hq + 16 * is;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = *reinterpret_cast<const float4*>(xb + 64 * r + 4 * k);
+                xr[r][4 * k + 0] = a.x; xr[r][4 * k + 1] = a.y; xr[r][4 * k + 2] = a.z; xr[r][4 * k + 3] = a.w;
+            }
+    }
+    float xs[2];
+    const uint8_t* wseg = w + (size_t)(8 * wave) * kQ6KBytes;
+    const int c1 = min(64 + lane, 104);   // chunks 105..127 re-read chunk 104 (same line), written to the spare area
+    auto load = [&](Q6Seg& u, int j) {
+        const uint8_t* src = wseg + (size_t)(nrows ? g + min(j, nrows - 1) * G : 0) * row_bytes;
+        u.a = *reinterpret_cast<const u32x4*>(src + 16 * lane);
+        u.b = *reinterpret_cast<const u32x4*>(src + 16 * c1);
+    };
+    // Aligned LDS reads.  Block b of the stage starts at byte 210b, which
+    // is 0 or 2 past a dword boundary (a3); each 16-byte field is read as the
+    // five aligned dwords around it and shifted into place (v_alignbit), and
+    // each scale byte / d as the aligned dword holding it.  (Unaligned
+    // 16-byte LDS reads at these offsets measured ~4 us slower per launch.)
+    const uint32_t* st32 = reinterpret_cast<const uint32_t*>(stage);
+    const int blkoff = blk * kQ6KBytes;
+    const uint32_t sh = 8u * (uint32_t)(blkoff & 3);
+    const int qlw = (blkoff + 16 * p) >> 2;
+    const int qhw = (blkoff + 128 + 32 * n + 16 * is) >> 2;
+    const int j1 = 192 + 8 * n + 2 * hq + is;        // scale bytes j1 (run 0) and j1 + 4 (run 1)
+    const int s0w = (blkoff + j1) >> 2, s1w = (blkoff + j1 + 4) >> 2;
+    const uint32_t s0sh = 8u * (uint32_t)((blkoff + j1) & 3), s1sh = 8u * (uint32_t)((blkoff + j1 + 4) & 3);
+    const int dww = (blkoff + 208) >> 2;
+    const uint32_t qsh = 2u * (uint32_t)hq;
+    auto field = [&](int w0) {
+        uint32_t d[5];
+#pragma unroll
+        for (int t = 0; t < 5; ++t) d[t] = st32[w0 + t];
+        return u32x4{__builtin_amdgcn_alignbit(d[1], d[0], sh), __builtin_amdgcn_alignbit(d[2], d[1], sh),
+                     __builtin_amdgcn_alignbit(d[3], d[2], sh), __builtin_amdgcn_alignbit(d[4], d[3], sh)};
+    };
+    auto process = [&](const Q6Seg& u, int j) {
+        *reinterpret_cast<u32x4*>(stage + 16 * lane) = u.a;
+        *reinterpret_cast<u32x4*>(stage + 16 * (64 + lane)) = u.b;
+        const u32x4 ql = field(qlw);
+        const u32x4 qh = field(qhw);
+        const float d = half_bits_to_float(st32[dww] >> sh);
+        const float s0 = d * (float)(int8_t)((st32[s0w] >> s0sh) & 0xFFu);
+        const float s1 = d * (float)(int8_t)((st32[s1w] >> s1sh) & 0xFFu);
+        const uint32_t L[4] = {ql.x, ql.y, ql.z, ql.w};
+        const uint32_t Q[4] = {qh.x, qh.y, qh.z, qh.w};
+        uint32_t v0[4], v1[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v0[t] = (L[t] & 0x0F0F0F0Fu) | (((Q[t] >> qsh) & 0x03030303u) << 4);
+            v1[t] = ((L[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> (qsh + 4)) & 0x03030303u) << 4);
+        }
+        float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
+        acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
+        const float tot = wave_sum(acc);
+        if (lane == 0) part[j * nwk + wave] = tot;
+    };
+    Q6Seg ring[NB];
+    ring_pipeline<NB>(nrows, ring, load, process, [&]() {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t += xr[r][i];
+            xs[r] = t;
+        }
+    });
+    __syncthreads();
+    for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
+        float t = 0.0f;
+        for (int k = 0; k < nwk; ++k) t += part[j * nwk + k];
+        y[g + j * G] = t;
+    }
+}
+
 }  // namespace rf
 
 using namespace rf;
@@ -402,7 +519,18 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
     const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
     const int nsb = n_rows / kQK;
-    if (gemv_q6_variant() == 0 && nsb <= 64) {
+    if (gemv_q6_variant() == 0 && nsb <= 64 && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0) {
+        const int nwk = nsb / 8;
+        const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
+        const int grid = ncols_dst < cap ? ncols_dst : cap;
+        const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
+        if (lds <= 64 * 1024) {
+            hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
+                               output, n_rows, ncols_dst);
+            return hipGetLastError();
+        }
+    }
+    if ((gemv_q6_variant() == 0 || gemv_q6_variant() == 2) && nsb <= 64) {
         const int nwk = (nsb + 7) / 8;
         // about 8 waves per CU: short K (few slices per workgroup) gets
         // several workgroups per CU
