@@ -7,13 +7,17 @@
 // rounding is the reference's: A via __float2half (wmma_gemm_q4_k.hip:86),
 // W via __float2half of the fp32 dequant value (:137, q6: :148).
 //
-// Two kernels:
-//  * rf_gemm_qk_v4_kernel (default when N % 256 == 0 and K % 512 == 0):
-//    512-thread workgroups over BM x 256 output tiles, A rounded to fp16
-//    once into LDS, W dequantised straight into MFMA B-operand registers,
-//    two waves per SIMD splitting each K chunk, optional split-K with float
-//    atomics when the tile count is below the CU count.  Its comment block
-//    below has the details.
+// Kernels (selected by the launcher from the shape):
+//  * rf_gemm_qk_v7_kernel (default when N % 256 == 0, K % 512 == 0 and, for
+//    Q6_K, K % 2048 == 0): 256-thread workgroups, one wave per SIMD, over a
+//    BM x 256 tile; weights stage through an LDS ring with coalesced loads,
+//    each wave dequantises its own B operands (the next chunk's, double
+//    buffered) in hand-scheduled slots between its MFMAs; XCD-aware tile
+//    order; split-K with float atomics when the tiles leave CUs idle.
+//  * rf_gemm_qk_v5_kernel: the previous 8-wave design with the same ring
+//    (RF_GEMM_V=5, kept for comparison measurements).
+//  * rf_gemm_qk_v4_kernel: 8 waves, weights loaded per lane (Q6_K with
+//    K % 2048 != 0, whose rows are not 16-byte aligned for the ring).
 //  * rf_gemm_qk_kernel (any M % 64 == 0, N % 64 == 0, K % 256 == 0): the
 //    general fallback.  4 wave64s in a 2x2 grid over a BM x BN tile of 32x32
 //    blocks of v_mfma_f32_32x32x16_f16; each 64-wide K chunk of A (fp32 ->
@@ -24,11 +28,7 @@
 #include <type_traits>
 
 #include "qk_common.h"
-#include "stream.h"
 
-#ifndef RF_GEMM_VPM
-#define RF_GEMM_VPM 6   // VALU instructions scheduled after each MFMA
-#endif
 
 namespace rf {
 
@@ -844,267 +844,6 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v5_kernel(const float* 
     }
 }
 
-template <typename T, bool IS_Q6, int FM, bool SPLIT>
-__global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v6_kernel(const float* __restrict__ A,
-                                                                    const uint8_t* __restrict__ W,
-                                                                    float* __restrict__ D, int M, int N, int K,
-                                                                    int tiles, int chunks_per_split) {
-    using G = RingGeom<IS_Q6>;
-    constexpr int BM = 32 * FM;
-    constexpr int BN = 256;
-    constexpr int A_F4 = BM * kKC / 4 / kV4Threads;   // float4 per thread per chunk
-    constexpr int kStageBytes = BN * G::kRS;
-    constexpr int kDepth = G::kStages - 1;             // super-blocks staged ahead
-    static_assert(G::kGroups * 1024 == kStageBytes && 8 * G::kNI >= G::kGroups && 8 * G::kNI < 2 * G::kGroups,
-                  "load groups cover the stage");
-    static_assert(4 * (FM / 2) * 2 * 16 * 64 * 4 <= G::kStages * kStageBytes, "reduction buffer");
-    __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
-    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 3, kh = wave >> 2;
-    const int h = lane >> 5;
-    const int tile = blockIdx.x % tiles;
-    const int split = blockIdx.x / tiles;
-    const int ntiles = N / BN;
-    const int m0 = (tile / ntiles) * BM;
-    const int nt0 = (tile % ntiles) * BN;   // first weight row of the tile
-    const int n0 = nt0 + wn * 64;
-    const int c_begin = split * chunks_per_split;
-    const int c_last = c_begin + chunks_per_split - 1;
-    const int sb_begin = c_begin / 4, sb_last = c_last / 4;
-    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
-    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
-
-    // per-lane staging source offsets (relative to the tile's rows at
-    // super-block 0) and LDS destinations
-    uint32_t goff[G::kNI];
-    uint32_t gdst[G::kNI];
-#pragma unroll
-    for (int t = 0; t < G::kNI; ++t) {
-        int g = wave * G::kNI + t;
-        if (g >= G::kGroups) g -= G::kGroups;
-        const int pc = 64 * g + lane;
-        gdst[t] = 16u * (uint32_t)pc;
-        const int row = pc / G::kNPR;
-        int piece = pc % G::kNPR;
-        if (IS_Q6 && piece == 14) piece = 13;
-        goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
-    }
-    u32x4 wst[G::kNI];
-    auto w_gload = [&](int sb) {
-        sb = min(sb, sb_last);
-        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
-#pragma unroll
-        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
-    };
-    auto w_lstore = [&](int slot) {
-        uint8_t* dst = w_ring + slot * kStageBytes;
-#pragma unroll
-        for (int t = 0; t < G::kNI; ++t) *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
-    };
-
-    const int a_row = tid >> 4;
-    const int a_col = 4 * (tid & 15);
-    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
-    float4 a_reg[2][A_F4];
-    auto a_load = [&](float4 (&r)[A_F4], int c) {
-        const float* src = a_base + (size_t)min(c, c_last) * kKC;
-#pragma unroll
-        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(32 * i) * K);
-    };
-    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
-        _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
-#pragma unroll
-        for (int i = 0; i < A_F4; ++i) {
-            f16x4 hv;
-            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
-            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
-            *reinterpret_cast<f16x4*>(dst + 32 * i * kLdsStride) = hv;
-        }
-    };
-
-    f32x16 acc[FM][2];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    const int frag = (lane & 31) * kLdsStride + 32 * kh + 16 * h;
-    const int row_lds0 = (wn * 64 + (lane & 31)) * G::kRS;
-    const int row_lds1 = row_lds0 + 32 * G::kRS;
-
-    // B operands are double buffered: iteration c runs the MFMAs of chunk c
-    // on bq[c & 1] while the lanes dequantise chunk c + 1 into
-    // bq[(c + 1) & 1]; the two streams are independent, and the scheduling
-    // hints below interleave them (one MFMA, then a few VALU operations), so
-    // the VALU work hides under the matrix core instead of running before it.
-    f16x8 bq[2][2][2];
-    // dequantise chunk with in-group index J (static) of super-block sb from
-    // ring slot `slot` into bq[J & 1]
-    auto w_dequant = [&](auto jj, auto khc, int sb, int slot) {
-        constexpr int J = decltype(jj)::value;
-        constexpr int KH = decltype(khc)::value;
-        constexpr int CQ = J & 3;
-        typename T::Hdr hd[2];
-        typename T::Qs qs[2];
-        const uint8_t* st = w_ring + slot * kStageBytes;
-        if constexpr (IS_Q6) {
-            const int shift = 2 * (sb & 7);
-            constexpr int nh = CQ >> 1;
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + shift;
-                qs[r].ql = ld16(rb + 64 * nh + 32 * KH + 16 * h);
-                qs[r].qh = ld16(rb + 128 + 32 * nh + 16 * h);
-                qs[r].sc = ld4(rb + 192 + 4 * CQ);
-                hd[r].d = ld_u16(rb + 208);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
-                hd[r].v = *reinterpret_cast<const u32x4*>(rb);
-                qs[r].q = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
-            }
-        }
-        T::template dequant_k<CQ, KH>(hd[0], qs[0], h, bq[J & 1][0]);
-        T::template dequant_k<CQ, KH>(hd[1], qs[1], h, bq[J & 1][1]);
-    };
-
-    // iteration I of the 8-chunk group starting at chunk c8 (super-blocks
-    // c8/4 and c8/4+1 in ring slots slot0, slot1, the next group's first
-    // super-block in slot2; staging targets sd0, sd1)
-    auto iteration = [&](auto it, auto khc, int c8, int slot0, int slot1, int slot2, int sd0, int sd1) {
-        constexpr int I = decltype(it)::value;
-        constexpr int P = I & 1, CQ = I & 3;
-        const int c = c8 + I;
-        const int sb = c8 / 4 + (I >> 2);
-        __builtin_amdgcn_sched_barrier(0);
-        // A fragments of chunk c (LDS buffer c & 1)
-        const _Float16* la = lds_a[P] + frag;
-        f16x8 af[2][FM];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int i = 0; i < FM; ++i) af[s2][i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride + 8 * s2);
-        a_store(a_reg[P ^ 1], P ^ 1);
-        if constexpr (CQ == 2) w_lstore((I >> 2) ? sd1 : sd0);
-        // next chunk's B operands (the chunk after the group's last one is
-        // the first of the next group, in slot2; past c_last it is unused)
-        if constexpr (I == 7)
-            w_dequant(std::integral_constant<int, 0>{}, khc, sb + 1, slot2);
-        else
-            w_dequant(std::integral_constant<int, I + 1>{}, khc, c8 / 4 + ((I + 1) >> 2), ((I + 1) >> 2) ? slot1 : slot0);
-        a_load(a_reg[P ^ 1], c + 3);
-        if constexpr (CQ == 0) w_gload(sb + kDepth);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s2][i], bq[P][j][s2], acc[i][j], 0, 0, 0);
-        // scheduling: fragment reads first, then MFMAs interleaved with the
-        // dequantisation / conversion VALU work and the LDS / global traffic
-        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);   // DS reads (A fragments of the first k16 step)
-#pragma unroll
-        for (int k = 0; k < 2 * FM * 2; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // 1 MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // 1 DS read
-            __builtin_amdgcn_sched_group_barrier(0x002, RF_GEMM_VPM, 0);  // VALU
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);    // 1 DS write
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // 1 VMEM read
-        }
-        lds_barrier();
-    };
-
-    // The K half of a wave is a template parameter of the main loop: with a
-    // runtime (wave-uniform) kh the compiler branches inside the
-    // dequantisation, which splits the loop body into several scheduling
-    // regions and defeats the MFMA / VALU interleave.
-    auto run = [&](auto khc) {
-    // prologue: super-blocks sb_begin .. sb_begin+kDepth-1 into slots 0..;
-    // A(c0) -> LDS 0; A(c0+1), A(c0+2) in flight
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        w_gload(sb_begin + d);
-        w_lstore(d);
-    }
-    a_load(a_reg[0], c_begin);
-    a_load(a_reg[1], c_begin + 1);
-    a_store(a_reg[0], 0);
-    a_load(a_reg[0], c_begin + 2);
-    lds_barrier();
-    w_dequant(std::integral_constant<int, 0>{}, khc, sb_begin, 0);
-
-    int slot0 = 0;   // ring slot of super-block c8/4
-    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
-        const int slot1 = slot0 + 1 == G::kStages ? 0 : slot0 + 1;
-        const int sd0 = slot0 + kDepth >= G::kStages ? slot0 + kDepth - G::kStages : slot0 + kDepth;
-        const int sd1 = sd0 + 1 == G::kStages ? 0 : sd0 + 1;
-        const int slot2 = slot1 + 1 == G::kStages ? 0 : slot1 + 1;
-        iteration(std::integral_constant<int, 0>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 1>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 2>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 3>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 4>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 5>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 6>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        iteration(std::integral_constant<int, 7>{}, khc, c8, slot0, slot1, slot2, sd0, sd1);
-        slot0 = slot2;
-    }
-    };
-    if (kh)
-        run(std::integral_constant<int, 1>{});
-    else
-        run(std::integral_constant<int, 0>{});
-
-    float* red = reinterpret_cast<float*>(w_ring) + wn * (FM / 2) * 2 * 16 * 64 + lane;
-    auto store = [&](int i, int j, const f32x16& v) {
-        const int col = n0 + 32 * j + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            if constexpr (SPLIT)
-                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
-            else
-                D[(size_t)row * N + col] = v[e];
-        }
-    };
-#pragma unroll
-    for (int round = 0; round < 2; ++round) {
-        const int giver = round == 0 ? 1 : 0;
-        if (kh == giver) {
-#pragma unroll
-            for (int ii = 0; ii < FM / 2; ++ii)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) red[((ii * 2 + j) * 16 + e) * 64] = acc[round * (FM / 2) + ii][j][e];
-        }
-        __syncthreads();
-        if (kh != giver) {
-#pragma unroll
-            for (int ii = 0; ii < FM / 2; ++ii)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    f32x16 v = acc[round * (FM / 2) + ii][j];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) v[e] += red[((ii * 2 + j) * 16 + e) * 64];
-                    store(round * (FM / 2) + ii, j, v);
-                }
-        }
-        __syncthreads();
-    }
-}
-
-
-
 // Workgroups are dispatched round-robin over the XCDs (b -> XCD b % 8).
 // Returns the virtual index of workgroup b such that XCD x processes the
 // contiguous virtual range [start_x, start_x + count_x): a bijection of
@@ -1482,7 +1221,6 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     }
     // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
     const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
-    const bool v6 = v5 && gemm_kernel_version() == 6;
     const bool v7 = v5 && gemm_kernel_version() == 0;
     if (s > 1) {
         const size_t n4 = (size_t)M * N / 4;
@@ -1490,9 +1228,6 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
                            st, reinterpret_cast<float4*>(D), n4);
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s);
-        else if (v6)
-            hipLaunchKernelGGL((rf_gemm_qk_v6_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
                                w, D, M, N, K, tiles, nchunks / s);
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
@@ -1503,9 +1238,6 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     } else {
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks);
-        else if (v6)
-            hipLaunchKernelGGL((rf_gemm_qk_v6_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
                                D, M, N, K, tiles, nchunks);
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,

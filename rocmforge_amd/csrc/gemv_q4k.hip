@@ -19,7 +19,7 @@
 //    difference to the reference is the fp32 summation order.
 //  * Workgroups stride over row groups; the grid is capped at a multiple of
 //    the CU count so a large N re-uses each workgroup's quantised vector.
-#include "stream.h"
+#include "qk_common.h"
 
 #ifndef RF_NB
 #define RF_NB 3   // register ring depth of the one-row-per-step GEMV (measured best)
@@ -170,137 +170,6 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     }
 }
 
-// ── LDS-streamed Q8-inline GEMV (main path) ──────────────────────────────
-// Same arithmetic as rf_q4k_q8_gemv_kernel; the weights travel HBM -> LDS
-// through each wave's S-stage ring (stream.h) instead of through registers:
-// every load instruction moves 1 KB of contiguous bytes, the prefetch depth
-// costs no VGPRs, and the lanes pick their 48-byte units out of LDS.
-template <int MODE, int R, int NW, int S>
-__global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_stream_kernel(const uint8_t* __restrict__ w0,
-                                                                         const uint8_t* __restrict__ w1,
-                                                                         const float* __restrict__ x,
-                                                                         const float* residual, float* y, int K,
-                                                                         int N) {
-    constexpr int M = (MODE == kGateUp) ? 2 : 1;
-    constexpr int NSEG = M * R;
-    using G = StepGeom<kQ4KBytes, NSEG>;
-    // The ring is its own LDS object, so alias analysis can tell the other
-    // LDS reads from the in-flight ring DMA.
-    __shared__ __align__(16) uint8_t ring_lds[NW * S * G::kStageBytes];
-    extern __shared__ __align__(16) uint8_t smem[];
-    const Q8Lds q8 = q8_lds_carve(smem, K);
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int s = lane >> 2;
-    const int p = lane & 3;
-    const int nsb = K / kQK;
-    const size_t row_bytes = (size_t)nsb * kQ4KBytes;
-    const int nwaves = gridDim.x * NW;
-    int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
-    const int max_rows = (N + nwaves - 1) / nwaves;
-    const size_t out_off = (q8_lds_bytes(K) + 15) & ~(size_t)15;
-    uint8_t* ring = ring_lds + (size_t)wave * S * G::kStageBytes;
-    float* out_lds = reinterpret_cast<float*>(smem + out_off) + wave * max_rows * M;
-
-    const int spr = (nsb + kSB - 1) / kSB;
-    const int nsteps = ((row_end - row_begin + R - 1) / R) * spr;
-    LaneChunks<kQ4KBytes, NSEG> lc;
-    lc.init(lane);
-    // issue(step i into ring slot `slot`): the tail re-issues the last step
-    // (clamped index) into the slot freed last iteration, never a live one.
-    auto issue = [&](int i, int slot) {
-        const int row0 = row_begin + (i / spr) * R;
-        const int sb0 = (i % spr) * kSB;
-        const uint8_t* segp[NSEG];
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = max(min(row0 + r, row_end - 1), 0);   // waves without rows re-read row 0
-                segp[m * R + r] = (m == 0 ? w0 : w1) + (size_t)row * row_bytes + (size_t)sb0 * kQ4KBytes;
-            }
-        issue_step<kQ4KBytes, NSEG>(lc, segp, min(kSB, nsb - sb0) * (kQ4KBytes / 16),
-                                    ring + slot * G::kStageBytes);
-    };
-
-    // Prologue: the first S-1 weight stages and x are put in flight together
-    // (all by DMA); the quantisation reads x from LDS once everything has
-    // landed, so it costs one memory latency shared with the weight ramp-up.
-    // (The compiler's wait counting turns conservative once LDS DMA is
-    // pending, which rules out a separate register prefetch of x.)
-    float* xs = reinterpret_cast<float*>(smem + out_off + (((size_t)NW * max_rows * M * 4 + 15) & ~(size_t)15));
-#pragma unroll
-    for (int k = 0; k < S - 1; ++k) issue(max(min(k, nsteps - 1), 0), k);   // unconditional: exact counts
-    stage_f32_to_lds(x, K, xs);
-    wait_vmcnt<0>();
-    lds_barrier();
-    q8_quantize_from_lds(xs, K, q8);
-    lds_barrier();
-
-    float acc[M][R];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-
-    for (int i = 0; i < nsteps; ++i) {
-        asm volatile("" ::: "memory");
-        issue(min(i + S - 1, nsteps - 1), (i + S - 1) % S);   // into the slot consumed last iteration
-        wait_vmcnt<(S - 1) * G::kNI>();      // step i has landed in LDS
-        const uint8_t* slot = ring + (i % S) * G::kStageBytes;
-        const int row0 = row_begin + (i / spr) * R;
-        const int sb = (i % spr) * kSB + s;
-        if (sb < nsb) {
-            // Q8 slab for this lane: 64 int8 at element sb*256 + 64p.
-            const u32x4* xs = reinterpret_cast<const u32x4*>(q8.qs + q8_pad(sb * kQK) + 64 * p);
-            const u32x4 xlo[2] = {xs[0], xs[1]};
-            const u32x4 xhi[2] = {xs[2], xs[3]};
-            const int b0 = sb * 8 + 2 * p;
-            const float xd0 = q8.xd[b0], xd1 = q8.xd[b0 + 1];
-            const int qs0 = q8.qsum[b0], qs1 = q8.qsum[b0 + 1];
-            static_assert(NSEG == 2, "ring reads are grouped for two segments");
-            Q4KUnit u[M][R];
-            u32x4 o[6];
-            ring_read_q4x2(slot + s * kQ4KBytes, slot + kSB * kQ4KBytes + s * kQ4KBytes, p, o);
-            u[0][0] = Q4KUnit{o[0], o[1], o[2]};
-            u[M - 1][R - 1] = Q4KUnit{o[3], o[4], o[5]};   // segment 1: (m=1,r=0) or (m=0,r=1)
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    acc[m][r] = q4k_q8_unit_dot(u[m][r], p, xlo, xhi, xd0, xd1, qs0, qs1, acc[m][r]);
-        }
-        if ((i % spr) == spr - 1) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float g = wave_sum(acc[0][r]);
-                const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
-                const int j = row0 + r - row_begin;
-                if (lane == 0 && row0 + r < row_end) {
-                    out_lds[M * j] = g;
-                    if (M == 2) out_lds[M * j + 1] = v;
-                }
-#pragma unroll
-                for (int m = 0; m < M; ++m) acc[m][r] = 0.0f;
-            }
-        }
-    }
-    wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
-    for (int j = lane; j < row_end - row_begin; j += kWave) {
-        const int row = row_begin + j;
-        const float g = out_lds[M * j];
-        if (MODE == kPlain) {
-            y[row] = g;
-        } else if (MODE == kResidual) {
-            y[row] = g + residual[row];
-        } else {
-            y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
-        }
-    }
-}
-
 // ── FP32-activation family (q4_k_gemv.hip) ───────────────────────────────
 // value = d*sc*nib - dmin*m (fp32, q4_k_gemv.hip:60-71), times x from LDS.
 // Same lane tiling as the Q8 kernel; x is staged in LDS as fp32 when it
@@ -408,31 +277,6 @@ template <int MODE>
 static hipError_t launch_q8(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
                             hipStream_t st) {
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
-    if (gemv_use_stream() && K <= 8192) {
-        constexpr int R = (MODE == kGateUp) ? 1 : 2;
-        constexpr int NW = 8, S = 3;
-        using G = StepGeom<kQ4KBytes, M * R>;
-        const int cap = device_cu_count() * gemv_wg_per_cu(2);
-        const int need = (N + NW - 1) / NW;
-        const int grid = need < cap ? need : cap;
-        const size_t out_off = (q8_lds_bytes(K) + 15) & ~(size_t)15;
-        const size_t max_rows = (N + (size_t)grid * NW - 1) / ((size_t)grid * NW);
-        const size_t lds = out_off + (((size_t)NW * max_rows * M * 4 + 15) & ~(size_t)15) + (size_t)K * 4;
-        if (lds + (size_t)NW * S * G::kStageBytes > 160 * 1024) return hipErrorInvalidValue;
-        auto kern = rf_q4k_q8_gemv_stream_kernel<MODE, R, NW, S>;
-        static bool attr = false;
-        if (!attr) {
-            // dynamic LDS may use what the static ring leaves of the 160 KB
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               160 * 1024 - NW * S * G::kStageBytes);
-            if (e != hipSuccess) return e;
-            attr = true;
-        }
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), lds, st, static_cast<const uint8_t*>(w0),
-                           static_cast<const uint8_t*>(w1), x, res, y, K, N);
-        return hipGetLastError();
-    }
     const int r = gemv_rows_per_step();
     const int nw = (r == 1) ? gemv_waves_per_wg(4) : 4;
     const int cap = device_cu_count() * gemv_wg_per_cu(2);

@@ -9,12 +9,17 @@
 //   q6 = (nibble of ql[64n + 32(q&1) + l], high for q>=2)
 //        | ((qh[32n + l] >> 2q) & 3) << 4,   value = d * sc[8n+2q+l/16] * (q6-32).
 //
-// Tiling: four lanes per 210-byte block (lane p: half n = p>>1, l in
-// [16c, 16c+16) with c = p&1), sixteen blocks per wave row step.  Each lane
-// reads its 16 B of low-ql, 16 B of high-ql and 16 B of qh with unaligned
-// 16-byte loads (blocks are only 2-byte aligned), 8 scale bytes and d, and
-// produces 64 products against x held in LDS.
-#include "stream.h"
+// Kernels (the launcher picks the first that applies):
+//  * rf_q6k_gemv_lin_kernel: K <= 16384, K/256 % 8 == 0, 16-byte aligned
+//    matrix.  K split across the waves of a workgroup (8 super-blocks per
+//    wave), x held in registers, weights read with lane-linear aligned
+//    16-byte loads and restaged per wave through LDS.
+//  * rf_q6k_gemv_xreg_kernel: K <= 16384 otherwise.  Same K split and x
+//    registers, each lane loading its block fields directly (16-byte loads
+//    at the 2-byte aligned block offsets).
+//  * rf_q6k_gemv_kernel: larger K.  One row per wave step, four lanes per
+//    block, x in L2 (K*4 > 64 KB).
+#include "qk_common.h"
 
 #ifndef RF_Q6_NB
 #define RF_Q6_NB 3   // register ring depth (rows in flight + 1) of the K-split GEMV (measured best)
@@ -185,78 +190,6 @@ __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_kernel(const uint8_t* __r
                       });
     for (int j = lane; j < row_end - row_begin; j += kWave) y[row_begin + j] = out_lds[j];
 }
-
-// ── LDS-streamed Q6_K GEMV (main path) ───────────────────────────────────
-// Weights travel HBM -> LDS through each wave's S-stage ring (stream.h); x
-// is staged in LDS as fp32.  A step covers 16 super-blocks (3360 B, 16-byte
-// aligned when the row is), so the path needs K/256 % 8 == 0, a 16-byte
-// aligned weight pointer and K <= KMAX; other layouts use
-// rf_q6k_gemv_kernel.  Both LDS buffers are static objects: the compiler
-// only separates LDS reads from in-flight LDS DMA for such objects (for
-// anything else it waits for all DMA), and a wave's row results are held in
-// lane registers (lane j keeps row begin+j, at most 64 rows per wave).
-template <int NW, int S, int KMAX>
-__global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_stream_kernel(const uint8_t* __restrict__ w,
-                                                                      const float* __restrict__ x,
-                                                                      float* __restrict__ y, int K, int N) {
-    using G = StepGeom<kQ6KBytes, 1>;
-    __shared__ __align__(16) uint8_t ring_lds[NW * S * G::kStageBytes];
-    __shared__ __align__(16) float xs[x_padded_floats(KMAX) + 4];
-    __shared__ __align__(16) float xsum16[KMAX / 16];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int s = lane >> 2;
-    const int p = lane & 3;
-    const int nsb = K / kQK;
-    const size_t row_bytes = (size_t)nsb * kQ6KBytes;
-    const int nwaves = gridDim.x * NW;
-    int row_begin, row_end;
-    wave_row_range(N, blockIdx.x * NW + wave, nwaves, &row_begin, &row_end);
-    uint8_t* ring = ring_lds + (size_t)wave * S * G::kStageBytes;
-
-    const int spr = (nsb + kSB - 1) / kSB;
-    const int nsteps = (row_end - row_begin) * spr;
-    LaneChunks<kQ6KBytes, 1> lc;
-    lc.init(lane);
-    // issue(step i into ring slot `slot`): the tail re-issues the last step
-    // (clamped index) into the slot freed last iteration, never a live one.
-    auto issue = [&](int i, int slot) {
-        const int row = max(min(row_begin + i / spr, row_end - 1), 0);
-        const int sb0 = (i % spr) * kSB;
-        const uint8_t* segp[1] = {w + (size_t)row * row_bytes + (size_t)sb0 * kQ6KBytes};
-        issue_step<kQ6KBytes, 1>(lc, segp, min(kSB, nsb - sb0) * kQ6KBytes / 16, ring + slot * G::kStageBytes);
-    };
-
-#pragma unroll
-    for (int k = 0; k < S - 1; ++k) issue(max(min(k, nsteps - 1), 0), k);   // unconditional: exact counts
-    stage_f32_to_lds_regs(x, K, xs);   // padded layout (bank-conflict free reads)
-    wait_vmcnt<0>();
-    lds_barrier();
-    q6_xsum16<true>(xs, K, xsum16);
-    lds_barrier();
-
-    float acc = 0.0f, out = 0.0f;
-    for (int i = 0; i < nsteps; ++i) {
-        asm volatile("" ::: "memory");
-        issue(min(i + S - 1, nsteps - 1), (i + S - 1) % S);
-        wait_vmcnt<(S - 1) * G::kNI>();
-        const uint8_t* slot = ring + (i % S) * G::kStageBytes;
-        const int sb = (i % spr) * kSB + s;
-        if (sb < nsb) {
-            Q6Unit u;
-            ring_read_q6(slot + s * kQ6KBytes, p, u.lo, u.hi, u.qh, u.sc, u.d);
-            acc = q6k_unit_dot<132>(u, p, xs + x_pad(sb * kQK), xsum16 + sb * 16, acc);
-        }
-        if ((i % spr) == spr - 1) {
-            const float g = wave_sum(acc);
-            out = (lane == i / spr) ? g : out;
-            acc = 0.0f;
-        }
-    }
-    wait_vmcnt<0>();
-    if (lane < row_end - row_begin) y[row_begin + lane] = out;
-}
-
 
 // ── K-split Q6_K GEMV with x held in registers (main path) ───────────────
 // A workgroup has one wave per 8-super-block slice of K (NWK = nsb/8
@@ -540,26 +473,6 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
         if (lds <= 64 * 1024) {
             hipLaunchKernelGGL((rf_q6k_gemv_xreg_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
                                output, n_rows, ncols_dst);
-            return hipGetLastError();
-        }
-    }
-    if (gemv_use_stream() && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
-        (reinterpret_cast<uintptr_t>(input) & 15u) == 0) {
-        constexpr int NW = 8, S = 3;
-        const int cap = device_cu_count() * gemv_wg_per_cu(1);
-        const int need = (ncols_dst + NW - 1) / NW;
-        const int grid = need < cap ? need : cap;
-        const size_t max_rows = (ncols_dst + (size_t)grid * NW - 1) / ((size_t)grid * NW);
-        if (max_rows <= (size_t)kWave && n_rows <= 14336) {
-            const void* kern = n_rows <= 4096 ? reinterpret_cast<const void*>(rf_q6k_gemv_stream_kernel<NW, S, 4096>)
-                                              : reinterpret_cast<const void*>(rf_q6k_gemv_stream_kernel<NW, S, 14336>);
-            if (n_rows <= 4096)
-                hipLaunchKernelGGL((rf_q6k_gemv_stream_kernel<NW, S, 4096>), dim3(grid), dim3(NW * 64), 0, stream, w,
-                                   input, output, n_rows, ncols_dst);
-            else
-                hipLaunchKernelGGL((rf_q6k_gemv_stream_kernel<NW, S, 14336>), dim3(grid), dim3(NW * 64), 0, stream, w,
-                                   input, output, n_rows, ncols_dst);
-            (void)kern;
             return hipGetLastError();
         }
     }

@@ -336,15 +336,20 @@ __device__ __forceinline__ float q4k_q8_combine(float acc, float xd, float d, fl
     return acc + xd * (d * (float)sc * (float)dot - dmin * (float)mn * (float)qsum);
 }
 
+// Workgroup barrier that does not wait for outstanding global loads
+// (__syncthreads() implies a fence, i.e. vmcnt(0), which would drain the
+// loads a pipeline keeps in flight across the barrier).  LDS writes of this
+// wave are completed first.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Device CU count, cached per device (host side).
 int device_cu_count();
 // GEMV workgroups per CU and waves per workgroup (host side).  Each kernel
 // family passes its measured-best default; RF_GEMV_WG_PER_CU / RF_GEMV_NW
 // override them for tuning sweeps.
 int gemv_wg_per_cu(int dflt);
-// Whether the LDS-DMA streamed GEMV kernels are used (default no: the
-// register-pipelined kernels measure faster; RF_GEMV_STREAM=1 selects them).
-bool gemv_use_stream();
 // Rows per pipeline step of the register GEMV (default 1; RF_GEMV_R=2|4
 // for tuning sweeps).
 int gemv_rows_per_step();
@@ -352,8 +357,8 @@ int gemv_waves_per_wg(int dflt);
 // Q6_K GEMV kernel family (0 = K-split register kernel, 1 = row-step kernel).
 int gemv_q6_variant();
 // GEMM kernel selection for tuning comparisons: RF_GEMM_V=1 forces the
-// general 2x2-wave kernel, =4 the register-weight kernel; default (0) picks
-// the weight-ring kernel where it applies.
+// general 2x2-wave kernel, =4 the register-weight kernel, =5 the 8-wave
+// ring kernel; default (0) picks the one-wave-per-SIMD ring kernel (v7).
 int gemm_kernel_version();
 
 }  // namespace rf

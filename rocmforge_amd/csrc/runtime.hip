@@ -29,15 +29,6 @@ int gemv_wg_per_cu(int dflt) {
     return v ? v : dflt;
 }
 
-bool gemv_use_stream() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("RF_GEMV_STREAM");
-        v = (e && e[0] == '1') ? 1 : 0;
-    }
-    return v == 1;
-}
-
 int gemv_rows_per_step() {
     static int v = 0;
     if (v == 0) {
@@ -72,7 +63,7 @@ int gemm_kernel_version() {
     if (v < 0) {
         const char* e = getenv("RF_GEMM_V");
         const int n = e ? atoi(e) : 0;
-        v = (n == 1 || n == 4 || n == 5 || n == 6) ? n : 0;
+        v = (n == 1 || n == 4 || n == 5) ? n : 0;
     }
     return v;
 }
