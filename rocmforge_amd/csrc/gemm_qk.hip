@@ -867,15 +867,16 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
 // for many cycles while the SIMD issues the independent VALU work).
 constexpr int kV7Threads = 256;
 
+// Weight ring of the 256-row tile: one super-block of every row per stage
+// (Q4_K: 144-byte blocks; Q6_K: the 16-byte aligned 240-byte window around
+// the 2-byte aligned block), two stages.  A stage is kGroups KB; each of
+// the 4 waves moves kNI of them.
 template <bool IS_Q6>
-struct RingGeom7;
-template <>
-struct RingGeom7<false> {
-    static constexpr int kRS = 144, kNPR = 9, kStages = 3, kGroups = 36, kNI = 9;
-};
-template <>
-struct RingGeom7<true> {
-    static constexpr int kRS = 240, kNPR = 15, kStages = 2, kGroups = 60, kNI = 15;
+struct RingGeom7 {
+    static constexpr int kRS = IS_Q6 ? 240 : 144, kNPR = IS_Q6 ? 15 : 9;
+    static constexpr int kStages = 2;
+    static constexpr int kGroups = 256 * kRS / 1024;
+    static constexpr int kNI = kGroups / 4;
 };
 
 template <typename T, bool IS_Q6, int FM, bool SPLIT>
@@ -884,15 +885,23 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
                                                                     float* __restrict__ D, int M, int N, int K,
                                                                     int tiles, int chunks_per_split) {
     using G = RingGeom7<IS_Q6>;
+    constexpr int FN = 2;                               // 32-column blocks per wave
     constexpr int BM = 32 * FM;
-    constexpr int BN = 256;
+    constexpr int BN = 128 * FN;
     constexpr int A_RPP = kV7Threads / 16;              // A rows per staging pass
     constexpr int A_F4 = BM * kKC / 4 / kV7Threads;     // float4 per thread per chunk
     constexpr int kStageBytes = BN * G::kRS;
     constexpr int kDepth = G::kStages - 1;
+    constexpr int NS = 4 * FM * FN;                     // MFMA slots per iteration
     static_assert(G::kGroups * 1024 == kStageBytes && 4 * G::kNI == G::kGroups, "load groups cover the stage");
+    static_assert(A_F4 <= 8, "A register double buffer");
     __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
-    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
+    // A_PF (where LDS allows): four A buffers, chunk c + 2 stored during
+    // iteration c, so the first A fragments of chunk c + 1 are read before
+    // the end of iteration c (no LDS latency exposed after the per-chunk
+    // barrier).  Otherwise two buffers, chunk c + 1 stored in iteration c.
+    constexpr bool A_PF = G::kStages * kStageBytes + 4 * BM * kLdsStride * 2 <= 160 * 1024;
+    __shared__ __align__(16) _Float16 lds_a[A_PF ? 4 : 2][BM * kLdsStride];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -908,7 +917,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     const int ntiles = N / BN;
     const int m0 = (tile / ntiles) * BM;
     const int nt0 = (tile % ntiles) * BN;
-    const int n0 = nt0 + wave * 64;
+    const int n0 = nt0 + wave * 32 * FN;
     const int c_begin = split * chunks_per_split;
     const int c_last = c_begin + chunks_per_split - 1;
     const int sb_begin = c_begin / 4, sb_last = c_last / 4;
@@ -928,11 +937,15 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
     }
     u32x4 wst[G::kNI];
-    auto w_gload = [&](int sb) {
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wtile);
+    auto w_soff = [&](int sb) -> uint32_t {
         sb = min(sb, sb_last);
-        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
+        return IS_Q6 ? (((uint32_t)sb * kQ6KBytes) & ~15u) : (uint32_t)sb * kQ4KBytes;
+    };
+    auto w_gload = [&](int sb) {
+        const uint32_t so = w_soff(sb);
 #pragma unroll
-        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
+        for (int t = 0; t < G::kNI; ++t) wst[t] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, goff[t], so, 0);
     };
     auto w_lstore = [&](int slot) {
         uint8_t* dst = w_ring + slot * kStageBytes;
@@ -942,12 +955,19 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
 
     const int a_row = tid >> 4;
     const int a_col = 4 * (tid & 15);
-    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
+    // A float4 i of chunk c: buffer load with the workgroup-uniform part of
+    // the offset in a scalar register and the lane's part in a vector one,
+    // so the load costs no per-lane address arithmetic
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(A + (size_t)m0 * K);
+    const uint32_t a_voff = (uint32_t)(a_row * K + a_col) * 4u;
+    auto a_ld = [&](int c, int i) -> float4 {
+        const uint32_t so = (uint32_t)(A_RPP * i * K + min(c, c_last) * kKC) * 4u;
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, so, 0));
+    };
     float4 a_reg[2][A_F4];
     auto a_load = [&](float4 (&r)[A_F4], int c) {
-        const float* src = a_base + (size_t)min(c, c_last) * kKC;
 #pragma unroll
-        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(A_RPP * i) * K);
+        for (int i = 0; i < A_F4; ++i) r[i] = a_ld(c, i);
     };
     auto a_store = [&](const float4 (&r)[A_F4], int buf) {
         _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
@@ -960,45 +980,44 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         }
     };
 
-    f32x16 acc[FM][2];
+    f32x16 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     const int frag = (lane & 31) * kLdsStride + 16 * h;
-    const int row_lds0 = (wave * 64 + (lane & 31)) * G::kRS;
-    const int row_lds1 = row_lds0 + 32 * G::kRS;
+    const int row_lds0 = (wave * 32 * FN + (lane & 31)) * G::kRS;
 
     // bq[buffer][k half][column block][k16 step]
-    f16x8 bq[2][2][2][2];
+    f16x8 bq[2][2][FN][2];
     // Raw operand bytes of chunk c + 1 for the lane's two weight rows, read
     // from the ring at the start of iteration c, and the per-(row, k half)
     // scale terms: Q4_K value = a * byte - b (a = d*sc, or d*sc/16 for the
     // high-nibble half read as 16*nibble; b = dmin*m); Q6_K value = a * q - b
     // (a = d*sc, b = 32a).
-    u32x4 wq[2][2];     // Q4: [row][0] = header, [1] = qs bytes; Q6: [row][0] = ql (kh 0), [1] = ql (kh 1)
-    u32x4 wqh[2];       // Q6: qh bytes per row
-    uint32_t wsc[2];    // Q6: scale word per row
-    uint32_t wd[2];     // Q6: d per row
-    float pa[2][2], pb[2][2];
+    u32x4 wq[FN][2];     // Q4: [row][0] = header, [1] = qs bytes; Q6: [row][0] = ql (kh 0), [1] = ql (kh 1)
+    u32x4 wqh[FN];       // Q6: qh bytes per row
+    uint32_t wsc[FN];    // Q6: scale word per row
+    uint32_t wd[FN];     // Q6: d per row
+    float pa[FN][2], pb[FN][2];
     auto w_read = [&](auto jj, int sb, int slot) {
         constexpr int CQ = decltype(jj)::value & 3;
         const uint8_t* st = w_ring + slot * kStageBytes;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < FN; ++r) {
             if constexpr (IS_Q6) {
                 constexpr int nh = CQ >> 1;
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + 2 * (sb & 7);
+                const uint8_t* rb = st + row_lds0 + 32 * r * G::kRS + 2 * (sb & 7);
                 wq[r][0] = ld16(rb + 64 * nh + 16 * h);
                 wq[r][1] = ld16(rb + 64 * nh + 32 + 16 * h);
                 wqh[r] = ld16(rb + 128 + 32 * nh + 16 * h);
                 wsc[r] = ld4(rb + 192 + 4 * CQ);
                 wd[r] = ld_u16(rb + 208);
             } else {
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
+                const uint8_t* rb = st + row_lds0 + 32 * r * G::kRS;
                 wq[r][0] = *reinterpret_cast<const u32x4*>(rb);
                 wq[r][1] = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
             }
@@ -1044,7 +1063,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     };
     auto w_dequant_all = [&](auto jj, int buf) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < FN; ++r) {
             w_prep(jj, r);
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
@@ -1065,6 +1084,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     // previous pair) and one slice of the side work -- a piece of the next
     // chunk's dequantisation, one A float4 to LDS, one global load, one ring
     // store -- so the VALU work runs while the matrix core executes.
+    f16x8 af[2][FM];
     auto iteration = [&](auto it, int c8, int slot0, int slot1, int slot2, int sd0, int sd1) {
         constexpr int I = decltype(it)::value;
         constexpr int P = I & 1, CQ = I & 3;
@@ -1074,12 +1094,16 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         const int sb = c8 / 4 + (I >> 2);
         const int sbn = I == 7 ? sb + 1 : c8 / 4 + ((I + 1) >> 2);
         const int slotn = I == 7 ? slot2 : (((I + 1) >> 2) ? slot1 : slot0);
-        const _Float16* la = lds_a[P] + frag;
+        const _Float16* la = lds_a[A_PF ? (I & 3) : P] + frag;
+        // with A_PF the first MFMAs need no fresh LDS data, so the
+        // dequantisation starts two slots later, behind the ring reads
+        constexpr int DQ0 = A_PF ? 2 : 0;
         __builtin_amdgcn_sched_barrier(0);
         w_read(JN{}, sbn, slotn);
-        f16x8 af[2][FM];
+        if constexpr (!A_PF) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride);
+            for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int step = 0; step < 4; ++step) {
@@ -1087,12 +1111,11 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < FN; ++j) {
                     // slot t: one MFMA, then ~7 VALU operations of side work
                     // (the MFMA occupies the matrix core for 32 cycles, the
                     // time the SIMD needs to issue about 8 VALU operations)
-                    const int t = (step * FM + i) * 2 + j;   // 0 .. 8*FM-1
-                    constexpr int NS = 8 * FM;
+                    const int t = (step * FM + i) * FN + j;   // 0 .. NS-1
                     if (i == 0 && j == 0 && step < 3) {
                         const int nk = (step + 1) >> 1, ns = (step + 1) & 1;
 #pragma unroll
@@ -1100,38 +1123,52 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
                             af[(step + 1) & 1][ii] =
                                 *reinterpret_cast<const f16x8*>(la + 32 * ii * kLdsStride + 32 * nk + 8 * ns);
                     }
+                    if constexpr (A_PF) {
+                        // first fragments of chunk c + 1 (stored during
+                        // iteration c - 1, behind the last barrier)
+                        if (i == 0 && j == 0 && step == 3) {
+                            const _Float16* ln = lds_a[(I + 1) & 3] + frag;
+#pragma unroll
+                            for (int ii = 0; ii < FM; ++ii)
+                                af[0][ii] = *reinterpret_cast<const f16x8*>(ln + 32 * ii * kLdsStride);
+                        }
+                    }
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[step & 1][i], bq[P][kh][j][s2], acc[i][j],
                                                                        0, 0, 0);
-                    // dequantisation of chunk c + 1: prep row 0 at slot 0,
-                    // its 8 pieces at 1..8, prep row 1 at 9, pieces 10..17
-                    // (packed into 16 slots when FM = 2)
-                    if constexpr (NS >= 18) {
-                        if (t == 0) w_prep(JN{}, 0);
-                        if (t >= 1 && t <= 8) w_piece(JN{}, P ^ 1, 0, (t - 1) >> 2, (t - 1) & 3);
-                        if (t == 9) w_prep(JN{}, 1);
-                        if (t >= 10 && t <= 17) w_piece(JN{}, P ^ 1, 1, (t - 10) >> 2, (t - 10) & 3);
-                    } else if constexpr (NS < 18) {
+                    // dequantisation of chunk c + 1: prep row r at slot
+                    // DQ0 + 9r, its 8 pieces at the next 8 slots (packed
+                    // into 16 slots when NS = 16)
+                    if constexpr (NS >= 9 * FN + DQ0) {
+#pragma unroll
+                        for (int r = 0; r < FN; ++r) {
+                            if (t == DQ0 + 9 * r) w_prep(JN{}, r);
+                            if (t >= DQ0 + 9 * r + 1 && t <= DQ0 + 9 * r + 8)
+                                w_piece(JN{}, P ^ 1, r, (t - DQ0 - 9 * r - 1) >> 2, (t - DQ0 - 9 * r - 1) & 3);
+                        }
+                    } else {
+                        static_assert(NS == 16, "packed dequantisation schedule");
                         if (t == 0) {
                             w_prep(JN{}, 0);
                             w_prep(JN{}, 1);
                         }
                         if (t < 16) w_piece(JN{}, P ^ 1, t >> 3, (t >> 2) & 1, t & 3);
                     }
-                    // A: store float4 k of chunk c + 1 at slot NS-14+k, reload
-                    // it (chunk c + 3) six slots later
-                    if (t >= NS - 14 && t < NS - 14 + A_F4) a_store1(a_reg[P ^ 1][t - (NS - 14)], P ^ 1, t - (NS - 14));
-                    if (t >= NS - 8 && t < NS - 8 + A_F4) {
-                        const int k = t - (NS - 8);
-                        a_reg[P ^ 1][k] = *reinterpret_cast<const float4*>(
-                            a_base + (size_t)min(c + 3, c_last) * kKC + (size_t)(A_RPP * k) * K);
+                    {
+                        // A: store float4 k of chunk c + 1 (A_PF: c + 2) at
+                        // slot NS-14+k, reload the register with chunk c + 3
+                        // (A_PF: c + 4) six slots later
+                        constexpr int RB = A_PF ? P : P ^ 1;
+                        constexpr int LB = A_PF ? ((I + 2) & 3) : (P ^ 1);
+                        if (t >= NS - 14 && t < NS - 14 + A_F4)
+                            a_store1(a_reg[RB][t - (NS - 14)], LB, t - (NS - 14));
+                        if (t >= NS - 8 && t < NS - 8 + A_F4) {
+                            const int k = t - (NS - 8);
+                            a_reg[RB][k] = a_ld(c + (A_PF ? 4 : 3), k);
+                        }
                     }
                     if constexpr (CQ == 0) {
-                        if (t < G::kNI) {
-                            const int sbl = min(sb + kDepth, sb_last);
-                            const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sbl * kQ6KBytes) & ~(size_t)15)
-                                                                : (size_t)sbl * kQ4KBytes);
-                            wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
-                        }
+                        if (t < G::kNI)
+                            wst[t] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, goff[t], w_soff(sb + kDepth), 0);
                     }
                     if constexpr (CQ == 2) {
                         if (t < G::kNI) {
@@ -1142,7 +1179,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
                     __builtin_amdgcn_sched_barrier(0);
                 }
         }
-        static_assert(8 * FM >= 16 && 8 * FM >= G::kNI && 8 * FM >= 14, "side work fits the slots");
+        static_assert(NS >= 16 && NS >= G::kNI && NS >= 14, "side work fits the slots");
         lds_barrier();
     };
 
@@ -1151,13 +1188,26 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         w_gload(sb_begin + d);
         w_lstore(d);
     }
-    a_load(a_reg[0], c_begin);
-    a_load(a_reg[1], c_begin + 1);
-    a_store(a_reg[0], 0);
-    a_load(a_reg[0], c_begin + 2);
+    if constexpr (A_PF) {
+        a_load(a_reg[0], c_begin);
+        a_load(a_reg[1], c_begin + 1);
+        a_store(a_reg[0], 0);
+        a_store(a_reg[1], 1);
+        a_load(a_reg[0], c_begin + 2);
+        a_load(a_reg[1], c_begin + 3);
+    } else {
+        a_load(a_reg[0], c_begin);
+        a_load(a_reg[1], c_begin + 1);
+        a_store(a_reg[0], 0);
+        a_load(a_reg[0], c_begin + 2);
+    }
     lds_barrier();
     w_read(std::integral_constant<int, 0>{}, sb_begin, 0);
     w_dequant_all(std::integral_constant<int, 0>{}, 0);
+    if constexpr (A_PF) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(lds_a[0] + frag + 32 * i * kLdsStride);
+    }
 
     int slot0 = 0;
     for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
@@ -1179,11 +1229,258 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int col = n0 + 32 * j + (lane & 31);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if constexpr (SPLIT)
+                    unsafeAtomicAdd(&D[(size_t)row * N + col], acc[i][j][e]);
+                else
+                    D[(size_t)row * N + col] = acc[i][j][e];
+            }
+        }
+}
+
+// ── sq: 256 x 256 tiles, 2 x 2 waves, dequantised B shared through LDS ───
+// Workgroup = 256 threads (one wave per SIMD) over a 256 x 256 tile; wave
+// (wm, wn) owns the quarter [m0 + 128 wm, +128) x [n0 + 128 wn, +128) as
+// 4 x 4 blocks of v_mfma_f32_32x32x16_f16 (accumulators in AGPRs).  Per
+// 64-wide K chunk both operands sit in LDS as [row][k] fp16 with the padded
+// stride: A (fp32 -> fp16) and B, which thread t dequantises for weight row
+// n0 + t once per workgroup -- one dequantisation per weight per 256 rows of
+// A, shared by the two waves that use it.  Used where 256 x 256 tiles fill
+// the CUs without a K split (M >= 1024 at the Llama FFN shapes).  The next chunk's A store, B dequantisation and global loads
+// run in hand-scheduled slots between the MFMAs of the current chunk (both
+// LDS operands double buffered, one barrier per chunk).
+constexpr int kSqThreads = 256;
+constexpr int kSqTile = 256;
+
+// Raw quant bytes of one chunk of one weight row (thread-private).
+struct SqRawQ4 {
+    u32x4 hdr;        // d, dmin, scales[12]
+    u32x4 q[2];       // qs [32CQ, 32CQ + 32)
+};
+struct SqRawQ6 {
+    u32x4 ql[4];      // ql [64nh, 64nh + 64)
+    u32x4 qh[2];      // qh [32nh, 32nh + 32)
+    uint32_t sc;      // scales [4CQ, 4CQ + 4)
+    uint32_t d;       // fp16 bits of d
+};
+
+template <bool IS_Q6, bool SPLIT>
+__global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ W,
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int tiles, int chunks_per_split) {
+    using Raw = typename std::conditional<IS_Q6, SqRawQ6, SqRawQ4>::type;
+    constexpr int kBytes = IS_Q6 ? kQ6KBytes : kQ4KBytes;
+    constexpr int BAR = 48;                            // slot of the barrier (start of step 3)
+    constexpr int WLD = 20;                            // slot of the next-but-one chunk's weight loads
+    constexpr int A0 = 28;                             // first A store slot
+    constexpr int A_RPP = kSqThreads / 16;             // A rows per staging pass
+    constexpr int A_F4 = kSqTile * kKC / 4 / kSqThreads;   // 16 float4 per thread per chunk
+    static_assert(A0 + A_F4 <= BAR && 2 + 16 <= WLD, "side work before the barrier");
+    __shared__ __align__(16) _Float16 lds_a[2][kSqTile * kLdsStride];
+    __shared__ __align__(16) _Float16 lds_b[2][kSqTile * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5;
+    const int vidx = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int splits = (int)gridDim.x / tiles;
+    const int tile = vidx / splits;
+    const int split = vidx % splits;
+    const int ntiles = N / kSqTile;
+    const int m0 = (tile / ntiles) * kSqTile;
+    const int n0 = (tile % ntiles) * kSqTile;
+    const int c_begin = split * chunks_per_split;
+    const int c_last = c_begin + chunks_per_split - 1;
+    const uint32_t row_bytes = (uint32_t)(K / kQK) * kBytes;
+
+    // ---- A: 16 float4 per thread per chunk, buffer loads -----------------
+    const int a_row = tid >> 4;
+    const int a_col = 4 * (tid & 15);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(A + (size_t)m0 * K);
+    const uint32_t a_voff = (uint32_t)(a_row * K + a_col) * 4u;
+    auto a_ld = [&](int c, int i) -> float4 {
+        const uint32_t so = (uint32_t)(A_RPP * i * K + min(c, c_last) * kKC) * 4u;
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, so, 0));
+    };
+    auto a_st = [&](const float4& v, int buf, int i) {
+        f16x4 hv;
+        hv[0] = (_Float16)v.x; hv[1] = (_Float16)v.y;
+        hv[2] = (_Float16)v.z; hv[3] = (_Float16)v.w;
+        *reinterpret_cast<f16x4*>(&lds_a[buf][(a_row + A_RPP * i) * kLdsStride + a_col]) = hv;
+    };
+    float4 a_reg[A_F4];
+
+    // ---- W: thread tid dequantises weight row n0 + tid -----------------
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W + (size_t)n0 * row_bytes);
+    const uint32_t w_voff = (uint32_t)tid * row_bytes;
+    Raw wr[2];
+    auto w_ld = [&](auto cq, Raw& r, int c) {
+        constexpr int CQ = decltype(cq)::value;
+        const uint32_t blk = (uint32_t)(min(c, c_last) >> 2) * kBytes;
+        if constexpr (IS_Q6) {
+            constexpr int nh = CQ >> 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                r.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff, blk + 64 * nh + 16 * i, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff, blk + 128 + 32 * nh + 16 * i, 0);
+            r.sc = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, w_voff, blk + 192 + 4 * CQ, 0);
+            r.d = __builtin_amdgcn_raw_buffer_load_b16(w_rsrc, w_voff, blk + 208, 0);
+        } else {
+            r.hdr = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff, blk, 0);
+            r.q[0] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff, blk + 16 + 32 * CQ, 0);
+            r.q[1] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff, blk + 32 + 32 * CQ, 0);
+        }
+    };
+    // Scale terms: Q4_K value = pa[kh] * byte - pb[kh] (kh 0: low nibbles,
+    // k 0..31; kh 1: high nibbles read as 16 * nibble, k 32..63); Q6_K
+    // value = ps[g] * q - 32 ps[g] for the 16-wide group g = k / 16.
+    float pa[2], pb[2], ps[4];
+    auto w_prep = [&](auto cq, const Raw& r) {
+        constexpr int CQ = decltype(cq)::value;
+        if constexpr (IS_Q6) {
+            const float d = half_bits_to_float(r.d);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) ps[g] = d * (float)(int8_t)((r.sc >> (8 * g)) & 0xFFu);
+        } else {
+            int sc0, mn0, sc1, mn1;
+            q4k_scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, CQ, &sc0, &mn0, &sc1, &mn1);
+            const float d = half_bits_to_float(r.hdr.x), dmin = half_bits_to_float(r.hdr.x >> 16);
+            pa[0] = d * (float)sc0;
+            pb[0] = dmin * (float)mn0;
+            pa[1] = d * (float)sc1 * 0.0625f;
+            pb[1] = dmin * (float)mn1;
+        }
+    };
+    // piece p (0..15) = 4 weights k = 32 kh + 4 j .. + 3 (kh = p >> 3,
+    // j = p & 7); the pair (p - 1, p) for odd p completes 8 weights, stored
+    // to LDS
+    f16x8 wout;
+    auto w_piece = [&](auto cq, const Raw& r, int buf, int p) {
+        constexpr int CQ = decltype(cq)::value;
+        const int kh = p >> 3, j = p & 7;
+        uint32_t q;
+        float a, b;
+        if constexpr (IS_Q6) {
+            constexpr uint32_t t4 = 4u * (CQ & 1);
+            const int li = 8 * kh + j;
+            q = ((r.ql[li >> 2][li & 3] >> t4) & 0x0F0F0F0Fu) |
+                (((r.qh[j >> 2][j & 3] >> (t4 + 2u * (uint32_t)kh)) & 0x03030303u) << 4);
+            a = ps[2 * kh + (j >> 2)];
+            b = 32.0f * a;
+        } else {
+            q = r.q[j >> 2][j & 3] & (kh ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+            a = pa[kh];
+            b = pb[kh];
+        }
+        // opaque to the optimiser: otherwise it folds the mask into per-byte
+        // bit-field extracts instead of one v_cvt_f32_ubyteN per weight
+        asm("" : "+v"(q));
+        put4(wout, j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b, a * byte_f(q, 3) - b);
+        if (p & 1)
+            *reinterpret_cast<f16x8*>(&lds_b[buf][tid * kLdsStride + 8 * (p >> 1)]) = wout;
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int fa = (128 * wm + (lane & 31)) * kLdsStride + 8 * h;
+    const int fb = (128 * wn + (lane & 31)) * kLdsStride + 8 * h;
+    f16x8 af[2][4], bf[2][4];
+    auto frag_ld = [&](int buf, int step, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            af[slot][i] = *reinterpret_cast<const f16x8*>(&lds_a[buf][fa + 32 * i * kLdsStride + 16 * step]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bf[slot][j] = *reinterpret_cast<const f16x8*>(&lds_b[buf][fb + 32 * j * kLdsStride + 16 * step]);
+    };
+
+    // Iteration I of the 8-chunk group at c8: 64 slots separated by
+    // scheduling fences, slot t = 16 step + 4 i + j issuing MFMA (i, j)
+    // of k16 step `step` plus one slice of side work for chunk c + 1 (B
+    // dequantisation into LDS, A store) or c + 2 (weight loads).  The one
+    // barrier per chunk sits before step 3: by then every wave has written
+    // its share of chunk c + 1 and issued its last read of chunk c's
+    // buffers (step 3's fragments are read during step 2), so step 0 of
+    // chunk c + 1 is read during step 3 and the next iteration starts with
+    // its operands in registers.
+    auto iteration = [&](auto it, int c8) {
+        constexpr int I = decltype(it)::value;
+        constexpr int P = I & 1;
+        using CQN = std::integral_constant<int, (I + 1) & 3>;
+        using CQ2 = std::integral_constant<int, (I + 2) & 3>;
+        const int c = c8 + I;
+#pragma unroll
+        for (int step = 0; step < 4; ++step)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 16 * step + 4 * i + j;
+                    if (t == BAR) lds_barrier();
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[step & 1][i], bf[step & 1][j], acc[i][j],
+                                                                       0, 0, 0);
+                    if (t % 16 == 1 && step < 3) frag_ld(P, step + 1, (step + 1) & 1);
+                    if (t == BAR + 1) frag_ld(P ^ 1, 0, 0);
+                    if (t == 1) w_prep(CQN{}, wr[P ^ 1]);
+                    if (t >= 2 && t < 18) w_piece(CQN{}, wr[P ^ 1], P ^ 1, t - 2);
+                    if (t == WLD) w_ld(CQ2{}, wr[P], c + 2);
+                    if (t >= A0 && t < A0 + A_F4) {
+                        a_st(a_reg[t - A0], P ^ 1, t - A0);
+                        a_reg[t - A0] = a_ld(c + 2, t - A0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+    };
+
+    w_ld(std::integral_constant<int, 0>{}, wr[0], c_begin);
+    w_ld(std::integral_constant<int, 1>{}, wr[1], c_begin + 1);
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) a_reg[i] = a_ld(c_begin, i);
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+        a_st(a_reg[i], 0, i);
+        a_reg[i] = a_ld(c_begin + 1, i);
+    }
+    w_prep(std::integral_constant<int, 0>{}, wr[0]);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) w_piece(std::integral_constant<int, 0>{}, wr[0], 0, p);
+    lds_barrier();
+    frag_ld(0, 0, 0);
+
+    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
+        iteration(std::integral_constant<int, 0>{}, c8);
+        iteration(std::integral_constant<int, 1>{}, c8);
+        iteration(std::integral_constant<int, 2>{}, c8);
+        iteration(std::integral_constant<int, 3>{}, c8);
+        iteration(std::integral_constant<int, 4>{}, c8);
+        iteration(std::integral_constant<int, 5>{}, c8);
+        iteration(std::integral_constant<int, 6>{}, c8);
+        iteration(std::integral_constant<int, 7>{}, c8);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = n0 + 128 * wn + 32 * j + (lane & 31);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + 128 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if constexpr (SPLIT)
                     unsafeAtomicAdd(&D[(size_t)row * N + col], acc[i][j][e]);
                 else
@@ -1221,7 +1518,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     }
     // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
     const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
-    const bool v7 = v5 && gemm_kernel_version() == 0;
+    const bool v7 = v5 && (gemm_kernel_version() == 0 || gemm_kernel_version() == 7);
     if (s > 1) {
         const size_t n4 = (size_t)M * N / 4;
         hipLaunchKernelGGL(rf_fill_zero_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 2048)), dim3(256), 0,
@@ -1248,11 +1545,24 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     }
 }
 
+// 256 x 256 tiles without a K split; the caller checks that they fill the
+// CUs (split-K adds float atomics on M x N outputs, which cost more than
+// the tile shape saves).
+template <bool IS_Q6>
+static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st) {
+    const int tiles = (M / kSqTile) * (N / kSqTile);
+    hipLaunchKernelGGL((rf_gemm_qk_sq_kernel<IS_Q6, false>), dim3(tiles), dim3(kSqThreads), 0, st, A, w, D, M, N, K,
+                       tiles, K / kKC);
+}
+
 template <bool IS_Q6>
 static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     if (N % 256 == 0 && K % 512 == 0 && gemm_kernel_version() != 1) {
-        if (M % 128 == 0)
+        const long sq_tiles = (long)(M / kSqTile) * (N / kSqTile);
+        if (M % kSqTile == 0 && gemm_kernel_version() == 0 && 8 * sq_tiles >= 7L * device_cu_count())
+            launch_sq<IS_Q6>(A, w, D, M, N, K, st);
+        else if (M % 128 == 0)
             launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
         else
             launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st);

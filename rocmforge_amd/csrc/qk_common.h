@@ -31,6 +31,14 @@ struct __attribute__((packed, aligned(2))) Un16 { u32x4 v; };
 struct __attribute__((packed, aligned(2))) Un8 { u32x2 v; };
 struct __attribute__((packed, aligned(2))) Un4 { uint32_t v; };
 
+// Buffer resource over [p, p + 4 GiB): raw buffer loads through it take a
+// vector byte offset and a scalar byte offset (no per-lane 64-bit address
+// arithmetic).  Word 3 is the gfx9 family's raw-buffer format (data format
+// 32, no swizzle); no bounds checking is relied on.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
     return reinterpret_cast<const Un16*>(p)->v;
 }
@@ -358,7 +366,9 @@ int gemv_waves_per_wg(int dflt);
 int gemv_q6_variant();
 // GEMM kernel selection for tuning comparisons: RF_GEMM_V=1 forces the
 // general 2x2-wave kernel, =4 the register-weight kernel, =5 the 8-wave
-// ring kernel; default (0) picks the one-wave-per-SIMD ring kernel (v7).
+// ring kernel, =7 the one-wave-per-SIMD ring kernel (v7) for every shape;
+// default (0) picks v7, or the 256 x 256 shared-dequantisation kernel where
+// its tiles fill the CUs without a K split.
 int gemm_kernel_version();
 
 }  // namespace rf

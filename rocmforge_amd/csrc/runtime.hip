@@ -63,7 +63,7 @@ int gemm_kernel_version() {
     if (v < 0) {
         const char* e = getenv("RF_GEMM_V");
         const int n = e ? atoi(e) : 0;
-        v = (n == 1 || n == 4 || n == 5) ? n : 0;
+        v = (n == 1 || n == 4 || n == 5 || n == 7) ? n : 0;
     }
     return v;
 }
