@@ -147,12 +147,15 @@ def bench_decode(lib, torch, steps, warmup):
 
 
 # the full decode weight stream of a Llama-3.1-8B-shaped
-# stack at batch 1 -- per layer the QKV GEMV (Q4_K 6144x4096, Q8-inline), the
-# O projection with the residual add fused (Q4_K 4096x4096), the fused
-# gate+up+SwiGLU (2 x Q4_K 14336x4096) and ffn_down (Q6_K 4096x14336); then
-# the Q6_K lm_head (128256x4096).  Attention, norms and RoPE are not part of
-# the path: the O projection reads the first 4096 QKV outputs in their place.
-L_LAYERS, QKV_N, VOCAB = 32, 6144, 128256
+# stack at batch 1 -- per layer the QKV projection (Q4_K, 4096 + 1024 + 1024
+# rows x 4096, one fused Q8-inline launch over the three tensors), the O
+# projection with the residual add fused (Q4_K 4096x4096), the fused
+# gate+up+SwiGLU (2 x Q4_K 14336x4096) and ffn_down with the residual add
+# fused (Q6_K 4096x14336); then the Q6_K lm_head (128256x4096).  Attention,
+# norms and RoPE are not part of the path: the O projection reads the Q
+# output in place of the attention output.
+L_LAYERS, Q_N, KV_N, VOCAB = 32, 4096, 1024, 128256
+QKV_N = Q_N + 2 * KV_N
 STREAM_WEIGHT_BYTES = (L_LAYERS * (QKV_N * (K_FFN // 256) * Q4K_BYTES + K_FFN * (K_FFN // 256) * Q4K_BYTES
                                    + 2 * N_FFN * (K_FFN // 256) * Q4K_BYTES + K_FFN * (N_FFN // 256) * Q6K_BYTES)
                        + VOCAB * (K_FFN // 256) * Q6K_BYTES)   # 4,841,250,816
@@ -164,7 +167,9 @@ def bench_decode_stream(lib, torch, tokens):
     dev = torch.device("cuda:0")
     layers = []
     for l in range(L_LAYERS):
-        layers.append((synth.torch_weights("q4_k", QKV_N, K_FFN, seed=1000 + 5 * l, device=dev),
+        # Q, K, V as the three separate GGUF tensors (4096 + 1024 + 1024 rows)
+        layers.append(([synth.torch_weights("q4_k", n, K_FFN, seed=1000 + 5 * l + 7919 * i, device=dev)
+                        for i, n in enumerate((Q_N, KV_N, KV_N))],
                        synth.torch_weights("q4_k", K_FFN, K_FFN, seed=1001 + 5 * l, device=dev),
                        synth.torch_weights("q4_k", N_FFN, K_FFN, seed=1002 + 5 * l, device=dev),
                        synth.torch_weights("q4_k", N_FFN, K_FFN, seed=1003 + 5 * l, device=dev),
@@ -174,19 +179,21 @@ def bench_decode_stream(lib, torch, tokens):
     g.manual_seed(1)
     x = torch.randn(K_FFN, device=dev, generator=g)
     hidden = torch.randn(K_FFN, device=dev, generator=g)
-    qkv = torch.empty(QKV_N, device=dev)
+    q, k, v = torch.empty(Q_N, device=dev), torch.empty(KV_N, device=dev), torch.empty(KV_N, device=dev)
     ffn = torch.empty(N_FFN, device=dev)
     logits = torch.empty(VOCAB, device=dev)
 
     def token(st):
         rc = 0
         for wqkv, wo, wg, wu, wd in layers:
-            rc |= lib.gemv_q4_k_f32_q8_inline_launch(vp(wqkv), vp(x), vp(qkv), K_FFN, QKV_N, st)
-            rc |= lib.gemv_q4_k_f32_q8_inline_residual_launch(vp(wo), vp(qkv), vp(hidden), vp(hidden), K_FFN, K_FFN,
+            wq, wk, wv = wqkv
+            rc |= lib.gemv_qkv_q4_k_f32_q8_inline_launch(vp(wq), vp(wk), vp(wv), None, None, None, vp(x), vp(q),
+                                                         vp(k), vp(v), K_FFN, Q_N, KV_N, st)
+            rc |= lib.gemv_q4_k_f32_q8_inline_residual_launch(vp(wo), vp(q), vp(hidden), vp(hidden), K_FFN, K_FFN,
                                                               st)
             rc |= lib.gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch(vp(wg), vp(wu), vp(hidden), vp(ffn), K_FFN, N_FFN,
                                                                     st)
-            rc |= lib.gemv_q6_k_f32_launch(vp(wd), vp(ffn), vp(x), N_FFN, K_FFN, st)
+            rc |= lib.gemv_q6_k_f32_residual_launch(vp(wd), vp(ffn), vp(hidden), vp(x), N_FFN, K_FFN, st)
         rc |= lib.gemv_q6_k_f32_launch(vp(lm_head), vp(x), vp(logits), K_FFN, VOCAB, st)
         if rc:
             raise RuntimeError(f"decode stream launch failed: hipError {rc}")
@@ -212,8 +219,9 @@ def bench_decode_stream(lib, torch, tokens):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / tokens
     gbs = STREAM_WEIGHT_BYTES / (ms * 1e-3) / 1e9
-    return {"workload": "BASELINE config 2: 32 x (QKV 6144x4096 Q4_K, O 4096x4096 Q4_K + residual, "
-                        "gate+up 2x14336x4096 Q4_K, down 4096x14336 Q6_K) + lm_head 128256x4096 Q6_K, batch 1",
+    return {"workload": "BASELINE config 2: 32 x (QKV 6144x4096 Q4_K as one fused launch over the 4096/1024/1024-row "
+                        "Q, K, V tensors, O 4096x4096 Q4_K + residual, gate+up 2x14336x4096 Q4_K, "
+                        "down 4096x14336 Q6_K + residual) + lm_head 128256x4096 Q6_K, batch 1",
             "launches_per_token": 4 * L_LAYERS + 1, "weight_bytes_per_token": STREAM_WEIGHT_BYTES,
             "tokens": tokens, "ms_per_token": round(ms, 4), "gbs": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}

@@ -53,6 +53,18 @@ hipError_t gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch(const void* weights_gat
                                                          float* swiglu_out, int n_rows, int ncols_dst,
                                                          hipStream_t stream);
 
+/* Fused Q/K/V projection over three Q4_K matrices sharing one quantised
+ * activation vector: out_q[i] = Wq[i,:]·x + bias_q[i] (i < n_q), likewise
+ * out_k / out_v over n_kv rows; each bias may be null.  No Q4_K counterpart
+ * in the reference (its Q4_K_M attention input is three GEMV launches,
+ * src/gpu/ops.rs:851-853); signature and bias semantics follow its Q4_0
+ * fused launcher gemv_qkv_q4_0_f32_launch (hip_kernels/quant/
+ * q4_0_fused.hip:674).  Same K limits and alignment as the launcher above. */
+hipError_t gemv_qkv_q4_k_f32_q8_inline_launch(const void* w_q, const void* w_k, const void* w_v,
+                                              const float* bias_q, const float* bias_k, const float* bias_v,
+                                              const float* input, float* out_q, float* out_k, float* out_v,
+                                              int n_rows, int n_q, int n_kv, hipStream_t stream);
+
 /* ---- Q4_K decode GEMV, fp32 activations (fallback family) --------------
  * hip_kernels/quant/q4_k_gemv.hip:517 / :548 / :480 -- same outputs as the
  * three launchers above but with fp32 x (no activation quantisation); no
@@ -70,6 +82,14 @@ hipError_t gemv_gate_up_swiglu_q4_k_f32_launch(const void* weights_gate_q4_k, co
  * wrapper gemv_q6_k_f32_on_stream quant.rs:3737). */
 hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float* input, float* output, int n_rows,
                                 int ncols_dst, hipStream_t stream);
+
+/* output[n] = y[n] + residual[n] for the Q6_K GEMV above; output may alias
+ * residual.  No counterpart in the reference (its Q6_K ffn_down runs a GEMV
+ * and a separate add: gpu_dispatch_gemv_residual_on_stream returns
+ * Ok(false) for Q6_K, src/gpu/ops.rs:666-695); arguments and checks follow
+ * gemv_q4_k_f32_q8_inline_residual_launch. */
+hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* input, const float* residual,
+                                         float* output, int n_rows, int ncols_dst, hipStream_t stream);
 
 /* ---- Prefill GEMM, dequant-in-register, fp16 MFMA, fp32 accumulate ------
  * hip_kernels/wmma/wmma_gemm_q4_k.hip:506 and wmma_gemm_q6_k.hip:212 (Rust

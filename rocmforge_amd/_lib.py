@@ -22,7 +22,9 @@ SIGNATURES = {
     "gemv_q4_k_f32_launch": [_vp, _vp, _vp, _i, _i, _vp],
     "gemv_q4_k_f32_residual_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
     "gemv_gate_up_swiglu_q4_k_f32_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
+    "gemv_qkv_q4_k_f32_q8_inline_launch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "gemv_q6_k_f32_launch": [_vp, _vp, _vp, _i, _i, _vp],
+    "gemv_q6_k_f32_residual_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
     "wmma_gemm_q4_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "wmma_gemm_q6_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],

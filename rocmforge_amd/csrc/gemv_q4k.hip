@@ -31,7 +31,17 @@ constexpr int kThreads = 256;
 constexpr int kWavesPerWg = kThreads / kWave;
 constexpr int kSbPerStep = 16;  // super-blocks per wave row step
 
-enum Q4Mode { kPlain = 0, kResidual = 1, kGateUp = 2 };
+enum Q4Mode { kPlain = 0, kResidual = 1, kGateUp = 2, kQkv = 3 };
+
+// kQkv: three matrices (Q, K, V projections) as one row space of
+// n_q + 2 n_kv rows -- rows [0, n_q) of w[0], then n_kv of w[1], then n_kv
+// of w[2] -- each output row optionally plus its bias.
+struct QkvArgs {
+    const uint8_t* w[3];
+    const float* bias[3];
+    float* y[3];
+    int n_q, n_kv;
+};
 
 // Q8-inline LDS rule of the reference launchers (q4_k_q8_inline.hip:374-378):
 // (K/32) * 34 bytes <= 32 KB.  Kept so callers see identical validation.
@@ -66,7 +76,8 @@ template <int MODE, int R, int NW, int NB>
 __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
                                                                    const uint8_t* __restrict__ w1,
                                                                    const float* __restrict__ x,
-                                                                   const float* residual, float* y, int K, int N) {
+                                                                   const float* residual, float* y, int K, int N,
+                                                                   QkvArgs qkv) {
     extern __shared__ __align__(16) uint8_t smem[];
     const Q8Lds q8 = q8_lds_carve(smem, K);
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
@@ -94,9 +105,18 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
         const int sb = min((i % spr) * kSbPerStep + s, nsb - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t off = (size_t)row_of((i / spr) * R + r) * row_bytes + (size_t)sb * kQ4KBytes;
-            u[0][r] = q4k_load_unit(w0 + off, p);
-            if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
+            const int row = row_of((i / spr) * R + r);
+            if constexpr (MODE == kQkv) {
+                // wave-uniform: the matrix select stays in scalar registers
+                const int m = row < qkv.n_q ? 0 : (row < qkv.n_q + qkv.n_kv ? 1 : 2);
+                const int local = row - (m == 0 ? 0 : qkv.n_q + (m - 1) * qkv.n_kv);
+                const uint8_t* base = m == 0 ? qkv.w[0] : (m == 1 ? qkv.w[1] : qkv.w[2]);
+                u[0][r] = q4k_load_unit(base + (size_t)local * row_bytes + (size_t)sb * kQ4KBytes, p);
+            } else {
+                const size_t off = (size_t)row * row_bytes + (size_t)sb * kQ4KBytes;
+                u[0][r] = q4k_load_unit(w0 + off, p);
+                if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
+            }
         }
     };
     float acc[M][R];
@@ -164,6 +184,12 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
             y[row] = g;
         } else if (MODE == kResidual) {
             y[row] = g + residual[row];
+        } else if (MODE == kQkv) {
+            const int m = row < qkv.n_q ? 0 : (row < qkv.n_q + qkv.n_kv ? 1 : 2);
+            const int local = row - (m == 0 ? 0 : qkv.n_q + (m - 1) * qkv.n_kv);
+            const float* b = m == 0 ? qkv.bias[0] : (m == 1 ? qkv.bias[1] : qkv.bias[2]);
+            float* o = m == 0 ? qkv.y[0] : (m == 1 ? qkv.y[1] : qkv.y[2]);
+            o[local] = g + (b ? b[local] : 0.0f);
         } else {
             y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
         }
@@ -275,7 +301,7 @@ static inline int gemv_grid(int N, int min_rows) {
 
 template <int MODE>
 static hipError_t launch_q8(const void* w0, const void* w1, const float* x, const float* res, float* y, int K, int N,
-                            hipStream_t st) {
+                            hipStream_t st, const QkvArgs& qkv = QkvArgs{}) {
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
     const int r = gemv_rows_per_step();
     const int nw = (r == 1) ? gemv_waves_per_wg(4) : 4;
@@ -288,15 +314,15 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     const uint8_t* b = static_cast<const uint8_t*>(w1);
     const size_t lds = q8_lds_bytes(K) + out_bytes;
     if (r == 1 && nw == 16)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 16, RF_NB>), dim3(grid), dim3(16 * 64), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 16, RF_NB>), dim3(grid), dim3(16 * 64), lds, st, a, b, x, res, y, K, N, qkv);
     else if (r == 1 && nw == 8)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 8, RF_NB>), dim3(grid), dim3(8 * 64), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 8, RF_NB>), dim3(grid), dim3(8 * 64), lds, st, a, b, x, res, y, K, N, qkv);
     else if (r == 1)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 4, RF_NB>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 4, RF_NB>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N, qkv);
     else if (r == 4 && MODE != kGateUp)
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N, qkv);
     else
-        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N);
+        hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2, 4, 3>), dim3(grid), dim3(4 * 64), lds, st, a, b, x, res, y, K, N, qkv);
     return hipGetLastError();
 }
 
@@ -408,6 +434,37 @@ extern "C" hipError_t gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch(const void* 
     if (!aligned16(weights_gate_q4_k) || !aligned16(weights_up_q4_k)) return hipErrorInvalidValue;
     return launch_q8<kGateUp>(weights_gate_q4_k, weights_up_q4_k, input, nullptr, swiglu_out, n_rows, ncols_dst,
                               stream);
+}
+
+// Fused Q/K/V projection: one launch over the three Q4_K matrices with the
+// Q8 activations quantised once.  No counterpart for Q4_K in the reference:
+// its Q4_K_M attention input takes three GEMV launches (ops.rs:851-853).
+// The signature, bias handling (out = dot + bias, bias optional) and size
+// arguments follow its Q4_0 fused QKV launcher (q4_0_fused.hip:674-680, :80-86).
+extern "C" hipError_t gemv_qkv_q4_k_f32_q8_inline_launch(const void* w_q, const void* w_k, const void* w_v,
+                                                         const float* bias_q, const float* bias_k, const float* bias_v,
+                                                         const float* input, float* out_q, float* out_k, float* out_v,
+                                                         int n_rows, int n_q, int n_kv, hipStream_t stream) {
+    if (n_rows <= 0 || n_q <= 0 || n_kv <= 0) return hipErrorInvalidValue;
+    if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
+    if (w_q == nullptr || w_k == nullptr || w_v == nullptr) return hipErrorInvalidValue;
+    if (out_q == nullptr || out_k == nullptr || out_v == nullptr) return hipErrorInvalidValue;
+    if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v)) return hipErrorInvalidValue;
+    if ((long)n_q + 2L * n_kv > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    QkvArgs a;
+    a.w[0] = static_cast<const uint8_t*>(w_q);
+    a.w[1] = static_cast<const uint8_t*>(w_k);
+    a.w[2] = static_cast<const uint8_t*>(w_v);
+    a.bias[0] = bias_q;
+    a.bias[1] = bias_k;
+    a.bias[2] = bias_v;
+    a.y[0] = out_q;
+    a.y[1] = out_k;
+    a.y[2] = out_v;
+    a.n_q = n_q;
+    a.n_kv = n_kv;
+    return launch_q8<kQkv>(w_q, nullptr, input, nullptr, nullptr, n_rows, n_q + 2 * n_kv, stream, a);
 }
 
 extern "C" hipError_t gemv_q4_k_f32_launch(const void* weights_q4_k, const float* input, float* output, int n_rows,

@@ -119,8 +119,8 @@ __device__ __forceinline__ void q6_xsum16(const float* xs, int K, float* xsum16)
 
 template <int R, bool LDS, int NW, int NB>
 __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_kernel(const uint8_t* __restrict__ w,
-                                                                  const float* __restrict__ x, float* __restrict__ y,
-                                                                  int K, int N) {
+                                                                  const float* __restrict__ x, const float* residual,
+                                                                  float* y, int K, int N) {
     extern __shared__ __align__(16) uint8_t smem[];
     float* xs = reinterpret_cast<float*>(smem);
     const int lane = threadIdx.x & (kWave - 1);
@@ -188,7 +188,8 @@ __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_kernel(const uint8_t* __r
                           q6_xsum16<LDS>(xv, K, xsum16);
                           __syncthreads();
                       });
-    for (int j = lane; j < row_end - row_begin; j += kWave) y[row_begin + j] = out_lds[j];
+    for (int j = lane; j < row_end - row_begin; j += kWave)
+        y[row_begin + j] = out_lds[j] + (residual ? residual[row_begin + j] : 0.0f);
 }
 
 // ── K-split Q6_K GEMV with x held in registers (main path) ───────────────
@@ -238,8 +239,8 @@ __device__ __forceinline__ float q6_dot16(const uint32_t v[4], const float* xv) 
 
 template <int NB>
 __global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __restrict__ w,
-                                                                const float* __restrict__ x,
-                                                                float* __restrict__ y, int K, int N) {
+                                                                const float* __restrict__ x, const float* residual,
+                                                                float* y, int K, int N) {
     extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK]
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __
     for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
         float t = 0.0f;
         for (int k = 0; k < nwk; ++k) t += part[j * nwk + k];
-        y[g + j * G] = t;
+        y[g + j * G] = t + (residual ? residual[g + j * G] : 0.0f);
     }
 }
 
@@ -339,8 +340,8 @@ struct Q6Seg {
 
 template <int NB>
 __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __restrict__ w,
-                                                               const float* __restrict__ x,
-                                                               float* __restrict__ y, int K, int N) {
+                                                               const float* __restrict__ x, const float* residual,
+                                                               float* y, int K, int N) {
     __shared__ __align__(16) uint8_t stage_lds[8 * 2048];
     extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK]
     const int lane = threadIdx.x & (kWave - 1);
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
     for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
         float t = 0.0f;
         for (int k = 0; k < nwk; ++k) t += part[j * nwk + k];
-        y[g + j * G] = t;
+        y[g + j * G] = t + (residual ? residual[g + j * G] : 0.0f);
     }
 }
 
@@ -445,11 +446,8 @@ using namespace rf;
 
 // Validation as q6_k_gemv.hip:284-285 (K > 0, N > 0, K % 256 == 0), plus
 // 2-byte weight alignment (the fp16 d field is read as one 16-bit word).
-extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float* input, float* output, int n_rows,
-                                           int ncols_dst, hipStream_t stream) {
-    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
-    if (n_rows % kQK != 0) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
+static hipError_t launch_q6(const void* weights_q6_k, const float* input, const float* residual, float* output,
+                            int n_rows, int ncols_dst, hipStream_t stream) {
     const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
     const int nsb = n_rows / kQK;
     if (gemv_q6_variant() == 0 && nsb <= 64 && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0) {
@@ -459,7 +457,7 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
         if (lds <= 64 * 1024) {
             hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
-                               output, n_rows, ncols_dst);
+                               residual, output, n_rows, ncols_dst);
             return hipGetLastError();
         }
     }
@@ -472,7 +470,7 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
         if (lds <= 64 * 1024) {
             hipLaunchKernelGGL((rf_q6k_gemv_xreg_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
-                               output, n_rows, ncols_dst);
+                               residual, output, n_rows, ncols_dst);
             return hipGetLastError();
         }
     }
@@ -488,8 +486,8 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     if (out_bytes > 64 * 1024) return hipErrorInvalidValue;
     const dim3 blk(nw * 64);
 #define RF_Q6_LAUNCH(RR, L, W) \
-    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, 3>), dim3(grid), blk, lds + out_bytes, stream, w, input, output, \
-                       n_rows, ncols_dst)
+    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, 3>), dim3(grid), blk, lds + out_bytes, stream, w, input, \
+                       residual, output, n_rows, ncols_dst)
     if (r >= 2) {
         if (in_lds) RF_Q6_LAUNCH(2, true, 4); else RF_Q6_LAUNCH(2, false, 4);
     } else if (nw == 16) {
@@ -501,4 +499,26 @@ extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float
     }
 #undef RF_Q6_LAUNCH
     return hipGetLastError();
+}
+
+extern "C" hipError_t gemv_q6_k_f32_launch(const void* weights_q6_k, const float* input, float* output, int n_rows,
+                                           int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
+    if (n_rows % kQK != 0) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
+    return launch_q6(weights_q6_k, input, nullptr, output, n_rows, ncols_dst, stream);
+}
+
+// output[n] = y[n] + residual[n], output may alias residual.  No
+// counterpart in the reference, whose Q6_K ffn_down takes a GEMV and a
+// separate add (gpu_dispatch_gemv_residual_on_stream returns Ok(false) for
+// Q6_K, ops.rs:666-695); the argument order and checks follow the Q4_K
+// residual launcher (q4_k_q8_inline.hip:404-415).
+extern "C" hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* input,
+                                                    const float* residual, float* output, int n_rows, int ncols_dst,
+                                                    hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || residual == nullptr) return hipErrorInvalidValue;
+    if (n_rows % kQK != 0) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
+    return launch_q6(weights_q6_k, input, residual, output, n_rows, ncols_dst, stream);
 }

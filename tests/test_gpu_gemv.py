@@ -85,6 +85,30 @@ def test_q4k_q8_inline_residual_in_place(rf, dev, k, n):
     _check(G.host(dr), O.gemv_q4k_q8(w, x, k, n) + r.astype(np.float64), f"q8 residual {n}x{k}")
 
 
+@pytest.mark.parametrize("k,nq,nkv,bias", [(4096, 4096, 1024, False), (4096, 4096, 1024, True),
+                                           (512, 96, 32, True), (256, 7, 3, False)])
+def test_q4k_q8_fused_qkv(rf, dev, k, nq, nkv, bias):
+    # one launch over three matrices == three single-matrix launches (+ bias
+    # in fp32), bit for bit, and the oracle within tolerance
+    ws = [synth.q4_k_weights(n, k, seed=40 + i) for i, n in enumerate((nq, nkv, nkv))]
+    bs = [synth.activations(n, seed=50 + i) if bias else None for i, n in enumerate((nq, nkv, nkv))]
+    x = synth.activations(k, seed=60)
+    dws = [G.to_dev(w) for w in ws]
+    dbs = [G.to_dev(b) if b is not None else None for b in bs]
+    dx = G.to_dev(x)
+    outs = [G.empty(n, torch.float32) for n in (nq, nkv, nkv)]
+    G.call(rf.gemv_qkv_q4_k_f32_q8_inline_launch, *[G.ptr(d) for d in dws],
+           *[G.ptr(d) if d is not None else None for d in dbs], G.ptr(dx), *[G.ptr(o) for o in outs], k, nq, nkv)
+    for i, n in enumerate((nq, nkv, nkv)):
+        single = G.empty(n, torch.float32)
+        G.call(rf.gemv_q4_k_f32_q8_inline_launch, G.ptr(dws[i]), G.ptr(dx), G.ptr(single), k, n)
+        expect = G.host(single) + (bs[i] if bias else np.float32(0))
+        got = G.host(outs[i])
+        assert np.array_equal(got, expect.astype(np.float32)), f"qkv matrix {i}"
+        ref = O.gemv_q4k_q8(ws[i], x, k, n) + (bs[i].astype(np.float64) if bias else 0.0)
+        _check(got, ref, f"qkv {i} {n}x{k}")
+
+
 @pytest.mark.parametrize("k,n", [(4096, 14336), (256, 50), (14336, 64)])
 def test_q4k_q8_gate_up_swiglu(rf, dev, k, n):
     wg = synth.q4_k_weights(n, k, seed=11)
@@ -122,6 +146,22 @@ def test_q6k_gemv(rf, dev, k, n):
     y = G.empty(n, torch.float32)
     G.call(rf.gemv_q6_k_f32_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
     _check(G.host(y), O.gemv_q6k(w, x, k, n), f"q6 gemv {n}x{k}")
+
+
+@pytest.mark.parametrize("k,n", [(14336, 4096), (768, 64), (40960, 16)])
+def test_q6k_gemv_residual_in_place(rf, dev, k, n):
+    # one path per Q6_K kernel (lane-linear, register, row-step); output
+    # aliases residual; equal bit for bit to the GEMV plus an fp32 add
+    w = synth.q6_k_weights(n, k, seed=71)
+    x = synth.activations(k, seed=72)
+    r = synth.activations(n, seed=73) * 10
+    dw, dx, dr = G.to_dev(w), G.to_dev(x), G.to_dev(r)
+    y = G.empty(n, torch.float32)
+    G.call(rf.gemv_q6_k_f32_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    G.call(rf.gemv_q6_k_f32_residual_launch, G.ptr(dw), G.ptr(dx), G.ptr(dr), G.ptr(dr), k, n)
+    got = G.host(dr)
+    assert np.array_equal(got, G.host(y) + r)
+    _check(got, O.gemv_q6k(w, x, k, n) + r.astype(np.float64), f"q6 residual {n}x{k}")
 
 
 def test_q6k_unaligned_blocks(rf, dev):
