@@ -161,6 +161,19 @@ int rf_gpu_dispatch_fused_gate_up(const void* w_gate, const rf_weight_meta* gate
                                   const rf_weight_meta* up_meta, const float* input, float* output, size_t ff_size,
                                   size_t h, hipStream_t stream);
 
+/* gpu_dispatch_fused_qkv_on_stream (ops.rs:748): three Q4_K matrices with
+ * the Q8 fast path on and (h/32)*34 <= 32 KB -> one fused launch
+ * (gemv_qkv_q4_k_f32_q8_inline_launch, biases folded in; the reference
+ * fuses only Q4_0 here); otherwise, or on its error, three
+ * rf_gpu_dispatch_gemv calls (ops.rs:851-853) -- with a non-null bias that
+ * route returns RF_DISPATCH_NOT_IN_LIBRARY (its bias add is an elementwise
+ * kernel outside this library). */
+int rf_gpu_dispatch_fused_qkv(const void* w_q, const rf_weight_meta* q_meta, const float* q_bias, const void* w_k,
+                              const rf_weight_meta* k_meta, const float* k_bias, const void* w_v,
+                              const rf_weight_meta* v_meta, const float* v_bias, const float* input, float* out_q,
+                              float* out_k, float* out_v, size_t q_size, size_t kv_size, size_t h,
+                              hipStream_t stream);
+
 /* gpu_dispatch_gemm (ops.rs:1591), null stream as in the reference:
  * seq_len == 1 -> GEMV; Q4_K / Q6_K with out_dim % 64 == 0, in_dim % 256 == 0
  * -> WMMA-equivalent GEMM at padded_m = round_up(seq_len, 64) (input and
@@ -190,6 +203,9 @@ typedef struct rf_launchers {
     hipError_t (*gemv_q6_k_f32)(const void*, const float*, float*, int, int, hipStream_t);
     hipError_t (*wmma_gemm_q4_k)(const float*, const void*, float*, int, int, int, hipStream_t);
     hipError_t (*wmma_gemm_q6_k)(const float*, const void*, float*, int, int, int, hipStream_t);
+    hipError_t (*gemv_qkv_q4_k_q8_inline)(const void*, const void*, const void*, const float*, const float*,
+                                          const float*, const float*, float*, float*, float*, int, int, int,
+                                          hipStream_t);
 } rf_launchers;
 void rf_dispatch_set_launchers(const rf_launchers* table);
 

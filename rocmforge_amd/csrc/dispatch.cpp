@@ -5,6 +5,8 @@
 //   rf_gpu_dispatch_gemv_residual  <- gpu_dispatch_gemv_residual_on_stream (ops.rs:509)
 //   rf_gpu_dispatch_fused_gate_up  <- the Q4_K arm of
 //                                     gpu_dispatch_fused_gate_up_with_scratch_on_stream (ops.rs:1316-1355)
+//   rf_gpu_dispatch_fused_qkv      <- gpu_dispatch_fused_qkv_on_stream (ops.rs:748), with a Q4_K
+//                                     fused arm in place of its Q4_0 one
 //   rf_gpu_dispatch_gemm           <- gpu_dispatch_gemm (ops.rs:1591)
 // with the layout check validate_gemv_layout (ops.rs:82) and the runtime
 // flags of src/gpu/safety.rs (cached environment flags, refreshable).
@@ -80,6 +82,7 @@ rf_launchers g_default = {
     gemv_q6_k_f32_launch,
     wmma_gemm_q4_k_launch,
     wmma_gemm_q6_k_launch,
+    gemv_qkv_q4_k_f32_q8_inline_launch,
 };
 rf_launchers g_table = g_default;
 
@@ -185,6 +188,33 @@ int rf_gpu_dispatch_fused_gate_up(const void* w_gate, const rf_weight_meta* gate
             return RF_DISPATCH_OK;
     }
     return (int)g_table.gemv_gate_up_q4_k_f32(w_gate, w_up, input, output, k, n, stream);
+}
+
+int rf_gpu_dispatch_fused_qkv(const void* w_q, const rf_weight_meta* q_meta, const float* q_bias, const void* w_k,
+                              const rf_weight_meta* k_meta, const float* k_bias, const void* w_v,
+                              const rf_weight_meta* v_meta, const float* v_bias, const float* input, float* out_q,
+                              float* out_k, float* out_v, size_t q_size, size_t kv_size, size_t h,
+                              hipStream_t stream) {
+    if (q_meta == nullptr || k_meta == nullptr || v_meta == nullptr) return RF_DISPATCH_INVALID_LAYOUT;
+    if (!fits_int(q_size) || !fits_int(kv_size) || !fits_int(h) || !fits_int(q_size + 2 * kv_size))
+        return hipErrorInvalidValue;
+    // fused arm (the reference's is Q4_0-only, ops.rs:768-847; this library
+    // fuses Q4_K): all three Q4_K, Q8 fast path on, LDS image fits
+    if (q_meta->wtype == RF_GGML_Q4_K && k_meta->wtype == RF_GGML_Q4_K && v_meta->wtype == RF_GGML_Q4_K &&
+        q8_fastpath_enabled() && q4_k_q8_inline_fits(h) && layout_ok(q_meta, q_size, h) &&
+        layout_ok(k_meta, kv_size, h) && layout_ok(v_meta, kv_size, h)) {
+        if (g_table.gemv_qkv_q4_k_q8_inline(w_q, w_k, w_v, q_bias, k_bias, v_bias, input, out_q, out_k, out_v, (int)h,
+                                            (int)q_size, (int)kv_size, stream) == hipSuccess)
+            return RF_DISPATCH_OK;
+    }
+    // individual dispatches (ops.rs:851-853); the reference then adds the
+    // biases with an elementwise kernel that is not part of this library
+    if (q_bias != nullptr || k_bias != nullptr || v_bias != nullptr) return RF_DISPATCH_NOT_IN_LIBRARY;
+    int rc = rf_gpu_dispatch_gemv(w_q, q_meta, input, out_q, q_size, h, stream);
+    if (rc != RF_DISPATCH_OK) return rc;
+    rc = rf_gpu_dispatch_gemv(w_k, k_meta, input, out_k, kv_size, h, stream);
+    if (rc != RF_DISPATCH_OK) return rc;
+    return rf_gpu_dispatch_gemv(w_v, v_meta, input, out_v, kv_size, h, stream);
 }
 
 int rf_gpu_dispatch_gemm(const void* weights, const rf_weight_meta* meta, const float* input, float* output,

@@ -6,6 +6,7 @@ Function names, argument order and error behaviour follow ops.rs:
   gpu_dispatch_gemv / gpu_dispatch_gemv_on_stream      (ops.rs:455, :484)
   gpu_dispatch_gemv_residual_on_stream -> bool         (ops.rs:509)
   gpu_dispatch_fused_gate_up_on_stream (Q4_K arm)      (ops.rs:1441, :1316-1355)
+  gpu_dispatch_fused_qkv_on_stream (Q4_K fused arm)    (ops.rs:748, individual GEMVs :851-853)
   gpu_dispatch_gemm                                    (ops.rs:1591)
   refresh_runtime_env_flags                            (safety.rs:123)
 Errors map to the reference's GpuError variants: InvalidWeightLayout,
@@ -118,6 +119,8 @@ _SIGS = {
     "rf_gpu_dispatch_fused_gate_up": [_vp, ctypes.POINTER(_CMeta), _vp, ctypes.POINTER(_CMeta), _vp, _vp, _sz, _sz,
                                       _vp],
     "rf_gpu_dispatch_gemm": [_vp, ctypes.POINTER(_CMeta), _vp, _vp, _sz, _sz, _sz],
+    "rf_gpu_dispatch_fused_qkv": [_vp, ctypes.POINTER(_CMeta), _vp, _vp, ctypes.POINTER(_CMeta), _vp, _vp,
+                                  ctypes.POINTER(_CMeta), _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "rf_dispatch_parse_env_flag": [ctypes.c_char_p, _i],
 }
 
@@ -177,6 +180,18 @@ def gpu_dispatch_fused_gate_up_on_stream(w_gate, gate_meta: WeightMeta, w_up, up
     rc = _lib().rf_gpu_dispatch_fused_gate_up(_ptr(w_gate), ctypes.byref(g), _ptr(w_up), ctypes.byref(u),
                                               _ptr(input), _ptr(output), ff_size, h, _ptr(stream))
     _check(rc, "gpu_dispatch_fused_gate_up_on_stream", gate_meta)
+
+
+def gpu_dispatch_fused_qkv_on_stream(w_q, q_meta: WeightMeta, q_bias, w_k, k_meta: WeightMeta, k_bias, w_v,
+                                     v_meta: WeightMeta, v_bias, input, out_q, out_k, out_v, q_size: int,
+                                     kv_size: int, h: int, stream=None) -> None:
+    """Biases may be None.  Three Q4_K tensors go to one fused launch; other
+    type mixes to three GEMV dispatches (NotInLibrary if a bias is given)."""
+    q, k, v = _cmeta(q_meta), _cmeta(k_meta), _cmeta(v_meta)
+    rc = _lib().rf_gpu_dispatch_fused_qkv(_ptr(w_q), ctypes.byref(q), _ptr(q_bias), _ptr(w_k), ctypes.byref(k),
+                                          _ptr(k_bias), _ptr(w_v), ctypes.byref(v), _ptr(v_bias), _ptr(input),
+                                          _ptr(out_q), _ptr(out_k), _ptr(out_v), q_size, kv_size, h, _ptr(stream))
+    _check(rc, "gpu_dispatch_fused_qkv_on_stream", q_meta)
 
 
 def gpu_dispatch_gemm(weights, meta: WeightMeta, input, output, out_dim: int, in_dim: int, seq_len: int) -> None:

@@ -2,7 +2,7 @@
 CPU: recording stand-ins replace the launchers, so every arm of the routing
 restated from src/gpu/ops.rs runs without a GPU.  Expected call sequences
 come from ops.rs:387-446 (GEMV), :666-695 (residual), :1316-1355 (fused
-gate+up), :1591-1963 (GEMM) and safety.rs (flags)."""
+gate+up), :748-853 (fused QKV), :1591-1963 (GEMM) and safety.rs (flags)."""
 import ctypes
 import os
 
@@ -17,9 +17,11 @@ GEMV = ctypes.CFUNCTYPE(_i, _vp, _vp, _vp, _i, _i, _vp)
 RES = ctypes.CFUNCTYPE(_i, _vp, _vp, _vp, _vp, _i, _i, _vp)
 FUSED = ctypes.CFUNCTYPE(_i, _vp, _vp, _vp, _vp, _i, _i, _vp)
 GEMM = ctypes.CFUNCTYPE(_i, _vp, _vp, _vp, _i, _i, _i, _vp)
+QKV = ctypes.CFUNCTYPE(_i, *([_vp] * 10), _i, _i, _i, _vp)
 NAMES = [("gemv_q4_k_q8_inline", GEMV), ("gemv_q4_k_q8_inline_residual", RES), ("gemv_gate_up_q4_k_q8_inline", FUSED),
          ("gemv_q4_k_f32", GEMV), ("gemv_q4_k_f32_residual", RES), ("gemv_gate_up_q4_k_f32", FUSED),
-         ("gemv_q6_k_f32", GEMV), ("wmma_gemm_q4_k", GEMM), ("wmma_gemm_q6_k", GEMM)]
+         ("gemv_q6_k_f32", GEMV), ("wmma_gemm_q4_k", GEMM), ("wmma_gemm_q6_k", GEMM),
+         ("gemv_qkv_q4_k_q8_inline", QKV)]
 
 
 class Table(ctypes.Structure):
@@ -212,3 +214,36 @@ def test_gemm_wmma_failure_falls_through(rec):
     # shapes off the WMMA grid (N % 64 != 0) skip it
     ops.gpu_dispatch_gemm(W, WeightMeta(GgmlType.Q6_K, [4096, 96]), X, Y, 96, 4096, 4)
     assert rec.names() == ["gemv_q6_k_f32"] * 4
+
+
+WQ, WK, WV, BQ, OQ, OK, OV = 0x5000, 0x6000, 0x7000, 0x8000, 0x9000, 0xA000, 0xB000
+
+
+def test_fused_qkv_q4k_one_launch(rec):
+    ops.gpu_dispatch_fused_qkv_on_stream(WQ, q4k(4096, 4096), BQ, WK, q4k(1024, 4096), None, WV, q4k(1024, 4096),
+                                         None, X, OQ, OK, OV, 4096, 1024, 4096, 0x77)
+    assert rec.calls == [("gemv_qkv_q4_k_q8_inline", [WQ, WK, WV, BQ, 0, 0, X, OQ, OK, OV, 4096, 4096, 1024, 0x77])]
+
+
+def test_fused_qkv_mixed_types_individual_gemvs(rec):
+    # Q4_K_M keeps some attn_v tensors in Q6_K: three GEMV dispatches
+    q6 = WeightMeta(GgmlType.Q6_K, [4096, 1024])
+    ops.gpu_dispatch_fused_qkv_on_stream(WQ, q4k(4096, 4096), None, WK, q4k(1024, 4096), None, WV, q6, None, X, OQ,
+                                         OK, OV, 4096, 1024, 4096)
+    assert rec.names() == ["gemv_q4_k_q8_inline", "gemv_q4_k_q8_inline", "gemv_q6_k_f32"]
+    assert rec.calls[2][1] == [WV, X, OV, 4096, 1024, 0]
+
+
+def test_fused_qkv_falls_back_without_fast_path(rec):
+    setenv("ROCMFORGE_ENABLE_EXPERIMENTAL_Q8_ACTIVATION_FASTPATH", "0")
+    ops.gpu_dispatch_fused_qkv_on_stream(WQ, q4k(4096, 4096), None, WK, q4k(1024, 4096), None, WV, q4k(1024, 4096),
+                                         None, X, OQ, OK, OV, 4096, 1024, 4096)
+    assert rec.names() == ["gemv_q4_k_f32"] * 3
+
+
+def test_fused_qkv_bias_outside_fused_arm_not_in_library(rec):
+    rec.codes["gemv_qkv_q4_k_q8_inline"] = HIP_INVALID
+    with pytest.raises(ops.NotInLibrary):
+        ops.gpu_dispatch_fused_qkv_on_stream(WQ, q4k(4096, 4096), BQ, WK, q4k(1024, 4096), None, WV,
+                                             q4k(1024, 4096), None, X, OQ, OK, OV, 4096, 1024, 4096)
+    assert rec.names() == ["gemv_qkv_q4_k_q8_inline"]

@@ -36,6 +36,32 @@ def test_gemv_arms_match_direct_launch(rf, dev):
         np.testing.assert_array_equal(G.host(y0), G.host(y1))
 
 
+def test_fused_qkv_arm(rf, dev):
+    # all-Q4_K (one fused launch, bias folded in) and a Q6_K V (three GEMVs)
+    k, nq, nkv = 4096, 1024, 256
+    ws = [synth.q4_k_weights(n, k, seed=31 + i) for i, n in enumerate((nq, nkv, nkv))]
+    w6 = synth.q6_k_weights(nkv, k, seed=34)
+    bq = synth.activations(nq, seed=35)
+    x = synth.activations(k, seed=36)
+    dws, dw6, dbq, dx = [G.to_dev(w) for w in ws], G.to_dev(w6), G.to_dev(bq), G.to_dev(x)
+    outs = [G.empty(n, torch.float32) for n in (nq, nkv, nkv)]
+    metas = [WeightMeta(GgmlType.Q4_K, [k, n]) for n in (nq, nkv, nkv)]
+    print("[gpu] dispatch fused qkv, all Q4_K", flush=True)
+    ops.gpu_dispatch_fused_qkv_on_stream(dws[0], metas[0], dbq, dws[1], metas[1], None, dws[2], metas[2], None, dx,
+                                         outs[0], outs[1], outs[2], nq, nkv, k, G.stream())
+    torch.cuda.synchronize()
+    for i, n in enumerate((nq, nkv, nkv)):
+        ref = O.gemv_q4k_q8(ws[i], x, k, n) + (bq.astype(np.float64) if i == 0 else 0.0)
+        assert np.abs(G.host(outs[i]) - ref).max() / np.abs(ref).max() < 1e-5, i
+    print("[gpu] dispatch fused qkv, Q6_K V", flush=True)
+    ops.gpu_dispatch_fused_qkv_on_stream(dws[0], metas[0], None, dws[1], metas[1], None, dw6,
+                                         WeightMeta(GgmlType.Q6_K, [k, nkv]), None, dx, outs[0], outs[1], outs[2],
+                                         nq, nkv, k, G.stream())
+    torch.cuda.synchronize()
+    ref = O.gemv_q6k(w6, x, k, nkv)
+    assert np.abs(G.host(outs[2]) - ref).max() / np.abs(ref).max() < 1e-5
+
+
 def test_residual_and_fused_arms(rf, dev):
     k, n = 4096, 512
     wq = synth.q4_k_weights(n, k, seed=21)
