@@ -1562,7 +1562,11 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long sq_tiles = (long)(M / kSqTile) * (N / kSqTile);
         if (M % kSqTile == 0 && gemm_kernel_version() == 0 && 8 * sq_tiles >= 7L * device_cu_count())
             launch_sq<IS_Q6>(A, w, D, M, N, K, st);
-        else if (M % 128 == 0)
+        // 128-row tiles, except for Q4_K when they would need a K split
+        // (M = 128, 256 at N = 14336): 64-row tiles halve the split and
+        // its float atomics (measured 3-5 % faster; Q6_K's heavier
+        // dequantisation makes them slower there)
+        else if (M % 128 == 0 && (IS_Q6 || 8L * (M / 128) * (N / 256) >= 7L * device_cu_count()))
             launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
         else
             launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st);

@@ -62,14 +62,15 @@ def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
 
 # One case per launcher branch for N % 256 == 0, K % 512 == 0 (the tiled
 # kernels): 256 x 256 shared-dequantisation tiles (M % 256 == 0 and at least
-# 7/8 as many tiles as CUs), otherwise 128 x 256 (M % 128 == 0) or 64 x 256
-# ring tiles with split-K when the tiles leave CUs idle, and (Q6_K with
+# 7/8 as many tiles as CUs); otherwise ring tiles of 128 rows (Q6_K, or
+# Q4_K when they fill the CUs unsplit -- the M = 512 Llama case below) or
+# 64 rows, with split-K when the tiles leave CUs idle; and (Q6_K with
 # K % 2048 != 0) the register-weight kernel.
 @pytest.mark.parametrize("fmt,m,n,k", [
     ("q4_k", 64, 256, 512),      # ring, 64-row tiles, 1 split
     ("q4_k", 192, 256, 1024),    # ring, 64-row tiles, 2 splits
-    ("q4_k", 128, 512, 2048),    # ring, 128-row tiles, 4 splits
-    ("q4_k", 384, 512, 512),     # ring, 128-row tiles, 1 split
+    ("q4_k", 128, 512, 2048),    # ring, 64-row tiles, 4 splits
+    ("q4_k", 384, 512, 512),     # ring, 64-row tiles, 1 split
     ("q4_k", 2048, 8192, 512),   # 256 x 256 shared-dequantisation tiles (256 tiles)
     ("q6_k", 64, 256, 2048),     # ring, 64-row tiles, 4 splits
     ("q6_k", 256, 512, 4096),    # ring, 128-row tiles, 8 splits
