@@ -224,6 +224,14 @@ __device__ __forceinline__ Q6Lane q6k_load_lane(const uint8_t* blk, int p) {
     return u;
 }
 
+// (m & a) | (~m & b) in one v_bfi_b32 (the compiler forms and/or pairs
+// from the equivalent C expression)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(d) : "s"(m), "v"(a), "v"(b));
+    return d;
+}
+
 // 16 weights of one scale group (four dwords of 6-bit values) against 16 x.
 __device__ __forceinline__ float q6_dot16(const uint32_t v[4], const float* xv) {
     float t = 0.0f;
@@ -236,6 +244,7 @@ __device__ __forceinline__ float q6_dot16(const uint32_t v[4], const float* xv) 
     }
     return t;
 }
+
 
 template <int NB>
 __global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __restrict__ w,
@@ -394,18 +403,21 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
     const uint32_t s0sh = 8u * (uint32_t)((blkoff + j1) & 3), s1sh = 8u * (uint32_t)((blkoff + j1 + 4) & 3);
     const int dww = (blkoff + 208) >> 2;
     const uint32_t qsh = 2u * (uint32_t)hq;
-    auto field = [&](int w0) {
+    auto field = [&](int w0, uint32_t s) {
         uint32_t d[5];
 #pragma unroll
         for (int t = 0; t < 5; ++t) d[t] = st32[w0 + t];
-        return u32x4{__builtin_amdgcn_alignbit(d[1], d[0], sh), __builtin_amdgcn_alignbit(d[2], d[1], sh),
-                     __builtin_amdgcn_alignbit(d[3], d[2], sh), __builtin_amdgcn_alignbit(d[4], d[3], sh)};
+        return u32x4{__builtin_amdgcn_alignbit(d[1], d[0], s), __builtin_amdgcn_alignbit(d[2], d[1], s),
+                     __builtin_amdgcn_alignbit(d[3], d[2], s), __builtin_amdgcn_alignbit(d[4], d[3], s)};
     };
     auto process = [&](const Q6Seg& u, int j) {
         *reinterpret_cast<u32x4*>(stage + 16 * lane) = u.a;
         *reinterpret_cast<u32x4*>(stage + 16 * (64 + lane)) = u.b;
-        const u32x4 ql = field(qlw);
-        const u32x4 qh = field(qhw);
+        const u32x4 ql = field(qlw, sh);
+        // qh shifted right by a further 2 hq bits in the same funnel shift:
+        // only bits 0-1 and 4-5 of each byte are used below, so the bits
+        // pulled in from the next dword at the top do not matter
+        const u32x4 qh = field(qhw, sh + qsh);
         const float d = half_bits_to_float(st32[dww] >> sh);
         const float s0 = d * (float)(int8_t)((st32[s0w] >> s0sh) & 0xFFu);
         const float s1 = d * (float)(int8_t)((st32[s1w] >> s1sh) & 0xFFu);
@@ -414,8 +426,11 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
         uint32_t v0[4], v1[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            v0[t] = (L[t] & 0x0F0F0F0Fu) | (((Q[t] >> qsh) & 0x03030303u) << 4);
-            v1[t] = ((L[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> (qsh + 4)) & 0x03030303u) << 4);
+            // per byte: q0 = (l & 15) | (h & 3) << 4, q1 = (l >> 4) | ((h >> 4) & 3) << 4,
+            // as bit-field selects (v_bfi) of l and h with bits 2-3, 6-7 of h cleared
+            const uint32_t hm = Q[t] & 0x33333333u;
+            v0[t] = bfi(0x0F0F0F0Fu, L[t], hm << 4);
+            v1[t] = bfi(0x0F0F0F0Fu, L[t] >> 4, hm);
         }
         float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
         acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
