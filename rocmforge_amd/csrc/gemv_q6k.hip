@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NW * 64) void rf_q6k_gemv_kernel(const uint8_t* __r
         y[row_begin + j] = out_lds[j] + (residual ? residual[row_begin + j] : 0.0f);
 }
 
-// ── K-split Q6_K GEMV with x held in registers (main path) ───────────────
+// ── K-split Q6_K GEMV with x held in registers (other K <= 16384) ───────────────
 // A workgroup has one wave per 8-super-block slice of K (NWK = nsb/8
 // rounded up, at most 8 waves: K <= 16384).  The 8 lanes p = 0..7 of a
 // super-block sb = 8w + l/8 read its bytes with three 16-byte loads each,
@@ -489,7 +489,7 @@ static hipError_t launch_q6(const void* weights_q6_k, const float* input, const 
             return hipGetLastError();
         }
     }
-    const int r = gemv_rows_per_step();
+    const int r = gemv_rows_per_step(1);
     const int nw = (r == 1) ? gemv_waves_per_wg(8) : 4;
     const int need = (ncols_dst + nw - 1) / nw;
     const int cap = device_cu_count() * gemv_wg_per_cu(nw == 8 ? 1 : 2);

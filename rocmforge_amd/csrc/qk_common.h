@@ -358,9 +358,9 @@ int device_cu_count();
 // family passes its measured-best default; RF_GEMV_WG_PER_CU / RF_GEMV_NW
 // override them for tuning sweeps.
 int gemv_wg_per_cu(int dflt);
-// Rows per pipeline step of the register GEMV (default 1; RF_GEMV_R=2|4
-// for tuning sweeps).
-int gemv_rows_per_step();
+// Rows per pipeline step of the register GEMVs (each kernel family passes
+// its measured-best default; RF_GEMV_R=1|2|4 overrides it for tuning sweeps).
+int gemv_rows_per_step(int dflt);
 int gemv_waves_per_wg(int dflt);
 // Q6_K GEMV kernel family (0 = K-split register kernel, 1 = row-step kernel).
 int gemv_q6_variant();

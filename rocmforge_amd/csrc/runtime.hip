@@ -29,14 +29,14 @@ int gemv_wg_per_cu(int dflt) {
     return v ? v : dflt;
 }
 
-int gemv_rows_per_step() {
-    static int v = 0;
-    if (v == 0) {
+int gemv_rows_per_step(int dflt) {
+    static int v = -1;
+    if (v < 0) {
         const char* e = getenv("RF_GEMV_R");
         int n = e ? atoi(e) : 0;
-        v = (n == 1 || n == 2 || n == 4) ? n : 1;
+        v = (n == 1 || n == 2 || n == 4) ? n : 0;
     }
-    return v;
+    return v ? v : dflt;
 }
 
 int gemv_waves_per_wg(int dflt) {
