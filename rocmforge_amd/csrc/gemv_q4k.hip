@@ -33,15 +33,37 @@ constexpr int kSbPerStep = 16;  // super-blocks per wave row step
 
 enum Q4Mode { kPlain = 0, kResidual = 1, kGateUp = 2, kQkv = 3 };
 
-// kQkv: three matrices (Q, K, V projections) as one row space of
-// n_q + 2 n_kv rows -- rows [0, n_q) of w[0], then n_kv of w[1], then n_kv
-// of w[2] -- each output row optionally plus its bias.
+// kQkv: three matrices (Q, K, V projections) in one launch.  The grid's
+// waves are split over the matrices in proportion to their rows (qkv_split),
+// so each wave streams rows of one matrix and its weight, output and bias
+// pointers are fixed for the whole launch; output = dot + bias (bias may be
+// null).
 struct QkvArgs {
     const uint8_t* w[3];
     const float* bias[3];
     float* y[3];
     int n_q, n_kv;
 };
+
+// Waves per matrix: [0, nw[0]) on Q, then nw[1] on K, nw[2] on V (each >= 1;
+// nwaves >= 3).  Host and device compute the same split.
+struct QkvSplit {
+    int nw[3];
+};
+__host__ __device__ inline QkvSplit qkv_split(int nwaves, int n_q, int n_kv) {
+    const long n = (long)n_q + 2L * n_kv;
+    int q = (int)(((long)nwaves * n_q + n / 2) / n);
+    q = q < 1 ? 1 : (q > nwaves - 2 ? nwaves - 2 : q);
+    const int k = (nwaves - q) / 2;
+    return QkvSplit{{q, k, nwaves - q - k}};
+}
+// Largest number of rows one wave owns (its LDS result slots).
+__host__ __device__ inline int qkv_max_rows(const QkvSplit& sp, int n_q, int n_kv) {
+    const int a = (n_q + sp.nw[0] - 1) / sp.nw[0];
+    const int b = (n_kv + sp.nw[1] - 1) / sp.nw[1];
+    const int c = (n_kv + sp.nw[2] - 1) / sp.nw[2];
+    return a > b ? (a > c ? a : c) : (b > c ? b : c);
+}
 
 // Q8-inline LDS rule of the reference launchers (q4_k_q8_inline.hip:374-378):
 // (K/32) * 34 bytes <= 32 KB.  Kept so callers see identical validation.
@@ -94,9 +116,26 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     // time, which keeps the open DRAM pages few (measured: an interleaved
     // read of 64 MB runs ~12% faster than per-wave contiguous stretches).
     const int gw = blockIdx.x * NW + wave;
-    const int rstride = nwaves, rfirst = gw;
-    const int nrows = gw < N ? (N - 1 - gw) / nwaves + 1 : 0;
-    const int max_rows = (N + nwaves - 1) / nwaves;
+    int rstride = nwaves, rfirst = gw, nrows_of = N, max_rows = (N + nwaves - 1) / nwaves;
+    const uint8_t* wm = w0;
+    float* ym = y;
+    const float* bm = nullptr;
+    if constexpr (MODE == kQkv) {
+        // this wave's matrix and its rank among the waves on that matrix
+        const QkvSplit sp = qkv_split(nwaves, qkv.n_q, qkv.n_kv);
+        // (selects, not indexing: a runtime index into the argument arrays
+        // would put them in scratch memory)
+        const int m = gw < sp.nw[0] ? 0 : (gw < sp.nw[0] + sp.nw[1] ? 1 : 2);
+        const int w_first = m == 0 ? 0 : (m == 1 ? sp.nw[0] : sp.nw[0] + sp.nw[1]);
+        rfirst = gw - w_first;
+        rstride = m == 0 ? sp.nw[0] : (m == 1 ? sp.nw[1] : sp.nw[2]);
+        nrows_of = m == 0 ? qkv.n_q : qkv.n_kv;
+        max_rows = qkv_max_rows(sp, qkv.n_q, qkv.n_kv);
+        wm = m == 0 ? qkv.w[0] : (m == 1 ? qkv.w[1] : qkv.w[2]);
+        ym = m == 0 ? qkv.y[0] : (m == 1 ? qkv.y[1] : qkv.y[2]);
+        bm = m == 0 ? qkv.bias[0] : (m == 1 ? qkv.bias[1] : qkv.bias[2]);
+    }
+    const int nrows = rfirst < nrows_of ? (nrows_of - 1 - rfirst) / rstride + 1 : 0;
 
     const int spr = (nsb + kSbPerStep - 1) / kSbPerStep;        // steps per row group
     const int nsteps = ((nrows + R - 1) / R) * spr;
@@ -105,18 +144,9 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
         const int sb = min((i % spr) * kSbPerStep + s, nsb - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = row_of((i / spr) * R + r);
-            if constexpr (MODE == kQkv) {
-                // wave-uniform: the matrix select stays in scalar registers
-                const int m = row < qkv.n_q ? 0 : (row < qkv.n_q + qkv.n_kv ? 1 : 2);
-                const int local = row - (m == 0 ? 0 : qkv.n_q + (m - 1) * qkv.n_kv);
-                const uint8_t* base = m == 0 ? qkv.w[0] : (m == 1 ? qkv.w[1] : qkv.w[2]);
-                u[0][r] = q4k_load_unit(base + (size_t)local * row_bytes + (size_t)sb * kQ4KBytes, p);
-            } else {
-                const size_t off = (size_t)row * row_bytes + (size_t)sb * kQ4KBytes;
-                u[0][r] = q4k_load_unit(w0 + off, p);
-                if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
-            }
+            const size_t off = (size_t)row_of((i / spr) * R + r) * row_bytes + (size_t)sb * kQ4KBytes;
+            u[0][r] = q4k_load_unit(wm + off, p);
+            if (M == 2) u[M - 1][r] = q4k_load_unit(w1 + off, p);
         }
     };
     float acc[M][R];
@@ -185,11 +215,7 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
         } else if (MODE == kResidual) {
             y[row] = g + residual[row];
         } else if (MODE == kQkv) {
-            const int m = row < qkv.n_q ? 0 : (row < qkv.n_q + qkv.n_kv ? 1 : 2);
-            const int local = row - (m == 0 ? 0 : qkv.n_q + (m - 1) * qkv.n_kv);
-            const float* b = m == 0 ? qkv.bias[0] : (m == 1 ? qkv.bias[1] : qkv.bias[2]);
-            float* o = m == 0 ? qkv.y[0] : (m == 1 ? qkv.y[1] : qkv.y[2]);
-            o[local] = g + (b ? b[local] : 0.0f);
+            ym[row] = g + (bm ? bm[row] : 0.0f);
         } else {
             y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
         }
@@ -313,7 +339,11 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     const int cap = device_cu_count() * gemv_wg_per_cu(1);
     const int need = (N + nw - 1) / nw;
     const int grid = need < cap ? need : cap;
-    const size_t out_bytes = (size_t)nw * ((N + (size_t)grid * nw - 1) / ((size_t)grid * nw)) * M * 4;
+    // result slots per wave: its largest row count
+    const size_t wave_rows = MODE == kQkv ? (size_t)qkv_max_rows(qkv_split(grid * nw, qkv.n_q, qkv.n_kv), qkv.n_q,
+                                                                  qkv.n_kv)
+                                          : (N + (size_t)grid * nw - 1) / ((size_t)grid * nw);
+    const size_t out_bytes = (size_t)nw * wave_rows * M * 4;
     if (q8_lds_bytes(K) + out_bytes > 160 * 1024) return hipErrorInvalidValue;
     const uint8_t* a = static_cast<const uint8_t*>(w0);
     const uint8_t* b = static_cast<const uint8_t*>(w1);
