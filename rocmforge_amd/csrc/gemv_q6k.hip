@@ -352,7 +352,7 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
                                                                const float* __restrict__ x, const float* residual,
                                                                float* y, int K, int N) {
     __shared__ __align__(16) uint8_t stage_lds[8 * 2048];
-    extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK]
+    extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK][4 lane rows]
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nwk = blockDim.x / kWave;
@@ -434,8 +434,10 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
         }
         float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
         acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
-        const float tot = wave_sum(acc);
-        if (lane == 0) part[j * nwk + wave] = tot;
+        // the four 16-lane row sums go to LDS (no cross-row broadcast and
+        // no read-lane per row); the final pass adds them in fixed order
+        const float r16 = row16_sum(acc);
+        if ((lane & 15) == 0) part[(j * nwk + wave) * 4 + (lane >> 4)] = r16;
     };
     Q6Seg ring[NB];
     ring_pipeline<NB>(nrows, ring, load, process, [&]() {
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
     __syncthreads();
     for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
         float t = 0.0f;
-        for (int k = 0; k < nwk; ++k) t += part[j * nwk + k];
+        for (int k = 0; k < 4 * nwk; ++k) t += part[j * nwk * 4 + k];
         y[g + j * G] = t + (residual ? residual[g + j * G] : 0.0f);
     }
 }
@@ -469,7 +471,7 @@ static hipError_t launch_q6(const void* weights_q6_k, const float* input, const 
         const int nwk = nsb / 8;
         const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
         const int grid = ncols_dst < cap ? ncols_dst : cap;
-        const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
+        const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * 4 * sizeof(float);
         if (lds <= 64 * 1024) {
             hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
                                residual, output, n_rows, ncols_dst);

@@ -75,6 +75,16 @@ constexpr int kQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
 // Sum over the 64 lanes of a wave, returned to every lane: rows of 16 are
 // reduced with quad permutes and row rotates, rows are combined with
 // row_bcast into lane 63, which is read back as a scalar.
+// Sum over each 16-lane DPP row: every lane holds its row's sum (the first
+// four steps of wave_sum).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<kQuadXor1>(v);
+    v += dpp_f<kQuadXor2>(v);
+    v += dpp_f<0x124>(v);          // row_ror:4
+    v += dpp_f<0x128>(v);          // row_ror:8
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<kQuadXor1>(v);
     v += dpp_f<kQuadXor2>(v);
