@@ -157,7 +157,8 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     // Row results are parked in this wave's LDS slots and written to HBM
     // after the loop: no global store (or residual load) sits between the
     // prefetch loads in the in-order memory counter.
-    float* out_lds = reinterpret_cast<float*>(smem + q8_lds_bytes(K)) + wave * max_rows * M;
+    // [row][matrix][16-lane row of the wave]
+    float* out_lds = reinterpret_cast<float*>(smem + q8_lds_bytes(K)) + wave * max_rows * M * 4;
     auto process = [&](const Q4KUnit (&u)[M][R], int i) {
         const int j0 = (i / spr) * R;
         const int sb = (i % spr) * kSbPerStep + s;
@@ -180,12 +181,14 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
         if ((i % spr) == spr - 1) {  // row group finished: reduce into the wave's LDS slots
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float g = wave_sum(acc[0][r]);
-                const float v = (M == 2) ? wave_sum(acc[M - 1][r]) : 0.0f;
+                // per-16-lane sums only; the four are added after the loop
+                // (same association as wave_sum: (r0 + r1) + (r2 + r3))
+                const float g = row16_sum(acc[0][r]);
+                const float v = (M == 2) ? row16_sum(acc[M - 1][r]) : 0.0f;
                 const int j = j0 + r;
-                if (lane == 0 && j < nrows) {
-                    out_lds[M * j] = g;
-                    if (M == 2) out_lds[M * j + 1] = v;
+                if ((lane & 15) == 0 && j < nrows) {
+                    out_lds[4 * M * j + (lane >> 4)] = g;
+                    if (M == 2) out_lds[4 * (M * j + 1) + (lane >> 4)] = v;
                 }
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[m][r] = 0.0f;
@@ -209,7 +212,10 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
                       });
     for (int j = lane; j < nrows; j += kWave) {
         const int row = rfirst + j * rstride;
-        const float g = out_lds[M * j];
+        auto sum4 = [&](int s4) {
+            return (out_lds[s4] + out_lds[s4 + 1]) + (out_lds[s4 + 2] + out_lds[s4 + 3]);
+        };
+        const float g = sum4(4 * M * j);
         if (MODE == kPlain) {
             y[row] = g;
         } else if (MODE == kResidual) {
@@ -217,7 +223,7 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
         } else if (MODE == kQkv) {
             ym[row] = g + (bm ? bm[row] : 0.0f);
         } else {
-            y[row] = g / (1.0f + expf(-g)) * out_lds[M * j + 1];
+            y[row] = g / (1.0f + expf(-g)) * sum4(4 * (M * j + 1));
         }
     }
 }
@@ -343,7 +349,7 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     const size_t wave_rows = MODE == kQkv ? (size_t)qkv_max_rows(qkv_split(grid * nw, qkv.n_q, qkv.n_kv), qkv.n_q,
                                                                   qkv.n_kv)
                                           : (N + (size_t)grid * nw - 1) / ((size_t)grid * nw);
-    const size_t out_bytes = (size_t)nw * wave_rows * M * 4;
+    const size_t out_bytes = (size_t)nw * wave_rows * M * 4 * sizeof(float);
     if (q8_lds_bytes(K) + out_bytes > 160 * 1024) return hipErrorInvalidValue;
     const uint8_t* a = static_cast<const uint8_t*>(w0);
     const uint8_t* b = static_cast<const uint8_t*>(w1);
