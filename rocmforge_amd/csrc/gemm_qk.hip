@@ -8,12 +8,16 @@
 // W via __float2half of the fp32 dequant value (:137, q6: :148).
 //
 // Kernels (selected by the launcher from the shape):
-//  * rf_gemm_qk_v7_kernel (default when N % 256 == 0, K % 512 == 0 and, for
-//    Q6_K, K % 2048 == 0): 256-thread workgroups, one wave per SIMD, over a
-//    BM x 256 tile; weights stage through an LDS ring with coalesced loads,
-//    each wave dequantises its own B operands (the next chunk's, double
-//    buffered) in hand-scheduled slots between its MFMAs; XCD-aware tile
-//    order; split-K with float atomics when the tiles leave CUs idle.
+//  * rf_gemm_qk_sq_kernel (M % 256 == 0, N % 256 == 0, K % 512 == 0 and
+//    enough 256 x 256 tiles to fill the CUs unsplit): 2 x 2 waves, each
+//    weight dequantised once per workgroup into an LDS B tile shared by the
+//    two waves that use it.
+//  * rf_gemm_qk_v7_kernel (otherwise when N % 256 == 0, K % 512 == 0 and,
+//    for Q6_K, K % 2048 == 0): 256-thread workgroups, one wave per SIMD,
+//    over a BM x 256 tile; weights stage through an LDS ring with coalesced
+//    loads, each wave dequantises its own B operands (the next chunk's,
+//    double buffered) in hand-scheduled slots between its MFMAs; XCD-aware
+//    tile order; split-K with float atomics when the tiles leave CUs idle.
 //  * rf_gemm_qk_v5_kernel: the previous 8-wave design with the same ring
 //    (RF_GEMM_V=5, kept for comparison measurements).
 //  * rf_gemm_qk_v4_kernel: 8 waves, weights loaded per lane (Q6_K with
@@ -1268,11 +1272,10 @@ struct SqRawQ6 {
     uint32_t d;       // fp16 bits of d
 };
 
-template <bool IS_Q6, bool SPLIT>
+template <bool IS_Q6>
 __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
-                                                                    float* __restrict__ D, int M, int N, int K,
-                                                                    int tiles, int chunks_per_split) {
+                                                                    float* __restrict__ D, int M, int N, int K) {
     using Raw = typename std::conditional<IS_Q6, SqRawQ6, SqRawQ4>::type;
     constexpr int kBytes = IS_Q6 ? kQ6KBytes : kQ4KBytes;
     constexpr int BAR = 48;                            // slot of the barrier (start of step 3)
@@ -1289,15 +1292,12 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int h = lane >> 5;
-    const int vidx = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int splits = (int)gridDim.x / tiles;
-    const int tile = vidx / splits;
-    const int split = vidx % splits;
+    const int tile = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int ntiles = N / kSqTile;
     const int m0 = (tile / ntiles) * kSqTile;
     const int n0 = (tile % ntiles) * kSqTile;
-    const int c_begin = split * chunks_per_split;
-    const int c_last = c_begin + chunks_per_split - 1;
+    const int c_begin = 0;
+    const int c_last = K / kKC - 1;
     const uint32_t row_bytes = (uint32_t)(K / kQK) * kBytes;
 
     // ---- A: 16 float4 per thread per chunk, buffer loads -----------------
@@ -1481,10 +1481,7 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + 128 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if constexpr (SPLIT)
-                    unsafeAtomicAdd(&D[(size_t)row * N + col], acc[i][j][e]);
-                else
-                    D[(size_t)row * N + col] = acc[i][j][e];
+                D[(size_t)row * N + col] = acc[i][j][e];
             }
         }
 }
@@ -1551,8 +1548,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
 template <bool IS_Q6>
 static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st) {
     const int tiles = (M / kSqTile) * (N / kSqTile);
-    hipLaunchKernelGGL((rf_gemm_qk_sq_kernel<IS_Q6, false>), dim3(tiles), dim3(kSqThreads), 0, st, A, w, D, M, N, K,
-                       tiles, K / kKC);
+    hipLaunchKernelGGL((rf_gemm_qk_sq_kernel<IS_Q6>), dim3(tiles), dim3(kSqThreads), 0, st, A, w, D, M, N, K);
 }
 
 template <bool IS_Q6>
