@@ -61,8 +61,8 @@ def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
 
 
 # One case per launcher branch for N % 256 == 0, K % 512 == 0 (the tiled
-# kernels): 256 x 256 shared-dequantisation tiles (M % 256 == 0 and at least
-# 7/8 as many tiles as CUs); otherwise ring tiles of 128 rows (Q6_K, or
+# kernels): 256 x 256 or 128 x 128 shared-dequantisation tiles (where they
+# come to about one workgroup per CU); otherwise ring tiles of 128 rows (Q6_K, or
 # Q4_K when they fill the CUs unsplit -- the M = 512 Llama case below) or
 # 64 rows, with split-K when the tiles leave CUs idle; and (Q6_K with
 # K % 2048 != 0) the register-weight kernel.
@@ -72,11 +72,13 @@ def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
     ("q4_k", 128, 512, 2048),    # ring, 64-row tiles, 4 splits
     ("q4_k", 384, 512, 512),     # ring, 64-row tiles, 1 split
     ("q4_k", 2048, 8192, 512),   # 256 x 256 shared-dequantisation tiles (256 tiles)
+    ("q4_k", 256, 14336, 512),   # 128 x 128 shared-dequantisation tiles (224 tiles)
     ("q6_k", 64, 256, 2048),     # ring, 64-row tiles, 4 splits
     ("q6_k", 256, 512, 4096),    # ring, 128-row tiles, 8 splits
     ("q6_k", 128, 256, 1536),    # register weights, 128-row tiles, 3 splits
     ("q6_k", 64, 256, 512),      # register weights, 64-row tiles, 1 split
     ("q6_k", 2048, 7168, 512),   # 256 x 256 tiles, rows 2-byte aligned (420 bytes)
+    ("q6_k", 256, 14336, 1536),  # 128 x 128 tiles (two threads per weight row), 1260-byte rows
 ])
 def test_gemm_tiled_kernel_branches(rf, dev, fmt, m, n, k):
     a = synth.activations(k, seed=m + 3 * n, m=m)
