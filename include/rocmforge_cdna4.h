@@ -209,6 +209,116 @@ typedef struct rf_launchers {
 } rf_launchers;
 void rf_dispatch_set_launchers(const rf_launchers* table);
 
+/* ---- Layer operations around the matmuls (model_ops.hip) ---------------
+ * Same names, argument order and meaning as the reference's launchers;
+ * KV caches are fp16 [max_seq][num_kv_heads * head_dim] per layer.  The
+ * *_state variants read the position / sequence length from device memory
+ * (decode state int[2] = {pos, seq_len}), so a captured graph replays them. */
+
+/* hip_kernels/norm.hip:154 -- out = x * rsqrt(mean(x^2) + eps) * w; out may alias x. */
+hipError_t gpu_rms_norm(const float* d_x, const float* d_weight, float* d_out, const int n, const float eps,
+                        hipStream_t stream);
+/* hip_kernels/norm.hip:173, :184 -- seq_len rows of n (also the per-head Q/K norms). */
+hipError_t gpu_rms_norm_batched(const float* d_x, const float* d_weight, float* d_out, const int n, const float eps,
+                                const int seq_len);
+hipError_t gpu_rms_norm_batched_on_stream(const float* d_x, const float* d_weight, float* d_out, const int n,
+                                          const float eps, const int seq_len, hipStream_t stream);
+
+/* hip_kernels/rope.hip:293-420 -- RoPE over [num_heads][head_dim] in place;
+ * neox != 0: pairs (i, i + d/2), else (2i, 2i + 1); freq_scale divides theta_i. */
+hipError_t gpu_rope_heads(float* d_x, const int pos, const int num_heads, const int head_dim, const float theta_base,
+                          const int neox, hipStream_t stream);
+hipError_t gpu_rope_heads_scaled(float* d_x, const int pos, const int num_heads, const int head_dim,
+                                 const float theta_base, const int neox, const float* d_freq_scale,
+                                 hipStream_t stream);
+hipError_t gpu_rope_heads_state(float* d_x, const int* d_pos, const int num_heads, const int head_dim,
+                                const float theta_base, const int neox, hipStream_t stream);
+hipError_t gpu_rope_heads_state_scaled(float* d_x, const int* d_pos, const int num_heads, const int head_dim,
+                                       const float theta_base, const int neox, const float* d_freq_scale,
+                                       hipStream_t stream);
+/* rows s = 0..seq_len-1 of [seq_len][num_heads * head_dim] at positions start_pos + s (null stream). */
+hipError_t gpu_rope_heads_batched(float* d_x, const int start_pos, const int num_heads, const int head_dim,
+                                  const float theta_base, const int seq_len, const int neox);
+hipError_t gpu_rope_heads_batched_scaled(float* d_x, const int start_pos, const int num_heads, const int head_dim,
+                                         const float theta_base, const int seq_len, const int neox,
+                                         const float* d_freq_scale);
+/* No counterpart: gpu_rope_heads_batched_scaled on a caller's stream. */
+hipError_t rf_rope_heads_batched_on_stream(float* d_x, const int start_pos, const int num_heads, const int head_dim,
+                                           const float theta_base, const int seq_len, const int neox,
+                                           const float* d_freq_scale, hipStream_t stream);
+
+/* hip_kernels/attention.hip:1627-1665 -- V[pos] = fp16(v), K[pos] = fp16(rope(k, pos)). */
+hipError_t gpu_kv_write_rope(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v, const int pos,
+                             const int num_kv_heads, const int head_dim, const float theta_base, const int neox,
+                             hipStream_t stream);
+hipError_t gpu_kv_write_rope_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                    const int pos, const int num_kv_heads, const int head_dim,
+                                    const float theta_base, const int neox, const float* d_freq_scale,
+                                    hipStream_t stream);
+hipError_t gpu_kv_write_rope_state(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                   const int* d_pos, const int num_kv_heads, const int head_dim,
+                                   const float theta_base, const int neox, hipStream_t stream);
+hipError_t gpu_kv_write_rope_state_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                          const int* d_pos, const int num_kv_heads, const int head_dim,
+                                          const float theta_base, const int neox, const float* d_freq_scale,
+                                          hipStream_t stream);
+/* hip_kernels/attention.hip:1667 -- rows [start_pos, start_pos + seq_len) of both caches (null stream);
+ * start_pos + seq_len > max_seq is rejected. */
+hipError_t gpu_kv_write_batched(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                const int start_pos, const int kv_size, const int max_seq, const int seq_len);
+/* No counterpart: gpu_kv_write_batched on a caller's stream. */
+hipError_t rf_kv_write_batched_on_stream(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                         const int start_pos, const int kv_size, const int max_seq,
+                                         const int seq_len, hipStream_t stream);
+
+/* No counterpart (the reference takes gpu_rms_norm_batched_on_stream twice,
+ * gpu_rope_heads_state_scaled and gpu_kv_write_rope_state_scaled,
+ * src/gpu/forward.rs:2384-2430): per-head RMSNorm of q (d_q_norm) and k
+ * (d_k_norm; either may be null to skip), RoPE of both at *d_pos, q written
+ * back in place, fp16 k and v written to the caches at *d_pos.  head_dim <= 512. */
+hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const float* d_v, const float* d_q_norm,
+                                          const float* d_k_norm, uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_pos,
+                                          const int num_heads, const int num_kv_heads, const int head_dim,
+                                          const float eps, const float theta_base, const int neox,
+                                          const float* d_freq_scale, hipStream_t stream);
+
+/* hip_kernels/attention.hip:950, :972 -- one query token over seq_len cached
+ * positions (fp16 bits): out[h] = softmax(q[h] . K[0..seq_len) * scale) V, GQA head h / (nh / nkv).
+ * head_dim 64, 128 or 256. */
+hipError_t gpu_flash_attn_decode_strided_multi_head(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                    const uint16_t* d_v_cache, const int seq_len, const int num_heads,
+                                                    const int num_kv_heads, const int head_dim, const float scale,
+                                                    hipStream_t stream);
+hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                          const uint16_t* d_v_cache, const int* d_seq_len,
+                                                          const int num_heads, const int num_kv_heads,
+                                                          const int head_dim, const float scale, hipStream_t stream);
+
+/* hip_kernels/elementwise.hip:615, :651 -- index of the maximum of d_input[n]
+ * (ties: the larger index; NaN never wins); partial buffers hold ceil(n / 1024). */
+hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_partial_values, int* d_partial_indices,
+                                    int* d_output_index, const int n, hipStream_t stream);
+hipError_t gpu_argmax_f32(const float* d_input, float* d_partial_values, int* d_partial_indices,
+                          int* d_output_index, const int n);
+
+/* hip_kernels/elementwise.hip:780, :804 -- Q4_K rows of a [vocab][hidden]
+ * embedding dequantised to fp32; ids outside [0, vocab) leave their row untouched. */
+hipError_t gpu_embed_q4_k_token(const uint8_t* d_embedding, float* d_out, const int hidden_size,
+                                const int vocab_size, const int token_id, hipStream_t stream);
+hipError_t gpu_embed_q4_k_batch(const uint8_t* d_embedding, const int* d_token_ids, float* d_out,
+                                const int hidden_size, const int vocab_size, const int seq_len, hipStream_t stream);
+
+/* hip_kernels/elementwise.hip:450-750 and quant/dequant_q4_0_to_f16.hip:103. */
+hipError_t gpu_add(const float* d_x, const float* d_y, float* d_out, const int n, hipStream_t stream);
+hipError_t gpu_mul_on_stream(const float* d_x, const float* d_y, float* d_out, const int n, hipStream_t stream);
+hipError_t gpu_silu_on_stream(const float* d_x, float* d_out, const int n, hipStream_t stream);
+hipError_t gpu_increment_decode_state_on_stream(int* d_state, hipStream_t stream);
+hipError_t convert_f32_to_f16(const float* input, void* output, int n, hipStream_t stream);
+/* No counterpart (the reference takes gpu_silu_on_stream then gpu_mul_on_stream,
+ * src/gpu/forward.rs:1133-1143): out = silu(gate) * up. */
+hipError_t rf_silu_mul_on_stream(const float* d_gate, const float* d_up, float* d_out, const int n,
+                                 hipStream_t stream);
+
 /* ---- Parity probes (no reference counterpart) ---------------------------
  * Expose the intermediate integers of the Q8-inline path so tests can check
  * them bit-exactly.  They run the same device code as the GEMV. */

@@ -48,6 +48,11 @@ def lib() -> ctypes.CDLL:
             "or_round_f16": [_p, ctypes.c_size_t, _p],
             "or_q4k_dequant_f16": [_p, _i, _i, _p],
             "or_q6k_dequant_f16": [_p, _i, _i, _p],
+            "or_rms_norm": [_p, _p, _i, _i, ctypes.c_float, _p],
+            "or_rope": [_p, _i, _i, _i, _i, ctypes.c_float, _i, _p],
+            "or_attn_decode": [_p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p],
+            "or_attn_prefill_f16": [_p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p],
+            "or_silu_mul": [_p, _p, _i, _p],
             "cb_gemv_q4k_q8k": [_p, _p, _p, _i, _i, _i],
             "cb_gemm_q4k_q8k": [_p, _p, _p, _i, _i, _i, _i],
             "cb_gemv_q6k": [_p, _p, _p, _i, _i, _i],
@@ -58,6 +63,10 @@ def lib() -> ctypes.CDLL:
             f.argtypes = args
             f.restype = None
         L.cb_max_threads.restype = _i
+        L.or_rope_theta.argtypes = [_i, _i, ctypes.c_float, _p]
+        L.or_rope_theta.restype = ctypes.c_float
+        L.or_argmax.argtypes = [_p, _i]
+        L.or_argmax.restype = _i
         _lib = L
     return _lib
 
@@ -194,3 +203,56 @@ def cpu_gemm(fmt, w, a, m, n, k, threads):
 
 def cpu_threads() -> int:
     return int(lib().cb_max_threads())
+
+
+# ---- layer operations -------------------------------------------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def rms_norm(x, w, eps: float, rows: int = 1) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    n = x.size // rows
+    out = np.empty(x.size, np.float64)
+    lib().or_rms_norm(_ptr(x), _ptr(w), n, rows, eps, _ptr(out))
+    return out
+
+
+def rope_theta(i: int, d: int, base: float, freq_scale=None) -> float:
+    fs = None if freq_scale is None else _f32(freq_scale)
+    return lib().or_rope_theta(i, d, base, None if fs is None else _ptr(fs))
+
+
+def rope(x, seq: int, nh: int, d: int, pos0: int, base: float, neox: bool, freq_scale=None) -> np.ndarray:
+    out = np.ascontiguousarray(x, np.float64).copy()
+    fs = None if freq_scale is None else _f32(freq_scale)
+    lib().or_rope(_ptr(out), seq, nh, d, pos0, base, int(neox), None if fs is None else _ptr(fs))
+    return out
+
+
+def attn_decode(q, kc16, vc16, seq: int, nh: int, nkv: int, d: int, scale: float) -> np.ndarray:
+    q = _f32(q)
+    kc16, vc16 = np.ascontiguousarray(kc16, np.uint16), np.ascontiguousarray(vc16, np.uint16)
+    out = np.empty(nh * d, np.float64)
+    lib().or_attn_decode(_ptr(q), _ptr(kc16), _ptr(vc16), seq, nh, nkv, d, scale, _ptr(out))
+    return out
+
+
+def attn_prefill_f16(q, k, v, seq: int, nh: int, nkv: int, d: int, scale: float) -> np.ndarray:
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.empty(seq * nh * d, np.float64)
+    lib().or_attn_prefill_f16(_ptr(q), _ptr(k), _ptr(v), seq, nh, nkv, d, scale, _ptr(out))
+    return out
+
+
+def silu_mul(g, u) -> np.ndarray:
+    g, u = _f32(g), _f32(u)
+    out = np.empty(g.size, np.float64)
+    lib().or_silu_mul(_ptr(g), _ptr(u), g.size, _ptr(out))
+    return out
+
+
+def argmax(x) -> int:
+    x = _f32(x)
+    return lib().or_argmax(_ptr(x), x.size)

@@ -327,3 +327,141 @@ void or_q6k_dequant_f16(const uint8_t* w, int N, int K, float* out) {
         for (int k = 0; k < K; ++k) o[k] = or_f16_to_f32(or_f32_to_f16(o[k]));
     }
 }
+
+/* ==== Layer operations around the matmuls ==================================
+ * Pins (tests/test_oracle_ops.py): the reference's own op tests
+ * (src/cpu/ops_tests.rs: rms_norm on [3, 4], rope at position 0, silu(+-1),
+ * the two-position decode attention, argmax), closed forms (unit RMS,
+ * scale invariance, rotation by exact angles, pair-norm preservation,
+ * classic = interleaved NeoX, uniform / one-hot attention) and brute force
+ * (direct softmax over all positions, full causal attention). */
+
+/* src/cpu/ops.rs:33-46 -- out = x / sqrt(mean(x^2) + eps) * w, per row. */
+void or_rms_norm(const float* x, const float* w, int n, int rows, float eps, double* out) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * n;
+        double ss = 0.0;
+        for (int i = 0; i < n; ++i) ss += (double)xr[i] * xr[i];
+        const double inv = 1.0 / sqrt(ss / n + (double)eps);
+        for (int i = 0; i < n; ++i) out[(size_t)r * n + i] = (double)xr[i] * inv * w[i];
+    }
+}
+
+/* theta_i of src/cpu/ops.rs:79 / hip_kernels/rope.hip:66-70: exponent in
+ * fp32, 1 / base^e evaluated in double and rounded once to float, divided
+ * (fp32) by freq_scale[i] when given. */
+float or_rope_theta(int i, int d, float base, const float* freq_scale) {
+    const float e = (float)(2 * i) / (float)d;
+    float t = (float)(1.0 / pow((double)base, (double)e));
+    if (freq_scale) t = t / freq_scale[i];
+    return t;
+}
+
+/* src/cpu/ops.rs:69-98 -- RoPE of rows [seq][nh][d] in place (double
+ * values), row s at position pos0 + s, angle = (float)pos * theta in fp32. */
+void or_rope(double* x, int seq, int nh, int d, int pos0, float base, int neox, const float* freq_scale) {
+    const int half = d / 2;
+    for (int s = 0; s < seq; ++s)
+        for (int h = 0; h < nh; ++h) {
+            double* row = x + ((size_t)s * nh + h) * d;
+            for (int i = 0; i < half; ++i) {
+                const float a = (float)(pos0 + s) * or_rope_theta(i, d, base, freq_scale);
+                const double c = cos((double)a), sn = sin((double)a);
+                const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
+                const double x0 = row[i0], x1 = row[i1];
+                row[i0] = x0 * c - x1 * sn;
+                row[i1] = x0 * sn + x1 * c;
+            }
+        }
+}
+
+/* src/cpu/ops.rs:195-249 -- one query over seq cached positions with the
+ * online softmax of :150-172; K/V are fp16 bits [seq][nkv * d]. */
+void or_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, int seq, int nh, int nkv, int d,
+                    float scale, double* out) {
+    const int group = nh / nkv;
+    double acc[1024];
+    for (int h = 0; h < nh; ++h) {
+        const int kh = h / group;
+        double m = -INFINITY, l = 0.0;
+        for (int i = 0; i < d; ++i) acc[i] = 0.0;
+        for (int t = 0; t < seq; ++t) {
+            const uint16_t* kr = kc + (size_t)t * nkv * d + (size_t)kh * d;
+            const uint16_t* vr = vc + (size_t)t * nkv * d + (size_t)kh * d;
+            double s = 0.0;
+            for (int i = 0; i < d; ++i) s += (double)q[h * d + i] * or_f16_to_f32(kr[i]);
+            s *= scale;
+            const double mn = s > m ? s : m;
+            const double ed = exp(m - mn), es = exp(s - mn);
+            for (int i = 0; i < d; ++i) acc[i] = acc[i] * ed + es * or_f16_to_f32(vr[i]);
+            l = l * ed + es;
+            m = mn;
+        }
+        for (int i = 0; i < d; ++i) out[h * d + i] = acc[i] / l;
+    }
+}
+
+/* Causal prefill attention with the rounding of the reference's default
+ * prefill path (src/gpu/forward.rs:768-824 ->
+ * hip_kernels/wmma/wmma_attention_prefill.hip:386-660): Q, K, V rounded to
+ * fp16; S = Q K^T (exact products, wide sum) * scale; keys in tiles of 64
+ * with a running row max m; per tile P = fp16(exp(S - m_new)) for
+ * unmasked keys, l += sum of the unrounded exp, O = O * exp(m_old - m_new)
+ * + P V; out = O / l.  q: [seq][nh * d], k, v: [seq][nkv * d] (fp32). */
+void or_attn_prefill_f16(const float* q, const float* k, const float* v, int seq, int nh, int nkv, int d, float scale,
+                         double* out) {
+    const int group = nh / nkv;
+    double acc[1024];
+    for (int h = 0; h < nh; ++h) {
+        const int kh = h / group;
+        for (int r = 0; r < seq; ++r) {
+            double m = -3.402823466e+38, l = 0.0;
+            for (int i = 0; i < d; ++i) acc[i] = 0.0;
+            for (int t0 = 0; t0 <= r; t0 += 64) {
+                double s[64];
+                double tmax = -3.402823466e+38;
+                const int tn = (r - t0 + 1) < 64 ? (r - t0 + 1) : 64;
+                for (int j = 0; j < tn; ++j) {
+                    double dot = 0.0;
+                    for (int i = 0; i < d; ++i)
+                        dot += (double)or_f16_to_f32(or_f32_to_f16(q[(size_t)r * nh * d + h * d + i])) *
+                               or_f16_to_f32(or_f32_to_f16(k[(size_t)(t0 + j) * nkv * d + kh * d + i]));
+                    s[j] = (double)(float)dot * scale;
+                    if (s[j] > tmax) tmax = s[j];
+                }
+                const double mn = tmax > m ? tmax : m;
+                const double alpha = exp(m - mn);
+                double rs = 0.0;
+                for (int i = 0; i < d; ++i) acc[i] *= alpha;
+                for (int j = 0; j < tn; ++j) {
+                    const double e = exp(s[j] - mn);
+                    rs += e;
+                    const double p = or_f16_to_f32(or_f32_to_f16((float)e));
+                    for (int i = 0; i < d; ++i)
+                        acc[i] += p * or_f16_to_f32(or_f32_to_f16(v[(size_t)(t0 + j) * nkv * d + kh * d + i]));
+                }
+                l = alpha * l + rs;
+                m = mn;
+            }
+            for (int i = 0; i < d; ++i) out[((size_t)r * nh + h) * d + i] = acc[i] / l;
+        }
+    }
+}
+
+/* src/cpu/ops.rs:120-123 -- silu(g) * u. */
+void or_silu_mul(const float* g, const float* u, int n, double* out) {
+    for (int i = 0; i < n; ++i) out[i] = (double)g[i] / (1.0 + exp(-(double)g[i])) * u[i];
+}
+
+/* hip_kernels/elementwise.hip:150-160 -- the maximum; equal values go to
+ * the larger index; NaN never replaces the running best. */
+int or_argmax(const float* x, int n) {
+    float bv = -3.402823466e+38f;
+    int bi = 0;
+    for (int i = 0; i < n; ++i)
+        if (x[i] > bv || (x[i] == bv && i > bi)) {
+            bv = x[i];
+            bi = i;
+        }
+    return bi;
+}

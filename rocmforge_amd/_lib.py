@@ -13,6 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "librocmforge_cdna4.so"
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
+_f = ctypes.c_float
 
 # name -> argtypes (all return hipError_t as int)
 SIGNATURES = {
@@ -27,6 +28,35 @@ SIGNATURES = {
     "gemv_q6_k_f32_residual_launch": [_vp, _vp, _vp, _vp, _i, _i, _vp],
     "wmma_gemm_q4_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "wmma_gemm_q6_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "gpu_rms_norm": [_vp, _vp, _vp, _i, _f, _vp],
+    "gpu_rms_norm_batched": [_vp, _vp, _vp, _i, _f, _i],
+    "gpu_rms_norm_batched_on_stream": [_vp, _vp, _vp, _i, _f, _i, _vp],
+    "gpu_rope_heads": [_vp, _i, _i, _i, _f, _i, _vp],
+    "gpu_rope_heads_scaled": [_vp, _i, _i, _i, _f, _i, _vp, _vp],
+    "gpu_rope_heads_state": [_vp, _vp, _i, _i, _f, _i, _vp],
+    "gpu_rope_heads_state_scaled": [_vp, _vp, _i, _i, _f, _i, _vp, _vp],
+    "gpu_rope_heads_batched": [_vp, _i, _i, _i, _f, _i, _i],
+    "gpu_rope_heads_batched_scaled": [_vp, _i, _i, _i, _f, _i, _i, _vp],
+    "rf_rope_heads_batched_on_stream": [_vp, _i, _i, _i, _f, _i, _i, _vp, _vp],
+    "gpu_kv_write_rope": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp],
+    "gpu_kv_write_rope_scaled": [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _vp],
+    "gpu_kv_write_rope_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp],
+    "gpu_kv_write_rope_state_scaled": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp],
+    "gpu_kv_write_batched": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
+    "rf_kv_write_batched_on_stream": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "rf_qk_norm_rope_kv_write_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp, _vp],
+    "gpu_flash_attn_decode_strided_multi_head": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
+    "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
+    "gpu_argmax_f32_on_stream": [_vp, _vp, _vp, _vp, _i, _vp],
+    "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
+    "gpu_embed_q4_k_token": [_vp, _vp, _i, _i, _i, _vp],
+    "gpu_embed_q4_k_batch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "gpu_add": [_vp, _vp, _vp, _i, _vp],
+    "gpu_mul_on_stream": [_vp, _vp, _vp, _i, _vp],
+    "gpu_silu_on_stream": [_vp, _vp, _i, _vp],
+    "rf_silu_mul_on_stream": [_vp, _vp, _vp, _i, _vp],
+    "gpu_increment_decode_state_on_stream": [_vp, _vp],
+    "convert_f32_to_f16": [_vp, _vp, _i, _vp],
     "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],
     "rf_q4_k_q8_int_dots_launch": [_vp, _vp, _vp, _i, _i, _vp],
 }

@@ -1,0 +1,732 @@
+// model_ops.hip -- the decode/prefill operations around the quantised
+// matmuls of a llama/qwen-style layer, on CDNA4 (gfx950, wave64).
+//
+// Drop-in for the reference's launchers of the same names (argument order,
+// meaning and error returns kept):
+//   gpu_rms_norm / gpu_rms_norm_batched(_on_stream)   hip_kernels/norm.hip:154-199
+//   gpu_rope_heads(_state)(_scaled), gpu_rope_heads_batched(_scaled)
+//                                                     hip_kernels/rope.hip:238-420
+//   gpu_kv_write_rope(_state)(_scaled), gpu_kv_write_batched
+//                                                     hip_kernels/attention.hip:1627-1670
+//   gpu_flash_attn_decode_strided_multi_head(_state)  hip_kernels/attention.hip:950-993
+//   gpu_argmax_f32(_on_stream)                        hip_kernels/elementwise.hip:615-666
+//   gpu_embed_q4_k_token / gpu_embed_q4_k_batch       hip_kernels/elementwise.hip:780-827
+//   gpu_add, gpu_mul_on_stream, gpu_silu_on_stream, gpu_increment_decode_state_on_stream
+//                                                     hip_kernels/elementwise.hip:450-750
+//   convert_f32_to_f16                                hip_kernels/quant/dequant_q4_0_to_f16.hip:103
+// plus entry points without a counterpart (declared as such in the header):
+// stream variants of the null-stream batched launchers, a fused SwiGLU, and
+// rf_qk_norm_rope_kv_write_state, which does a Qwen3 decode step's per-head
+// Q/K RMSNorm, both RoPEs and the fp16 KV write in one launch (the reference
+// takes four).
+//
+// RoPE frequencies: theta_i = 1 / base^(e_i) with e_i = (float)(2i) / (float)d
+// as the reference, evaluated in double and rounded once to float (the
+// reference's 1.0f / powf(..) is within an ulp of this), then divided by
+// freq_scale[i] when given; angle = (float)pos * theta_i in fp32.
+#include <hip/hip_fp16.h>
+
+#include "qk_common.h"
+
+namespace rf {
+
+constexpr float kNegMax = -3.402823466e+38f;
+
+__device__ __forceinline__ float wave_max(float v) {
+    // butterfly over the 64 lanes: every lane ends with the maximum
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_all(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float rope_theta(int i, int d, float base, const float* freq_scale) {
+    const float e = (float)(2 * i) / (float)d;
+    float t = (float)(1.0 / pow((double)base, (double)e));
+    if (freq_scale != nullptr) t /= freq_scale[i];
+    return t;
+}
+
+// (x0, x1) rotated by angle pos * theta
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, int pos, float theta) {
+    const float a = (float)pos * theta;
+    const float c = cosf(a), s = sinf(a);
+    const float y0 = x0 * c - x1 * s;
+    const float y1 = x0 * s + x1 * c;
+    x0 = y0;
+    x1 = y1;
+}
+
+// element indices of pair p of a head: NeoX pairs (p, p + d/2), classic (2p, 2p + 1)
+__device__ __forceinline__ void pair_idx(int p, int d, int neox, int* i0, int* i1) {
+    if (neox) {
+        *i0 = p;
+        *i1 = p + d / 2;
+    } else {
+        *i0 = 2 * p;
+        *i1 = 2 * p + 1;
+    }
+}
+
+// ---- RMSNorm ------------------------------------------------------------------
+// out = x * rsqrt(mean(x^2) + eps) * w, rows of n; out may alias x.
+// Long rows: one 256-thread workgroup per row.  Short rows (n <= 512, the
+// per-head norms): one wave per row, four rows per workgroup.
+__global__ __launch_bounds__(256) void rf_rms_norm_long_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                               float* out, int n, float eps, int rows) {
+    __shared__ float part[4];
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    const float* xr = x + (size_t)r * n;
+    float* orow = out + (size_t)r * n;
+    float ss = 0.0f;
+    const bool v4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow) |
+                                      reinterpret_cast<uintptr_t>(w)) & 15u) == 0;
+    if (v4) {
+        for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
+            const float4 a = reinterpret_cast<const float4*>(xr)[i];
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
+    }
+    ss = wave_sum_all(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv = rsqrtf(tot / (float)n + eps);
+    if (v4) {
+        for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
+            const float4 a = reinterpret_cast<const float4*>(xr)[i];
+            const float4 g = reinterpret_cast<const float4*>(w)[i];
+            reinterpret_cast<float4*>(orow)[i] = make_float4(a.x * inv * g.x, a.y * inv * g.y, a.z * inv * g.z,
+                                                             a.w * inv * g.w);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = xr[i] * inv * w[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void rf_rms_norm_short_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ w, float* out, int n,
+                                                                float eps, int rows) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* xr = x + (size_t)r * n;
+    float v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int i = lane + 64 * k;
+        v[k] = i < n ? xr[i] : 0.0f;
+        ss += v[k] * v[k];
+    }
+    ss = wave_sum_all(ss);
+    const float inv = rsqrtf(ss / (float)n + eps);
+    float* orow = out + (size_t)r * n;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int i = lane + 64 * k;
+        if (i < n) orow[i] = v[k] * inv * w[i];
+    }
+}
+
+static hipError_t rms_rows(const float* x, const float* w, float* out, int n, float eps, int rows, hipStream_t st) {
+    if (x == nullptr || w == nullptr || out == nullptr || n <= 0 || rows <= 0) return hipErrorInvalidValue;
+    if (n <= 512)
+        hipLaunchKernelGGL(rf_rms_norm_short_kernel, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, out, n, eps, rows);
+    else
+        hipLaunchKernelGGL(rf_rms_norm_long_kernel, dim3(rows), dim3(256), 0, st, x, w, out, n, eps, rows);
+    return hipGetLastError();
+}
+
+// ---- RoPE over heads (in place) ---------------------------------------------------
+__global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, int pos0, int nh, int d, float base,
+                                     int neox, const float* __restrict__ freq_scale, int seq_len) {
+    const int half = d / 2;
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    const int s = blockIdx.y;
+    if (p >= nh * half || s >= seq_len) return;
+    const int pos = (pos_ptr ? *pos_ptr : pos0) + s;
+    const int head = p / half, i = p % half;
+    float* row = x + (size_t)s * nh * d + (size_t)head * d;
+    int i0, i1;
+    pair_idx(i, d, neox, &i0, &i1);
+    float x0 = row[i0], x1 = row[i1];
+    rope_pair(x0, x1, pos, rope_theta(i, d, base, freq_scale));
+    row[i0] = x0;
+    row[i1] = x1;
+}
+
+static hipError_t rope_heads(float* x, const int* pos_ptr, int pos, int nh, int d, float base, int neox,
+                             const float* fs, int seq_len, hipStream_t st) {
+    if (x == nullptr || nh <= 0 || d <= 0 || (d & 1) || seq_len <= 0) return hipErrorInvalidValue;
+    const int pairs = nh * (d / 2);
+    hipLaunchKernelGGL(rf_rope_heads_kernel, dim3((pairs + 255) / 256, seq_len), dim3(256), 0, st, x, pos_ptr, pos, nh,
+                       d, base, neox, fs, seq_len);
+    return hipGetLastError();
+}
+
+// ---- KV cache writes ------------------------------------------------------------------
+// Cache layout [max_seq][n_kv * d] fp16 per layer; V copied, K rotated.
+__global__ void rf_kv_write_rope_kernel(__half* kc, __half* vc, const float* __restrict__ k,
+                                        const float* __restrict__ v, const int* __restrict__ pos_ptr, int pos0,
+                                        int nkv, int d, float base, int neox, const float* __restrict__ freq_scale) {
+    const int half = d / 2;
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nkv * half) return;
+    const int pos = pos_ptr ? *pos_ptr : pos0;
+    const int head = p / half, i = p % half;
+    int i0, i1;
+    pair_idx(i, d, neox, &i0, &i1);
+    const size_t base_in = (size_t)head * d;
+    const size_t base_c = (size_t)pos * nkv * d + base_in;
+    float x0 = k[base_in + i0], x1 = k[base_in + i1];
+    rope_pair(x0, x1, pos, rope_theta(i, d, base, freq_scale));
+    kc[base_c + i0] = __float2half(x0);
+    kc[base_c + i1] = __float2half(x1);
+    vc[base_c + i0] = __float2half(v[base_in + i0]);
+    vc[base_c + i1] = __float2half(v[base_in + i1]);
+}
+
+__global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* __restrict__ k,
+                                           const float* __restrict__ v, int start_pos, int kv_size, int seq_len) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int s = blockIdx.y;
+    if (i >= kv_size || s >= seq_len) return;
+    const size_t c = (size_t)(start_pos + s) * kv_size + i, in = (size_t)s * kv_size + i;
+    kc[c] = __float2half(k[in]);
+    vc[c] = __float2half(v[in]);
+}
+
+// ---- fused Qwen3 decode step: Q/K RMSNorm, RoPE, KV write ----------------------------
+// One wave per head: heads [0, nh) are query heads (normalised with
+// q_norm when given, rotated, written back in place), heads [nh, nh + nkv)
+// key heads (normalised with k_norm, rotated, written to the K cache at
+// *pos as fp16; the matching V head is copied to the V cache).  The
+// arithmetic of each step is that of the separate launchers.
+__global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
+    float* q, const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ q_norm,
+    const float* __restrict__ k_norm, __half* kc, __half* vc, const int* __restrict__ pos_ptr, int nh, int nkv, int d,
+    float eps, float base, int neox, const float* __restrict__ freq_scale) {
+    const int lane = threadIdx.x & 63;
+    const int hidx = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (hidx >= nh + nkv) return;
+    const bool is_q = hidx < nh;
+    const int head = is_q ? hidx : hidx - nh;
+    const float* src = is_q ? q + (size_t)head * d : k + (size_t)head * d;
+    const float* g = is_q ? q_norm : k_norm;
+    const int half = d / 2;
+    const int pos = *pos_ptr;
+    // lane holds pairs lane, lane + 64, ... (d <= 512)
+    float a[4], b[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int p = lane + 64 * t;
+        int i0, i1;
+        pair_idx(p < half ? p : 0, d, neox, &i0, &i1);
+        a[t] = p < half ? src[i0] : 0.0f;
+        b[t] = p < half ? src[i1] : 0.0f;
+        ss += a[t] * a[t] + b[t] * b[t];
+    }
+    float inv = 0.0f;
+    if (g != nullptr) inv = rsqrtf(wave_sum_all(ss) / (float)d + eps);
+    const size_t cbase = (size_t)pos * nkv * d + (size_t)head * d;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int p = lane + 64 * t;
+        if (p >= half) break;
+        int i0, i1;
+        pair_idx(p, d, neox, &i0, &i1);
+        float x0 = a[t], x1 = b[t];
+        if (g != nullptr) {
+            x0 = x0 * inv * g[i0];
+            x1 = x1 * inv * g[i1];
+        }
+        rope_pair(x0, x1, pos, rope_theta(p, d, base, freq_scale));
+        if (is_q) {
+            q[(size_t)head * d + i0] = x0;
+            q[(size_t)head * d + i1] = x1;
+        } else {
+            kc[cbase + i0] = __float2half(x0);
+            kc[cbase + i1] = __float2half(x1);
+            vc[cbase + i0] = __float2half(v[(size_t)head * d + i0]);
+            vc[cbase + i1] = __float2half(v[(size_t)head * d + i1]);
+        }
+    }
+}
+
+// ---- decode attention -----------------------------------------------------------------
+// One workgroup (4 waves) per query head.  Scores: LPP lanes per position
+// (8 fp16 of K per lane, one 16-byte load), so a wave-instruction covers
+// 64 / LPP positions with coalesced K rows; the partial dots are reduced
+// across the LPP lanes with shuffles.  Scores go to LDS in chunks of
+// kAttnChunk positions; each chunk's max/exp/sum and its pass over V
+// (lane pairs of output dims, positions split over the waves) update a
+// running (m, l, acc) exactly as an online softmax over chunks.
+constexpr int kAttnChunk = 4096;
+
+template <int LPP>
+__global__ __launch_bounds__(256) void rf_attn_decode_kernel(float* __restrict__ out, const float* __restrict__ q,
+                                                             const __half* __restrict__ kc,
+                                                             const __half* __restrict__ vc,
+                                                             const int* __restrict__ len_ptr, int len0, int nh,
+                                                             int nkv, float scale) {
+    constexpr int D = LPP * 8;
+    constexpr int PPW = 64 / LPP;                 // positions per wave-instruction
+    constexpr int DPL = (D + 127) / 128;          // output dim pairs per lane in the V pass
+    __shared__ float sc[kAttnChunk];
+    __shared__ float red[4][D];
+    __shared__ float wred[8];
+    const int seq = len_ptr ? *len_ptr : len0;
+    const int head = blockIdx.x;
+    const int kvh = head / (nh / nkv);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row = (size_t)nkv * D;
+    const __half* kh = kc + (size_t)kvh * D;
+    const __half* vh = vc + (size_t)kvh * D;
+    // this lane's 8 query values (dims 8 (lane % LPP) ..)
+    float qv[8];
+    {
+        const float* qh = q + (size_t)head * D + 8 * (lane % LPP);
+        const float4 a = *reinterpret_cast<const float4*>(qh), b = *reinterpret_cast<const float4*>(qh + 4);
+        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+    }
+    float m_run = kNegMax, l_run = 0.0f;
+    float acc[DPL * 2];
+#pragma unroll
+    for (int i = 0; i < DPL * 2; ++i) acc[i] = 0.0f;
+
+    for (int c0 = 0; c0 < seq; c0 += kAttnChunk) {
+        const int cn = min(kAttnChunk, seq - c0);
+        // scores
+        for (int p0 = wave * PPW; p0 < cn; p0 += 4 * PPW) {
+            const int p = p0 + lane / LPP;
+            float s = 0.0f;
+            if (p < cn) {
+                const u32x4 kk = *reinterpret_cast<const u32x4*>(kh + (size_t)(c0 + p) * row + 8 * (lane % LPP));
+                const uint32_t w4[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const __half2 h2 = __builtin_bit_cast(__half2, w4[t]);
+                    const float2 f = __half22float2(h2);
+                    s += qv[2 * t] * f.x + qv[2 * t + 1] * f.y;
+                }
+            }
+#pragma unroll
+            for (int o = LPP / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+            if (p < cn && lane % LPP == 0) sc[p] = s * scale;
+        }
+        __syncthreads();
+        // chunk max
+        float mx = kNegMax;
+        for (int i = threadIdx.x; i < cn; i += 256) mx = fmaxf(mx, sc[i]);
+        mx = wave_max(mx);
+        if (lane == 0) wred[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+        const float m_new = fmaxf(m_run, mx);
+        float ls = 0.0f;
+        for (int i = threadIdx.x; i < cn; i += 256) {
+            const float e = expf(sc[i] - m_new);
+            sc[i] = e;
+            ls += e;
+        }
+        ls = wave_sum_all(ls);
+        __syncthreads();   // wred reads done, exps published
+        if (lane == 0) wred[4 + wave] = ls;
+        __syncthreads();
+        const float alpha = expf(m_run - m_new);
+        l_run = l_run * alpha + ((wred[4] + wred[5]) + (wred[6] + wred[7]));
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < DPL * 2; ++i) acc[i] *= alpha;
+        // V pass: wave w takes positions w, w + 4, ...; lane holds dims 2 (lane + 64 j) .. + 1
+        for (int p = wave; p < cn; p += 4) {
+            const float e = sc[p];
+            const __half* vr = vh + (size_t)(c0 + p) * row;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                const int dd = 2 * (lane + 64 * j);
+                if (dd < D) {
+                    const float2 f = __half22float2(*reinterpret_cast<const __half2*>(vr + dd));
+                    acc[2 * j] += e * f.x;
+                    acc[2 * j + 1] += e * f.y;
+                }
+            }
+        }
+        __syncthreads();   // sc reused by the next chunk
+    }
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+        const int dd = 2 * (lane + 64 * j);
+        if (dd < D) {
+            red[wave][dd] = acc[2 * j];
+            red[wave][dd + 1] = acc[2 * j + 1];
+        }
+    }
+    __syncthreads();
+    const float inv_l = 1.0f / l_run;
+    for (int dd = threadIdx.x; dd < D; dd += 256)
+        out[(size_t)head * D + dd] = ((red[0][dd] + red[1][dd]) + (red[2][dd] + red[3][dd])) * inv_l;
+}
+
+static hipError_t attn_decode(float* out, const float* q, const __half* kc, const __half* vc, const int* len_ptr,
+                              int len, int nh, int nkv, int d, float scale, hipStream_t st) {
+    if (out == nullptr || q == nullptr || kc == nullptr || vc == nullptr) return hipErrorInvalidValue;
+    if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || (len_ptr == nullptr && len <= 0)) return hipErrorInvalidValue;
+    switch (d) {
+    case 64: hipLaunchKernelGGL(rf_attn_decode_kernel<8>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len, nh,
+                                nkv, scale); break;
+    case 128: hipLaunchKernelGGL(rf_attn_decode_kernel<16>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len,
+                                 nh, nkv, scale); break;
+    case 256: hipLaunchKernelGGL(rf_attn_decode_kernel<32>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len,
+                                 nh, nkv, scale); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- argmax (ties: the larger index) -----------------------------------------------------
+constexpr int kArgmaxItems = 1024;   // per partial (the caller sizes partials as ceil(n / 1024))
+
+__device__ __forceinline__ void amax_take(float v, int i, float& bv, int& bi) {
+    if (v > bv || (v == bv && i > bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void amax_block(float& bv, int& bi, float* sv, int* si) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_take(__shfl_xor(bv, o), __shfl_xor(bi, o), bv, bi);
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int w = 1; w < 4; ++w) amax_take(sv[w], si[w], bv, bi);
+}
+
+__global__ __launch_bounds__(256) void rf_argmax_stage1_kernel(const float* __restrict__ x, float* pv, int* pi, int n) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    float bv = kNegMax;
+    int bi = 0;
+    const int base = blockIdx.x * kArgmaxItems;
+#pragma unroll
+    for (int t = 0; t < kArgmaxItems / 256; ++t) {
+        const int i = base + threadIdx.x + 256 * t;
+        if (i < n) amax_take(x[i], i, bv, bi);
+    }
+    amax_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+    }
+}
+
+__global__ __launch_bounds__(256) void rf_argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                              int* out, int np) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    float bv = kNegMax;
+    int bi = 0;
+    for (int i = threadIdx.x; i < np; i += 256) amax_take(pv[i], pi[i], bv, bi);
+    amax_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) *out = bi;
+}
+
+// ---- Q4_K embedding rows ---------------------------------------------------------------
+// One 256-thread workgroup per (super-block, token): thread t dequantises
+// element t.  Tokens outside [0, vocab) leave their row untouched.
+__global__ __launch_bounds__(256) void rf_embed_q4k_kernel(const uint8_t* __restrict__ emb,
+                                                           const int* __restrict__ ids, int id0, float* out,
+                                                           int hidden, int vocab) {
+    const int s = blockIdx.y;
+    const int tok = ids ? ids[s] : id0;
+    if (tok < 0 || tok >= vocab) return;
+    const int nb = hidden / kQK;
+    const uint8_t* blk = emb + ((size_t)tok * nb + blockIdx.x) * kQ4KBytes;
+    const int t = threadIdx.x;
+    const int j = t / 32;                 // sub-block
+    const uint8_t* sc = blk + 4;
+    int scl, mn;
+    if (j < 4) {
+        scl = sc[j] & 63;
+        mn = sc[j + 4] & 63;
+    } else {
+        scl = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+        mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+    const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+    const float dmin = half_bits_to_float(blk[2] | (blk[3] << 8));
+    const uint8_t qb = blk[16 + 32 * (j >> 1) + (t & 31)];
+    const int nib = (j & 1) ? (qb >> 4) : (qb & 15);
+    out[(size_t)s * hidden + blockIdx.x * kQK + t] = d * (float)scl * (float)nib - dmin * (float)mn;
+}
+
+// ---- elementwise ----------------------------------------------------------------------------
+__global__ void rf_add_kernel(const float* __restrict__ x, const float* __restrict__ y, float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = x[i] + y[i];
+}
+__global__ void rf_mul_kernel(const float* __restrict__ x, const float* __restrict__ y, float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = x[i] * y[i];
+}
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__global__ void rf_silu_kernel(const float* __restrict__ x, float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_f(x[i]);
+}
+__global__ void rf_silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_f(g[i]) * u[i];
+}
+__global__ void rf_f32_to_f16_kernel(const float* __restrict__ x, __half* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = __float2half(x[i]);
+}
+__global__ void rf_inc_state_kernel(int* st) {
+    // vector stores only (one lane)
+    if (threadIdx.x == 0) {
+        const int a = st[0], b = st[1];
+        st[0] = a + 1;
+        st[1] = b + 1;
+    }
+}
+
+static inline dim3 grid1(int n) { return dim3((unsigned)((n + 255) / 256)); }
+
+}  // namespace rf
+
+using namespace rf;
+
+// ---- RMSNorm ----
+extern "C" hipError_t gpu_rms_norm(const float* d_x, const float* d_weight, float* d_out, const int n, const float eps,
+                                   hipStream_t stream) {
+    return rms_rows(d_x, d_weight, d_out, n, eps, 1, stream);
+}
+extern "C" hipError_t gpu_rms_norm_batched_on_stream(const float* d_x, const float* d_weight, float* d_out, const int n,
+                                                     const float eps, const int seq_len, hipStream_t stream) {
+    return rms_rows(d_x, d_weight, d_out, n, eps, seq_len, stream);
+}
+extern "C" hipError_t gpu_rms_norm_batched(const float* d_x, const float* d_weight, float* d_out, const int n,
+                                           const float eps, const int seq_len) {
+    return rms_rows(d_x, d_weight, d_out, n, eps, seq_len, nullptr);
+}
+
+// ---- RoPE ----
+extern "C" hipError_t gpu_rope_heads_scaled(float* d_x, const int pos, const int num_heads, const int head_dim,
+                                            const float theta_base, const int neox, const float* d_freq_scale,
+                                            hipStream_t stream) {
+    return rope_heads(d_x, nullptr, pos, num_heads, head_dim, theta_base, neox, d_freq_scale, 1, stream);
+}
+extern "C" hipError_t gpu_rope_heads(float* d_x, const int pos, const int num_heads, const int head_dim,
+                                     const float theta_base, const int neox, hipStream_t stream) {
+    return rope_heads(d_x, nullptr, pos, num_heads, head_dim, theta_base, neox, nullptr, 1, stream);
+}
+extern "C" hipError_t gpu_rope_heads_state_scaled(float* d_x, const int* d_pos, const int num_heads,
+                                                  const int head_dim, const float theta_base, const int neox,
+                                                  const float* d_freq_scale, hipStream_t stream) {
+    if (d_pos == nullptr) return hipErrorInvalidValue;
+    return rope_heads(d_x, d_pos, 0, num_heads, head_dim, theta_base, neox, d_freq_scale, 1, stream);
+}
+extern "C" hipError_t gpu_rope_heads_state(float* d_x, const int* d_pos, const int num_heads, const int head_dim,
+                                           const float theta_base, const int neox, hipStream_t stream) {
+    if (d_pos == nullptr) return hipErrorInvalidValue;
+    return rope_heads(d_x, d_pos, 0, num_heads, head_dim, theta_base, neox, nullptr, 1, stream);
+}
+extern "C" hipError_t gpu_rope_heads_batched_scaled(float* d_x, const int start_pos, const int num_heads,
+                                                    const int head_dim, const float theta_base, const int seq_len,
+                                                    const int neox, const float* d_freq_scale) {
+    return rope_heads(d_x, nullptr, start_pos, num_heads, head_dim, theta_base, neox, d_freq_scale, seq_len, nullptr);
+}
+extern "C" hipError_t gpu_rope_heads_batched(float* d_x, const int start_pos, const int num_heads, const int head_dim,
+                                             const float theta_base, const int seq_len, const int neox) {
+    return rope_heads(d_x, nullptr, start_pos, num_heads, head_dim, theta_base, neox, nullptr, seq_len, nullptr);
+}
+extern "C" hipError_t rf_rope_heads_batched_on_stream(float* d_x, const int start_pos, const int num_heads,
+                                                      const int head_dim, const float theta_base, const int seq_len,
+                                                      const int neox, const float* d_freq_scale, hipStream_t stream) {
+    return rope_heads(d_x, nullptr, start_pos, num_heads, head_dim, theta_base, neox, d_freq_scale, seq_len, stream);
+}
+
+// ---- KV writes ----
+static hipError_t kv_write_rope(uint16_t* kc, uint16_t* vc, const float* k, const float* v, const int* pos_ptr, int pos,
+                                int nkv, int d, float base, int neox, const float* fs, hipStream_t st) {
+    if (kc == nullptr || vc == nullptr || k == nullptr || v == nullptr || nkv <= 0 || d <= 0 || (d & 1))
+        return hipErrorInvalidValue;
+    const int pairs = nkv * (d / 2);
+    hipLaunchKernelGGL(rf_kv_write_rope_kernel, grid1(pairs), dim3(256), 0, st, reinterpret_cast<__half*>(kc),
+                       reinterpret_cast<__half*>(vc), k, v, pos_ptr, pos, nkv, d,
+                       base, neox, fs);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_kv_write_rope_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                               const int pos, const int num_kv_heads, const int head_dim,
+                                               const float theta_base, const int neox, const float* d_freq_scale,
+                                               hipStream_t stream) {
+    return kv_write_rope(d_k_cache, d_v_cache, d_k, d_v, nullptr, pos, num_kv_heads, head_dim, theta_base, neox,
+                         d_freq_scale, stream);
+}
+extern "C" hipError_t gpu_kv_write_rope(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                        const int pos, const int num_kv_heads, const int head_dim,
+                                        const float theta_base, const int neox, hipStream_t stream) {
+    return kv_write_rope(d_k_cache, d_v_cache, d_k, d_v, nullptr, pos, num_kv_heads, head_dim, theta_base, neox,
+                         nullptr, stream);
+}
+extern "C" hipError_t gpu_kv_write_rope_state_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k,
+                                                     const float* d_v, const int* d_pos, const int num_kv_heads,
+                                                     const int head_dim, const float theta_base, const int neox,
+                                                     const float* d_freq_scale, hipStream_t stream) {
+    if (d_pos == nullptr) return hipErrorInvalidValue;
+    return kv_write_rope(d_k_cache, d_v_cache, d_k, d_v, d_pos, 0, num_kv_heads, head_dim, theta_base, neox,
+                         d_freq_scale, stream);
+}
+extern "C" hipError_t gpu_kv_write_rope_state(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                              const int* d_pos, const int num_kv_heads, const int head_dim,
+                                              const float theta_base, const int neox, hipStream_t stream) {
+    if (d_pos == nullptr) return hipErrorInvalidValue;
+    return kv_write_rope(d_k_cache, d_v_cache, d_k, d_v, d_pos, 0, num_kv_heads, head_dim, theta_base, neox, nullptr,
+                         stream);
+}
+extern "C" hipError_t rf_kv_write_batched_on_stream(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k,
+                                                    const float* d_v, const int start_pos, const int kv_size,
+                                                    const int max_seq, const int seq_len, hipStream_t stream) {
+    if (d_k_cache == nullptr || d_v_cache == nullptr || d_k == nullptr || d_v == nullptr || kv_size <= 0 ||
+        seq_len <= 0 || start_pos < 0 || start_pos + seq_len > max_seq)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_kv_write_batched_kernel, dim3((kv_size + 255) / 256, seq_len), dim3(256), 0, stream,
+                       reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache), d_k, d_v, start_pos,
+                       kv_size, seq_len);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_kv_write_batched(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
+                                           const int start_pos, const int kv_size, const int max_seq,
+                                           const int seq_len) {
+    return rf_kv_write_batched_on_stream(d_k_cache, d_v_cache, d_k, d_v, start_pos, kv_size, max_seq, seq_len,
+                                         nullptr);
+}
+
+extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const float* d_v,
+                                                     const float* d_q_norm, const float* d_k_norm, uint16_t* d_k_cache,
+                                                     uint16_t* d_v_cache, const int* d_pos, const int num_heads,
+                                                     const int num_kv_heads, const int head_dim, const float eps,
+                                                     const float theta_base, const int neox,
+                                                     const float* d_freq_scale, hipStream_t stream) {
+    if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_k_cache == nullptr || d_v_cache == nullptr ||
+        d_pos == nullptr || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || (head_dim & 1) ||
+        head_dim > 512)
+        return hipErrorInvalidValue;
+    const int heads = num_heads + num_kv_heads;
+    hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel, dim3((heads + 3) / 4), dim3(256), 0, stream, d_q, d_k, d_v,
+                       d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
+                       d_pos, num_heads, num_kv_heads, head_dim, eps,
+                       theta_base, neox, d_freq_scale);
+    return hipGetLastError();
+}
+
+// ---- decode attention ----
+extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                               const uint16_t* d_v_cache, const int seq_len,
+                                                               const int num_heads, const int num_kv_heads,
+                                                               const int head_dim, const float scale,
+                                                               hipStream_t stream) {
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), nullptr, seq_len, num_heads, num_kv_heads, head_dim, scale,
+                       stream);
+}
+extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_out, const float* d_q,
+                                                                     const uint16_t* d_k_cache, const uint16_t* d_v_cache,
+                                                                     const int* d_seq_len, const int num_heads,
+                                                                     const int num_kv_heads, const int head_dim,
+                                                                     const float scale, hipStream_t stream) {
+    if (d_seq_len == nullptr) return hipErrorInvalidValue;
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim, scale,
+                       stream);
+}
+
+// ---- argmax ----
+extern "C" hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_partial_values, int* d_partial_indices,
+                                               int* d_output_index, const int n, hipStream_t stream) {
+    if (d_input == nullptr || d_partial_values == nullptr || d_partial_indices == nullptr ||
+        d_output_index == nullptr || n <= 0)
+        return hipErrorInvalidValue;
+    const int np = (n + kArgmaxItems - 1) / kArgmaxItems;
+    hipLaunchKernelGGL(rf_argmax_stage1_kernel, dim3(np), dim3(256), 0, stream, d_input, d_partial_values,
+                       d_partial_indices, n);
+    hipLaunchKernelGGL(rf_argmax_final_kernel, dim3(1), dim3(256), 0, stream, d_partial_values, d_partial_indices,
+                       d_output_index, np);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_argmax_f32(const float* d_input, float* d_partial_values, int* d_partial_indices,
+                                     int* d_output_index, const int n) {
+    return gpu_argmax_f32_on_stream(d_input, d_partial_values, d_partial_indices, d_output_index, n, nullptr);
+}
+
+// ---- embeddings ----
+extern "C" hipError_t gpu_embed_q4_k_token(const uint8_t* d_embedding, float* d_out, const int hidden_size,
+                                           const int vocab_size, const int token_id, hipStream_t stream) {
+    if (d_embedding == nullptr || d_out == nullptr || hidden_size <= 0 || vocab_size <= 0 || token_id < 0 ||
+        token_id >= vocab_size || hidden_size % kQK != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_embed_q4k_kernel, dim3(hidden_size / kQK, 1), dim3(256), 0, stream, d_embedding, nullptr,
+                       token_id, d_out, hidden_size, vocab_size);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_embed_q4_k_batch(const uint8_t* d_embedding, const int* d_token_ids, float* d_out,
+                                           const int hidden_size, const int vocab_size, const int seq_len,
+                                           hipStream_t stream) {
+    if (d_embedding == nullptr || d_token_ids == nullptr || d_out == nullptr || hidden_size <= 0 || vocab_size <= 0 ||
+        seq_len <= 0 || hidden_size % kQK != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_embed_q4k_kernel, dim3(hidden_size / kQK, seq_len), dim3(256), 0, stream, d_embedding,
+                       d_token_ids, 0, d_out, hidden_size, vocab_size);
+    return hipGetLastError();
+}
+
+// ---- elementwise ----
+extern "C" hipError_t gpu_add(const float* d_x, const float* d_y, float* d_out, const int n, hipStream_t stream) {
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_add_kernel, grid1(n), dim3(256), 0, stream, d_x, d_y, d_out, n);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_mul_on_stream(const float* d_x, const float* d_y, float* d_out, const int n,
+                                        hipStream_t stream) {
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_mul_kernel, grid1(n), dim3(256), 0, stream, d_x, d_y, d_out, n);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_silu_on_stream(const float* d_x, float* d_out, const int n, hipStream_t stream) {
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_silu_kernel, grid1(n), dim3(256), 0, stream, d_x, d_out, n);
+    return hipGetLastError();
+}
+extern "C" hipError_t rf_silu_mul_on_stream(const float* d_gate, const float* d_up, float* d_out, const int n,
+                                            hipStream_t stream) {
+    if (d_gate == nullptr || d_up == nullptr || d_out == nullptr || n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_silu_mul_kernel, grid1(n), dim3(256), 0, stream, d_gate, d_up, d_out, n);
+    return hipGetLastError();
+}
+extern "C" hipError_t convert_f32_to_f16(const float* input, void* output, int n, hipStream_t stream) {
+    if (input == nullptr || output == nullptr || n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_f32_to_f16_kernel, grid1(n), dim3(256), 0, stream, input, static_cast<__half*>(output), n);
+    return hipGetLastError();
+}
+extern "C" hipError_t gpu_increment_decode_state_on_stream(int* d_state, hipStream_t stream) {
+    if (d_state == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_inc_state_kernel, dim3(1), dim3(64), 0, stream, d_state);
+    return hipGetLastError();
+}

@@ -1,0 +1,253 @@
+"""GPU parity of the layer operations around the matmuls (model_ops.hip),
+through the C ABI, against the oracle (oracle/qk_oracle.c or_rms_norm ..
+or_argmax, pinned in tests/test_oracle_ops.py).
+
+Bars: bit-exact for integer and conversion work (argmax index, fp16 V
+copies, f32->f16, the decode-state counter); fp32 arithmetic against the
+float64 oracle at REL = 1e-5 of the output's max magnitude (per element,
+plus 1e-5 relative), the fp16 K cache within one fp16 ulp of the oracle's
+rounded value (the fp32 rotation may sit either side of a rounding
+boundary), and the Q4_K embedding at 2 fp32 ulps of the f64 dequant.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests import gpu_util as G
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+
+
+def _close(y, ref, what, rel=REL):
+    y = np.asarray(y, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    scale = np.abs(ref).max()
+    err = np.abs(y - ref)
+    bad = err > rel * scale + rel * np.abs(ref)
+    print(f"{what}: max err {err.max() / scale:.3e} of max|ref|", flush=True)
+    assert not bad.any(), f"{what}: {bad.sum()} elements off, worst {err.max() / scale:.3e}"
+
+
+def _call0(fn, *args):
+    """Launchers whose reference signature has no stream (null stream)."""
+    print(f"[gpu] {fn.__name__}", flush=True)
+    assert fn(*args) == 0
+    torch.cuda.synchronize()
+
+
+def _f16_ulps(got_bits, ref):
+    got = got_bits.view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    return np.abs(got - ref) / np.maximum(ulp, 2.0 ** -24)
+
+
+@pytest.mark.parametrize("n,rows", [(4096, 1), (128, 40), (4096, 70), (12288, 3), (100, 9), (1000, 2)])
+def test_rms_norm(rf, dev, n, rows):
+    rng = np.random.default_rng(n + rows)
+    x = (rng.standard_normal(n * rows) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    dx, dw = G.to_dev(x), G.to_dev(w)
+    out = G.empty(n * rows, torch.float32)
+    if rows == 1:
+        G.call(rf.gpu_rms_norm, G.ptr(dx), G.ptr(dw), G.ptr(out), n, 1e-6)
+    else:
+        G.call(rf.gpu_rms_norm_batched_on_stream, G.ptr(dx), G.ptr(dw), G.ptr(out), n, 1e-6, rows)
+    _close(G.host(out), O.rms_norm(x, w, 1e-6, rows), f"rms_norm {n}x{rows}")
+    # in place (the per-head Q/K norms write back into q / k)
+    _call0(rf.gpu_rms_norm_batched, G.ptr(dx), G.ptr(dw), G.ptr(dx), n, 1e-6, rows)
+    np.testing.assert_array_equal(G.host(dx), G.host(out))
+
+
+@pytest.mark.parametrize("neox", [1, 0])
+@pytest.mark.parametrize("pos", [0, 7, 639, 40000])
+def test_rope_heads(rf, dev, neox, pos):
+    nh, d = 32, 128
+    rng = np.random.default_rng(pos + neox)
+    x = rng.standard_normal(nh * d).astype(np.float32)
+    ref = O.rope(x, 1, nh, d, pos, 1e6, bool(neox))
+    dx = G.to_dev(x)
+    G.call(rf.gpu_rope_heads, G.ptr(dx), pos, nh, d, 1e6, neox)
+    _close(G.host(dx), ref, f"rope pos {pos} neox {neox}")
+    # state variant reads the position from device memory; freq_scale divides theta
+    fs = (1.0 + rng.random(d // 2)).astype(np.float32)
+    dx, dpos, dfs = G.to_dev(x), G.to_dev(np.array([pos, pos + 1], np.int32)), G.to_dev(fs)
+    G.call(rf.gpu_rope_heads_state_scaled, G.ptr(dx), G.ptr(dpos), nh, d, 1e6, neox, G.ptr(dfs))
+    _close(G.host(dx), O.rope(x, 1, nh, d, pos, 1e6, bool(neox), fs), f"rope state scaled pos {pos}")
+
+
+def test_rope_heads_batched(rf, dev):
+    seq, nh, d = 33, 8, 128
+    x = np.random.default_rng(9).standard_normal(seq * nh * d).astype(np.float32)
+    dx = G.to_dev(x)
+    _call0(rf.gpu_rope_heads_batched, G.ptr(dx), 5, nh, d, 1e4, seq, 1)
+    _close(G.host(dx), O.rope(x, seq, nh, d, 5, 1e4, True), "rope batched")
+    dx = G.to_dev(x)
+    G.call(rf.rf_rope_heads_batched_on_stream, G.ptr(dx), 5, nh, d, 1e4, seq, 0, None)
+    _close(G.host(dx), O.rope(x, seq, nh, d, 5, 1e4, False), "rope batched on stream, classic")
+
+
+@pytest.mark.parametrize("state", [False, True])
+def test_kv_write_rope(rf, dev, state):
+    nkv, d, max_seq, pos = 8, 128, 64, 37
+    rng = np.random.default_rng(11)
+    k = rng.standard_normal(nkv * d).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    kc = G.to_dev(np.full(max_seq * nkv * d, 0x7E00, np.uint16))    # NaN fill: untouched rows stay NaN
+    vc = G.to_dev(np.full(max_seq * nkv * d, 0x7E00, np.uint16))
+    dk, dv = G.to_dev(k), G.to_dev(v)
+    if state:
+        dpos = G.to_dev(np.array([pos, pos + 1], np.int32))
+        G.call(rf.gpu_kv_write_rope_state, G.ptr(kc), G.ptr(vc), G.ptr(dk), G.ptr(dv), G.ptr(dpos), nkv, d, 1e6, 1)
+    else:
+        G.call(rf.gpu_kv_write_rope, G.ptr(kc), G.ptr(vc), G.ptr(dk), G.ptr(dv), pos, nkv, d, 1e6, 1)
+    kc, vc = G.host(kc).reshape(max_seq, -1), G.host(vc).reshape(max_seq, -1)
+    np.testing.assert_array_equal(vc[pos], v.astype(np.float16).view(np.uint16))
+    assert (_f16_ulps(kc[pos], O.rope(k, 1, nkv, d, pos, 1e6, True)) <= 1.0).all()
+    others = np.delete(np.arange(max_seq), pos)
+    assert (kc[others] == 0x7E00).all() and (vc[others] == 0x7E00).all()
+
+
+def test_kv_write_batched(rf, dev):
+    kv, max_seq, start, seq = 1024, 80, 9, 40
+    rng = np.random.default_rng(12)
+    k = rng.standard_normal(seq * kv).astype(np.float32)
+    v = rng.standard_normal(seq * kv).astype(np.float32)
+    kc, vc = G.empty(max_seq * kv, torch.int16), G.empty(max_seq * kv, torch.int16)
+    dk, dv = G.to_dev(k), G.to_dev(v)           # held: a temporary's block would be reused by the next copy
+    _call0(rf.gpu_kv_write_batched, G.ptr(kc), G.ptr(vc), G.ptr(dk), G.ptr(dv), start, kv, max_seq, seq)
+    kc, vc = G.host(kc).view(np.uint16).reshape(max_seq, kv), G.host(vc).view(np.uint16).reshape(max_seq, kv)
+    np.testing.assert_array_equal(kc[start:start + seq], k.astype(np.float16).view(np.uint16).reshape(seq, kv))
+    np.testing.assert_array_equal(vc[start:start + seq], v.astype(np.float16).view(np.uint16).reshape(seq, kv))
+    # beyond the cache: rejected before any launch
+    import ctypes
+    p = ctypes.c_void_p(0x100000)               # never dereferenced: the range check rejects first
+    assert rf.gpu_kv_write_batched(p, p, p, p, 50, kv, max_seq, seq) != 0
+
+
+@pytest.mark.parametrize("with_norm", [True, False])
+@pytest.mark.parametrize("neox", [1, 0])
+def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox):
+    # the one-launch Qwen3 step against the oracle, and against the separate launchers
+    nh, nkv, d, max_seq, pos = 32, 8, 128, 700, 641
+    rng = np.random.default_rng(13 + neox)
+    q = (rng.standard_normal(nh * d) * 4).astype(np.float32)
+    k = (rng.standard_normal(nkv * d) * 4).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    dq, dk, dv, dqn, dkn = (G.to_dev(a) for a in (q, k, v, qn, kn))
+    kc, vc = G.empty(max_seq * nkv * d, torch.int16), G.empty(max_seq * nkv * d, torch.int16)
+    dpos = G.to_dev(np.array([pos, pos + 1], np.int32))
+    G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn) if with_norm else None,
+           G.ptr(dkn) if with_norm else None, G.ptr(kc), G.ptr(vc), G.ptr(dpos), nh, nkv, d, 1e-6, 1e6, neox, None)
+    qr = O.rms_norm(q, qn, 1e-6, nh) if with_norm else q.astype(np.float64)
+    kr = O.rms_norm(k, kn, 1e-6, nkv) if with_norm else k.astype(np.float64)
+    _close(G.host(dq), O.rope(qr, 1, nh, d, pos, 1e6, bool(neox)), "fused q")
+    kc_h = G.host(kc).view(np.uint16).reshape(max_seq, -1)
+    vc_h = G.host(vc).view(np.uint16).reshape(max_seq, -1)
+    assert (_f16_ulps(kc_h[pos], O.rope(kr, 1, nkv, d, pos, 1e6, bool(neox))) <= 1.0).all()
+    np.testing.assert_array_equal(vc_h[pos], v.astype(np.float16).view(np.uint16))
+    # same results as norm + rope + kv_write launched separately
+    dq2, dk2 = G.to_dev(q), G.to_dev(k)
+    kc2, vc2 = G.empty(max_seq * nkv * d, torch.int16), G.empty(max_seq * nkv * d, torch.int16)
+    if with_norm:
+        G.call(rf.gpu_rms_norm_batched_on_stream, G.ptr(dq2), G.ptr(dqn), G.ptr(dq2), d, 1e-6, nh)
+        G.call(rf.gpu_rms_norm_batched_on_stream, G.ptr(dk2), G.ptr(dkn), G.ptr(dk2), d, 1e-6, nkv)
+    G.call(rf.gpu_rope_heads_state, G.ptr(dq2), G.ptr(dpos), nh, d, 1e6, neox)
+    G.call(rf.gpu_kv_write_rope_state, G.ptr(kc2), G.ptr(vc2), G.ptr(dk2), G.ptr(dv), G.ptr(dpos), nkv, d, 1e6, neox)
+    a, b = G.host(dq), G.host(dq2)
+    assert np.abs(a - b).max() <= 4 * np.spacing(np.abs(b).max())
+    kc2_h = G.host(kc2).view(np.uint16).reshape(max_seq, -1)
+    assert (np.abs(kc_h[pos].view(np.float16).astype(np.float64) - kc2_h[pos].view(np.float16).astype(np.float64))
+            <= np.spacing(np.abs(kc2_h[pos].view(np.float16))).astype(np.float64)).all()
+
+
+@pytest.mark.parametrize("seq,nh,nkv,d", [(1, 32, 8, 128), (2, 32, 8, 128), (100, 32, 8, 128), (640, 32, 8, 128),
+                                          (5000, 32, 8, 128), (300, 16, 16, 64), (257, 8, 2, 256)])
+def test_attn_decode(rf, dev, seq, nh, nkv, d):
+    rng = np.random.default_rng(seq + d)
+    max_seq = seq + 3
+    q = rng.standard_normal(nh * d).astype(np.float32)
+    kc = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.uint16)
+    scale = 1.0 / math.sqrt(d)
+    ref = O.attn_decode(q, kc, vc, seq, nh, nkv, d, scale)
+    dq, dkc, dvc = G.to_dev(q), G.to_dev(kc.view(np.int16)), G.to_dev(vc.view(np.int16))
+    out = G.empty(nh * d, torch.float32)
+    G.call(rf.gpu_flash_attn_decode_strided_multi_head, G.ptr(out), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), seq, nh, nkv,
+           d, scale)
+    _close(G.host(out), ref, f"attn decode seq {seq} d {d}")
+    out2 = G.empty(nh * d, torch.float32)
+    dlen = G.to_dev(np.array([seq], np.int32))
+    G.call(rf.gpu_flash_attn_decode_strided_multi_head_state, G.ptr(out2), G.ptr(dq), G.ptr(dkc), G.ptr(dvc),
+           G.ptr(dlen), nh, nkv, d, scale)
+    np.testing.assert_array_equal(G.host(out2), G.host(out))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1024, 1025, 151936])
+def test_argmax(rf, dev, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    cases = [x]
+    if n > 10:
+        t = x.copy()
+        t[[3, n // 2, n - 2]] = 50.0           # ties: the larger index
+        c = x.copy()
+        c[5] = np.nan
+        c[7] = np.inf
+        cases += [t, c, np.full(n, -np.inf, np.float32)]
+    np_ = (n + 1023) // 1024
+    for c in cases:
+        dx = G.to_dev(c)
+        pv, pi, out = G.empty(np_, torch.float32), G.empty(np_, torch.int32), G.empty(1, torch.int32)
+        G.call(rf.gpu_argmax_f32_on_stream, G.ptr(dx), G.ptr(pv), G.ptr(pi), G.ptr(out), n)
+        assert int(G.host(out)[0]) == O.argmax(c)
+
+
+def test_embed_q4_k(rf, dev):
+    from rocmforge_amd import synth
+    hidden, vocab = 4096, 300
+    emb = synth.q4_k_weights(vocab, hidden, seed=21)
+    de = G.to_dev(emb)
+    out = G.empty(hidden, torch.float32)
+    G.call(rf.gpu_embed_q4_k_token, G.ptr(de), G.ptr(out), hidden, vocab, 123)
+    ref = O.q4k_dequant(emb[123], hidden // 256)
+    np.testing.assert_allclose(G.host(out), ref, rtol=2.5e-7, atol=1e-12)
+    ids = np.array([0, 299, 5, -1, 300, 123], np.int32)
+    outb = G.to_dev(np.full(len(ids) * hidden, 7.0, np.float32))
+    dids = G.to_dev(ids)
+    G.call(rf.gpu_embed_q4_k_batch, G.ptr(de), G.ptr(dids), G.ptr(outb), hidden, vocab, len(ids))
+    ob = G.host(outb).reshape(len(ids), hidden)
+    for s, t in enumerate(ids):
+        if 0 <= t < vocab:
+            np.testing.assert_allclose(ob[s], O.q4k_dequant(emb[t], hidden // 256), rtol=2.5e-7, atol=1e-12)
+        else:
+            assert (ob[s] == 7.0).all()       # out-of-range ids leave the row untouched
+    assert rf.gpu_embed_q4_k_token(G.ptr(de), G.ptr(out), hidden, vocab, vocab, None) != 0
+
+
+def test_elementwise(rf, dev):
+    n = 12288 + 5
+    rng = np.random.default_rng(31)
+    a = (rng.standard_normal(n) * 4).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    da, db, out = G.to_dev(a), G.to_dev(b), G.empty(n, torch.float32)
+    G.call(rf.gpu_add, G.ptr(da), G.ptr(db), G.ptr(out), n)
+    np.testing.assert_array_equal(G.host(out), a + b)
+    G.call(rf.gpu_mul_on_stream, G.ptr(da), G.ptr(db), G.ptr(out), n)
+    np.testing.assert_array_equal(G.host(out), a * b)
+    G.call(rf.gpu_silu_on_stream, G.ptr(da), G.ptr(out), n)
+    _close(G.host(out), O.silu_mul(a, np.ones(n, np.float32)), "silu")
+    G.call(rf.rf_silu_mul_on_stream, G.ptr(da), G.ptr(db), G.ptr(out), n)
+    _close(G.host(out), O.silu_mul(a, b), "silu_mul")
+    h = G.empty(n, torch.int16)
+    G.call(rf.convert_f32_to_f16, G.ptr(da), G.ptr(h), n)
+    np.testing.assert_array_equal(G.host(h).view(np.uint16), a.astype(np.float16).view(np.uint16))
+    st = G.to_dev(np.array([4, 5], np.int32))
+    G.call(rf.gpu_increment_decode_state_on_stream, G.ptr(st))
+    assert list(G.host(st)) == [5, 6]
