@@ -319,6 +319,14 @@ hipError_t convert_f32_to_f16(const float* input, void* output, int n, hipStream
 hipError_t rf_silu_mul_on_stream(const float* d_gate, const float* d_up, float* d_out, const int n,
                                  hipStream_t stream);
 
+/* hip_kernels/wmma/wmma_attention_prefill.hip:711 -- causal (or full) GQA
+ * attention over seq_len % 64 == 0 rows: Q [seq][nq*128], K, V [seq][nkv*128]
+ * fp16 bits, 16-byte aligned; O [seq][nq*128] fp32.  The reference's
+ * rounding: fp32 S, 64-key tiles, P rounded to fp16 per tile, fp32 O. */
+hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K, const void* V, float* O,
+                                                    int seq_len, int num_q_heads, int num_kv_heads, int causal,
+                                                    float scale, hipStream_t stream);
+
 /* ---- Parity probes (no reference counterpart) ---------------------------
  * Expose the intermediate integers of the Q8-inline path so tests can check
  * them bit-exactly.  They run the same device code as the GEMV. */

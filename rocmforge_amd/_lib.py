@@ -57,6 +57,7 @@ SIGNATURES = {
     "rf_silu_mul_on_stream": [_vp, _vp, _vp, _i, _vp],
     "gpu_increment_decode_state_on_stream": [_vp, _vp],
     "convert_f32_to_f16": [_vp, _vp, _i, _vp],
+    "wmma_attention_prefill_gqa_causal_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],
     "rf_q4_k_q8_int_dots_launch": [_vp, _vp, _vp, _i, _i, _vp],
 }

@@ -730,3 +730,168 @@ extern "C" hipError_t gpu_increment_decode_state_on_stream(int* d_state, hipStre
     hipLaunchKernelGGL(rf_inc_state_kernel, dim3(1), dim3(64), 0, stream, d_state);
     return hipGetLastError();
 }
+
+// ---- prefill attention (causal, GQA), fp16 operands on MFMA ---------------------------
+// Drop-in for wmma_attention_prefill_gqa_causal_launch
+// (hip_kernels/wmma/wmma_attention_prefill.hip:711-750): Q [seq][nq*128],
+// K, V [seq][nkv*128] fp16, O [seq][nq*128] fp32, seq % 64 == 0.  Same
+// arithmetic as the reference: S = Q K^T accumulated in fp32 and scaled;
+// keys in tiles of 64 with a running row max m; P = fp16(exp(S - m_new))
+// for the tile, l = l * alpha + sum of the unrounded exps, O = O * alpha +
+// P V (fp32 accumulate), out = O / l.
+//
+// Workgroup: 4 waves over 128 queries of one head (wave w: queries
+// q0 + 32w ..), sharing the head's K tile ([key][dim]) and transposed V
+// tile ([dim][key]) in LDS.  Each wave computes S^T = K Q^T (two 32x32
+// blocks of v_mfma_f32_32x32x16_f16, Q^T from registers), so a lane owns
+// one query column: the row max / sum are in-lane plus one exchange with
+// lane ^ 32, alpha is a per-lane scale of the O^T accumulators, and the
+// accumulator values of P feed the B operand of O^T = V^T P^T directly --
+// the key order they come in is matched by the order the V^T operand is
+// read in.
+namespace rf {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int kAttD = 128;
+constexpr int kKStr = kAttD + 8;     // K tile row stride (halves)
+constexpr int kVStr = 64 + 8;        // V^T tile row stride (halves)
+
+__global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
+                                                              const _Float16* __restrict__ K,
+                                                              const _Float16* __restrict__ V, float* __restrict__ O,
+                                                              int seq, int nq, int nkv, int causal, float scale) {
+    __shared__ __align__(16) _Float16 ks[64 * kKStr];
+    __shared__ __align__(16) _Float16 vt[kAttD * kVStr];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int head = blockIdx.y;
+    const int kvh = head / (nq / nkv);
+    const int qb = blockIdx.x * 128;
+    const int q0 = qb + 32 * wave;
+    const int hi = lane >> 5, col = lane & 31;
+    const size_t qrow = (size_t)nq * kAttD, kvrow = (size_t)nkv * kAttD;
+    const bool active = q0 < seq;
+
+    // Q^T operands of this lane's query: dims 16 ks + 8 hi .. + 7
+    h8 qf[8];
+#pragma unroll
+    for (int ks_ = 0; ks_ < 8; ++ks_) {
+        if (active)
+            qf[ks_] = *reinterpret_cast<const h8*>(Q + (size_t)(q0 + col) * qrow + (size_t)head * kAttD + 16 * ks_ +
+                                                   8 * hi);
+        else
+            qf[ks_] = h8{};
+    }
+    f16v o[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[b][e] = 0.0f;
+    float m = kNegMax, l = 0.0f;
+    const int query = q0 + col;
+
+    const int wg_last_q = min(qb + 127, seq - 1);
+    const int ntiles = causal ? wg_last_q / 64 + 1 : seq / 64;
+    const int wave_tiles = causal ? (q0 + 31) / 64 + 1 : seq / 64;
+    for (int t = 0; t < ntiles; ++t) {
+        const int t0 = 64 * t;
+        __syncthreads();   // previous tile's reads done
+        // K tile: 64 keys x 128 dims, 16-byte chunks; V tile transposed
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i;          // 0..1023
+            const int key = c >> 4, d8 = (c & 15) * 8;
+            const h8 kv = *reinterpret_cast<const h8*>(K + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
+            *reinterpret_cast<h8*>(&ks[key * kKStr + d8]) = kv;
+            const h8 vv = *reinterpret_cast<const h8*>(V + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vt[(d8 + j) * kVStr + key] = vv[j];
+        }
+        __syncthreads();
+        if (!active || t >= wave_tiles) continue;
+
+        // S^T = K Q^T: blocks b = keys 32 b .. + 31
+        f16v s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[b][e] = 0.0f;
+#pragma unroll
+            for (int ks_ = 0; ks_ < 8; ++ks_) {
+                const h8 a = *reinterpret_cast<const h8*>(&ks[(32 * b + col) * kKStr + 16 * ks_ + 8 * hi]);
+                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks_], s[b], 0, 0, 0);
+            }
+        }
+        // scale, mask, tile max
+        float tmax = kNegMax;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = t0 + 32 * b + 8 * (e >> 2) + 4 * hi + (e & 3);
+                float v = s[b][e] * scale;
+                if (causal && key > query) v = kNegMax;
+                s[b][e] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m, tmax);
+        const float alpha = expf(m - m_new);
+        float rs = 0.0f;
+        h8 p[4];   // B operands, k-step j = (block j / 2, keys 16 (j % 2) ..)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float ex = expf(s[b][e] - m_new);
+                rs += ex;
+                p[2 * b + (e >> 3)][e & 7] = (_Float16)ex;
+            }
+        rs += __shfl_xor(rs, 32);
+        l = l * alpha + rs;
+        m = m_new;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[b][e] *= alpha;
+        // O^T += V^T P^T: A operand lane (dim = 32 bd + col) keys of k-step j in
+        // the accumulator order: 32 (j/2) + 16 (j%2) + 4 hi + {0..3, 8..11}
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kb = 32 * (j >> 1) + 16 * (j & 1) + 4 * hi;
+#pragma unroll
+            for (int bd = 0; bd < 4; ++bd) {
+                const _Float16* vr = &vt[(32 * bd + col) * kVStr + kb];
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 lo = *reinterpret_cast<const h4*>(vr);
+                const h4 hi4 = *reinterpret_cast<const h4*>(vr + 8);
+                const h8 a = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                o[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[j], o[bd], 0, 0, 0);
+            }
+        }
+    }
+    if (!active) return;
+    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+    float* orow = O + (size_t)query * qrow + (size_t)head * kAttD;
+#pragma unroll
+    for (int bd = 0; bd < 4; ++bd)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) orow[32 * bd + 8 * (e >> 2) + 4 * hi + (e & 3)] = o[bd][e] * inv_l;
+}
+
+}  // namespace rf
+
+extern "C" hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K, const void* V, float* O,
+                                                               int seq_len, int num_q_heads, int num_kv_heads,
+                                                               int causal, float scale, hipStream_t stream) {
+    if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr) return hipErrorInvalidValue;
+    if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return hipErrorInvalidValue;
+    if (seq_len <= 0 || seq_len % 64 != 0) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) & 15u)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf::rf_attn_prefill_kernel, dim3((seq_len + 127) / 128, num_q_heads), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+                       static_cast<const _Float16*>(V), O, seq_len, num_q_heads, num_kv_heads, causal, scale);
+    return hipGetLastError();
+}

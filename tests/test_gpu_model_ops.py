@@ -251,3 +251,37 @@ def test_elementwise(rf, dev):
     st = G.to_dev(np.array([4, 5], np.int32))
     G.call(rf.gpu_increment_decode_state_on_stream, G.ptr(st))
     assert list(G.host(st)) == [5, 6]
+
+
+# fp16 operands: P rounded per tile may land on the other side of an fp16
+# rounding boundary than the oracle's; the GEMM bar applies
+PREFILL_REL = 2e-3
+
+
+@pytest.mark.parametrize("seq,nq,nkv,causal", [(64, 2, 1, 1), (128, 4, 2, 1), (512, 32, 8, 1), (192, 4, 4, 0),
+                                               (320, 8, 2, 1)])
+def test_attn_prefill(rf, dev, seq, nq, nkv, causal):
+    rng = np.random.default_rng(seq + nq)
+    d = 128
+    q = rng.standard_normal(seq * nq * d).astype(np.float32)
+    k = rng.standard_normal(seq * nkv * d).astype(np.float32)
+    v = rng.standard_normal(seq * nkv * d).astype(np.float32)
+    scale = 1.0 / math.sqrt(d)
+    dq, dk, dv = (G.to_dev(a.astype(np.float16).view(np.int16)) for a in (q, k, v))
+    out = G.empty(seq * nq * d, torch.float32)
+    G.call(rf.wmma_attention_prefill_gqa_causal_launch, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(out), seq, nq, nkv,
+           causal, scale)
+    got = G.host(out).reshape(seq, nq, d)
+    if causal:
+        ref = O.attn_prefill_f16(q, k, v, seq, nq, nkv, d, scale).reshape(seq, nq, d)
+    else:
+        # full attention of query r = the causal oracle's last row with q[r] there
+        rows = [0, 63, 64, seq - 1]
+        got = got[rows]
+        ref = np.empty((len(rows), nq, d))
+        for i, r in enumerate(rows):
+            qq = np.tile(q.reshape(seq, -1)[r], (seq, 1))
+            ref[i] = O.attn_prefill_f16(qq, k, v, seq, nq, nkv, d, scale).reshape(seq, nq, d)[-1]
+    err = np.abs(got - ref)
+    print(f"prefill attention seq {seq}: max err {err.max() / np.abs(ref).max():.3e}", flush=True)
+    assert (err <= PREFILL_REL * np.abs(ref).max() + PREFILL_REL * np.abs(ref)).all()
