@@ -1,0 +1,355 @@
+"""A llama/qwen-style model on the library's kernels: prefill and greedy
+decode, the decode step capturable as one HIP graph.
+
+The layer order is the reference's GPU decode step
+(src/gpu/forward.rs:2327-2535): RMSNorm -> QKV (fused when all Q4_K) ->
+per-head Q/K RMSNorm + RoPE + fp16 KV write -> attention -> O projection
+with the residual -> RMSNorm -> fused gate/up + SwiGLU -> down projection
+with the residual; then the output norm, the LM head and a greedy argmax
+(forward.rs:290-376).  Decode reads the position from device memory
+(state = {pos, seq_len}, advanced by a kernel at the end of the step), so a
+captured step replays for every token.  Prefill follows
+gpu_prefill_layer_forward_hybrid (forward.rs:886-1198): GEMMs over rows
+padded to 64, batched norms / RoPE / KV write, the MFMA prefill attention,
+residual adds, and the LM head on the last row.
+
+Weights come from a GGUF file (gguf.load_model) or are generated on the
+device from a seed in the Q4_K_M type mix (synthetic_weights).  Everything
+runs through the C ABI of librocmforge_cdna4.so; there is no other
+implementation to fall back to.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+from . import _lib, ops
+from .ops import GgmlType, TensorRole, WeightMeta
+
+
+@dataclass
+class ModelConfig:
+    n_layers: int
+    hidden: int
+    ff: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    vocab: int
+    eps: float = 1e-6
+    rope_base: float = 1e6
+    neox: bool = True
+    qk_norm: bool = True
+
+    @property
+    def q_size(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def kv_size(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    @classmethod
+    def qwen3_8b(cls) -> "ModelConfig":
+        return cls(36, 4096, 12288, 32, 8, 128, 151936)
+
+    @classmethod
+    def from_gguf(cls, f) -> "ModelConfig":
+        m = f.metadata
+        arch = m.architecture
+        return cls(m.block_count(), m.embedding_length(), m.feed_forward_length(), m.attention_head_count(),
+                   m.attention_head_count_kv() or m.attention_head_count(), m.head_dim(),
+                   m.vocab_size() or f.desc("token_embd.weight").dims[1], m.rms_norm_eps(1e-6),
+                   m.rope_freq_base(1e6 if arch == "qwen3" else 1e4), arch in ("qwen2", "qwen3"),
+                   f.has_tensor("blk.0.attn_q_norm.weight"))
+
+
+@dataclass
+class Layer:
+    attn_norm: object
+    ffn_norm: object
+    mats: dict            # name -> (uint8 device tensor, WeightMeta)
+    q_norm: object = None
+    k_norm: object = None
+
+
+@dataclass
+class Weights:
+    token_emb: tuple
+    output_norm: object
+    lm_head: tuple
+    layers: list
+
+
+def weights_from_gguf(f, device="cuda:0") -> Weights:
+    from . import gguf
+    mw = gguf.load_model(f, device)
+    layers = [Layer(lw.attn_norm, lw.ffn_norm, dict(lw.matrices), lw.attn_q_norm, lw.attn_k_norm)
+              for lw in mw.layers]
+    return Weights(mw.token_emb, mw.output_norm, mw.lm_head, layers)
+
+
+def synthetic_weights(cfg: ModelConfig, seed: int = 0, device="cuda:0") -> Weights:
+    """Seeded random weights of the configuration in the Q4_K_M type mix
+    (Q6_K attn_v / ffn_down on the layers gguf.q4_k_m_uses_q6_k picks and
+    Q6_K output.weight), generated in device memory."""
+    import torch
+
+    from . import synth
+    from .gguf import q4_k_m_uses_q6_k
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    s = [seed * 7919]
+
+    def mat(n, k, q6=False):
+        s[0] += 1
+        fmt = "q6_k" if q6 else "q4_k"
+        w = synth.torch_weights(fmt, n, k, seed=s[0], device=device).reshape(-1)
+        return w, WeightMeta(GgmlType.Q6_K if q6 else GgmlType.Q4_K, [k, n])
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, device=device, generator=gen)).float()
+
+    h, kv, q = cfg.hidden, cfg.kv_size, cfg.q_size
+    layers = []
+    for i in range(cfg.n_layers):
+        q6 = q4_k_m_uses_q6_k(i, cfg.n_layers)
+        mats = {"attn_q": mat(q, h), "attn_k": mat(kv, h), "attn_v": mat(kv, h, q6), "attn_output": mat(h, q),
+                "ffn_gate": mat(cfg.ff, h), "ffn_up": mat(cfg.ff, h), "ffn_down": mat(h, cfg.ff, q6)}
+        layers.append(Layer(norm(h), norm(h), mats, norm(cfg.head_dim) if cfg.qk_norm else None,
+                            norm(cfg.head_dim) if cfg.qk_norm else None))
+    emb = mat(cfg.vocab, h)
+    lm_w, lm_meta = mat(cfg.vocab, h, True)
+    lm_meta.role = TensorRole.LM_HEAD
+    return Weights(emb, norm(h), (lm_w, lm_meta), layers)
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _chk(rc, what):
+    if rc != 0:
+        raise ops.HipApiError(rc, what)
+
+
+class Engine:
+    """Prefill + greedy decode of one sequence of up to max_seq tokens."""
+
+    def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0"):
+        import torch
+        self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
+        self.lib = _lib.load()
+        ops._lib()
+        f32, i16 = torch.float32, torch.int16
+        z = lambda n, dt=f32: torch.zeros(n, dtype=dt, device=device)
+        c = cfg
+        self.kc = [z(max_seq * c.kv_size, i16) for _ in range(c.n_layers)]
+        self.vc = [z(max_seq * c.kv_size, i16) for _ in range(c.n_layers)]
+        self.hidden, self.normed = z(c.hidden), z(c.hidden)
+        self.q, self.k, self.v, self.attn = z(c.q_size), z(c.kv_size), z(c.kv_size), z(c.q_size)
+        self.act, self.tmp, self.logits = z(c.ff), z(c.hidden), z(c.vocab)
+        n_part = (c.vocab + 1023) // 1024
+        self.part_v, self.part_i = z(n_part), z(n_part, torch.int32)
+        self.token = z(1, torch.int32)
+        self.state = z(2, torch.int32)      # {pos, seq_len}
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+        self._graph = None
+        self._pf = None
+
+    # ---- decode ---------------------------------------------------------------------------
+    def _stream(self):
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def decode_launches(self, trace=None):
+        """One token: reads self.token and self.state, writes the next token
+        into self.token and advances the state.  trace(name, layer) is called
+        after each operation when given (eager runs only)."""
+        import torch
+        L, c, st = self.lib, self.cfg, self._stream()
+        t = trace or (lambda name, layer: None)
+        _chk(L.gpu_embed_q4_k_batch(_p(self.w.token_emb[0]), _p(self.token), _p(self.hidden), c.hidden, c.vocab, 1,
+                                    st), "embed")
+        t("embed", -1)
+        pos_p = _p(self.state)
+        len_p = ctypes.c_void_p(self.state.data_ptr() + 4)
+        for i, lw in enumerate(self.w.layers):
+            m = lw.mats
+            _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.attn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+            t("attn_norm", i)
+            ops.gpu_dispatch_fused_qkv_on_stream(m["attn_q"][0], m["attn_q"][1], None, m["attn_k"][0], m["attn_k"][1],
+                                                 None, m["attn_v"][0], m["attn_v"][1], None, self.normed, self.q,
+                                                 self.k, self.v, c.q_size, c.kv_size, c.hidden, st)
+            t("qkv", i)
+            _chk(L.rf_qk_norm_rope_kv_write_state(_p(self.q), _p(self.k), _p(self.v), _p(lw.q_norm), _p(lw.k_norm),
+                                                  _p(self.kc[i]), _p(self.vc[i]), pos_p, c.n_heads, c.n_kv_heads,
+                                                  c.head_dim, c.eps, c.rope_base, int(c.neox), None, st), "qk_rope_kv")
+            t("qk_rope_kv", i)
+            _chk(L.gpu_flash_attn_decode_strided_multi_head_state(_p(self.attn), _p(self.q), _p(self.kc[i]),
+                                                                  _p(self.vc[i]), len_p, c.n_heads, c.n_kv_heads,
+                                                                  c.head_dim, self.scale, st), "attention")
+            t("attention", i)
+            self._residual_gemv(m["attn_output"], self.attn, c.q_size, st)
+            t("attn_output", i)
+            _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.ffn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+            t("ffn_norm", i)
+            ops.gpu_dispatch_fused_gate_up_on_stream(m["ffn_gate"][0], m["ffn_gate"][1], m["ffn_up"][0],
+                                                     m["ffn_up"][1], self.normed, self.act, c.ff, c.hidden, st)
+            t("gate_up", i)
+            self._residual_gemv(m["ffn_down"], self.act, c.ff, st)
+            t("ffn_down", i)
+        _chk(L.gpu_rms_norm(_p(self.hidden), _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+        t("output_norm", -1)
+        ops.gpu_dispatch_gemv_on_stream(self.w.lm_head[0], self.w.lm_head[1], self.normed, self.logits, c.vocab,
+                                        c.hidden, st)
+        t("lm_head", -1)
+        _chk(L.gpu_argmax_f32_on_stream(_p(self.logits), _p(self.part_v), _p(self.part_i), _p(self.token), c.vocab,
+                                        st), "argmax")
+        _chk(L.gpu_increment_decode_state_on_stream(_p(self.state), st), "state")
+        t("argmax", -1)
+
+    def _residual_gemv(self, wm, x, k, st):
+        """hidden += W x: the fused residual kernels (Q4_K through the
+        dispatch arm, Q6_K through its residual launcher), else GEMV + add."""
+        w, meta = wm
+        c = self.cfg
+        if meta.wtype == GgmlType.Q6_K:
+            _chk(self.lib.gemv_q6_k_f32_residual_launch(_p(w), _p(x), _p(self.hidden), _p(self.hidden), k, c.hidden,
+                                                        st), "q6_k residual")
+            return
+        if not ops.gpu_dispatch_gemv_residual_on_stream(w, meta, x, self.hidden, self.hidden, k, c.hidden, st):
+            ops.gpu_dispatch_gemv_on_stream(w, meta, x, self.tmp, c.hidden, k, st)
+            _chk(self.lib.gpu_add(_p(self.hidden), _p(self.tmp), _p(self.hidden), c.hidden, st), "add")
+
+    def capture_decode(self):
+        """Capture one decode step as a graph (after one eager warm-up step
+        on the capture stream, whose effect on the state is undone)."""
+        import torch
+        s = torch.cuda.Stream()
+        saved = (self.token.clone(), self.state.clone(), [k.clone() for k in self.kc], [v.clone() for v in self.vc])
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.decode_launches()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.token.copy_(saved[0])
+        self.state.copy_(saved[1])
+        for a, b in zip(self.kc + self.vc, saved[2] + saved[3]):
+            a.copy_(b)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self.decode_launches()
+        torch.cuda.synchronize()
+        self._graph = g
+        return g
+
+    def decode(self, n: int, graph: bool = True) -> list:
+        """n greedy steps from the current token/state; returns the tokens
+        produced (each step's argmax), reading them back once at the end."""
+        import torch
+        if self.state.cpu()[0].item() + n > self.max_seq:
+            raise ValueError("sequence would exceed max_seq")
+        out = torch.empty(n, dtype=torch.int32, device=self.dev)
+        if graph and self._graph is None:
+            self.capture_decode()
+        for i in range(n):
+            if graph:
+                self._graph.replay()
+            else:
+                self.decode_launches()
+            out[i:i + 1].copy_(self.token)
+        torch.cuda.synchronize()
+        return out.cpu().tolist()
+
+    # ---- prefill ------------------------------------------------------------------------------
+    def _prefill_buffers(self, mp):
+        import torch
+        if self._pf is not None and self._pf["mp"] >= mp:
+            return self._pf
+        c = self.cfg
+        z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device=self.dev)
+        self._pf = {"mp": mp, "x": z(mp * c.hidden), "xn": z(mp * c.hidden), "q": z(mp * c.q_size),
+                    "k": z(mp * c.kv_size), "v": z(mp * c.kv_size), "q16": z(mp * c.q_size, torch.int16),
+                    "k16": z(mp * c.kv_size, torch.int16), "v16": z(mp * c.kv_size, torch.int16),
+                    "att": z(mp * c.q_size), "tmp": z(mp * c.hidden), "g": z(mp * c.ff), "u": z(mp * c.ff),
+                    "ids": z(mp, torch.int32)}
+        return self._pf
+
+    def prefill(self, tokens, trace=None) -> int:
+        """Runs the prompt (positions 0..M-1), fills the KV caches, sets the
+        state to {M, M + 1} and self.token to the greedy next token, which
+        it returns."""
+        import torch
+        L, c = self.lib, self.cfg
+        M = len(tokens)
+        if M < 1 or M > self.max_seq:
+            raise ValueError("prompt length out of range")
+        mp = -(-M // 64) * 64
+        b = self._prefill_buffers(mp)
+        t = trace or (lambda name, layer: None)
+        st = self._stream()
+        for key in ("x", "q", "k", "v"):
+            b[key].zero_()
+        b["ids"][:M].copy_(torch.as_tensor(tokens, dtype=torch.int32))
+        _chk(L.gpu_embed_q4_k_batch(_p(self.w.token_emb[0]), _p(b["ids"]), _p(b["x"]), c.hidden, c.vocab, M, st),
+             "embed")
+        t("embed", -1)
+        for i, lw in enumerate(self.w.layers):
+            m = lw.mats
+            _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn"]), c.hidden, c.eps, mp,
+                                                  st), "norm")
+            for name, out, n in (("attn_q", b["q"], c.q_size), ("attn_k", b["k"], c.kv_size),
+                                 ("attn_v", b["v"], c.kv_size)):
+                self._gemm(m[name], b["xn"], out, n, c.hidden, M, st)
+            t("qkv", i)
+            if lw.q_norm is not None:
+                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["q"]), _p(lw.q_norm), _p(b["q"]), c.head_dim, c.eps,
+                                                      M * c.n_heads, st), "q norm")
+                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["k"]), _p(lw.k_norm), _p(b["k"]), c.head_dim, c.eps,
+                                                      M * c.n_kv_heads, st), "k norm")
+            _chk(L.rf_rope_heads_batched_on_stream(_p(b["q"]), 0, c.n_heads, c.head_dim, c.rope_base, M, int(c.neox),
+                                                   None, st), "rope q")
+            _chk(L.rf_rope_heads_batched_on_stream(_p(b["k"]), 0, c.n_kv_heads, c.head_dim, c.rope_base, M,
+                                                   int(c.neox), None, st), "rope k")
+            _chk(L.rf_kv_write_batched_on_stream(_p(self.kc[i]), _p(self.vc[i]), _p(b["k"]), _p(b["v"]), 0,
+                                                 c.kv_size, self.max_seq, M, st), "kv write")
+            t("qk_rope_kv", i)
+            for src, dst, n in (("q", "q16", mp * c.q_size), ("k", "k16", mp * c.kv_size),
+                                ("v", "v16", mp * c.kv_size)):
+                _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), n, st), "to f16")
+            _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(b["k16"]), _p(b["v16"]), _p(b["att"]),
+                                                           mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
+                 "attention")
+            t("attention", i)
+            self._gemm(m["attn_output"], b["att"], b["tmp"], c.hidden, c.q_size, M, st)
+            _chk(L.gpu_add(_p(b["x"]), _p(b["tmp"]), _p(b["x"]), M * c.hidden, st), "add")
+            t("attn_output", i)
+            _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp, st),
+                 "norm")
+            self._gemm(m["ffn_gate"], b["xn"], b["g"], c.ff, c.hidden, M, st)
+            self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
+            _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
+            t("gate_up", i)
+            self._gemm(m["ffn_down"], b["g"], b["tmp"], c.hidden, c.ff, M, st)
+            _chk(L.gpu_add(_p(b["x"]), _p(b["tmp"]), _p(b["x"]), M * c.hidden, st), "add")
+            t("ffn_down", i)
+        last = ctypes.c_void_p(b["x"].data_ptr() + 4 * (M - 1) * c.hidden)
+        _chk(L.gpu_rms_norm(last, _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+        ops.gpu_dispatch_gemv_on_stream(self.w.lm_head[0], self.w.lm_head[1], self.normed, self.logits, c.vocab,
+                                        c.hidden, st)
+        _chk(L.gpu_argmax_f32_on_stream(_p(self.logits), _p(self.part_v), _p(self.part_i), _p(self.token), c.vocab,
+                                        st), "argmax")
+        self.state.copy_(torch.tensor([M, M + 1], dtype=torch.int32))
+        t("lm_head", -1)
+        torch.cuda.synchronize()
+        return int(self.token.item())
+
+    def _gemm(self, wm, a, out, n, k, m, st):
+        """out[m_pad x n] = a[m_pad x k] W^T through the prefill GEMM launchers
+        (rows padded to 64; the padding rows of a are zero)."""
+        w, meta = wm
+        mp = -(-m // 64) * 64
+        fn = self.lib.wmma_gemm_q4_k_launch if meta.wtype == GgmlType.Q4_K else self.lib.wmma_gemm_q6_k_launch
+        _chk(fn(_p(a), _p(w), _p(out), mp, n, k, st), "gemm")
