@@ -23,6 +23,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -44,6 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end leg (config 4)")
     ap.add_argument("--no-stream", action="store_true", help="skip the full decode weight stream leg (config 2)")
     ap.add_argument("--stream-tokens", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -317,6 +320,49 @@ def cpu_baseline(seconds):
     }
 
 
+def bench_e2e(torch, prompt_len=512, steps=128):
+    """Qwen3-8B-shaped greedy generation (36 layers, hidden
+    4096, FFN 12288, 32 q / 8 kv heads of 128, per-head Q/K RMSNorm, vocab
+    151936, Q4_K_M type mix, seeded random weights): a 512-token prompt,
+    then 128 decode steps replayed from one captured HIP graph."""
+    from rocmforge_amd import engine as E
+    cfg = E.ModelConfig.qwen3_8b()
+    w = E.synthetic_weights(cfg, seed=0)
+    eng = E.Engine(cfg, w, max_seq=prompt_len + steps + 64)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, cfg.vocab, prompt_len)]
+    eng.prefill(prompt)                                   # warm
+    eng.capture_decode()
+    times = []
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.prefill(prompt)
+        times.append(time.perf_counter() - t0)
+    t_pf = min(times)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    eng._graph.replay()                                   # one warm replay, then back to the prompt's end
+    eng.prefill(prompt)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        eng._graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_tok = start.elapsed_time(end) / steps
+    stream_bytes = sum(t[0].numel() for lw in w.layers for t in lw.mats.values()) + w.lm_head[0].numel()
+    return {
+        "workload": "BASELINE config 4: Qwen3-8B-shaped greedy decode, Q4_K_M mix, seeded random weights",
+        "prefill_tokens": prompt_len, "prefill_ms": round(t_pf * 1e3, 3),
+        "prefill_tok_s": round(prompt_len / t_pf, 1),
+        "decode_steps": steps, "decode_ms_per_token": round(ms_tok, 4),
+        "decode_tok_s": round(1e3 / ms_tok, 1),
+        "decode_weight_bytes_per_token": int(stream_bytes),
+        "decode_weight_GBps": round(stream_bytes / (ms_tok * 1e-3) / 1e9, 1),
+        "note": "prefill wall time includes host launch of every kernel (no graph); decode timed with HIP "
+                "events over graph replays",
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -366,6 +412,8 @@ def main():
         out["prefill_gemm"] = bench_gemm(lib, torch)
     if not args.no_stream:
         out["decode_stream"] = bench_decode_stream(lib, torch, args.stream_tokens)
+    if not args.no_e2e:
+        out["e2e_qwen3_8b"] = bench_e2e(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
 }
 
 // ---- decode attention -----------------------------------------------------------------
-// One workgroup (4 waves) per query head.  Scores: LPP lanes per position
+// Single-workgroup path (GQA groups larger than 8): one workgroup (4 waves) per query head.  Scores: LPP lanes per position
 // (8 fp16 of K per lane, one 16-byte load), so a wave-instruction covers
 // 64 / LPP positions with coalesced K rows; the partial dots are reduced
 // across the LPP lanes with shuffles.  Scores go to LDS in chunks of
@@ -378,18 +378,235 @@ __global__ __launch_bounds__(256) void rf_attn_decode_kernel(float* __restrict__
         out[(size_t)head * D + dd] = ((red[0][dd] + red[1][dd]) + (red[2][dd] + red[3][dd])) * inv_l;
 }
 
+// Split decode attention (the path used when the GQA group is at most 8
+// query heads).  Grid = (kv head, split); a workgroup has one wave per
+// query head of the kv head's group, so the group's K/V rows are read once
+// per workgroup (the other waves hit L1).  Positions go out in chunks of
+// kSplitChunk, chunk c to split c mod S, each wave keeping an online
+// (m, l, acc) over its chunks.  Within a chunk a wave issues all its K and
+// V loads (LPP lanes x 16 bytes per position, 64 / LPP positions per
+// instruction) before the first use, so the loads overlap.  The partial
+// (m, l, acc) of every (head, split) goes to a workspace and a second
+// kernel merges the S partials of each head (rows of D + 4 floats: acc, m, l):
+//   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s.
+constexpr int kSplitChunk = 32;
+
+template <int LPP>
+__global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restrict__ q,
+                                                            const __half* __restrict__ kc,
+                                                            const __half* __restrict__ vc,
+                                                            const int* __restrict__ len_ptr, int len0, int nh,
+                                                            int nkv, float scale, float* __restrict__ ws, int S) {
+    constexpr int D = LPP * 8;
+    constexpr int PPW = 64 / LPP;
+    constexpr int NI = kSplitChunk / PPW;       // load instructions per chunk (K and V each)
+    const int seq = len_ptr ? *len_ptr : len0;
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int head = kvh * (nh / nkv) + wave;
+    const size_t row = (size_t)nkv * D;
+    const int sub = lane % LPP, grp = lane / LPP;
+    const __half* kh = kc + (size_t)kvh * D + 8 * sub;
+    const __half* vh = vc + (size_t)kvh * D + 8 * sub;
+    float qv[8];
+    {
+        const float* qh = q + (size_t)head * D + 8 * sub;
+        const float4 a = *reinterpret_cast<const float4*>(qh), b = *reinterpret_cast<const float4*>(qh + 4);
+        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+    }
+    float m = kNegMax, l = 0.0f, acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (int c0 = split * kSplitChunk; c0 < seq; c0 += S * kSplitChunk) {
+        u32x4 kk[NI], vv[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int p = c0 + i * PPW + grp;
+            const bool ok = p < seq;
+            kk[i] = ok ? *reinterpret_cast<const u32x4*>(kh + (size_t)p * row) : u32x4{0, 0, 0, 0};
+            vv[i] = ok ? *reinterpret_cast<const u32x4*>(vh + (size_t)p * row) : u32x4{0, 0, 0, 0};
+        }
+        float sc[NI];
+        float cm = kNegMax;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t w4[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+            float t = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 f = __half22float2(__builtin_bit_cast(__half2, w4[u]));
+                t += qv[2 * u] * f.x + qv[2 * u + 1] * f.y;
+            }
+#pragma unroll
+            for (int o = LPP / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            sc[i] = (c0 + i * PPW + grp < seq) ? t * scale : kNegMax;
+            cm = fmaxf(cm, sc[i]);
+        }
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+        const float m_new = fmaxf(m, cm);
+        const float alpha = expf(m - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float e = (c0 + i * PPW + grp < seq) ? expf(sc[i] - m_new) : 0.0f;
+            ls += e;
+            const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 f = __half22float2(__builtin_bit_cast(__half2, w4[u]));
+                acc[2 * u] += e * f.x;
+                acc[2 * u + 1] += e * f.y;
+            }
+        }
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) ls += __shfl_xor(ls, o);
+        l = l * alpha + ls;
+        m = m_new;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) acc[j] += __shfl_xor(acc[j], o);
+    float* dst = ws + ((size_t)head * S + split) * (D + 4);
+    if (grp == 0) {
+        *reinterpret_cast<float4*>(dst + 8 * sub) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4*>(dst + 8 * sub + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    if (lane == 0) {
+        dst[D] = m;
+        dst[D + 1] = l;
+    }
+}
+
+// One workgroup per head: thread t takes float4 dim-chunk t % (D / 4) of
+// the splits congruent to t / (D / 4), all its loads issued together; the
+// split groups are added in LDS.
+__global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restrict__ ws, float* __restrict__ out,
+                                                            int nh, int D, int S) {
+    __shared__ float fs[64];
+    __shared__ float4 part[256];
+    __shared__ float lt_s;
+    const int head = blockIdx.x;
+    const int t = threadIdx.x;
+    const float* base = ws + (size_t)head * S * (D + 4);
+    if (t < 64) {
+        float mv = kNegMax, lv = 0.0f;
+        if (t < S) {
+            mv = base[(size_t)t * (D + 4) + D];
+            lv = base[(size_t)t * (D + 4) + D + 1];
+        }
+        float M = mv;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+        const float f = lv > 0.0f ? expf(mv - M) : 0.0f;   // splits without positions count 0
+        fs[t] = f;
+        float lt = f * lv;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) lt += __shfl_xor(lt, o);
+        if (t == 0) lt_s = lt;
+    }
+    __syncthreads();
+    const int nch = D / 4;                  // 16, 32 or 64 dim-chunks
+    const int ngr = 256 / nch;              // split groups
+    const int ch = t % nch, gr = t / nch;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = gr; s0 < S; s0 += 4 * ngr) {
+        float4 v[4];
+        float f[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int s = s0 + u * ngr;
+            f[u] = s < S ? fs[s] : 0.0f;
+            v[u] = s < S ? *reinterpret_cast<const float4*>(base + (size_t)s * (D + 4) + 4 * ch)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            a.x += f[u] * v[u].x; a.y += f[u] * v[u].y; a.z += f[u] * v[u].z; a.w += f[u] * v[u].w;
+        }
+    }
+    part[t] = a;
+    __syncthreads();
+    if (t < nch) {
+        float4 r = part[t];
+        for (int g = 1; g < ngr; ++g) {
+            const float4 b = part[g * nch + t];
+            r.x += b.x; r.y += b.y; r.z += b.z; r.w += b.w;
+        }
+        const float inv = 1.0f / lt_s;
+        *reinterpret_cast<float4*>(out + (size_t)head * D + 4 * t) = make_float4(r.x * inv, r.y * inv, r.z * inv,
+                                                                                r.w * inv);
+    }
+}
+
+// Workspace of the split path: one allocation per device, made on the first
+// call that needs more than it has (so not inside a graph capture: a
+// capturing stream with too small a workspace gets an error instead).
+static float* g_attn_ws[64];
+static size_t g_attn_ws_bytes[64];
+
+static hipError_t attn_workspace(size_t bytes, hipStream_t st, float** ws) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (g_attn_ws_bytes[dev] < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return hipErrorStreamCaptureUnsupported;
+        const size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
+        float* p = nullptr;
+        e = hipMalloc(&p, want);
+        if (e != hipSuccess) return e;
+        if (g_attn_ws[dev] != nullptr) {
+            hipDeviceSynchronize();
+            hipFree(g_attn_ws[dev]);
+        }
+        g_attn_ws[dev] = p;
+        g_attn_ws_bytes[dev] = want;
+    }
+    *ws = g_attn_ws[dev];
+    return hipSuccess;
+}
+
 static hipError_t attn_decode(float* out, const float* q, const __half* kc, const __half* vc, const int* len_ptr,
                               int len, int nh, int nkv, int d, float scale, hipStream_t st) {
     if (out == nullptr || q == nullptr || kc == nullptr || vc == nullptr) return hipErrorInvalidValue;
     if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || (len_ptr == nullptr && len <= 0)) return hipErrorInvalidValue;
+    if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
+    const int group = nh / nkv;
+    if (group <= 8) {
+        int S = (2 * device_cu_count() + nkv - 1) / nkv;
+        S = S < 1 ? 1 : (S > 64 ? 64 : S);
+        if (len_ptr == nullptr) {
+            const int chunks = (len + kSplitChunk - 1) / kSplitChunk;
+            S = chunks < S ? chunks : S;
+        }
+        float* ws = nullptr;
+        const hipError_t e = attn_workspace((size_t)nh * S * (d + 4) * sizeof(float), st, &ws);
+        if (e != hipSuccess) return e;
+        const dim3 grid(nkv, S), blk(64 * group);
+        switch (d) {
+        case 64: hipLaunchKernelGGL(rf_attn_split_kernel<8>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
+                                    scale, ws, S); break;
+        case 128: hipLaunchKernelGGL(rf_attn_split_kernel<16>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
+                                     scale, ws, S); break;
+        default: hipLaunchKernelGGL(rf_attn_split_kernel<32>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
+                                    scale, ws, S); break;
+        }
+        hipLaunchKernelGGL(rf_attn_merge_kernel, dim3(nh), dim3(256), 0, st, ws, out, nh, d, S);
+        return hipGetLastError();
+    }
     switch (d) {
     case 64: hipLaunchKernelGGL(rf_attn_decode_kernel<8>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len, nh,
                                 nkv, scale); break;
     case 128: hipLaunchKernelGGL(rf_attn_decode_kernel<16>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len,
                                  nh, nkv, scale); break;
-    case 256: hipLaunchKernelGGL(rf_attn_decode_kernel<32>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len,
-                                 nh, nkv, scale); break;
-    default: return hipErrorInvalidValue;
+    default: hipLaunchKernelGGL(rf_attn_decode_kernel<32>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len,
+                                nh, nkv, scale); break;
     }
     return hipGetLastError();
 }
