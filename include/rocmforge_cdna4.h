@@ -327,6 +327,25 @@ hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K
                                                     int seq_len, int num_q_heads, int num_kv_heads, int causal,
                                                     float scale, hipStream_t stream);
 
+/* ---- GEMVs with the RMSNorm of their input fused in (no counterpart) ----
+ * out = W * rmsnorm(input, norm_w, eps), bit-identical to gpu_rms_norm into a
+ * buffer followed by the plain launcher; one launch instead of two (the
+ * reference normalises with a separate launch before the QKV, gate/up and
+ * LM-head GEMVs, src/gpu/forward.rs:2349-2359, :2454-2464, :329-376).
+ * input and norm_w 16-byte aligned; otherwise the plain launchers' rules
+ * (the Q6_K one: K / 256 % 8 == 0, K <= 16384, 16-byte aligned weights). */
+hipError_t rf_gemv_q4_k_q8_rmsnorm_launch(const void* weights_q4_k, const float* input, const float* norm_w,
+                                          float eps, float* output, int n_rows, int ncols_dst, hipStream_t stream);
+hipError_t rf_gemv_gate_up_q4_k_q8_rmsnorm_launch(const void* weights_gate_q4_k, const void* weights_up_q4_k,
+                                                  const float* input, const float* norm_w, float eps,
+                                                  float* swiglu_out, int n_rows, int ncols_dst, hipStream_t stream);
+hipError_t rf_gemv_qkv_q4_k_q8_rmsnorm_launch(const void* w_q, const void* w_k, const void* w_v, const float* bias_q,
+                                              const float* bias_k, const float* bias_v, const float* input,
+                                              const float* norm_w, float eps, float* out_q, float* out_k,
+                                              float* out_v, int n_rows, int n_q, int n_kv, hipStream_t stream);
+hipError_t rf_gemv_q6_k_rmsnorm_launch(const void* weights_q6_k, const float* input, const float* norm_w, float eps,
+                                       float* output, int n_rows, int ncols_dst, hipStream_t stream);
+
 /* ---- Parity probes (no reference counterpart) ---------------------------
  * Expose the intermediate integers of the Q8-inline path so tests can check
  * them bit-exactly.  They run the same device code as the GEMV. */

@@ -45,6 +45,8 @@ struct QkvArgs {
     const float* bias[3];
     float* y[3];
     int n_q, n_kv;
+    const float* norm_w;   // RMSNorm weights applied to x first (any mode), or null
+    float eps;
 };
 
 // Waves per matrix: [0, nw[0]) on Q, then nw[1] on K, nw[2] on V (each >= 1;
@@ -205,13 +207,17 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     };
     // x is loaded before the weight prefetch: loads complete in issue
     // order, so the quantisation then waits only for x, not for the weights
-    X8Batch xb;
+    X8Batch xb, nb;
     q8_prefetch(x, K, xb);
+    const float* nw = qkv.norm_w;
+    if (nw) q8_prefetch(nw, K, nb);     // norm weights with x, ahead of the weight prefetch
+    __shared__ float red[4];
     Step ring[NB];
     ring_pipeline<NB>(nsteps, ring, [&](Step& b, int i) { load(b.u, i); },
                       [&](const Step& b, int i) { process(b.u, i); },
                       [&]() {
-                          q8_quantize_finish(x, K, q8, xb);
+                          const float inv = nw ? rms_inv_from_batch(xb, x, K, qkv.eps, red) : 1.0f;
+                          q8_quantize_finish(x, K, q8, xb, nw, &nb, inv);
                           __syncthreads();
                       });
     for (int j = lane; j < nrows; j += kWave) {
@@ -344,8 +350,9 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     // Measured on MI355X against 2 workgroups per CU / 1 row per step:
     // gate+up 14336x4096 12.9 vs 14.1 us, 6144x4096 5.1 vs 5.45 us,
     // 4096x4096 + residual 4.7 vs 5.1 us, 14336x4096 8.0 vs 8.1 us.
-    const int r = gemv_rows_per_step(MODE == kGateUp ? 1 : 2);
-    const int nw = (r == 1) ? gemv_waves_per_wg(4) : 4;
+    // a fused RMSNorm needs 256-thread workgroups (its summation order)
+    const int r = qkv.norm_w ? (MODE == kGateUp ? 1 : 2) : gemv_rows_per_step(MODE == kGateUp ? 1 : 2);
+    const int nw = (r == 1 && !qkv.norm_w) ? gemv_waves_per_wg(4) : 4;
     const int cap = device_cu_count() * gemv_wg_per_cu(1);
     const int need = (N + nw - 1) / nw;
     const int grid = need < cap ? need : cap;
@@ -512,7 +519,7 @@ extern "C" hipError_t gemv_qkv_q4_k_f32_q8_inline_launch(const void* w_q, const 
     if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
     if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v)) return hipErrorInvalidValue;
     if ((long)n_q + 2L * n_kv > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    QkvArgs a;
+    QkvArgs a{};
     a.w[0] = static_cast<const uint8_t*>(w_q);
     a.w[1] = static_cast<const uint8_t*>(w_k);
     a.w[2] = static_cast<const uint8_t*>(w_v);
@@ -524,6 +531,70 @@ extern "C" hipError_t gemv_qkv_q4_k_f32_q8_inline_launch(const void* w_q, const 
     a.y[2] = out_v;
     a.n_q = n_q;
     a.n_kv = n_kv;
+    return launch_q8<kQkv>(w_q, nullptr, input, nullptr, nullptr, n_rows, n_q + 2 * n_kv, stream, a);
+}
+
+// ---- RMSNorm fused into the Q8-inline GEMVs (no reference counterpart) ----
+// out = W * rmsnorm(input, norm_w, eps): the same bits as gpu_rms_norm into a
+// buffer followed by the plain launcher, one launch instead of two (the
+// reference runs gpu_dispatch_rms_norm before each of these GEMVs,
+// src/gpu/forward.rs:2349-2359, :2454-2464).  input and norm_w 16-byte aligned.
+static bool norm_args_ok(const float* x, const float* nw) {
+    return x != nullptr && nw != nullptr && aligned16(x) && aligned16(nw);
+}
+
+extern "C" hipError_t rf_gemv_q4_k_q8_rmsnorm_launch(const void* weights_q4_k, const float* input,
+                                                     const float* norm_w, float eps, float* output, int n_rows,
+                                                     int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (!aligned16(weights_q4_k) || !norm_args_ok(input, norm_w)) return hipErrorInvalidValue;
+    QkvArgs a{};
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return launch_q8<kPlain>(weights_q4_k, nullptr, input, nullptr, output, n_rows, ncols_dst, stream, a);
+}
+
+extern "C" hipError_t rf_gemv_gate_up_q4_k_q8_rmsnorm_launch(const void* weights_gate_q4_k,
+                                                             const void* weights_up_q4_k, const float* input,
+                                                             const float* norm_w, float eps, float* swiglu_out,
+                                                             int n_rows, int ncols_dst, hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows)) return hipErrorInvalidValue;
+    if (weights_gate_q4_k == nullptr || weights_up_q4_k == nullptr) return hipErrorInvalidValue;
+    if (!aligned16(weights_gate_q4_k) || !aligned16(weights_up_q4_k) || !norm_args_ok(input, norm_w))
+        return hipErrorInvalidValue;
+    QkvArgs a{};
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return launch_q8<kGateUp>(weights_gate_q4_k, weights_up_q4_k, input, nullptr, swiglu_out, n_rows, ncols_dst,
+                              stream, a);
+}
+
+extern "C" hipError_t rf_gemv_qkv_q4_k_q8_rmsnorm_launch(const void* w_q, const void* w_k, const void* w_v,
+                                                         const float* bias_q, const float* bias_k, const float* bias_v,
+                                                         const float* input, const float* norm_w, float eps,
+                                                         float* out_q, float* out_k, float* out_v, int n_rows, int n_q,
+                                                         int n_kv, hipStream_t stream) {
+    if (n_rows <= 0 || n_q <= 0 || n_kv <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows))
+        return hipErrorInvalidValue;
+    if (w_q == nullptr || w_k == nullptr || w_v == nullptr) return hipErrorInvalidValue;
+    if (out_q == nullptr || out_k == nullptr || out_v == nullptr) return hipErrorInvalidValue;
+    if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v) || !norm_args_ok(input, norm_w))
+        return hipErrorInvalidValue;
+    if ((long)n_q + 2L * n_kv > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    QkvArgs a{};
+    a.w[0] = static_cast<const uint8_t*>(w_q);
+    a.w[1] = static_cast<const uint8_t*>(w_k);
+    a.w[2] = static_cast<const uint8_t*>(w_v);
+    a.bias[0] = bias_q;
+    a.bias[1] = bias_k;
+    a.bias[2] = bias_v;
+    a.y[0] = out_q;
+    a.y[1] = out_k;
+    a.y[2] = out_v;
+    a.n_q = n_q;
+    a.n_kv = n_kv;
+    a.norm_w = norm_w;
+    a.eps = eps;
     return launch_q8<kQkv>(w_q, nullptr, input, nullptr, nullptr, n_rows, n_q + 2 * n_kv, stream, a);
 }
 

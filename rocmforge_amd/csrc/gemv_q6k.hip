@@ -350,7 +350,8 @@ struct Q6Seg {
 template <int NB>
 __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __restrict__ w,
                                                                const float* __restrict__ x, const float* residual,
-                                                               float* y, int K, int N) {
+                                                               float* y, int K, int N,
+                                                               const float* __restrict__ norm_w, float eps) {
     __shared__ __align__(16) uint8_t stage_lds[8 * 2048];
     extern __shared__ __align__(16) float part[];   // [rows of this workgroup][NWK][4 lane rows]
     const int lane = threadIdx.x & (kWave - 1);
@@ -371,12 +372,20 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
 
     float xr[2][16];
     {
-        const float* xb = x + (size_t)sb * kQK + 128 * n + 32 * hq + 16 * is;
+        // optional fused RMSNorm: x -> (x * inv) * norm_w, inv in the
+        // canonical order of the standalone norm (same bits)
+        __shared__ float red[4];
+        const float inv = norm_w ? rms_inv_canonical(x, K, eps, red) : 1.0f;
+        const size_t xo = (size_t)sb * kQK + 128 * n + 32 * hq + 16 * is;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float4 a = *reinterpret_cast<const float4*>(xb + 64 * r + 4 * k);
+                float4 a = *reinterpret_cast<const float4*>(x + xo + 64 * r + 4 * k);
+                if (norm_w) {
+                    const float4 g = *reinterpret_cast<const float4*>(norm_w + xo + 64 * r + 4 * k);
+                    a = make_float4((a.x * inv) * g.x, (a.y * inv) * g.y, (a.z * inv) * g.z, (a.w * inv) * g.w);
+                }
                 xr[r][4 * k + 0] = a.x; xr[r][4 * k + 1] = a.y; xr[r][4 * k + 2] = a.z; xr[r][4 * k + 3] = a.w;
             }
     }
@@ -474,7 +483,7 @@ static hipError_t launch_q6(const void* weights_q6_k, const float* input, const 
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * 4 * sizeof(float);
         if (lds <= 64 * 1024) {
             hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
-                               residual, output, n_rows, ncols_dst);
+                               residual, output, n_rows, ncols_dst, nullptr, 0.0f);
             return hipGetLastError();
         }
     }
@@ -538,4 +547,29 @@ extern "C" hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, co
     if (n_rows % kQK != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(weights_q6_k) & 1u) != 0) return hipErrorInvalidValue;
     return launch_q6(weights_q6_k, input, residual, output, n_rows, ncols_dst, stream);
+}
+
+// out = W * rmsnorm(input, norm_w, eps) with the standalone norm's bits
+// (gpu_rms_norm then gemv_q6_k_f32_launch), one launch.  No counterpart in
+// the reference (its LM head and Q6_K attn_v take a norm launch first,
+// src/gpu/forward.rs:329-376, :2349-2359).  Needs K / 256 % 8 == 0,
+// K <= 16384 and 16-byte aligned weights, input and norm_w.
+extern "C" hipError_t rf_gemv_q6_k_rmsnorm_launch(const void* weights_q6_k, const float* input, const float* norm_w,
+                                                  float eps, float* output, int n_rows, int ncols_dst,
+                                                  hipStream_t stream) {
+    if (n_rows <= 0 || ncols_dst <= 0 || n_rows % kQK != 0 || input == nullptr || norm_w == nullptr)
+        return hipErrorInvalidValue;
+    const int nsb = n_rows / kQK;
+    if (nsb > 64 || nsb % 8 != 0 || ((reinterpret_cast<uintptr_t>(weights_q6_k) | reinterpret_cast<uintptr_t>(input) |
+                                      reinterpret_cast<uintptr_t>(norm_w)) & 15u) != 0)
+        return hipErrorInvalidValue;
+    const int nwk = nsb / 8;
+    const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
+    const int grid = ncols_dst < cap ? ncols_dst : cap;
+    const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * 4 * sizeof(float);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream,
+                       static_cast<const uint8_t*>(weights_q6_k), input, nullptr, output, n_rows, ncols_dst, norm_w,
+                       eps);
+    return hipGetLastError();
 }

@@ -75,40 +75,39 @@ __device__ __forceinline__ void pair_idx(int p, int d, int neox, int* i0, int* i
 
 // ---- RMSNorm ------------------------------------------------------------------
 // out = x * rsqrt(mean(x^2) + eps) * w, rows of n; out may alias x.
-// Long rows: one 256-thread workgroup per row.  Short rows (n <= 512, the
-// per-head norms): one wave per row, four rows per workgroup.
+// Single vectors and long rows: one 256-thread workgroup per row.  Short
+// batched rows (n <= 512, the per-head norms): one wave per row, four rows
+// per workgroup.
 __global__ __launch_bounds__(256) void rf_rms_norm_long_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                                float* out, int n, float eps, int rows) {
-    __shared__ float part[4];
+    __shared__ float red[4];
     const int r = blockIdx.x;
     if (r >= rows) return;
     const float* xr = x + (size_t)r * n;
     float* orow = out + (size_t)r * n;
-    float ss = 0.0f;
-    const bool v4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow) |
+    // the canonical summation order (rms_inv_canonical) whenever the row is
+    // float4-addressable: the GEMVs with a fused norm use the same order
+    const bool v4 = (n & 7) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow) |
                                       reinterpret_cast<uintptr_t>(w)) & 15u) == 0;
+    float inv;
     if (v4) {
-        for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
-            const float4 a = reinterpret_cast<const float4*>(xr)[i];
-            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
-        }
+        inv = rms_inv_canonical(xr, n, eps, red);
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) ss = __fmaf_rn(xr[i], xr[i], ss);
+        ss = xor_sum64(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        inv = rms_inv_finish(red, n, eps);
     }
-    ss = wave_sum_all(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inv = rsqrtf(tot / (float)n + eps);
     if (v4) {
         for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
             const float4 a = reinterpret_cast<const float4*>(xr)[i];
             const float4 g = reinterpret_cast<const float4*>(w)[i];
-            reinterpret_cast<float4*>(orow)[i] = make_float4(a.x * inv * g.x, a.y * inv * g.y, a.z * inv * g.z,
-                                                             a.w * inv * g.w);
+            reinterpret_cast<float4*>(orow)[i] = make_float4((a.x * inv) * g.x, (a.y * inv) * g.y, (a.z * inv) * g.z,
+                                                             (a.w * inv) * g.w);
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = xr[i] * inv * w[i];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = (xr[i] * inv) * w[i];
     }
 }
 
@@ -139,7 +138,7 @@ __global__ __launch_bounds__(256) void rf_rms_norm_short_kernel(const float* __r
 
 static hipError_t rms_rows(const float* x, const float* w, float* out, int n, float eps, int rows, hipStream_t st) {
     if (x == nullptr || w == nullptr || out == nullptr || n <= 0 || rows <= 0) return hipErrorInvalidValue;
-    if (n <= 512)
+    if (n <= 512 && rows > 1)
         hipLaunchKernelGGL(rf_rms_norm_short_kernel, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, out, n, eps, rows);
     else
         hipLaunchKernelGGL(rf_rms_norm_long_kernel, dim3(rows), dim3(256), 0, st, x, w, out, n, eps, rows);

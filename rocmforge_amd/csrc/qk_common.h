@@ -142,6 +142,53 @@ __host__ __device__ constexpr int q8_padded_bytes(int K) { return K + 16 * (K >>
 __host__ __device__ constexpr int x_pad(int e) { return e + 4 * (e >> 7); }
 __host__ __device__ constexpr int x_padded_floats(int K) { return K + 4 * (K >> 7); }
 
+// ---- RMSNorm inverse in one fixed order --------------------------------------
+// inv = rsqrt(sum(x^2) / n + eps) for x[n] (n % 8 == 0, 16-byte aligned),
+// summed in one canonical order shared by every kernel that normalises: 256
+// virtual threads, thread v summing the squares of elements
+// [2048 u + 8 v, + 8) for u = 0, 1, .. (an explicit fma chain per 8), the 64
+// lanes of each virtual wave added by an xor butterfly, the four waves as
+// (w0 + w1) + (w2 + w3).  The standalone norm and the norm fused into the
+// GEMV prologues therefore produce identical bits.
+__device__ __forceinline__ float sq8(const float4& a, const float4& b) {
+    float t = a.x * a.x;
+    t = __fmaf_rn(a.y, a.y, t);
+    t = __fmaf_rn(a.z, a.z, t);
+    t = __fmaf_rn(a.w, a.w, t);
+    t = __fmaf_rn(b.x, b.x, t);
+    t = __fmaf_rn(b.y, b.y, t);
+    t = __fmaf_rn(b.z, b.z, t);
+    t = __fmaf_rn(b.w, b.w, t);
+    return t;
+}
+
+__device__ __forceinline__ float xor_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Combines the four virtual-wave sums (red: LDS float[4], written by lane 0
+// of each virtual wave before the barrier inside).
+__device__ __forceinline__ float rms_inv_finish(float* red, int n, float eps) {
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    return rsqrtf(tot / (float)n + eps);
+}
+
+// Any workgroup size that is a multiple of 64 (real threads take virtual
+// threads t, t + blockDim, ..).
+__device__ __forceinline__ float rms_inv_canonical(const float* __restrict__ x, int n, float eps, float* red) {
+    for (int v = threadIdx.x; v < 256; v += blockDim.x) {
+        float ss = 0.0f;
+        for (int idx = 8 * v; idx < n; idx += 2048)
+            ss += sq8(*reinterpret_cast<const float4*>(x + idx), *reinterpret_cast<const float4*>(x + idx + 4));
+        ss = xor_sum64(ss);
+        if ((v & 63) == 0) red[v >> 6] = ss;
+    }
+    return rms_inv_finish(red, n, eps);
+}
+
 // Whole-vector quantisation by one workgroup.  Each thread quantises 8
 // consecutive elements (two float4 loads); four neighbouring lanes form one
 // 32-element block and combine amax / int sums with two xor-shuffles.
@@ -164,13 +211,22 @@ __device__ __forceinline__ void q8_load_batch(const float* __restrict__ x, int K
     }
 }
 
-__device__ __forceinline__ void q8_quantize_batch(const X8Batch& b, int K, int base, Q8Lds lds) {
+// nb (optional): the matching batch of RMSNorm weights; the quantised
+// values are then (x * inv) * w, the standalone norm's arithmetic.
+__device__ __forceinline__ void q8_quantize_batch(const X8Batch& b, int K, int base, Q8Lds lds,
+                                                  const X8Batch* nb = nullptr, float inv = 1.0f) {
     const int per_pass = (int)blockDim.x * 8;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int idx = base + u * per_pass + (int)threadIdx.x * 8;
-        const float e[8] = {b.v[u][0].x, b.v[u][0].y, b.v[u][0].z, b.v[u][0].w,
-                            b.v[u][1].x, b.v[u][1].y, b.v[u][1].z, b.v[u][1].w};
+        float e[8] = {b.v[u][0].x, b.v[u][0].y, b.v[u][0].z, b.v[u][0].w,
+                      b.v[u][1].x, b.v[u][1].y, b.v[u][1].z, b.v[u][1].w};
+        if (nb != nullptr) {
+            const float g[8] = {nb->v[u][0].x, nb->v[u][0].y, nb->v[u][0].z, nb->v[u][0].w,
+                                nb->v[u][1].x, nb->v[u][1].y, nb->v[u][1].z, nb->v[u][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = (e[i] * inv) * g[i];
+        }
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(e[i]));
@@ -219,15 +275,35 @@ __device__ __forceinline__ void q8_prefetch(const float* __restrict__ x, int K, 
     q8_load_batch(x, K, 0, b0);
 }
 
-// Quantise all of x given the already loaded first batch.
-__device__ __forceinline__ void q8_quantize_finish(const float* __restrict__ x, int K, Q8Lds lds, const X8Batch& b0) {
+// Quantise all of x given the already loaded first batch; with nw (RMSNorm
+// weights, first batch nb0 already loaded) the values are normalised first.
+__device__ __forceinline__ void q8_quantize_finish(const float* __restrict__ x, int K, Q8Lds lds, const X8Batch& b0,
+                                                   const float* __restrict__ nw = nullptr,
+                                                   const X8Batch* nb0 = nullptr, float inv = 1.0f) {
     const int batch = (int)blockDim.x * 8 * 4;
-    q8_quantize_batch(b0, K, 0, lds);
+    q8_quantize_batch(b0, K, 0, lds, nw ? nb0 : nullptr, inv);
     for (int base = batch; base < K; base += batch) {
-        X8Batch b;
+        X8Batch b, nb;
         q8_load_batch(x, K, base, b);
-        q8_quantize_batch(b, K, base, lds);
+        if (nw) q8_load_batch(nw, K, base, nb);
+        q8_quantize_batch(b, K, base, lds, nw ? &nb : nullptr, inv);
     }
+}
+
+// The canonical RMS inverse from the first loaded batch (blockDim == 256:
+// the batch holds exactly the canonical elements of each thread), loading
+// the rest of x for K > 8192.
+__device__ __forceinline__ float rms_inv_from_batch(const X8Batch& b0, const float* __restrict__ x, int K, float eps,
+                                                    float* red) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (2048 * u + 8 * (int)threadIdx.x < K) ss += sq8(b0.v[u][0], b0.v[u][1]);
+    for (int idx = 8192 + 8 * (int)threadIdx.x; idx < K; idx += 2048)
+        ss += sq8(*reinterpret_cast<const float4*>(x + idx), *reinterpret_cast<const float4*>(x + idx + 4));
+    ss = xor_sum64(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    return rms_inv_finish(red, K, eps);
 }
 
 __device__ __forceinline__ void q8_0_quantize_to_lds(const float* __restrict__ x, int K, Q8Lds lds) {

@@ -137,9 +137,13 @@ def _chk(rc, what):
 class Engine:
     """Prefill + greedy decode of one sequence of up to max_seq tokens."""
 
-    def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0"):
+    def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0",
+                 fuse_norm: bool = True):
+        """fuse_norm: decode with the RMSNorms folded into the GEMVs that
+        consume them (same bits as the separate norm launches)."""
         import torch
         self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
+        self.fuse_norm = fuse_norm
         self.lib = _lib.load()
         ops._lib()
         f32, i16 = torch.float32, torch.int16
@@ -177,11 +181,15 @@ class Engine:
         len_p = ctypes.c_void_p(self.state.data_ptr() + 4)
         for i, lw in enumerate(self.w.layers):
             m = lw.mats
-            _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.attn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
-            t("attn_norm", i)
-            ops.gpu_dispatch_fused_qkv_on_stream(m["attn_q"][0], m["attn_q"][1], None, m["attn_k"][0], m["attn_k"][1],
-                                                 None, m["attn_v"][0], m["attn_v"][1], None, self.normed, self.q,
-                                                 self.k, self.v, c.q_size, c.kv_size, c.hidden, st)
+            if self.fuse_norm:
+                self._qkv_normed(m, lw.attn_norm, st)
+            else:
+                _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.attn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+                t("attn_norm", i)
+                ops.gpu_dispatch_fused_qkv_on_stream(m["attn_q"][0], m["attn_q"][1], None, m["attn_k"][0],
+                                                     m["attn_k"][1], None, m["attn_v"][0], m["attn_v"][1], None,
+                                                     self.normed, self.q, self.k, self.v, c.q_size, c.kv_size,
+                                                     c.hidden, st)
             t("qkv", i)
             _chk(L.rf_qk_norm_rope_kv_write_state(_p(self.q), _p(self.k), _p(self.v), _p(lw.q_norm), _p(lw.k_norm),
                                                   _p(self.kc[i]), _p(self.vc[i]), pos_p, c.n_heads, c.n_kv_heads,
@@ -193,22 +201,59 @@ class Engine:
             t("attention", i)
             self._residual_gemv(m["attn_output"], self.attn, c.q_size, st)
             t("attn_output", i)
-            _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.ffn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
-            t("ffn_norm", i)
-            ops.gpu_dispatch_fused_gate_up_on_stream(m["ffn_gate"][0], m["ffn_gate"][1], m["ffn_up"][0],
-                                                     m["ffn_up"][1], self.normed, self.act, c.ff, c.hidden, st)
+            if self.fuse_norm and m["ffn_gate"][1].wtype == GgmlType.Q4_K and m["ffn_up"][1].wtype == GgmlType.Q4_K:
+                _chk(L.rf_gemv_gate_up_q4_k_q8_rmsnorm_launch(_p(m["ffn_gate"][0]), _p(m["ffn_up"][0]),
+                                                              _p(self.hidden), _p(lw.ffn_norm), c.eps, _p(self.act),
+                                                              c.hidden, c.ff, st), "gate_up+norm")
+            else:
+                _chk(L.gpu_rms_norm(_p(self.hidden), _p(lw.ffn_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
+                t("ffn_norm", i)
+                ops.gpu_dispatch_fused_gate_up_on_stream(m["ffn_gate"][0], m["ffn_gate"][1], m["ffn_up"][0],
+                                                         m["ffn_up"][1], self.normed, self.act, c.ff, c.hidden, st)
             t("gate_up", i)
             self._residual_gemv(m["ffn_down"], self.act, c.ff, st)
             t("ffn_down", i)
-        _chk(L.gpu_rms_norm(_p(self.hidden), _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
-        t("output_norm", -1)
-        ops.gpu_dispatch_gemv_on_stream(self.w.lm_head[0], self.w.lm_head[1], self.normed, self.logits, c.vocab,
-                                        c.hidden, st)
+        lm_w, lm_meta = self.w.lm_head
+        if self.fuse_norm and lm_meta.wtype == GgmlType.Q6_K and self._q6_norm_ok(c.hidden):
+            _chk(L.rf_gemv_q6_k_rmsnorm_launch(_p(lm_w), _p(self.hidden), _p(self.w.output_norm), c.eps,
+                                               _p(self.logits), c.hidden, c.vocab, st), "lm_head+norm")
+        else:
+            _chk(L.gpu_rms_norm(_p(self.hidden), _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st),
+                 "norm")
+            t("output_norm", -1)
+            ops.gpu_dispatch_gemv_on_stream(lm_w, lm_meta, self.normed, self.logits, c.vocab, c.hidden, st)
         t("lm_head", -1)
         _chk(L.gpu_argmax_f32_on_stream(_p(self.logits), _p(self.part_v), _p(self.part_i), _p(self.token), c.vocab,
                                         st), "argmax")
         _chk(L.gpu_increment_decode_state_on_stream(_p(self.state), st), "state")
         t("argmax", -1)
+
+    @staticmethod
+    def _q6_norm_ok(k):
+        return (k // 256) % 8 == 0 and k <= 16384
+
+    def _qkv_normed(self, m, norm_w, st):
+        """q, k, v = W rmsnorm(hidden): one launch when all three are Q4_K,
+        else one normalising GEMV per matrix."""
+        L, c = self.lib, self.cfg
+        mats = [m["attn_q"], m["attn_k"], m["attn_v"]]
+        outs = [(self.q, c.q_size), (self.k, c.kv_size), (self.v, c.kv_size)]
+        if all(mt[1].wtype == GgmlType.Q4_K for mt in mats):
+            _chk(L.rf_gemv_qkv_q4_k_q8_rmsnorm_launch(_p(mats[0][0]), _p(mats[1][0]), _p(mats[2][0]), None, None,
+                                                      None, _p(self.hidden), _p(norm_w), c.eps, _p(self.q),
+                                                      _p(self.k), _p(self.v), c.hidden, c.q_size, c.kv_size, st),
+                 "qkv+norm")
+            return
+        for (w, meta), (out, n) in zip(mats, outs):
+            if meta.wtype == GgmlType.Q4_K:
+                _chk(L.rf_gemv_q4_k_q8_rmsnorm_launch(_p(w), _p(self.hidden), _p(norm_w), c.eps, _p(out), c.hidden,
+                                                      n, st), "gemv+norm")
+            elif meta.wtype == GgmlType.Q6_K and self._q6_norm_ok(c.hidden):
+                _chk(L.rf_gemv_q6_k_rmsnorm_launch(_p(w), _p(self.hidden), _p(norm_w), c.eps, _p(out), c.hidden, n,
+                                                   st), "gemv+norm")
+            else:
+                _chk(L.gpu_rms_norm(_p(self.hidden), _p(norm_w), _p(self.normed), c.hidden, c.eps, st), "norm")
+                ops.gpu_dispatch_gemv_on_stream(w, meta, self.normed, out, n, c.hidden, st)
 
     def _residual_gemv(self, wm, x, k, st):
         """hidden += W x: the fused residual kernels (Q4_K through the

@@ -44,9 +44,14 @@ def _gemv(wm, x, n, k):
 
 
 @pytest.fixture(scope="module")
-def eng(dev):
-    w = E.synthetic_weights(CFG, seed=3)
-    return E.Engine(CFG, w, max_seq=256)
+def weights(dev):
+    return E.synthetic_weights(CFG, seed=3)
+
+
+@pytest.fixture(scope="module")
+def eng(weights):
+    # separate norm launches, so the trace sees each normalised vector
+    return E.Engine(CFG, weights, max_seq=256, fuse_norm=False)
 
 
 def test_decode_step_per_operation(eng):
@@ -130,6 +135,19 @@ def test_graph_replays_eager_steps(eng):
     # a second replay sequence from a fresh prefill gives the same tokens again
     eng.prefill(prompt)
     assert eng.decode(6, graph=True) == eager
+
+
+def test_fused_norm_decode_equals_separate(weights, eng):
+    # the RMSNorm folded into the QKV / gate-up / LM-head GEMVs gives the same bits
+    fused = E.Engine(CFG, weights, max_seq=256)
+    prompt = list(range(7, 47))
+    fused.prefill(prompt)
+    eng.prefill(prompt)
+    assert fused.decode(5) == eng.decode(5, graph=False)
+    assert np.array_equal(_h(fused.logits), _h(eng.logits))
+    rows = (len(prompt) + 5) * CFG.kv_size          # the rows this run wrote (eng holds older ones beyond)
+    for a, b in zip(fused.kc + fused.vc, eng.kc + eng.vc):
+        assert np.array_equal(_h(a)[:rows], _h(b)[:rows])
 
 
 def test_prefill_stages(eng):

@@ -217,3 +217,43 @@ def test_against_reference_kernels(rf, dev, fmt, k, n):
             "f32": lambda: O.gemv_q4k_f32(w, x, k, n),
             "gu": lambda: O.swiglu(O.gemv_q4k_q8(w, x, k, n), O.gemv_q4k_q8(w2, x, k, n))}[fmt]()
     _check(b, oref, f"reference kernel vs oracle {fmt}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (12288, 4096), (512, 300), (4096, 151936)])
+def test_rmsnorm_fused_gemvs_equal_two_launches(rf, dev, k, n):
+    # y = W rmsnorm(x): the fused launch equals gpu_rms_norm + the plain launch bit for bit
+    rng = np.random.default_rng(k + n)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    dx, dg = G.to_dev(x), G.to_dev(g)
+    normed = G.empty(k, torch.float32)
+    G.call(rf.gpu_rms_norm, G.ptr(dx), G.ptr(dg), G.ptr(normed), k, 1e-6)
+    _check(G.host(normed), O.rms_norm(x, g, 1e-6), f"rms_norm {k}")
+    nq = min(n, 4096)
+    w4 = G.to_dev(synth.q4_k_weights(nq, k, seed=1))
+    a, b = G.empty(nq, torch.float32), G.empty(nq, torch.float32)
+    G.call(rf.gemv_q4_k_f32_q8_inline_launch, G.ptr(w4), G.ptr(normed), G.ptr(a), k, nq)
+    G.call(rf.rf_gemv_q4_k_q8_rmsnorm_launch, G.ptr(w4), G.ptr(dx), G.ptr(dg), 1e-6, G.ptr(b), k, nq)
+    np.testing.assert_array_equal(G.host(a), G.host(b))
+    wu = G.to_dev(synth.q4_k_weights(nq, k, seed=2))
+    G.call(rf.gemv_gate_up_swiglu_q4_k_f32_q8_inline_launch, G.ptr(w4), G.ptr(wu), G.ptr(normed), G.ptr(a), k, nq)
+    G.call(rf.rf_gemv_gate_up_q4_k_q8_rmsnorm_launch, G.ptr(w4), G.ptr(wu), G.ptr(dx), G.ptr(dg), 1e-6, G.ptr(b), k,
+           nq)
+    np.testing.assert_array_equal(G.host(a), G.host(b))
+    nkv = max(nq // 4, 64)
+    wk, wv = G.to_dev(synth.q4_k_weights(nkv, k, seed=3)), G.to_dev(synth.q4_k_weights(nkv, k, seed=4))
+    bq = G.to_dev(synth.activations(nq, seed=5))
+    outs1 = [G.empty(m, torch.float32) for m in (nq, nkv, nkv)]
+    outs2 = [G.empty(m, torch.float32) for m in (nq, nkv, nkv)]
+    G.call(rf.gemv_qkv_q4_k_f32_q8_inline_launch, G.ptr(w4), G.ptr(wk), G.ptr(wv), G.ptr(bq), None, None,
+           G.ptr(normed), *[G.ptr(o) for o in outs1], k, nq, nkv)
+    G.call(rf.rf_gemv_qkv_q4_k_q8_rmsnorm_launch, G.ptr(w4), G.ptr(wk), G.ptr(wv), G.ptr(bq), None, None, G.ptr(dx),
+           G.ptr(dg), 1e-6, *[G.ptr(o) for o in outs2], k, nq, nkv)
+    for o1, o2 in zip(outs1, outs2):
+        np.testing.assert_array_equal(G.host(o1), G.host(o2))
+    if (k // 256) % 8 == 0 and k <= 16384:
+        w6 = G.to_dev(synth.q6_k_weights(n, k, seed=6))
+        a6, b6 = G.empty(n, torch.float32), G.empty(n, torch.float32)
+        G.call(rf.gemv_q6_k_f32_launch, G.ptr(w6), G.ptr(normed), G.ptr(a6), k, n)
+        G.call(rf.rf_gemv_q6_k_rmsnorm_launch, G.ptr(w6), G.ptr(dx), G.ptr(dg), 1e-6, G.ptr(b6), k, n)
+        np.testing.assert_array_equal(G.host(a6), G.host(b6))
