@@ -275,7 +275,7 @@ hipError_t rf_kv_write_batched_on_stream(uint16_t* d_k_cache, uint16_t* d_v_cach
  * gpu_rope_heads_state_scaled and gpu_kv_write_rope_state_scaled,
  * src/gpu/forward.rs:2384-2430): per-head RMSNorm of q (d_q_norm) and k
  * (d_k_norm; either may be null to skip), RoPE of both at *d_pos, q written
- * back in place, fp16 k and v written to the caches at *d_pos.  head_dim <= 512. */
+ * back in place, fp16 k and v written to the caches at *d_pos.  head_dim 64, 128 or 256. */
 hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const float* d_v, const float* d_q_norm,
                                           const float* d_k_norm, uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_pos,
                                           const int num_heads, const int num_kv_heads, const int head_dim,
@@ -294,12 +294,31 @@ hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_out, const fl
                                                           const int num_heads, const int num_kv_heads,
                                                           const int head_dim, const float scale, hipStream_t stream);
 
+/* No counterpart (the reference launches the per-head norms, the q RoPE and
+ * the KV write before gpu_flash_attn_decode_strided_multi_head_state,
+ * src/gpu/forward.rs:2384-2440): the same step folded into the decode
+ * attention.  d_q, d_k, d_v are the raw projections (d_q is not modified);
+ * the K/V row at pos = d_state[0] is written, then attention runs over
+ * d_state[1] positions.  Same bits as rf_qk_norm_rope_kv_write_state followed
+ * by gpu_flash_attn_decode_strided_multi_head_state.  GQA group <= 8. */
+hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, const float* d_k, const float* d_v,
+                                             const float* d_q_norm, const float* d_k_norm, uint16_t* d_k_cache,
+                                             uint16_t* d_v_cache, const int* d_state, const int num_heads,
+                                             const int num_kv_heads, const int head_dim, const float eps,
+                                             const float theta_base, const int neox, const float* d_freq_scale,
+                                             const float scale, hipStream_t stream);
+
 /* hip_kernels/elementwise.hip:615, :651 -- index of the maximum of d_input[n]
  * (ties: the larger index; NaN never wins); partial buffers hold ceil(n / 1024). */
 hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_partial_values, int* d_partial_indices,
                                     int* d_output_index, const int n, hipStream_t stream);
 hipError_t gpu_argmax_f32(const float* d_input, float* d_partial_values, int* d_partial_indices,
                           int* d_output_index, const int n);
+/* No counterpart (the reference follows the argmax with
+ * gpu_increment_decode_state_on_stream): the argmax, then d_state[0..1] += 1. */
+hipError_t rf_argmax_f32_advance_state_on_stream(const float* d_input, float* d_partial_values,
+                                                 int* d_partial_indices, int* d_output_index, const int n,
+                                                 int* d_state, hipStream_t stream);
 
 /* hip_kernels/elementwise.hip:780, :804 -- Q4_K rows of a [vocab][hidden]
  * embedding dequantised to fp32; ids outside [0, vocab) leave their row untouched. */

@@ -54,6 +54,9 @@ SIGNATURES = {
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "gpu_argmax_f32_on_stream": [_vp, _vp, _vp, _vp, _i, _vp],
     "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
+    "rf_argmax_f32_advance_state_on_stream": [_vp, _vp, _vp, _vp, _i, _vp, _vp],
+    "rf_attn_decode_qk_norm_rope_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp,
+                                          _f, _vp],
     "gpu_embed_q4_k_token": [_vp, _vp, _i, _i, _i, _vp],
     "gpu_embed_q4_k_batch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "gpu_add": [_vp, _vp, _vp, _i, _vp],

@@ -23,7 +23,8 @@
 // RoPE frequencies: theta_i = 1 / base^(e_i) with e_i = (float)(2i) / (float)d
 // as the reference, evaluated in double and rounded once to float (the
 // reference's 1.0f / powf(..) is within an ulp of this), then divided by
-// freq_scale[i] when given; angle = (float)pos * theta_i in fp32.
+// freq_scale[i] when given; angle = (float)pos * theta_i in fp32.  The
+// values live in a small per-(device, d, base) table made on first use.
 #include <hip/hip_fp16.h>
 
 #include "qk_common.h"
@@ -45,11 +46,20 @@ __device__ __forceinline__ float wave_sum_all(float v) {
     return v;
 }
 
-__device__ __forceinline__ float rope_theta(int i, int d, float base, const float* freq_scale) {
-    const float e = (float)(2 * i) / (float)d;
-    float t = (float)(1.0 / pow((double)base, (double)e));
+// theta_i from the per-(device, d, base) table (filled once by
+// rf_theta_fill_kernel), divided by freq_scale[i] when given
+__device__ __forceinline__ float rope_theta(int i, const float* __restrict__ tab, const float* freq_scale) {
+    float t = tab[i];
     if (freq_scale != nullptr) t /= freq_scale[i];
     return t;
+}
+
+__global__ void rf_theta_fill_kernel(float* tab, int d, float base) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < d / 2) {
+        const float e = (float)(2 * i) / (float)d;
+        tab[i] = (float)(1.0 / pow((double)base, (double)e));
+    }
 }
 
 // (x0, x1) rotated by angle pos * theta
@@ -146,8 +156,9 @@ static hipError_t rms_rows(const float* x, const float* w, float* out, int n, fl
 }
 
 // ---- RoPE over heads (in place) ---------------------------------------------------
-__global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, int pos0, int nh, int d, float base,
-                                     int neox, const float* __restrict__ freq_scale, int seq_len) {
+__global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, int pos0, int nh, int d,
+                                     const float* __restrict__ tab, int neox, const float* __restrict__ freq_scale,
+                                     int seq_len) {
     const int half = d / 2;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     const int s = blockIdx.y;
@@ -158,17 +169,55 @@ __global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, 
     int i0, i1;
     pair_idx(i, d, neox, &i0, &i1);
     float x0 = row[i0], x1 = row[i1];
-    rope_pair(x0, x1, pos, rope_theta(i, d, base, freq_scale));
+    rope_pair(x0, x1, pos, rope_theta(i, tab, freq_scale));
     row[i0] = x0;
     row[i1] = x1;
+}
+
+// theta tables: (d, base) -> device float[d/2], per device, made on first
+// use (so, like the attention workspace, not inside a graph capture: a
+// capturing stream without its table gets an error).
+struct ThetaTab {
+    int dev, d;
+    float base;
+    float* p;
+};
+static ThetaTab g_theta[64];
+static int g_ntheta = 0;
+
+static hipError_t theta_table(int d, float base, hipStream_t st, const float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    for (int i = 0; i < g_ntheta; ++i)
+        if (g_theta[i].dev == dev && g_theta[i].d == d && g_theta[i].base == base) {
+            *out = g_theta[i].p;
+            return hipSuccess;
+        }
+    if (g_ntheta == 64) return hipErrorOutOfMemory;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return hipErrorStreamCaptureUnsupported;
+    float* p = nullptr;
+    e = hipMalloc(&p, (size_t)(d / 2 > 0 ? d / 2 : 1) * sizeof(float));
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(rf_theta_fill_kernel, dim3((d / 2 + 255) / 256 + 1), dim3(256), 0, st, p, d, base);
+    e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return e;
+    g_theta[g_ntheta++] = ThetaTab{dev, d, base, p};
+    *out = p;
+    return hipSuccess;
 }
 
 static hipError_t rope_heads(float* x, const int* pos_ptr, int pos, int nh, int d, float base, int neox,
                              const float* fs, int seq_len, hipStream_t st) {
     if (x == nullptr || nh <= 0 || d <= 0 || (d & 1) || seq_len <= 0) return hipErrorInvalidValue;
     const int pairs = nh * (d / 2);
+    const float* tab = nullptr;
+    const hipError_t e = theta_table(d, base, st, &tab);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rf_rope_heads_kernel, dim3((pairs + 255) / 256, seq_len), dim3(256), 0, st, x, pos_ptr, pos, nh,
-                       d, base, neox, fs, seq_len);
+                       d, tab, neox, fs, seq_len);
     return hipGetLastError();
 }
 
@@ -176,7 +225,8 @@ static hipError_t rope_heads(float* x, const int* pos_ptr, int pos, int nh, int 
 // Cache layout [max_seq][n_kv * d] fp16 per layer; V copied, K rotated.
 __global__ void rf_kv_write_rope_kernel(__half* kc, __half* vc, const float* __restrict__ k,
                                         const float* __restrict__ v, const int* __restrict__ pos_ptr, int pos0,
-                                        int nkv, int d, float base, int neox, const float* __restrict__ freq_scale) {
+                                        int nkv, int d, const float* __restrict__ tab, int neox,
+                                        const float* __restrict__ freq_scale) {
     const int half = d / 2;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= nkv * half) return;
@@ -187,7 +237,7 @@ __global__ void rf_kv_write_rope_kernel(__half* kc, __half* vc, const float* __r
     const size_t base_in = (size_t)head * d;
     const size_t base_c = (size_t)pos * nkv * d + base_in;
     float x0 = k[base_in + i0], x1 = k[base_in + i1];
-    rope_pair(x0, x1, pos, rope_theta(i, d, base, freq_scale));
+    rope_pair(x0, x1, pos, rope_theta(i, tab, freq_scale));
     kc[base_c + i0] = __float2half(x0);
     kc[base_c + i1] = __float2half(x1);
     vc[base_c + i0] = __float2half(v[base_in + i0]);
@@ -205,60 +255,87 @@ __global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* 
 }
 
 // ---- fused Qwen3 decode step: Q/K RMSNorm, RoPE, KV write ----------------------------
-// One wave per head: heads [0, nh) are query heads (normalised with
-// q_norm when given, rotated, written back in place), heads [nh, nh + nkv)
-// key heads (normalised with k_norm, rotated, written to the K cache at
-// *pos as fp16; the matching V head is copied to the V cache).  The
-// arithmetic of each step is that of the separate launchers.
+// Per-head layout shared with the decode attention: a head of D = 8 LPP
+// values is held by LPP consecutive lanes, 8 consecutive dims per lane.
+// The per-head RMSNorm sums each lane's 8 squares (fma chain) and adds the
+// LPP lanes by an xor butterfly; NeoX pairs (i, i + D/2) sit in lanes sub
+// and sub + LPP/2 (one xor shuffle), classic pairs (2i, 2i+1) in one lane.
+// Both the standalone step and the attention with the step folded in use
+// this function, so they produce the same bits.
+template <int LPP>
+__device__ __forceinline__ void head_norm_rope(float v[8], int sub, const float* __restrict__ g, float eps, int pos,
+                                               const float* __restrict__ tab, int neox,
+                                               const float* __restrict__ freq_scale) {
+    constexpr int D = 8 * LPP;
+    if (g != nullptr) {
+        float ss = v[0] * v[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) ss = __fmaf_rn(v[i], v[i], ss);
+#pragma unroll
+        for (int o = 1; o < LPP; o <<= 1) ss += __shfl_xor(ss, o);
+        const float inv = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * g[8 * sub + i];
+    }
+    if (neox) {
+        const bool lo = sub < LPP / 2;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float other = __shfl_xor(v[i], LPP / 2);
+            const int p = lo ? 8 * sub + i : 8 * sub + i - D / 2;
+            float x0 = lo ? v[i] : other, x1 = lo ? other : v[i];
+            rope_pair(x0, x1, pos, rope_theta(p, tab, freq_scale));
+            v[i] = lo ? x0 : x1;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) rope_pair(v[i], v[i + 1], pos, rope_theta((8 * sub + i) / 2, tab, freq_scale));
+    }
+}
+
+__device__ __forceinline__ void load8(const float* p, float v[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void store8_f16(__half* p, const float v[8]) {
+    typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+    hv8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (_Float16)v[i];
+    *reinterpret_cast<hv8*>(p) = h;
+}
+
+// Heads [0, nh) are query heads (normalised with q_norm when given,
+// rotated, written back in place), heads [nh, nh + nkv) key heads
+// (normalised with k_norm, rotated, written to the K cache at *pos as fp16;
+// the matching V head is copied to the V cache).  64 / LPP heads per wave.
+template <int LPP>
 __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     float* q, const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ q_norm,
-    const float* __restrict__ k_norm, __half* kc, __half* vc, const int* __restrict__ pos_ptr, int nh, int nkv, int d,
-    float eps, float base, int neox, const float* __restrict__ freq_scale) {
+    const float* __restrict__ k_norm, __half* kc, __half* vc, const int* __restrict__ pos_ptr, int nh, int nkv,
+    float eps, const float* __restrict__ tab, int neox, const float* __restrict__ freq_scale) {
+    constexpr int D = 8 * LPP;
     const int lane = threadIdx.x & 63;
-    const int hidx = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (hidx >= nh + nkv) return;
+    const int hidx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPP) + lane / LPP;
+    const int sub = lane % LPP;
+    if (hidx >= nh + nkv) return;            // whole LPP-lane groups leave together
     const bool is_q = hidx < nh;
     const int head = is_q ? hidx : hidx - nh;
-    const float* src = is_q ? q + (size_t)head * d : k + (size_t)head * d;
-    const float* g = is_q ? q_norm : k_norm;
-    const int half = d / 2;
     const int pos = *pos_ptr;
-    // lane holds pairs lane, lane + 64, ... (d <= 512)
-    float a[4], b[4];
-    float ss = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int p = lane + 64 * t;
-        int i0, i1;
-        pair_idx(p < half ? p : 0, d, neox, &i0, &i1);
-        a[t] = p < half ? src[i0] : 0.0f;
-        b[t] = p < half ? src[i1] : 0.0f;
-        ss += a[t] * a[t] + b[t] * b[t];
-    }
-    float inv = 0.0f;
-    if (g != nullptr) inv = rsqrtf(wave_sum_all(ss) / (float)d + eps);
-    const size_t cbase = (size_t)pos * nkv * d + (size_t)head * d;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int p = lane + 64 * t;
-        if (p >= half) break;
-        int i0, i1;
-        pair_idx(p, d, neox, &i0, &i1);
-        float x0 = a[t], x1 = b[t];
-        if (g != nullptr) {
-            x0 = x0 * inv * g[i0];
-            x1 = x1 * inv * g[i1];
-        }
-        rope_pair(x0, x1, pos, rope_theta(p, d, base, freq_scale));
-        if (is_q) {
-            q[(size_t)head * d + i0] = x0;
-            q[(size_t)head * d + i1] = x1;
-        } else {
-            kc[cbase + i0] = __float2half(x0);
-            kc[cbase + i1] = __float2half(x1);
-            vc[cbase + i0] = __float2half(v[(size_t)head * d + i0]);
-            vc[cbase + i1] = __float2half(v[(size_t)head * d + i1]);
-        }
+    float x[8];
+    load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
+    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, tab, neox, freq_scale);
+    if (is_q) {
+        float* dst = q + (size_t)head * D + 8 * sub;
+        *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    } else {
+        const size_t c = (size_t)pos * nkv * D + (size_t)head * D + 8 * sub;
+        store8_f16(kc + c, x);
+        float vv[8];
+        load8(v + (size_t)head * D + 8 * sub, vv);
+        store8_f16(vc + c, vv);
     }
 }
 
@@ -390,28 +467,59 @@ __global__ __launch_bounds__(256) void rf_attn_decode_kernel(float* __restrict__
 //   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s.
 constexpr int kSplitChunk = 32;
 
-template <int LPP>
+// QK: the decode step's per-head Q/K norm, RoPE and KV write are folded in
+// (qk.*): q, k, v are the raw projections; every wave normalises and
+// rotates its query head in registers, and the workgroup whose chunk holds
+// the new position (seq - 1) writes that K/V row first -- no other
+// workgroup reads it.
+struct QkStep {
+    const float* k;
+    const float* v;
+    const float* q_norm;
+    const float* k_norm;
+    __half* kc;
+    __half* vc;
+    float eps;
+    const float* tab;
+    int neox;
+    const float* freq_scale;
+};
+
+template <int LPP, bool QK>
 __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restrict__ q,
-                                                            const __half* __restrict__ kc,
-                                                            const __half* __restrict__ vc,
+                                                            const __half* kc,    // not restrict: QK writes a row
+                                                            const __half* vc,
                                                             const int* __restrict__ len_ptr, int len0, int nh,
-                                                            int nkv, float scale, float* __restrict__ ws, int S) {
+                                                            int nkv, float scale, float* __restrict__ ws, int S,
+                                                            QkStep qk) {
     constexpr int D = LPP * 8;
     constexpr int PPW = 64 / LPP;
     constexpr int NI = kSplitChunk / PPW;       // load instructions per chunk (K and V each)
+    __shared__ u32x4 new_kv[2][LPP];            // QK: the new position's fp16 K and V row of this kv head
     const int seq = len_ptr ? *len_ptr : len0;
     const int kvh = blockIdx.x, split = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int head = kvh * (nh / nkv) + wave;
     const size_t row = (size_t)nkv * D;
     const int sub = lane % LPP, grp = lane / LPP;
+    if (split * kSplitChunk >= seq) {       // no positions: an empty partial (l = 0) for the merge
+        if (lane == 0) {
+            float* dst = ws + ((size_t)head * S + split) * (D + 4);
+            dst[D] = kNegMax;
+            dst[D + 1] = 0.0f;
+        }
+        return;
+    }
     const __half* kh = kc + (size_t)kvh * D + 8 * sub;
     const __half* vh = vc + (size_t)kvh * D + 8 * sub;
-    float qv[8];
-    {
-        const float* qh = q + (size_t)head * D + 8 * sub;
-        const float4 a = *reinterpret_cast<const float4*>(qh), b = *reinterpret_cast<const float4*>(qh + 4);
-        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+    const int pos = seq - 1;
+    const bool owner = QK && split == (pos / kSplitChunk) % S;   // workgroup-uniform
+    // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
+    float qv[8], kx[8], vx[8];
+    load8(q + (size_t)head * D + 8 * sub, qv);
+    if (owner && wave == 0) {
+        load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
+        load8(qk.v + (size_t)kvh * D + 8 * sub, vx);
     }
     float m = kNegMax, l = 0.0f, acc[8];
 #pragma unroll
@@ -424,6 +532,40 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
             const bool ok = p < seq;
             kk[i] = ok ? *reinterpret_cast<const u32x4*>(kh + (size_t)p * row) : u32x4{0, 0, 0, 0};
             vv[i] = ok ? *reinterpret_cast<const u32x4*>(vh + (size_t)p * row) : u32x4{0, 0, 0, 0};
+        }
+        if constexpr (QK) {
+            if (c0 == split * kSplitChunk) {     // first chunk: the per-head step, while the loads fly
+                head_norm_rope<LPP>(qv, sub, qk.q_norm, qk.eps, pos, qk.tab, qk.neox, qk.freq_scale);
+                if (owner) {
+                    if (wave == 0) {
+                        head_norm_rope<LPP>(kx, sub, qk.k_norm, qk.eps, pos, qk.tab, qk.neox, qk.freq_scale);
+                        if (grp == 0) {
+                            const size_t c = (size_t)pos * row + (size_t)kvh * D + 8 * sub;
+                            store8_f16(qk.kc + c, kx);
+                            store8_f16(qk.vc + c, vx);
+                            typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+                            hv8 hk, hvv;
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) {
+                                hk[i] = (_Float16)kx[i];
+                                hvv[i] = (_Float16)vx[i];
+                            }
+                            new_kv[0][sub] = __builtin_bit_cast(u32x4, hk);
+                            new_kv[1][sub] = __builtin_bit_cast(u32x4, hvv);
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+            if (owner && pos >= c0 && pos < c0 + kSplitChunk) {
+                // the row at pos was loaded before it was written: take it from LDS
+#pragma unroll
+                for (int i = 0; i < NI; ++i)
+                    if (c0 + i * PPW + grp == pos) {
+                        kk[i] = new_kv[0][sub];
+                        vv[i] = new_kv[1][sub];
+                    }
+            }
         }
         float sc[NI];
         float cm = kNegMax;
@@ -561,8 +703,8 @@ static hipError_t attn_workspace(size_t bytes, hipStream_t st, float** ws) {
         e = hipMalloc(&p, want);
         if (e != hipSuccess) return e;
         if (g_attn_ws[dev] != nullptr) {
-            hipDeviceSynchronize();
-            hipFree(g_attn_ws[dev]);
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g_attn_ws[dev]);
         }
         g_attn_ws[dev] = p;
         g_attn_ws_bytes[dev] = want;
@@ -572,7 +714,8 @@ static hipError_t attn_workspace(size_t bytes, hipStream_t st, float** ws) {
 }
 
 static hipError_t attn_decode(float* out, const float* q, const __half* kc, const __half* vc, const int* len_ptr,
-                              int len, int nh, int nkv, int d, float scale, hipStream_t st) {
+                              int len, int nh, int nkv, int d, float scale, hipStream_t st,
+                              const QkStep* qk = nullptr) {
     if (out == nullptr || q == nullptr || kc == nullptr || vc == nullptr) return hipErrorInvalidValue;
     if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || (len_ptr == nullptr && len <= 0)) return hipErrorInvalidValue;
     if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
@@ -588,17 +731,24 @@ static hipError_t attn_decode(float* out, const float* q, const __half* kc, cons
         const hipError_t e = attn_workspace((size_t)nh * S * (d + 4) * sizeof(float), st, &ws);
         if (e != hipSuccess) return e;
         const dim3 grid(nkv, S), blk(64 * group);
+        const QkStep a = qk ? *qk : QkStep{};
+#define RF_SPLIT(LPP)                                                                                                  \
+    if (qk)                                                                                                            \
+        hipLaunchKernelGGL((rf_attn_split_kernel<LPP, true>), grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,      \
+                           scale, ws, S, a);                                                                           \
+    else                                                                                                               \
+        hipLaunchKernelGGL((rf_attn_split_kernel<LPP, false>), grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,     \
+                           scale, ws, S, a)
         switch (d) {
-        case 64: hipLaunchKernelGGL(rf_attn_split_kernel<8>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
-                                    scale, ws, S); break;
-        case 128: hipLaunchKernelGGL(rf_attn_split_kernel<16>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
-                                     scale, ws, S); break;
-        default: hipLaunchKernelGGL(rf_attn_split_kernel<32>, grid, blk, 0, st, q, kc, vc, len_ptr, len, nh, nkv,
-                                    scale, ws, S); break;
+        case 64: RF_SPLIT(8); break;
+        case 128: RF_SPLIT(16); break;
+        default: RF_SPLIT(32); break;
         }
+#undef RF_SPLIT
         hipLaunchKernelGGL(rf_attn_merge_kernel, dim3(nh), dim3(256), 0, st, ws, out, nh, d, S);
         return hipGetLastError();
     }
+    if (qk) return hipErrorInvalidValue;      // the folded step needs the split path (GQA group <= 8)
     switch (d) {
     case 64: hipLaunchKernelGGL(rf_attn_decode_kernel<8>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len, nh,
                                 nkv, scale); break;
@@ -652,14 +802,21 @@ __global__ __launch_bounds__(256) void rf_argmax_stage1_kernel(const float* __re
 }
 
 __global__ __launch_bounds__(256) void rf_argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
-                                                              int* out, int np) {
+                                                              int* out, int np, int* state) {
     __shared__ float sv[4];
     __shared__ int si[4];
     float bv = kNegMax;
     int bi = 0;
     for (int i = threadIdx.x; i < np; i += 256) amax_take(pv[i], pi[i], bv, bi);
     amax_block(bv, bi, sv, si);
-    if (threadIdx.x == 0) *out = bi;
+    if (threadIdx.x == 0) {
+        *out = bi;
+        if (state != nullptr) {          // decode state {pos, seq_len} advanced with the token
+            const int a = state[0], b = state[1];
+            state[0] = a + 1;
+            state[1] = b + 1;
+        }
+    }
 }
 
 // ---- Q4_K embedding rows ---------------------------------------------------------------
@@ -784,9 +941,11 @@ static hipError_t kv_write_rope(uint16_t* kc, uint16_t* vc, const float* k, cons
     if (kc == nullptr || vc == nullptr || k == nullptr || v == nullptr || nkv <= 0 || d <= 0 || (d & 1))
         return hipErrorInvalidValue;
     const int pairs = nkv * (d / 2);
+    const float* tab = nullptr;
+    const hipError_t e = theta_table(d, base, st, &tab);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rf_kv_write_rope_kernel, grid1(pairs), dim3(256), 0, st, reinterpret_cast<__half*>(kc),
-                       reinterpret_cast<__half*>(vc), k, v, pos_ptr, pos, nkv, d,
-                       base, neox, fs);
+                       reinterpret_cast<__half*>(vc), k, v, pos_ptr, pos, nkv, d, tab, neox, fs);
     return hipGetLastError();
 }
 extern "C" hipError_t gpu_kv_write_rope_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
@@ -842,14 +1001,25 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_
                                                      const float theta_base, const int neox,
                                                      const float* d_freq_scale, hipStream_t stream) {
     if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_k_cache == nullptr || d_v_cache == nullptr ||
-        d_pos == nullptr || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || (head_dim & 1) ||
-        head_dim > 512)
+        d_pos == nullptr || num_heads <= 0 || num_kv_heads <= 0)
         return hipErrorInvalidValue;
     const int heads = num_heads + num_kv_heads;
-    hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel, dim3((heads + 3) / 4), dim3(256), 0, stream, d_q, d_k, d_v,
-                       d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
-                       d_pos, num_heads, num_kv_heads, head_dim, eps,
-                       theta_base, neox, d_freq_scale);
+    __half* kc = reinterpret_cast<__half*>(d_k_cache);
+    __half* vc = reinterpret_cast<__half*>(d_v_cache);
+    const float* tab = nullptr;
+    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
+    if (e != hipSuccess) return e;
+#define RF_QKR(LPP)                                                                                                    \
+    hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel<LPP>, dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP))),      \
+                       dim3(256), 0, stream, d_q, d_k, d_v, d_q_norm, d_k_norm, kc, vc, d_pos, num_heads,         \
+                       num_kv_heads, eps, tab, neox, d_freq_scale)
+    switch (head_dim) {
+    case 64: RF_QKR(8); break;
+    case 128: RF_QKR(16); break;
+    case 256: RF_QKR(32); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef RF_QKR
     return hipGetLastError();
 }
 
@@ -874,6 +1044,25 @@ extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_ou
                        stream);
 }
 
+extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, const float* d_k,
+                                                        const float* d_v, const float* d_q_norm,
+                                                        const float* d_k_norm, uint16_t* d_k_cache, uint16_t* d_v_cache,
+                                                        const int* d_state, const int num_heads,
+                                                        const int num_kv_heads, const int head_dim, const float eps,
+                                                        const float theta_base, const int neox,
+                                                        const float* d_freq_scale, const float scale,
+                                                        hipStream_t stream) {
+    if (d_k == nullptr || d_v == nullptr || d_state == nullptr) return hipErrorInvalidValue;
+    const float* tab = nullptr;
+    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
+    if (e != hipSuccess) return e;
+    QkStep qk{d_k, d_v, d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
+              eps, tab, neox, d_freq_scale};
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
+                       scale, stream, &qk);
+}
+
 // ---- argmax ----
 extern "C" hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_partial_values, int* d_partial_indices,
                                                int* d_output_index, const int n, hipStream_t stream) {
@@ -884,7 +1073,20 @@ extern "C" hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_pa
     hipLaunchKernelGGL(rf_argmax_stage1_kernel, dim3(np), dim3(256), 0, stream, d_input, d_partial_values,
                        d_partial_indices, n);
     hipLaunchKernelGGL(rf_argmax_final_kernel, dim3(1), dim3(256), 0, stream, d_partial_values, d_partial_indices,
-                       d_output_index, np);
+                       d_output_index, np, nullptr);
+    return hipGetLastError();
+}
+extern "C" hipError_t rf_argmax_f32_advance_state_on_stream(const float* d_input, float* d_partial_values,
+                                                            int* d_partial_indices, int* d_output_index, const int n,
+                                                            int* d_state, hipStream_t stream) {
+    if (d_input == nullptr || d_partial_values == nullptr || d_partial_indices == nullptr ||
+        d_output_index == nullptr || d_state == nullptr || n <= 0)
+        return hipErrorInvalidValue;
+    const int np = (n + kArgmaxItems - 1) / kArgmaxItems;
+    hipLaunchKernelGGL(rf_argmax_stage1_kernel, dim3(np), dim3(256), 0, stream, d_input, d_partial_values,
+                       d_partial_indices, n);
+    hipLaunchKernelGGL(rf_argmax_final_kernel, dim3(1), dim3(256), 0, stream, d_partial_values, d_partial_indices,
+                       d_output_index, np, d_state);
     return hipGetLastError();
 }
 extern "C" hipError_t gpu_argmax_f32(const float* d_input, float* d_partial_values, int* d_partial_indices,

@@ -140,7 +140,12 @@ def test_graph_replays_eager_steps(eng):
 def test_fused_norm_decode_equals_separate(weights, eng):
     # the RMSNorm folded into the QKV / gate-up / LM-head GEMVs gives the same bits
     fused = E.Engine(CFG, weights, max_seq=256)
+    folded = E.Engine(CFG, weights, max_seq=256, fold_qk=True)
     prompt = list(range(7, 47))
+    folded.prefill(prompt)
+    fused.prefill(prompt)
+    assert folded.decode(5) == fused.decode(5)
+    assert np.array_equal(_h(folded.logits), _h(fused.logits))
     fused.prefill(prompt)
     eng.prefill(prompt)
     assert fused.decode(5) == eng.decode(5, graph=False)

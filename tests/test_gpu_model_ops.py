@@ -285,3 +285,46 @@ def test_attn_prefill(rf, dev, seq, nq, nkv, causal):
     err = np.abs(got - ref)
     print(f"prefill attention seq {seq}: max err {err.max() / np.abs(ref).max():.3e}", flush=True)
     assert (err <= PREFILL_REL * np.abs(ref).max() + PREFILL_REL * np.abs(ref)).all()
+
+
+@pytest.mark.parametrize("seq,nh,nkv,d", [(1, 32, 8, 128), (641, 32, 8, 128), (100, 8, 8, 64), (70, 8, 2, 256)])
+def test_attention_with_folded_qk_step(rf, dev, seq, nh, nkv, d):
+    # one launch = the standalone Q/K step + attention, bit for bit (caches too)
+    rng = np.random.default_rng(seq + nh)
+    max_seq = seq + 5
+    q = (rng.standard_normal(nh * d) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * d) * 3).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    qn, kn = ((1 + 0.1 * rng.standard_normal(d)).astype(np.float32) for _ in range(2))
+    cache = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.int16)
+    dq, dk, dv, dqn, dkn = (G.to_dev(a) for a in (q, k, v, qn, kn))
+    st = G.to_dev(np.array([seq - 1, seq], np.int32))
+    kc1, vc1, kc2, vc2 = (G.to_dev(cache) for _ in range(4))
+    out1, out2 = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
+    scale = 1.0 / math.sqrt(d)
+    G.call(rf.rf_attn_decode_qk_norm_rope_state, G.ptr(out1), G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn),
+           G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, scale)
+    np.testing.assert_array_equal(G.host(dq), q)        # the raw q is left as it was
+    G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(kc2),
+           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None)
+    dlen = G.to_dev(np.array([seq], np.int32))
+    G.call(rf.gpu_flash_attn_decode_strided_multi_head_state, G.ptr(out2), G.ptr(dq), G.ptr(kc2), G.ptr(vc2),
+           G.ptr(dlen), nh, nkv, d, scale)
+    np.testing.assert_array_equal(G.host(out1), G.host(out2))
+    np.testing.assert_array_equal(G.host(kc1), G.host(kc2))
+    np.testing.assert_array_equal(G.host(vc1), G.host(vc2))
+    # and against the oracle: normalised, rotated q over the updated caches
+    qr = O.rope(O.rms_norm(q, qn, 1e-6, nh), 1, nh, d, seq - 1, 1e6, True)
+    ref = O.attn_decode(qr.astype(np.float32), G.host(kc1).view(np.uint16), G.host(vc1).view(np.uint16), seq, nh,
+                        nkv, d, scale)
+    _close(G.host(out1), ref, f"attention with qk step seq {seq}")
+
+
+def test_argmax_advances_state(rf, dev):
+    x = np.random.default_rng(3).standard_normal(151936).astype(np.float32)
+    n = x.size
+    dx = G.to_dev(x)
+    pv, pi, out = G.empty(149, torch.float32), G.empty(149, torch.int32), G.empty(1, torch.int32)
+    st = G.to_dev(np.array([9, 10], np.int32))
+    G.call(rf.rf_argmax_f32_advance_state_on_stream, G.ptr(dx), G.ptr(pv), G.ptr(pi), G.ptr(out), n, G.ptr(st))
+    assert int(G.host(out)[0]) == O.argmax(x) and list(G.host(st)) == [10, 11]
