@@ -1586,8 +1586,11 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         // 128-row tiles, except for Q4_K when they would need a K split
         // (M = 128, 256 at N = 14336): 64-row tiles halve the split and
         // its float atomics (measured 3-5 % faster; Q6_K's heavier
-        // dequantisation makes them slower there)
-        else if (M % 128 == 0 && (IS_Q6 || 8L * (M / 128) * (N / 256) >= 7L * device_cu_count()))
+        // dequantisation makes them slower there).  Also 128-row tiles when
+        // they fit in one round of CUs but 64-row tiles would take two
+        // (M = 512 at N = 12288: 192 vs 384 tiles on 256 CUs)
+        else if (M % 128 == 0 && (IS_Q6 || 8L * (M / 128) * (N / 256) >= 7L * cus ||
+                                  (2L * (M / 128) * (N / 256) > cus && (long)(M / 128) * (N / 256) <= cus)))
             launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
         else
             launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st);

@@ -63,7 +63,8 @@ def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
 # One case per launcher branch for N % 256 == 0, K % 512 == 0 (the tiled
 # kernels): 256 x 256 or 128 x 128 shared-dequantisation tiles (where they
 # come to about one workgroup per CU); otherwise ring tiles of 128 rows (Q6_K, or
-# Q4_K when they fill the CUs unsplit -- the M = 512 Llama case below) or
+# Q4_K when they fill the CUs unsplit -- the M = 512 Llama case -- or fit one
+# round of CUs where 64-row tiles would need two) or
 # 64 rows, with split-K when the tiles leave CUs idle; and (Q6_K with
 # K % 2048 != 0) the register-weight kernel.
 @pytest.mark.parametrize("fmt,m,n,k", [
@@ -73,6 +74,7 @@ def test_gemm_small_shapes(rf, dev, fmt, m, n, k):
     ("q4_k", 384, 512, 512),     # ring, 64-row tiles, 1 split
     ("q4_k", 2048, 8192, 512),   # 256 x 256 shared-dequantisation tiles (256 tiles)
     ("q4_k", 256, 14336, 512),   # 128 x 128 shared-dequantisation tiles (224 tiles)
+    ("q4_k", 512, 12288, 512),   # ring, 128-row tiles: one round of CUs where 64-row tiles take two
     ("q6_k", 64, 256, 2048),     # ring, 64-row tiles, 4 splits
     ("q6_k", 256, 512, 4096),    # ring, 128-row tiles, 8 splits
     ("q6_k", 128, 256, 1536),    # register weights, 128-row tiles, 3 splits
