@@ -47,6 +47,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end leg (config 4)")
+    ap.add_argument("--gemm-pmc", action="store_true", help="only launch the M=512 GEMMs (for rocprofv3 --pmc)")
     ap.add_argument("--no-stream", action="store_true", help="skip the full decode weight stream leg (config 2)")
     ap.add_argument("--stream-tokens", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -320,6 +321,23 @@ def cpu_baseline(seconds):
     }
 
 
+def gemm_pmc(lib, torch):
+    """Ten untimed launches of each M = 512 prefill GEMM (Q4_K 14336x4096, Q6_K
+    4096x14336), for counter collection under rocprofv3 --pmc."""
+    from rocmforge_amd import synth
+    dev = torch.device("cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for fmt, n, k, fn in (("q4_k", N_FFN, K_FFN, lib.wmma_gemm_q4_k_launch),
+                          ("q6_k", K_FFN, N_FFN, lib.wmma_gemm_q6_k_launch)):
+        wsets = [synth.torch_weights(fmt, n, k, seed=50 + c, device=dev) for c in range(6)]
+        a = torch.randn(512, k, device=dev).to(torch.bfloat16).float()
+        d = torch.empty(512, n, device=dev)
+        for i in range(10):
+            fn(vp(a), vp(wsets[i % 6]), vp(d), 512, n, k, st)
+        torch.cuda.synchronize()
+    print(json.dumps({"gemm_pmc": "done"}), flush=True)
+
+
 def bench_e2e(torch, prompt_len=512, steps=128):
     """Qwen3-8B-shaped greedy generation (36 layers, hidden
     4096, FFN 12288, 32 q / 8 kv heads of 128, per-head Q/K RMSNorm, vocab
@@ -377,6 +395,9 @@ def main():
         raise SystemExit("bench.py needs a GPU (cuda:0)")
     if args.calibrate_copy:
         calibrate_copy(torch)
+        return
+    if args.gemm_pmc:
+        gemm_pmc(lib, torch)
         return
 
     r = bench_decode(lib, torch, args.steps, args.warmup)
