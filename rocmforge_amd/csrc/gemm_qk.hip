@@ -36,6 +36,18 @@
 
 namespace rf {
 
+// Row-block band of the v7 tile order (RF_GEMM_BAND, default 2), passed to
+// the kernel as an argument.
+static int g_gemm_band = -1;
+static int gemm_band_host() {
+    if (g_gemm_band < 0) {
+        const char* e = getenv("RF_GEMM_BAND");
+        g_gemm_band = e ? atoi(e) : 2;
+        if (g_gemm_band < 1 || g_gemm_band > 8) g_gemm_band = 2;
+    }
+    return g_gemm_band;
+}
+
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -887,7 +899,7 @@ template <typename T, bool IS_Q6, int FM, bool SPLIT>
 __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     float* __restrict__ D, int M, int N, int K,
-                                                                    int tiles, int chunks_per_split) {
+                                                                    int tiles, int chunks_per_split, int mg_arg) {
     using G = RingGeom7<IS_Q6>;
     constexpr int FN = 2;                               // 32-column blocks per wave
     constexpr int BM = 32 * FM;
@@ -919,8 +931,15 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     const int tile = vidx / splits;
     const int split = vidx % splits;
     const int ntiles = N / BN;
-    const int m0 = (tile / ntiles) * BM;
-    const int nt0 = (tile % ntiles) * BN;
+    // tiles ordered in bands of MG row blocks (column-major inside a band),
+    // so an XCD's contiguous run covers MG row blocks x (run / MG) column
+    // blocks: each weight column block is streamed by M/(BM MG) XCDs
+    // instead of M/BM (the A rows an XCD touches grow by MG)
+    const int mtiles = M / BM;
+    const int MG = (mg_arg > 1 && mtiles % mg_arg == 0) ? mg_arg : 1;
+    const int band = tile / (MG * ntiles), rb = tile % (MG * ntiles);
+    const int m0 = (band * MG + rb % MG) * BM;
+    const int nt0 = (rb / MG) * BN;
     const int n0 = nt0 + wave * 32 * FN;
     const int c_begin = split * chunks_per_split;
     const int c_last = c_begin + chunks_per_split - 1;
@@ -1537,7 +1556,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
                            st, reinterpret_cast<float4*>(D), n4);
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s);
+                               w, D, M, N, K, tiles, nchunks / s, gemm_band_host());
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
                                w, D, M, N, K, tiles, nchunks / s);
@@ -1547,7 +1566,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     } else {
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks);
+                               D, M, N, K, tiles, nchunks, gemm_band_host());
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
                                D, M, N, K, tiles, nchunks);
