@@ -328,3 +328,37 @@ def test_argmax_advances_state(rf, dev):
     st = G.to_dev(np.array([9, 10], np.int32))
     G.call(rf.rf_argmax_f32_advance_state_on_stream, G.ptr(dx), G.ptr(pv), G.ptr(pi), G.ptr(out), n, G.ptr(st))
     assert int(G.host(out)[0]) == O.argmax(x) and list(G.host(st)) == [10, 11]
+
+
+def test_attn_prefill_first_token_is_its_value(rf, dev):
+    # tests/wmma_attention_gqa_causal_correctness.rs:270-305 of the reference: row 0 attends to
+    # key 0 only, so its output is V[0] exactly (P = 1, l = 1) for every head
+    seq, nq, nkv, d = 128, 8, 2, 128
+    rng = np.random.default_rng(77)
+    q, k, v = (rng.standard_normal(seq * n * d).astype(np.float16) for n in (nq, nkv, nkv))
+    dq, dk, dv = (G.to_dev(a.view(np.int16)) for a in (q, k, v))
+    out = G.empty(seq * nq * d, torch.float32)
+    G.call(rf.wmma_attention_prefill_gqa_causal_launch, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(out), seq, nq, nkv, 1,
+           1.0 / math.sqrt(d))
+    row0 = G.host(out).reshape(seq, nq, d)[0]
+    v0 = v.reshape(seq, nkv, d)[0].astype(np.float32)
+    for h in range(nq):
+        np.testing.assert_array_equal(row0[h], v0[h // (nq // nkv)])
+
+
+def test_attn_prefill_gqa_full_seq256(rf, dev):
+    # the reference's gqa_only cases (non-causal), at its largest length
+    seq, nq, nkv, d = 256, 8, 2, 128
+    rng = np.random.default_rng(78)
+    q, k, v = (rng.standard_normal(seq * n * d).astype(np.float32) for n in (nq, nkv, nkv))
+    dq, dk, dv = (G.to_dev(a.astype(np.float16).view(np.int16)) for a in (q, k, v))
+    out = G.empty(seq * nq * d, torch.float32)
+    scale = 1.0 / math.sqrt(d)
+    G.call(rf.wmma_attention_prefill_gqa_causal_launch, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(out), seq, nq, nkv, 0,
+           scale)
+    got = G.host(out).reshape(seq, nq, d)
+    for r in (0, 100, 255):
+        qq = np.tile(q.reshape(seq, -1)[r], (seq, 1))
+        ref = O.attn_prefill_f16(qq, k, v, seq, nq, nkv, d, scale).reshape(seq, nq, d)[-1]
+        err = np.abs(got[r] - ref)
+        assert (err <= PREFILL_REL * np.abs(ref).max() + PREFILL_REL * np.abs(ref)).all(), r
