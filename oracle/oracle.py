@@ -14,6 +14,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libref_gemv.so"
+REF_OPS_LIB = HERE / "_ref" / "libref_ops.so"
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int

@@ -9,6 +9,7 @@ plus 1e-5 relative), the fp16 K cache within one fp16 ulp of the oracle's
 rounded value (the fp32 rotation may sit either side of a rounding
 boundary), and the Q4_K embedding at 2 fp32 ulps of the f64 dequant.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -362,3 +363,91 @@ def test_attn_prefill_gqa_full_seq256(rf, dev):
         ref = O.attn_prefill_f16(qq, k, v, seq, nq, nkv, d, scale).reshape(seq, nq, d)[-1]
         err = np.abs(got[r] - ref)
         assert (err <= PREFILL_REL * np.abs(ref).max() + PREFILL_REL * np.abs(ref)).all(), r
+
+
+# ---- against the reference's own layer kernels (oracle/_ref/libref_ops.so) -------------
+
+def _ref_ops():
+    if not O.REF_OPS_LIB.exists():
+        pytest.skip("oracle/_ref not built (needs the reference tree at build time)")
+    return ctypes.CDLL(str(O.REF_OPS_LIB), mode=ctypes.RTLD_LOCAL)
+
+
+def _both(ref, rf, name, argtypes, args_ours, args_ref):
+    for lib, args in ((rf, args_ours), (ref, args_ref)):
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+        print(f"[gpu] {name} ({'ours' if lib is rf else 'reference'})", flush=True)
+        assert fn(*args) == 0
+        torch.cuda.synchronize()
+
+
+def test_against_reference_layer_kernels(rf, dev):
+    """The same inputs through the reference's norm / rope / kv-write / decode
+    attention / argmax / embedding kernels and ours."""
+    ref = _ref_ops()
+    vp, i, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    rng = np.random.default_rng(123)
+    n = 4096
+    x = (rng.standard_normal(n) * 2).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    dx, dw = G.to_dev(x), G.to_dev(w)
+    a, b = G.empty(n, torch.float32), G.empty(n, torch.float32)
+    _both(ref, rf, "gpu_rms_norm", [vp, vp, vp, i, f, vp], (G.ptr(dx), G.ptr(dw), G.ptr(a), n, 1e-6, None),
+          (G.ptr(dx), G.ptr(dw), G.ptr(b), n, 1e-6, None))
+    assert _rel_err(G.host(a), G.host(b)) <= 1e-6
+    # rope (their theta uses powf in fp32; ours is within an ulp of it)
+    nh, d = 32, 128
+    q = rng.standard_normal(nh * d).astype(np.float32)
+    for pos in (3, 100):
+        qa, qb = G.to_dev(q), G.to_dev(q)
+        _both(ref, rf, "gpu_rope_heads", [vp, i, i, i, f, i, vp], (G.ptr(qa), pos, nh, d, 1e6, 1, None),
+              (G.ptr(qb), pos, nh, d, 1e6, 1, None))
+        assert _rel_err(G.host(qa), G.host(qb)) <= 1e-5
+    # kv write with rope into fp16 caches
+    nkv, max_seq, pos = 8, 16, 11
+    k = rng.standard_normal(nkv * d).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    dk, dv = G.to_dev(k), G.to_dev(v)
+    caches = [G.to_dev(np.zeros(max_seq * nkv * d, np.int16)) for _ in range(4)]
+    _both(ref, rf, "gpu_kv_write_rope", [vp, vp, vp, vp, i, i, i, f, i, vp],
+          (G.ptr(caches[0]), G.ptr(caches[1]), G.ptr(dk), G.ptr(dv), pos, nkv, d, 1e6, 1, None),
+          (G.ptr(caches[2]), G.ptr(caches[3]), G.ptr(dk), G.ptr(dv), pos, nkv, d, 1e6, 1, None))
+    np.testing.assert_array_equal(G.host(caches[1]), G.host(caches[3]))          # V: the same conversion
+    ko = G.host(caches[0]).view(np.float16).astype(np.float64)
+    kr = G.host(caches[2]).view(np.float16).astype(np.float64)
+    assert (np.abs(ko - kr) <= np.spacing(np.abs(kr).astype(np.float16)).astype(np.float64)).all()
+    # decode attention over 640 cached positions, GQA 4
+    seq, nkv = 640, 8
+    qd = rng.standard_normal(nh * d).astype(np.float32)
+    kc = G.to_dev(rng.standard_normal(seq * nkv * d).astype(np.float16).view(np.int16))
+    vc = G.to_dev(rng.standard_normal(seq * nkv * d).astype(np.float16).view(np.int16))
+    dq = G.to_dev(qd)
+    oa, ob = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
+    sc = 1.0 / math.sqrt(d)
+    _both(ref, rf, "gpu_flash_attn_decode_strided_multi_head", [vp, vp, vp, vp, i, i, i, i, f, vp],
+          (G.ptr(oa), G.ptr(dq), G.ptr(kc), G.ptr(vc), seq, nh, nkv, d, sc, None),
+          (G.ptr(ob), G.ptr(dq), G.ptr(kc), G.ptr(vc), seq, nh, nkv, d, sc, None))
+    assert _rel_err(G.host(oa), G.host(ob)) <= 1e-5
+    # argmax with ties
+    lg = rng.standard_normal(151936).astype(np.float32)
+    lg[[10, 5000, 151000]] = 9.0
+    dl = G.to_dev(lg)
+    parts = [G.empty(149, torch.float32), G.empty(149, torch.int32), G.empty(1, torch.int32)]
+    parts2 = [G.empty(149, torch.float32), G.empty(149, torch.int32), G.empty(1, torch.int32)]
+    _both(ref, rf, "gpu_argmax_f32", [vp, vp, vp, vp, i], (G.ptr(dl), *[G.ptr(t) for t in parts], 151936),
+          (G.ptr(dl), *[G.ptr(t) for t in parts2], 151936))
+    assert int(G.host(parts[2])[0]) == int(G.host(parts2[2])[0]) == 151000
+    # Q4_K embedding row
+    from rocmforge_amd import synth
+    emb = G.to_dev(synth.q4_k_weights(64, 4096, seed=5))
+    ea, eb = G.empty(4096, torch.float32), G.empty(4096, torch.float32)
+    _both(ref, rf, "gpu_embed_q4_k_token", [vp, vp, i, i, i, vp], (G.ptr(emb), G.ptr(ea), 4096, 64, 17, None),
+          (G.ptr(emb), G.ptr(eb), 4096, 64, 17, None))
+    assert _rel_err(G.host(ea), G.host(eb)) <= 1e-6
+
+
+def _rel_err(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.abs(a - b).max() / np.abs(b).max()
