@@ -27,6 +27,8 @@
 // values live in a small per-(device, d, base) table made on first use.
 #include <hip/hip_fp16.h>
 
+#include <mutex>
+
 #include "qk_common.h"
 
 namespace rf {
@@ -184,8 +186,10 @@ struct ThetaTab {
 };
 static ThetaTab g_theta[64];
 static int g_ntheta = 0;
+static std::mutex g_alloc_mutex;     // the theta tables and the attention workspace
 
 static hipError_t theta_table(int d, float base, hipStream_t st, const float** out) {
+    std::lock_guard<std::mutex> lock(g_alloc_mutex);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -686,10 +690,13 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
 // Workspace of the split path: one allocation per device, made on the first
 // call that needs more than it has (so not inside a graph capture: a
 // capturing stream with too small a workspace gets an error instead).
+// Calls that overlap on one device share it and race; the reference's
+// decode runs them in stream order.
 static float* g_attn_ws[64];
 static size_t g_attn_ws_bytes[64];
 
 static hipError_t attn_workspace(size_t bytes, hipStream_t st, float** ws) {
+    std::lock_guard<std::mutex> lock(g_alloc_mutex);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;

@@ -443,6 +443,18 @@ class GgufFile:
     def tokenizer_data(self) -> TokenizerData:
         return self._tokenizer
 
+    def close(self) -> None:
+        """Unmaps the file.  Tensor views still referenced keep the mapping
+        exported, and then mmap refuses (BufferError)."""
+        self._buf = None
+        self._mm.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
 
 # ---- matrix metadata and upload (weights.rs) --------------------------------------
 

@@ -385,3 +385,10 @@ def test_optional_layer_tensors(tmp_path, arch, bias, qk_norm):
         for t in ("q", "k"):
             v = f.tensor(f"blk.{i}.attn_{t}_norm.weight")
             assert (v is not None) == qk_norm and (v is None or v.dims == [hd])
+
+
+def test_file_closes(model):
+    p, tensors = model
+    with g.GgufFile.open(p) as f:
+        assert np.array_equal(f.tensor(tensors[0][0]).data, tensors[0][3])
+    assert f._mm.closed
