@@ -266,10 +266,35 @@ __global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* 
 // and sub + LPP/2 (one xor shuffle), classic pairs (2i, 2i+1) in one lane.
 // Both the standalone step and the attention with the step folded in use
 // this function, so they produce the same bits.
+// theta of the 8 pairs a lane rotates, loaded in one go (with the lane's x)
+template <int LPP>
+__device__ __forceinline__ void theta8(const float* __restrict__ tab, int sub, int neox,
+                                       const float* __restrict__ freq_scale, float t[8]) {
+    constexpr int D = 8 * LPP;
+    int p0;
+    if (neox) {
+        p0 = sub < LPP / 2 ? 8 * sub : 8 * sub - D / 2;
+        const float4 a = *reinterpret_cast<const float4*>(tab + p0);
+        const float4 b = *reinterpret_cast<const float4*>(tab + p0 + 4);
+        t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w; t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
+    } else {
+        p0 = 4 * sub;                          // pairs (2i, 2i+1): four per lane, t[i] for i even
+        const float4 a = *reinterpret_cast<const float4*>(tab + p0);
+        t[0] = a.x; t[2] = a.y; t[4] = a.z; t[6] = a.w;
+        t[1] = t[3] = t[5] = t[7] = 0.0f;
+    }
+    if (freq_scale != nullptr) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int p = neox ? p0 + i : p0 + i / 2;
+            if (neox || (i & 1) == 0) t[i] /= freq_scale[p];
+        }
+    }
+}
+
 template <int LPP>
 __device__ __forceinline__ void head_norm_rope(float v[8], int sub, const float* __restrict__ g, float eps, int pos,
-                                               const float* __restrict__ tab, int neox,
-                                               const float* __restrict__ freq_scale) {
+                                               const float t[8], int neox) {
     constexpr int D = 8 * LPP;
     if (g != nullptr) {
         float ss = v[0] * v[0];
@@ -286,14 +311,13 @@ __device__ __forceinline__ void head_norm_rope(float v[8], int sub, const float*
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float other = __shfl_xor(v[i], LPP / 2);
-            const int p = lo ? 8 * sub + i : 8 * sub + i - D / 2;
             float x0 = lo ? v[i] : other, x1 = lo ? other : v[i];
-            rope_pair(x0, x1, pos, rope_theta(p, tab, freq_scale));
+            rope_pair(x0, x1, pos, t[i]);
             v[i] = lo ? x0 : x1;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) rope_pair(v[i], v[i + 1], pos, rope_theta((8 * sub + i) / 2, tab, freq_scale));
+        for (int i = 0; i < 8; i += 2) rope_pair(v[i], v[i + 1], pos, t[i]);
     }
 }
 
@@ -327,9 +351,10 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     const bool is_q = hidx < nh;
     const int head = is_q ? hidx : hidx - nh;
     const int pos = *pos_ptr;
-    float x[8];
+    float x[8], th[8];
     load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
-    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, tab, neox, freq_scale);
+    theta8<LPP>(tab, sub, neox, freq_scale, th);
+    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
     if (is_q) {
         float* dst = q + (size_t)head * D + 8 * sub;
         *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
@@ -519,8 +544,9 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     const int pos = seq - 1;
     const bool owner = QK && split == (pos / kSplitChunk) % S;   // workgroup-uniform
     // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
-    float qv[8], kx[8], vx[8];
+    float qv[8], kx[8], vx[8], th[8];
     load8(q + (size_t)head * D + 8 * sub, qv);
+    if constexpr (QK) theta8<LPP>(qk.tab, sub, qk.neox, qk.freq_scale, th);
     if (owner && wave == 0) {
         load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
         load8(qk.v + (size_t)kvh * D + 8 * sub, vx);
@@ -539,10 +565,10 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
         }
         if constexpr (QK) {
             if (c0 == split * kSplitChunk) {     // first chunk: the per-head step, while the loads fly
-                head_norm_rope<LPP>(qv, sub, qk.q_norm, qk.eps, pos, qk.tab, qk.neox, qk.freq_scale);
+                head_norm_rope<LPP>(qv, sub, qk.q_norm, qk.eps, pos, th, qk.neox);
                 if (owner) {
                     if (wave == 0) {
-                        head_norm_rope<LPP>(kx, sub, qk.k_norm, qk.eps, pos, qk.tab, qk.neox, qk.freq_scale);
+                        head_norm_rope<LPP>(kx, sub, qk.k_norm, qk.eps, pos, th, qk.neox);
                         if (grp == 0) {
                             const size_t c = (size_t)pos * row + (size_t)kvh * D + 8 * sub;
                             store8_f16(qk.kc + c, kx);
