@@ -378,10 +378,18 @@ class Engine:
             _chk(L.rf_kv_write_batched_on_stream(_p(self.kc[i]), _p(self.vc[i]), _p(b["k"]), _p(b["v"]), 0,
                                                  c.kv_size, self.max_seq, M, st), "kv write")
             t("qk_rope_kv", i)
-            for src, dst, n in (("q", "q16", mp * c.q_size), ("k", "k16", mp * c.kv_size),
-                                ("v", "v16", mp * c.kv_size)):
-                _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), n, st), "to f16")
-            _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(b["k16"]), _p(b["v16"]), _p(b["att"]),
+            # K and V: the fp16 cache rows just written are the attention's operands
+            # (same [position][kv heads * d] layout; keys past the prompt are seen
+            # only by the padding queries, whose outputs are never used; real queries
+            # weigh them by an exact zero, and every cache row holds finite fp16)
+            _chk(L.convert_f32_to_f16(_p(b["q"]), _p(b["q16"]), mp * c.q_size, st), "to f16")
+            if mp <= self.max_seq:
+                k16, v16 = self.kc[i], self.vc[i]
+            else:
+                for src, dst in (("k", "k16"), ("v", "v16")):
+                    _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), mp * c.kv_size, st), "to f16")
+                k16, v16 = b["k16"], b["v16"]
+            _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(k16), _p(v16), _p(b["att"]),
                                                            mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
                  "attention")
             t("attention", i)
