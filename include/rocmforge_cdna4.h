@@ -101,6 +101,27 @@ hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, f
 hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N, int K,
                                  hipStream_t stream);
 
+/* No counterpart in the reference (its prefill issues one GEMM per weight
+ * and adds residuals with gpu_add).  Several weight matrices that share the
+ * input and K in one launch: out_i[M x n_i] = fp16(A) * fp16(dequant W_i)^T
+ * for i = 0..2, each output row-major with width n_i (n1 = 0 and n2 = 0
+ * drop segments; all n_i % 256 == 0).  The per-element arithmetic is the
+ * single GEMM's.  K % 512 == 0 (Q6_K: K % 2048 == 0), M % 64 == 0, A and
+ * outputs 16-byte aligned.  Used for the Q/K/V projections of a prefill. */
+hipError_t rf_gemm_q4_k_segments_launch(const float* input, const void* w0, const void* w1, const void* w2,
+                                        float* out0, float* out1, float* out2, int M, int n0, int n1, int n2, int K,
+                                        hipStream_t stream);
+hipError_t rf_gemm_q6_k_segments_launch(const float* input, const void* w0, const void* w1, const void* w2,
+                                        float* out0, float* out1, float* out2, int M, int n0, int n1, int n2, int K,
+                                        hipStream_t stream);
+/* No counterpart in the reference.  inout[M x N] += fp16(A) * fp16(dequant
+ * W)^T: the O and FFN-down projections of a prefill add straight into the
+ * residual stream.  N % 256 == 0, other rules as the segment launchers. */
+hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const void* weights_q4_k, float* inout, int M, int N,
+                                          int K, hipStream_t stream);
+hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const void* weights_q6_k, float* inout, int M, int N,
+                                          int K, hipStream_t stream);
+
 /* ---- Host dispatch (routing of the arms above) --------------------------
  * C counterparts of ROCmForge's src/gpu/ops.rs routing for the Q4_K / Q6_K
  * arms: which launcher a GGUF weight tensor goes to, in which order the

@@ -27,6 +27,10 @@
 //    blocks of v_mfma_f32_32x32x16_f16; each 64-wide K chunk of A (fp32 ->
 //    fp16) and of W (dequantised in registers, 2 threads per weight row)
 //    lands in LDS as [row][k] fp16 with a padded stride, double buffered.
+// The v7 kernel also serves two launchers with no reference counterpart:
+// several weight matrices over one input as column segments of a single
+// launch (rf_gemm_q*_k_segments_launch), and D += product
+// (rf_gemm_q*_k_accumulate_launch, also served by sq).
 #include <stdlib.h>
 
 #include <type_traits>
@@ -895,11 +899,28 @@ struct RingGeom7 {
     static constexpr int kNI = kGroups / 4;
 };
 
+// Output routing of one v7 launch.  The N columns fall into up to three
+// segments, each with its own weight rows and output matrix: [0, n1) -> (W,
+// D), [n1, n2) -> (w1, d1), [n2, N) -> (w2, d2), every boundary a multiple
+// of the 256-column tile (a single GEMM has n1 = n2 = N).  Each segment's
+// output is row-major with its own width.  accum != 0 adds the product to
+// the output's contents instead of storing it (the split-K path always
+// adds).
+struct GemmSegs {
+    const uint8_t* w1;
+    const uint8_t* w2;
+    float* d1;
+    float* d2;
+    int n1, n2;
+    int accum;
+};
+
 template <typename T, bool IS_Q6, int FM, bool SPLIT>
 __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     float* __restrict__ D, int M, int N, int K,
-                                                                    int tiles, int chunks_per_split, int mg_arg) {
+                                                                    int tiles, int chunks_per_split, int mg_arg,
+                                                                    GemmSegs segs) {
     using G = RingGeom7<IS_Q6>;
     constexpr int FN = 2;                               // 32-column blocks per wave
     constexpr int BM = 32 * FM;
@@ -945,7 +966,13 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     const int c_last = c_begin + chunks_per_split - 1;
     const int sb_begin = c_begin / 4, sb_last = c_last / 4;
     const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
-    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
+    // the column segment of this tile (selects, not an indexed argument array)
+    const int sgi = nt0 >= segs.n2 ? 2 : (nt0 >= segs.n1 ? 1 : 0);
+    const int nbase = sgi == 2 ? segs.n2 : (sgi == 1 ? segs.n1 : 0);
+    const int ldd = (sgi == 2 ? N : (sgi == 1 ? segs.n2 : segs.n1)) - nbase;
+    const uint8_t* wseg = sgi == 2 ? segs.w2 : (sgi == 1 ? segs.w1 : W);
+    float* dseg = sgi == 2 ? segs.d2 : (sgi == 1 ? segs.d1 : D);
+    const uint8_t* wtile = wseg + (size_t)(nt0 - nbase) * row_bytes;
 
     uint32_t goff[G::kNI];
     uint32_t gdst[G::kNI];
@@ -1253,14 +1280,15 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int col = n0 + 32 * j + (lane & 31);
+            const int col = n0 - nbase + 32 * j + (lane & 31);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                float* o = dseg + (size_t)row * ldd + col;
                 if constexpr (SPLIT)
-                    unsafeAtomicAdd(&D[(size_t)row * N + col], acc[i][j][e]);
+                    unsafeAtomicAdd(o, acc[i][j][e]);
                 else
-                    D[(size_t)row * N + col] = acc[i][j][e];
+                    *o = segs.accum ? *o + acc[i][j][e] : acc[i][j][e];
             }
         }
 }
@@ -1300,7 +1328,8 @@ struct SqRaw<true, TPR> {
 template <bool IS_Q6, int BM, int BN>
 __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
-                                                                    float* __restrict__ D, int M, int N, int K) {
+                                                                    float* __restrict__ D, int M, int N, int K,
+                                                                    int accum) {
     constexpr int FMW = BM / 64, FNW = BN / 64;          // MFMA blocks per wave along M, N
     constexpr int TPR = kSqThreads / BN;                 // threads per weight row
     constexpr int NP = 16 / TPR;                         // 4-weight pieces per thread per chunk
@@ -1515,14 +1544,10 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                D[(size_t)row * N + col] = acc[i][j][e];
+                float* o = D + (size_t)row * N + col;
+                *o = accum ? *o + acc[i][j][e] : acc[i][j][e];
             }
         }
-}
-
-__global__ void rf_fill_zero_kernel(float4* __restrict__ p, size_t n4) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
@@ -1537,8 +1562,28 @@ static int gemm_splits(int tiles, int nchunks, int cus) {
     return best;
 }
 
+// Zeroes the outputs of the column segments of a split-K launch: segment i
+// is m * widths[i] floats at its own pointer.
+__global__ void rf_fill_zero_segs_kernel(float4* __restrict__ p0, size_t n0, float4* __restrict__ p1, size_t n1,
+                                         float4* __restrict__ p2, size_t n2) {
+    const size_t total = n0 + n1 + n2;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        float4* p = i < n0 ? p0 + i : (i < n0 + n1 ? p1 + (i - n0) : p2 + (i - n0 - n1));
+        *p = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+static GemmSegs single_seg(int N) {
+    GemmSegs g{};
+    g.n1 = g.n2 = N;
+    return g;
+}
+
 template <bool IS_Q6, int FM>
-static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st) {
+static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
+                      const GemmSegs& sg) {
+    // column segments and accumulation exist only in v7
+    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum;
     using T = typename std::conditional<IS_Q6, Q6Ops, Q4Ops>::type;
     const int tiles = (M / (32 * FM)) * (N / 256);
     const int nchunks = K / kKC;
@@ -1549,14 +1594,19 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     }
     // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
     const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
-    const bool v7 = v5 && (gemm_kernel_version() == 0 || gemm_kernel_version() == 7);
+    const bool v7 = !plain || (v5 && (gemm_kernel_version() == 0 || gemm_kernel_version() == 7));
     if (s > 1) {
-        const size_t n4 = (size_t)M * N / 4;
-        hipLaunchKernelGGL(rf_fill_zero_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 2048)), dim3(256), 0,
-                           st, reinterpret_cast<float4*>(D), n4);
+        if (!sg.accum) {
+            const size_t a4 = (size_t)M * sg.n1 / 4, b4 = (size_t)M * (sg.n2 - sg.n1) / 4,
+                         c4 = (size_t)M * (N - sg.n2) / 4;
+            hipLaunchKernelGGL(rf_fill_zero_segs_kernel,
+                               dim3((unsigned)std::min<size_t>((a4 + b4 + c4 + 255) / 256, 2048)), dim3(256), 0, st,
+                               reinterpret_cast<float4*>(D), a4, reinterpret_cast<float4*>(sg.d1), b4,
+                               reinterpret_cast<float4*>(sg.d2), c4);
+        }
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s, gemm_band_host());
+                               w, D, M, N, K, tiles, nchunks / s, gemm_band_host(), sg);
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
                                w, D, M, N, K, tiles, nchunks / s);
@@ -1566,7 +1616,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     } else {
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks, gemm_band_host());
+                               D, M, N, K, tiles, nchunks, gemm_band_host(), sg);
         else if (v5)
             hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
                                D, M, N, K, tiles, nchunks);
@@ -1580,15 +1630,21 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
 // they fill the CUs (split-K adds float atomics on M x N outputs, which cost
 // more than the tile shape saves).
 template <bool IS_Q6, int BM, int BN>
-static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st) {
+static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st, int accum) {
     const int tiles = (M / BM) * (N / BN);
-    hipLaunchKernelGGL((rf_gemm_qk_sq_kernel<IS_Q6, BM, BN>), dim3(tiles), dim3(kSqThreads), 0, st, A, w, D, M, N, K);
+    hipLaunchKernelGGL((rf_gemm_qk_sq_kernel<IS_Q6, BM, BN>), dim3(tiles), dim3(kSqThreads), 0, st, A, w, D, M, N, K,
+                       accum);
 }
 
+// sg routes column segments / accumulation (v7 and sq only: the callers of
+// a non-trivial sg have checked N % 256 == 0, K % 512 == 0 and, for Q6_K,
+// K % 2048 == 0, and segments never reach sq)
 template <bool IS_Q6>
-static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
+static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
+                              const GemmSegs& sg) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    if (N % 256 == 0 && K % 512 == 0 && gemm_kernel_version() != 1) {
+    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum;
+    if (N % 256 == 0 && K % 512 == 0 && (gemm_kernel_version() != 1 || !plain)) {
         // shared-dequantisation tiles where they come to about one
         // workgroup per CU without a K split: 256 x 256 (M >= 1024 at the
         // Llama FFN shapes, 10 % faster than v7), else 128 x 128 at up to
@@ -1597,11 +1653,11 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long cus = device_cu_count();
         const long sq_tiles = (long)(M / 256) * (N / 256);
         const long sq128_tiles = (long)(M / 128) * (N / 128);
-        const bool sq_ok = gemm_kernel_version() == 0;
+        const bool sq_ok = gemm_kernel_version() == 0 && sg.n1 == N && sg.n2 == N;
         if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
-            launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st);
+            launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
-            launch_sq<IS_Q6, 128, 128>(A, w, D, M, N, K, st);
+            launch_sq<IS_Q6, 128, 128>(A, w, D, M, N, K, st, sg.accum);
         // 128-row tiles, except for Q4_K when they would need a K split
         // (M = 128, 256 at N = 14336): 64-row tiles halve the split and
         // its float atomics (measured 3-5 % faster; Q6_K's heavier
@@ -1610,9 +1666,9 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         // (M = 512 at N = 12288: 192 vs 384 tiles on 256 CUs)
         else if (M % 128 == 0 && (IS_Q6 || 8L * (M / 128) * (N / 256) >= 7L * cus ||
                                   (2L * (M / 128) * (N / 256) > cus && (long)(M / 128) * (N / 256) <= cus)))
-            launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st);
+            launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st, sg);
         else
-            launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st);
+            launch_v4<IS_Q6, 2>(A, w, D, M, N, K, st, sg);
         return hipGetLastError();
     }
     if (M % 128 == 0 && N % 128 == 0 && (size_t)(M / 128) * (N / 128) >= (size_t)device_cu_count()) {
@@ -1637,7 +1693,7 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
     if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(input) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
         return hipErrorInvalidValue;
-    return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream);
+    return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
 }
 
 extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,
@@ -1646,5 +1702,68 @@ extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weig
     if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(input) & 15u) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 1u))
         return hipErrorInvalidValue;
-    return launch_gemm<true>(input, weights_q6_k, output, M, N, K, stream);
+    return launch_gemm<true>(input, weights_q6_k, output, M, N, K, stream, single_seg(N));
+}
+
+// Shapes the segmented / accumulating launches take: whole 256-column tiles,
+// K in 512 steps (Q6_K: 2048, for the 16-byte aligned weight ring), the
+// GEMM launchers' M/K rules, 16-byte aligned A and outputs.
+template <bool IS_Q6>
+static bool seg_shape_ok(const float* A, int M, int K) {
+    if (M <= 0 || K <= 0 || M % 64 || K % (IS_Q6 ? 2048 : 512)) return false;
+    return (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <bool IS_Q6>
+static hipError_t gemm_segments(const float* A, const void* w0, const void* w1, const void* w2, float* d0,
+                                float* d1, float* d2, int M, int n0, int n1, int n2, int K, hipStream_t st) {
+    if (!seg_shape_ok<IS_Q6>(A, M, K) || !w0 || !d0 || n0 <= 0 || n1 < 0 || n2 < 0) return hipErrorInvalidValue;
+    if (n0 % 256 || n1 % 256 || n2 % 256 || (n1 == 0 && n2 > 0)) return hipErrorInvalidValue;
+    if ((n1 && (!w1 || !d1)) || (n2 && (!w2 || !d2))) return hipErrorInvalidValue;
+    const uintptr_t wal = IS_Q6 ? 1u : 15u;
+    for (const void* w : {w0, w1, w2})
+        if (w && (reinterpret_cast<uintptr_t>(w) & wal)) return hipErrorInvalidValue;
+    for (const float* d : {d0, d1, d2})
+        if (d && !aligned16(d)) return hipErrorInvalidValue;
+    GemmSegs sg{};
+    sg.w1 = static_cast<const uint8_t*>(w1);
+    sg.w2 = static_cast<const uint8_t*>(w2);
+    sg.d1 = d1;
+    sg.d2 = d2;
+    sg.n1 = n0;
+    sg.n2 = n0 + n1;
+    return launch_gemm<IS_Q6>(A, w0, d0, M, n0 + n1 + n2, K, st, sg);
+}
+
+template <bool IS_Q6>
+static hipError_t gemm_accumulate(const float* A, const void* w, float* D, int M, int N, int K, hipStream_t st) {
+    if (!seg_shape_ok<IS_Q6>(A, M, K) || !w || !D || N <= 0 || N % 256 || !aligned16(D)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(w) & (IS_Q6 ? 1u : 15u)) return hipErrorInvalidValue;
+    GemmSegs sg = single_seg(N);
+    sg.accum = 1;
+    return launch_gemm<IS_Q6>(A, w, D, M, N, K, st, sg);
+}
+
+extern "C" hipError_t rf_gemm_q4_k_segments_launch(const float* input, const void* w0, const void* w1, const void* w2,
+                                                   float* out0, float* out1, float* out2, int M, int n0, int n1,
+                                                   int n2, int K, hipStream_t stream) {
+    return gemm_segments<false>(input, w0, w1, w2, out0, out1, out2, M, n0, n1, n2, K, stream);
+}
+
+extern "C" hipError_t rf_gemm_q6_k_segments_launch(const float* input, const void* w0, const void* w1, const void* w2,
+                                                   float* out0, float* out1, float* out2, int M, int n0, int n1,
+                                                   int n2, int K, hipStream_t stream) {
+    return gemm_segments<true>(input, w0, w1, w2, out0, out1, out2, M, n0, n1, n2, K, stream);
+}
+
+extern "C" hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const void* weights_q4_k, float* inout,
+                                                     int M, int N, int K, hipStream_t stream) {
+    return gemm_accumulate<false>(input, weights_q4_k, inout, M, N, K, stream);
+}
+
+extern "C" hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const void* weights_q6_k, float* inout,
+                                                     int M, int N, int K, hipStream_t stream) {
+    return gemm_accumulate<true>(input, weights_q6_k, inout, M, N, K, stream);
 }

@@ -138,17 +138,22 @@ class Engine:
     """Prefill + greedy decode of one sequence of up to max_seq tokens."""
 
     def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0",
-                 fuse_norm: bool = True, fold_qk: bool = False):
+                 fuse_norm: bool = True, fold_qk: bool = False, fuse_gemm: bool = True):
         """fuse_norm: decode with the RMSNorms folded into the GEMVs that
         consume them, the per-head Q/K step into the attention and the state
         advance into the argmax (same bits as the separate launches);
         fold_qk: the per-head Q/K step folded into the attention (with
         fuse_norm; off by default: measured on MI355X at the Qwen3-8B shape
-        it is 2.28 ms/token against 2.20 with the separate step)."""
+        it is 2.28 ms/token against 2.20 with the separate step);
+        fuse_gemm: prefill projections that share an input in one segmented
+        GEMM launch, and the O / FFN-down products added straight into the
+        residual stream (same per-element products; the sums of a K split
+        land in another order)."""
         import torch
         self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
         self.fuse_norm = fuse_norm
         self.fold_qk = fold_qk and fuse_norm
+        self.fuse_gemm = fuse_gemm
         self.lib = _lib.load()
         ops._lib()
         f32, i16 = torch.float32, torch.int16
@@ -362,9 +367,8 @@ class Engine:
             m = lw.mats
             _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn"]), c.hidden, c.eps, mp,
                                                   st), "norm")
-            for name, out, n in (("attn_q", b["q"], c.q_size), ("attn_k", b["k"], c.kv_size),
-                                 ("attn_v", b["v"], c.kv_size)):
-                self._gemm(m[name], b["xn"], out, n, c.hidden, M, st)
+            self._gemm_group([(m["attn_q"], b["q"], c.q_size), (m["attn_k"], b["k"], c.kv_size),
+                              (m["attn_v"], b["v"], c.kv_size)], b["xn"], c.hidden, M, st)
             t("qkv", i)
             if lw.q_norm is not None:
                 _chk(L.gpu_rms_norm_batched_on_stream(_p(b["q"]), _p(lw.q_norm), _p(b["q"]), c.head_dim, c.eps,
@@ -393,17 +397,16 @@ class Engine:
                                                            mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
                  "attention")
             t("attention", i)
-            self._gemm(m["attn_output"], b["att"], b["tmp"], c.hidden, c.q_size, M, st)
-            _chk(L.gpu_add(_p(b["x"]), _p(b["tmp"]), _p(b["x"]), M * c.hidden, st), "add")
+            self._gemm_residual(m["attn_output"], b["att"], b["x"], b["tmp"], c.hidden, c.q_size, M, st)
             t("attn_output", i)
             _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp, st),
                  "norm")
+            # two launches: one over both (384 tiles of 128 rows at M = 512) was slower
             self._gemm(m["ffn_gate"], b["xn"], b["g"], c.ff, c.hidden, M, st)
             self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
             _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             t("gate_up", i)
-            self._gemm(m["ffn_down"], b["g"], b["tmp"], c.hidden, c.ff, M, st)
-            _chk(L.gpu_add(_p(b["x"]), _p(b["tmp"]), _p(b["x"]), M * c.hidden, st), "add")
+            self._gemm_residual(m["ffn_down"], b["g"], b["x"], b["tmp"], c.hidden, c.ff, M, st)
             t("ffn_down", i)
         last = ctypes.c_void_p(b["x"].data_ptr() + 4 * (M - 1) * c.hidden)
         _chk(L.gpu_rms_norm(last, _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
@@ -415,6 +418,47 @@ class Engine:
         t("lm_head", -1)
         torch.cuda.synchronize()
         return int(self.token.item())
+
+    def _fusable(self, wtype, n, k):
+        return (self.fuse_gemm and wtype in (GgmlType.Q4_K, GgmlType.Q6_K) and n % 256 == 0
+                and k % (2048 if wtype == GgmlType.Q6_K else 512) == 0)
+
+    def _gemm_group(self, items, a, k, m, st):
+        """items = [((w, meta), out, n), ...] over one input: runs of up to
+        three matrices of one type go through one segmented launch (the Q/K/V
+        projections); the rest one GEMM each."""
+        mp = -(-m // 64) * 64
+        i = 0
+        while i < len(items):
+            t = items[i][0][1].wtype
+            j = i
+            while j < len(items) and j - i < 3 and items[j][0][1].wtype == t and self._fusable(t, items[j][2], k):
+                j += 1
+            if j - i < 2:
+                (wm, out, n) = items[i]
+                self._gemm(wm, a, out, n, k, m, st)
+                i += 1
+                continue
+            run = items[i:j] + [((None, None), None, 0)] * (3 - (j - i))
+            fn = (self.lib.rf_gemm_q4_k_segments_launch if t == GgmlType.Q4_K
+                  else self.lib.rf_gemm_q6_k_segments_launch)
+            _chk(fn(_p(a), *[_p(r[0][0]) for r in run], *[_p(r[1]) for r in run], mp, *[r[2] for r in run], k, st),
+                 "gemm segments")
+            i = j
+
+    def _gemm_residual(self, wm, a, x, tmp, n, k, m, st):
+        """x[:m] += a W^T: one accumulating launch where the shape allows
+        (its padding rows then take the padding rows' product too), else a
+        GEMM into tmp and an add of the m real rows."""
+        w, meta = wm
+        if self._fusable(meta.wtype, n, k):
+            mp = -(-m // 64) * 64
+            fn = (self.lib.rf_gemm_q4_k_accumulate_launch if meta.wtype == GgmlType.Q4_K
+                  else self.lib.rf_gemm_q6_k_accumulate_launch)
+            _chk(fn(_p(a), _p(w), _p(x), mp, n, k, st), "gemm accumulate")
+            return
+        self._gemm(wm, a, tmp, n, k, m, st)
+        _chk(self.lib.gpu_add(_p(x), _p(tmp), _p(x), m * n, st), "add")
 
     def _gemm(self, wm, a, out, n, k, m, st):
         """out[m_pad x n] = a[m_pad x k] W^T through the prefill GEMM launchers

@@ -1,0 +1,112 @@
+"""GPU parity of the two prefill GEMM launchers that have no reference
+counterpart: several weight matrices as column segments of one launch
+(rf_gemm_q*_k_segments_launch) and D += product (rf_gemm_q*_k_accumulate_launch).
+
+Each segment / accumulated product is checked against the oracle's float64
+product of the fp16-rounded operands at the GEMM bar
+  |D - D_ref| <= 2e-3 * |D_ref| + 1e-5 * max|D_ref|   (plus 1e-6 * |R| for D = R + product),
+and, where the launch takes no K split, bit for bit against the single-GEMM
+launcher (the per-element arithmetic is the same: one fp32 add of R for the
+accumulating form).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from rocmforge_amd import synth
+from tests import gpu_util as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, ref, what, base=None):
+    scale = np.abs(ref).max()
+    err = np.abs(got.astype(np.float64) - ref - (0.0 if base is None else base.astype(np.float64)))
+    tol = 2e-3 * np.abs(ref) + 1e-5 * scale + (0.0 if base is None else 1e-6 * np.abs(base))
+    worst = (err / tol).max()
+    print(f"{what}: max_abs={err.max():.3e} max|ref|={scale:.3e} worst={worst:.3f}", flush=True)
+    assert worst <= 1.0, what
+
+
+def _single(rf, fmt, a_dev, w, m, n, k):
+    dw = G.to_dev(w)
+    d = G.empty(m * n, torch.float32)
+    fn = rf.wmma_gemm_q4_k_launch if fmt == "q4_k" else rf.wmma_gemm_q6_k_launch
+    G.call(fn, G.ptr(a_dev), G.ptr(dw), G.ptr(d), m, n, k)
+    return G.host(d).reshape(m, n)
+
+
+def _segments(rf, fmt, a_dev, ws, m, ns, k):
+    dws = [G.to_dev(w) for w in ws]
+    ds = [G.empty(m * n, torch.float32).fill_(float("nan")) for n in ns]
+    wp = [G.ptr(t) for t in dws] + [ctypes.c_void_p(0)] * (3 - len(ws))
+    dp = [G.ptr(t) for t in ds] + [ctypes.c_void_p(0)] * (3 - len(ns))
+    nn = list(ns) + [0] * (3 - len(ns))
+    fn = rf.rf_gemm_q4_k_segments_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_segments_launch
+    G.call(fn, G.ptr(a_dev), *wp, *dp, m, *nn, k)
+    return [G.host(d).reshape(m, n) for d, n in zip(ds, ns)]
+
+
+# (fmt, M, segment widths, K, K split taken by the fused launch)
+@pytest.mark.parametrize("fmt,m,ns,k,split", [
+    ("q4_k", 512, (1024, 256, 256), 512, False),    # 64-row tiles, one K pass (Q/K/V shape, narrowed)
+    ("q4_k", 64, (512, 256, 256), 1024, True),      # split-K: every segment zeroed, then atomics
+    ("q4_k", 128, (768, 256), 512, False),          # two segments (V in another type)
+    ("q6_k", 128, (512, 256), 2048, True),
+    ("q6_k", 256, (256, 256, 512), 2048, True),
+])
+def test_segments_match_oracle_and_single(rf, dev, fmt, m, ns, k, split):
+    a = synth.activations(k, seed=m + k, m=m)
+    ws = [synth.weights(fmt, n, k, seed=10 + i) for i, n in enumerate(ns)]
+    da = G.to_dev(a)
+    got = _segments(rf, fmt, da, ws, m, ns, k)
+    for i, (g, w, n) in enumerate(zip(got, ws, ns)):
+        _check(g, O.gemm(fmt, a, w, m, n, k), f"{fmt} segment {i} {m}x{n}x{k}")
+        if not split:
+            np.testing.assert_array_equal(g, _single(rf, fmt, da, w, m, n, k))
+
+
+@pytest.mark.parametrize("fmt,m,n,k,split", [
+    ("q4_k", 64, 256, 512, False),       # v7, 64-row tiles
+    ("q4_k", 256, 14336, 512, False),    # 128 x 128 shared-dequantisation tiles
+    ("q4_k", 128, 512, 2048, True),      # split-K adds onto the caller's values
+    ("q6_k", 256, 512, 4096, True),
+    ("q6_k", 512, 1024, 2048, True),
+])
+def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k, split):
+    a = synth.activations(k, seed=3 * m + n, m=m)
+    w = synth.weights(fmt, n, k, seed=k + 2)
+    r = np.random.default_rng(m + n).standard_normal((m, n)).astype(np.float32) * 4.0
+    da, dw, dr = G.to_dev(a), G.to_dev(w), G.to_dev(r.ravel())
+    fn = rf.rf_gemm_q4_k_accumulate_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_accumulate_launch
+    G.call(fn, G.ptr(da), G.ptr(dw), G.ptr(dr), m, n, k)
+    got = G.host(dr).reshape(m, n)
+    _check(got, O.gemm(fmt, a, w, m, n, k), f"{fmt} accumulate {m}x{n}x{k}", base=r)
+    if not split:
+        np.testing.assert_array_equal(got, r + _single(rf, fmt, da, w, m, n, k))
+
+
+def test_rejections(rf, dev):
+    m, k = 64, 512
+    da = G.to_dev(synth.activations(k, seed=1, m=m))
+    w = G.to_dev(synth.weights("q4_k", 512, k, seed=1))
+    d = G.empty(m * 512, torch.float32)
+    s = G.stream()
+    z = ctypes.c_void_p(0)
+    P = G.ptr
+    seg = rf.rf_gemm_q4_k_segments_launch
+    assert seg(P(da), P(w), z, z, P(d), z, z, m, 512, 0, 0, k, s) == 0
+    torch.cuda.synchronize()
+    assert seg(P(da), P(w), z, z, P(d), z, z, m, 320, 0, 0, k, s) != 0          # not whole 256-column tiles
+    assert seg(P(da), P(w), z, P(w), P(d), z, P(d), m, 256, 0, 256, k, s) != 0   # third segment without second
+    assert seg(P(da), P(w), z, z, P(d), z, z, m, 256, 256, 0, k, s) != 0         # segment without pointers
+    assert seg(P(da), P(w), z, z, P(d), z, z, 96, 256, 0, 0, k, s) != 0          # M % 64
+    assert seg(P(da), P(w), z, z, P(d), z, z, m, 256, 0, 0, 256, s) != 0         # K % 512
+    assert rf.rf_gemm_q6_k_segments_launch(P(da), P(w), z, z, P(d), z, z, m, 256, 0, 0, 1024, s) != 0  # Q6_K K % 2048
+    acc = rf.rf_gemm_q4_k_accumulate_launch
+    assert acc(P(da), P(w), z, m, 256, k, s) != 0                                # no output
+    assert acc(ctypes.c_void_p(da.data_ptr() + 4), P(w), P(d), m, 256, k, s) != 0   # A misaligned
+    assert acc(P(da), P(w), P(d), m, 64, k, s) != 0                              # N % 256
