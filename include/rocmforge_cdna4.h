@@ -302,6 +302,19 @@ hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const fl
                                           const int num_heads, const int num_kv_heads, const int head_dim,
                                           const float eps, const float theta_base, const int neox,
                                           const float* d_freq_scale, hipStream_t stream);
+/* No counterpart (the reference's prefill takes gpu_rms_norm_batched twice,
+ * gpu_rope_heads_batched twice, gpu_kv_write_batched and the fp16
+ * conversions, src/gpu/forward.rs prefill path): the same step over the rows
+ * of a prompt, row r at position start_pos + r.  Query rows [0, rows_q) are
+ * written as fp16 to d_q16 ([row][num_heads * head_dim]); key/value rows
+ * [0, rows_kv) go to the caches at start_pos + r (start_pos + rows_kv <=
+ * max_seq).  d_q, d_k, d_v and d_q16 16-byte aligned; rows_q <= 65535. */
+hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const float* d_k, const float* d_v, const float* d_q_norm,
+                                         const float* d_k_norm, uint16_t* d_q16, uint16_t* d_k_cache,
+                                         uint16_t* d_v_cache, const int start_pos, const int rows_q, const int rows_kv,
+                                         const int num_heads, const int num_kv_heads, const int head_dim,
+                                         const int max_seq, const float eps, const float theta_base, const int neox,
+                                         const float* d_freq_scale, hipStream_t stream);
 
 /* hip_kernels/attention.hip:950, :972 -- one query token over seq_len cached
  * positions (fp16 bits): out[h] = softmax(q[h] . K[0..seq_len) * scale) V, GQA head h / (nh / nkv).

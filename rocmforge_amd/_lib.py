@@ -53,6 +53,7 @@ SIGNATURES = {
     "gpu_kv_write_rope_state_scaled": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp],
     "gpu_kv_write_batched": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
     "rf_kv_write_batched_on_stream": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "rf_qk_norm_rope_kv_write_rows": [_vp] * 8 + [_i] * 7 + [_f, _f, _i, _vp, _vp],
     "rf_qk_norm_rope_kv_write_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp, _vp],
     "gpu_flash_attn_decode_strided_multi_head": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],

@@ -368,6 +368,42 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     }
 }
 
+// The same step over rows of a prompt (row r at position pos0 + r): query
+// rows [0, rows_q) are normalised, rotated and written as fp16 to q16 (the
+// prefill attention's operand); key rows [0, rows_kv) go to the caches, with
+// their V rows, as in the single-position kernel.  grid.y = rows_q.
+template <int LPP>
+__global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_rows_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, __half* __restrict__ q16, __half* kc,
+    __half* vc, int pos0, int rows_kv, int nh, int nkv, float eps, const float* __restrict__ tab, int neox,
+    const float* __restrict__ freq_scale) {
+    constexpr int D = 8 * LPP;
+    const int lane = threadIdx.x & 63;
+    const int hidx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPP) + lane / LPP;
+    const int sub = lane % LPP;
+    const int row = blockIdx.y;
+    if (hidx >= nh + nkv) return;            // whole LPP-lane groups leave together
+    const bool is_q = hidx < nh;
+    if (!is_q && row >= rows_kv) return;
+    const int head = is_q ? hidx : hidx - nh;
+    const int pos = pos0 + row;
+    const size_t src = (size_t)row * (is_q ? nh : nkv) * D + (size_t)head * D + 8 * sub;
+    float x[8], th[8];
+    load8((is_q ? q : k) + src, x);
+    theta8<LPP>(tab, sub, neox, freq_scale, th);
+    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
+    if (is_q) {
+        store8_f16(q16 + src, x);
+    } else {
+        const size_t c = (size_t)pos * nkv * D + (size_t)head * D + 8 * sub;
+        store8_f16(kc + c, x);
+        float vv[8];
+        load8(v + src, vv);
+        store8_f16(vc + c, vv);
+    }
+}
+
 // ---- decode attention -----------------------------------------------------------------
 // Single-workgroup path (GQA groups larger than 8): one workgroup (4 waves) per query head.  Scores: LPP lanes per position
 // (8 fp16 of K per lane, one 16-byte load), so a wave-instruction covers
@@ -1046,6 +1082,41 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_
     hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel<LPP>, dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP))),      \
                        dim3(256), 0, stream, d_q, d_k, d_v, d_q_norm, d_k_norm, kc, vc, d_pos, num_heads,         \
                        num_kv_heads, eps, tab, neox, d_freq_scale)
+    switch (head_dim) {
+    case 64: RF_QKR(8); break;
+    case 128: RF_QKR(16); break;
+    case 256: RF_QKR(32); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef RF_QKR
+    return hipGetLastError();
+}
+
+extern "C" hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const float* d_k, const float* d_v,
+                                                    const float* d_q_norm, const float* d_k_norm, uint16_t* d_q16,
+                                                    uint16_t* d_k_cache, uint16_t* d_v_cache, const int start_pos,
+                                                    const int rows_q, const int rows_kv, const int num_heads,
+                                                    const int num_kv_heads, const int head_dim, const int max_seq,
+                                                    const float eps, const float theta_base, const int neox,
+                                                    const float* d_freq_scale, hipStream_t stream) {
+    if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_q16 == nullptr || d_k_cache == nullptr ||
+        d_v_cache == nullptr || num_heads <= 0 || num_kv_heads <= 0 || start_pos < 0 || rows_q <= 0 ||
+        rows_kv < 0 || rows_kv > rows_q || rows_q > 65535 || start_pos + rows_kv > max_seq)
+        return hipErrorInvalidValue;
+    for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_q16})
+        if (reinterpret_cast<uintptr_t>(p) & 15u) return hipErrorInvalidValue;
+    const int heads = num_heads + num_kv_heads;
+    __half* kc = reinterpret_cast<__half*>(d_k_cache);
+    __half* vc = reinterpret_cast<__half*>(d_v_cache);
+    __half* q16 = reinterpret_cast<__half*>(d_q16);
+    const float* tab = nullptr;
+    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
+    if (e != hipSuccess) return e;
+#define RF_QKR(LPP)                                                                                                    \
+    hipLaunchKernelGGL(rf_qk_norm_rope_kv_rows_kernel<LPP>,                                                            \
+                       dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP)), rows_q), dim3(256), 0, stream, d_q, d_k, \
+                       d_v, d_q_norm, d_k_norm, q16, kc, vc, start_pos, rows_kv, num_heads, num_kv_heads, eps, tab,   \
+                       neox, d_freq_scale)
     switch (head_dim) {
     case 64: RF_QKR(8); break;
     case 128: RF_QKR(16); break;

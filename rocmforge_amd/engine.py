@@ -370,29 +370,40 @@ class Engine:
             self._gemm_group([(m["attn_q"], b["q"], c.q_size), (m["attn_k"], b["k"], c.kv_size),
                               (m["attn_v"], b["v"], c.kv_size)], b["xn"], c.hidden, M, st)
             t("qkv", i)
-            if lw.q_norm is not None:
-                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["q"]), _p(lw.q_norm), _p(b["q"]), c.head_dim, c.eps,
-                                                      M * c.n_heads, st), "q norm")
-                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["k"]), _p(lw.k_norm), _p(b["k"]), c.head_dim, c.eps,
-                                                      M * c.n_kv_heads, st), "k norm")
-            _chk(L.rf_rope_heads_batched_on_stream(_p(b["q"]), 0, c.n_heads, c.head_dim, c.rope_base, M, int(c.neox),
-                                                   None, st), "rope q")
-            _chk(L.rf_rope_heads_batched_on_stream(_p(b["k"]), 0, c.n_kv_heads, c.head_dim, c.rope_base, M,
-                                                   int(c.neox), None, st), "rope k")
-            _chk(L.rf_kv_write_batched_on_stream(_p(self.kc[i]), _p(self.vc[i]), _p(b["k"]), _p(b["v"]), 0,
-                                                 c.kv_size, self.max_seq, M, st), "kv write")
-            t("qk_rope_kv", i)
-            # K and V: the fp16 cache rows just written are the attention's operands
-            # (same [position][kv heads * d] layout; keys past the prompt are seen
-            # only by the padding queries, whose outputs are never used; real queries
-            # weigh them by an exact zero, and every cache row holds finite fp16)
-            _chk(L.convert_f32_to_f16(_p(b["q"]), _p(b["q16"]), mp * c.q_size, st), "to f16")
-            if mp <= self.max_seq:
+            if self.fuse_norm and c.head_dim in (64, 128, 256) and mp <= self.max_seq:
+                # per-head norms, RoPE, the KV-cache rows and fp16 Q in one launch (the
+                # launches below, with each head's sum of squares taken in another
+                # order); K and V for the attention are the fp16 cache rows
+                _chk(L.rf_qk_norm_rope_kv_write_rows(_p(b["q"]), _p(b["k"]), _p(b["v"]), _p(lw.q_norm),
+                                                     _p(lw.k_norm), _p(b["q16"]), _p(self.kc[i]), _p(self.vc[i]), 0,
+                                                     mp, M, c.n_heads, c.n_kv_heads, c.head_dim, self.max_seq, c.eps,
+                                                     c.rope_base, int(c.neox), None, st), "qk rows")
+                t("qk_rope_kv", i)
                 k16, v16 = self.kc[i], self.vc[i]
             else:
-                for src, dst in (("k", "k16"), ("v", "v16")):
-                    _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), mp * c.kv_size, st), "to f16")
-                k16, v16 = b["k16"], b["v16"]
+                if lw.q_norm is not None:
+                    _chk(L.gpu_rms_norm_batched_on_stream(_p(b["q"]), _p(lw.q_norm), _p(b["q"]), c.head_dim, c.eps,
+                                                          M * c.n_heads, st), "q norm")
+                    _chk(L.gpu_rms_norm_batched_on_stream(_p(b["k"]), _p(lw.k_norm), _p(b["k"]), c.head_dim, c.eps,
+                                                          M * c.n_kv_heads, st), "k norm")
+                _chk(L.rf_rope_heads_batched_on_stream(_p(b["q"]), 0, c.n_heads, c.head_dim, c.rope_base, M,
+                                                       int(c.neox), None, st), "rope q")
+                _chk(L.rf_rope_heads_batched_on_stream(_p(b["k"]), 0, c.n_kv_heads, c.head_dim, c.rope_base, M,
+                                                       int(c.neox), None, st), "rope k")
+                _chk(L.rf_kv_write_batched_on_stream(_p(self.kc[i]), _p(self.vc[i]), _p(b["k"]), _p(b["v"]), 0,
+                                                     c.kv_size, self.max_seq, M, st), "kv write")
+                t("qk_rope_kv", i)
+                # K and V: the fp16 cache rows just written are the attention's operands
+                # (same [position][kv heads * d] layout; keys past the prompt are seen
+                # only by the padding queries, whose outputs are never used; real queries
+                # weigh them by an exact zero, and every cache row holds finite fp16)
+                _chk(L.convert_f32_to_f16(_p(b["q"]), _p(b["q16"]), mp * c.q_size, st), "to f16")
+                if mp <= self.max_seq:
+                    k16, v16 = self.kc[i], self.vc[i]
+                else:
+                    for src, dst in (("k", "k16"), ("v", "v16")):
+                        _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), mp * c.kv_size, st), "to f16")
+                    k16, v16 = b["k16"], b["v16"]
             _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(k16), _p(v16), _p(b["att"]),
                                                            mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
                  "attention")

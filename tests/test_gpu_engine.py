@@ -13,6 +13,7 @@
 * A tiny GGUF file loads into the engine and decodes like the same weights
   generated in memory.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -267,3 +268,54 @@ def test_prefill_fused_gemms_match_separate(weights, eng):
     if ta != tb:        # a near tie may flip under reordered sums; then the logits must be close
         lg = _h(sep.logits)
         assert abs(lg[ta] - lg[tb]) <= 1e-3 * np.abs(lg).max()
+
+
+def test_prefill_fused_qk_rows_match_separate(weights, eng):
+    # rf_qk_norm_rope_kv_write_rows (per-head norms, RoPE, cache rows, fp16 Q
+    # in one launch) against the separate norm / rope / kv-write / convert
+    # launches.  The fused norm sums each head's squares in another order
+    # (8 consecutive per lane), so a rare element rounds to the neighbouring
+    # fp16: at most one fp16 ulp, in under 0.1 % of the elements
+    prompt = [int(t) for t in np.random.default_rng(9).integers(0, CFG.vocab, 77)]
+    M = len(prompt)
+    runs = []
+    for fused in (True, False):
+        e = E.Engine(CFG, weights, max_seq=256, fuse_norm=fused, fuse_gemm=False)
+        q16 = []
+
+        def trace(name, layer, e=e, q16=q16):
+            if name == "attention":
+                torch.cuda.synchronize()
+                q16.append(_h(e._pf["q16"]).reshape(-1, CFG.q_size)[:M].copy())
+
+        tok = e.prefill(prompt, trace)
+        runs.append((tok, q16, [_h(t).reshape(-1, CFG.kv_size)[:M].copy() for t in e.kc + e.vc], _h(e.logits).copy()))
+    (ta, qa, ca, la), (tb, qb, cb, lb) = runs
+    assert len(qa) == CFG.n_layers
+    # layer 0 (same inputs): the step's own difference
+    L = CFG.n_layers
+    for what, x, y in (("q16", qa[0], qb[0]), ("k cache", ca[0], cb[0]), ("v cache", ca[L], cb[L])):
+        ulps = np.abs(x.astype(np.int32) - y.astype(np.int32))          # fp16 bit patterns: neighbours differ by 1
+        assert ulps.max() <= 1 and (ulps > 0).mean() < 1e-3, f"{what}: {ulps.max()} {(ulps > 0).mean()}"
+    # later layers carry it forward through the residual stream
+    for x, y in zip(qa + ca, qb + cb):
+        assert _rel(x.view(np.float16), y.view(np.float16)) <= 1e-3
+    assert _rel(la, lb) <= 1e-4
+    if ta != tb:
+        assert abs(lb[ta] - lb[tb]) <= 1e-4 * np.abs(lb).max()
+
+
+def test_qk_rows_rejections(rf, dev):
+    z = torch.zeros(4096, dtype=torch.float32, device="cuda:0")
+    h = torch.zeros(4096, dtype=torch.int16, device="cuda:0")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    f = rf.rf_qk_norm_rope_kv_write_rows
+    ok = (P(z), P(z), P(z), None, None, P(h), P(h), P(h))
+    assert f(*ok, 0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) == 0
+    torch.cuda.synchronize()
+    assert f(*ok, 7, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0     # past max_seq
+    assert f(*ok, 0, 2, 3, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0     # more K rows than Q rows
+    assert f(*ok, 0, 2, 2, 2, 1, 96, 8, 1e-6, 1e4, 1, None, s) != 0      # head_dim
+    assert f(P(z), P(z), P(z), None, None, ctypes.c_void_p(h.data_ptr() + 2), P(h), P(h),
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0          # q16 misaligned
