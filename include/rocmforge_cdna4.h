@@ -121,6 +121,15 @@ hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const void* weight
                                           int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const void* weights_q6_k, float* inout, int M, int N,
                                           int K, hipStream_t stream);
+/* No counterpart in the reference (its prefill runs the gate and up GEMMs
+ * and then a SwiGLU kernel).  out[M x N] = silu(fp16(A) fp16(Wg)^T) *
+ * (fp16(A) fp16(Wu)^T), silu(g) = g / (1 + exp(-g)), with both products
+ * summed in one launch (no K split).  N % 128 == 0, other rules as the
+ * segment launchers. */
+hipError_t rf_gemm_q4_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out, int M,
+                                      int N, int K, hipStream_t stream);
+hipError_t rf_gemm_q6_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out, int M,
+                                      int N, int K, hipStream_t stream);
 
 /* ---- Host dispatch (routing of the arms above) --------------------------
  * C counterparts of ROCmForge's src/gpu/ops.rs routing for the Q4_K / Q6_K

@@ -905,7 +905,10 @@ struct RingGeom7 {
 // of the 256-column tile (a single GEMM has n1 = n2 = N).  Each segment's
 // output is row-major with its own width.  accum != 0 adds the product to
 // the output's contents instead of storing it (the split-K path always
-// adds).
+// adds).  pair != 0 (one segment, no K split): the N columns are N/2 gate
+// rows (W) and N/2 up rows (w1) taken 128 at a time -- tile j covers gate
+// rows [128j, +128) on waves 0-1 and the same up rows on waves 2-3 -- and
+// D[M x N/2] = silu(gate) * up.
 struct GemmSegs {
     const uint8_t* w1;
     const uint8_t* w2;
@@ -913,6 +916,7 @@ struct GemmSegs {
     float* d2;
     int n1, n2;
     int accum;
+    int pair;
 };
 
 template <typename T, bool IS_Q6, int FM, bool SPLIT>
@@ -972,7 +976,10 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
     const int ldd = (sgi == 2 ? N : (sgi == 1 ? segs.n2 : segs.n1)) - nbase;
     const uint8_t* wseg = sgi == 2 ? segs.w2 : (sgi == 1 ? segs.w1 : W);
     float* dseg = sgi == 2 ? segs.d2 : (sgi == 1 ? segs.d1 : D);
-    const uint8_t* wtile = wseg + (size_t)(nt0 - nbase) * row_bytes;
+    // pair mode: waves 0-1 stream gate rows, waves 2-3 the same up rows
+    const bool up_wave = segs.pair && wave >= 2;
+    const uint8_t* wtile = segs.pair ? (up_wave ? segs.w1 : W) + (size_t)(nt0 / 2) * row_bytes
+                                     : wseg + (size_t)(nt0 - nbase) * row_bytes;
 
     uint32_t goff[G::kNI];
     uint32_t gdst[G::kNI];
@@ -981,7 +988,9 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         const int g = wave * G::kNI + t;
         const int pc = 64 * g + lane;
         gdst[t] = 16u * (uint32_t)pc;
-        const int row = pc / G::kNPR;
+        // a wave's load groups lie in ring rows [128 (w >> 1), +128): up waves
+        // address their rows from the up matrix's tile base
+        const int row = pc / G::kNPR - (up_wave ? 128 : 0);
         int piece = pc % G::kNPR;
         if (IS_Q6 && piece == 14) piece = 13;
         goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
@@ -1276,6 +1285,42 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         slot0 = slot2;
     }
 
+    if (segs.pair) {
+        // up waves hand their accumulators to the gate waves through the
+        // (now idle) weight ring, lane-fastest so each access is one
+        // contiguous 256-byte run
+        constexpr int NE = FM * FN * 16;
+        static_assert(2 * NE * 64 * 4 <= G::kStages * kStageBytes, "exchange fits the ring");
+        float* xch = reinterpret_cast<float*>(w_ring);
+        __syncthreads();
+        if (wave >= 2) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        xch[((wave - 2) * NE + (i * FN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const int ldo = N / 2;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int col = nt0 / 2 + 64 * wave + 32 * j + (lane & 31);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                        const float g = acc[i][j][e];
+                        const float u = xch[(wave * NE + (i * FN + j) * 16 + e) * 64 + lane];
+                        D[(size_t)row * ldo + col] = g / (1.0f + expf(-g)) * u;
+                    }
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1582,8 +1627,8 @@ static GemmSegs single_seg(int N) {
 template <bool IS_Q6, int FM>
 static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
                       const GemmSegs& sg) {
-    // column segments and accumulation exist only in v7
-    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum;
+    // column segments, accumulation and gate/up pairs exist only in v7
+    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum && !sg.pair;
     using T = typename std::conditional<IS_Q6, Q6Ops, Q4Ops>::type;
     const int tiles = (M / (32 * FM)) * (N / 256);
     const int nchunks = K / kKC;
@@ -1592,6 +1637,7 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
         const int v = atoi(e);
         if (v >= 1 && (nchunks / 8) % v == 0) s = v;
     }
+    if (sg.pair) s = 1;                              // silu(gate) * up needs the whole sums
     // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
     const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
     const bool v7 = !plain || (v5 && (gemm_kernel_version() == 0 || gemm_kernel_version() == 7));
@@ -1643,7 +1689,7 @@ template <bool IS_Q6>
 static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
                               const GemmSegs& sg) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum;
+    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum && !sg.pair;
     if (N % 256 == 0 && K % 512 == 0 && (gemm_kernel_version() != 1 || !plain)) {
         // shared-dequantisation tiles where they come to about one
         // workgroup per CU without a K split: 256 x 256 (M >= 1024 at the
@@ -1653,7 +1699,7 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long cus = device_cu_count();
         const long sq_tiles = (long)(M / 256) * (N / 256);
         const long sq128_tiles = (long)(M / 128) * (N / 128);
-        const bool sq_ok = gemm_kernel_version() == 0 && sg.n1 == N && sg.n2 == N;
+        const bool sq_ok = gemm_kernel_version() == 0 && sg.n1 == N && sg.n2 == N && !sg.pair;
         if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
             launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
@@ -1766,4 +1812,27 @@ extern "C" hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const v
 extern "C" hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const void* weights_q6_k, float* inout,
                                                      int M, int N, int K, hipStream_t stream) {
     return gemm_accumulate<true>(input, weights_q6_k, inout, M, N, K, stream);
+}
+
+template <bool IS_Q6>
+static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, float* D, int M, int N, int K,
+                              hipStream_t st) {
+    if (!seg_shape_ok<IS_Q6>(A, M, K) || !wg || !wu || !D || N <= 0 || N % 128 || !aligned16(D))
+        return hipErrorInvalidValue;
+    const uintptr_t wal = IS_Q6 ? 1u : 15u;
+    if ((reinterpret_cast<uintptr_t>(wg) & wal) || (reinterpret_cast<uintptr_t>(wu) & wal)) return hipErrorInvalidValue;
+    GemmSegs sg = single_seg(2 * N);
+    sg.w1 = static_cast<const uint8_t*>(wu);
+    sg.pair = 1;
+    return launch_gemm<IS_Q6>(A, wg, D, M, 2 * N, K, st, sg);
+}
+
+extern "C" hipError_t rf_gemm_q4_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out,
+                                                 int M, int N, int K, hipStream_t stream) {
+    return gemm_swiglu<false>(input, w_gate, w_up, out, M, N, K, stream);
+}
+
+extern "C" hipError_t rf_gemm_q6_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out,
+                                                 int M, int N, int K, hipStream_t stream) {
+    return gemm_swiglu<true>(input, w_gate, w_up, out, M, N, K, stream);
 }

@@ -412,10 +412,16 @@ class Engine:
             t("attn_output", i)
             _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp, st),
                  "norm")
-            # two launches: one over both (384 tiles of 128 rows at M = 512) was slower
-            self._gemm(m["ffn_gate"], b["xn"], b["g"], c.ff, c.hidden, M, st)
-            self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
-            _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
+            gt, ut = m["ffn_gate"][1].wtype, m["ffn_up"][1].wtype
+            if gt == ut and c.ff % 128 == 0 and self._fusable(gt, 256, c.hidden):
+                # gate and up in one launch, SwiGLU in its epilogue
+                fn = L.rf_gemm_q4_k_swiglu_launch if gt == GgmlType.Q4_K else L.rf_gemm_q6_k_swiglu_launch
+                _chk(fn(_p(b["xn"]), _p(m["ffn_gate"][0]), _p(m["ffn_up"][0]), _p(b["g"]), mp, c.ff, c.hidden, st),
+                     "gemm swiglu")
+            else:
+                self._gemm(m["ffn_gate"], b["xn"], b["g"], c.ff, c.hidden, M, st)
+                self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
+                _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             t("gate_up", i)
             self._gemm_residual(m["ffn_down"], b["g"], b["x"], b["tmp"], c.hidden, c.ff, M, st)
             t("ffn_down", i)

@@ -1,6 +1,7 @@
 """GPU parity of the two prefill GEMM launchers that have no reference
 counterpart: several weight matrices as column segments of one launch
-(rf_gemm_q*_k_segments_launch) and D += product (rf_gemm_q*_k_accumulate_launch).
+(rf_gemm_q*_k_segments_launch), D += product (rf_gemm_q*_k_accumulate_launch)
+and gate/up with SwiGLU in the epilogue (rf_gemm_q*_k_swiglu_launch).
 
 Each segment / accumulated product is checked against the oracle's float64
 product of the fp16-rounded operands at the GEMM bar
@@ -89,6 +90,41 @@ def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k, split):
         np.testing.assert_array_equal(got, r + _single(rf, fmt, da, w, m, n, k))
 
 
+@pytest.mark.parametrize("fmt,m,n,k", [
+    ("q4_k", 128, 384, 512),       # 3 tile pairs, 128-row tiles
+    ("q4_k", 64, 256, 1024),       # 64-row tiles (no K split even where one would pay)
+    ("q4_k", 512, 1536, 2048),
+    ("q6_k", 128, 256, 2048),
+])
+def test_swiglu_pairs(rf, dev, fmt, m, n, k):
+    # out = silu(A Wg^T) * (A Wu^T): the products within the GEMM bar of the
+    # oracle, and within fp32 rounding of silu(g) * u over the two single
+    # GEMMs (which may sum in another order where they take a K split)
+    a = synth.activations(k, seed=m + n + 1, m=m)
+    wg = synth.weights(fmt, n, k, seed=21)
+    wu = synth.weights(fmt, n, k, seed=22)
+    da, dg, du = G.to_dev(a), G.to_dev(wg), G.to_dev(wu)
+    d = G.empty(m * n, torch.float32).fill_(float("nan"))
+    fn = rf.rf_gemm_q4_k_swiglu_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_swiglu_launch
+    G.call(fn, G.ptr(da), G.ptr(dg), G.ptr(du), G.ptr(d), m, n, k)
+    got = G.host(d).reshape(m, n).astype(np.float64)
+    g = O.gemm(fmt, a, wg, m, n, k)
+    u = O.gemm(fmt, a, wu, m, n, k)
+    ref = g / (1.0 + np.exp(-g)) * u
+    # the bar on each product carries through silu(g) * u: d(silu)/dg <= 1.1
+    eg = 2e-3 * np.abs(g) + 1e-5 * np.abs(g).max()
+    eu = 2e-3 * np.abs(u) + 1e-5 * np.abs(u).max()
+    tol = 1.1 * eg * np.abs(u) + np.abs(g / (1.0 + np.exp(-g))) * eu + 1e-6 * np.abs(ref).max()
+    worst = (np.abs(got - ref) / tol).max()
+    print(f"{fmt} swiglu {m}x{n}x{k}: worst={worst:.3f}", flush=True)
+    assert worst <= 1.0
+    gs = _single(rf, fmt, da, wg, m, n, k)
+    us = _single(rf, fmt, da, wu, m, n, k)
+    with np.errstate(over="ignore"):          # exp(-g) = inf for g << 0 gives silu = -0
+        sil = (gs / (np.float32(1.0) + np.exp(-gs)) * us).astype(np.float32)
+    assert np.allclose(got, sil, rtol=1e-5, atol=1e-6 * np.abs(sil).max())
+
+
 def test_rejections(rf, dev):
     m, k = 64, 512
     da = G.to_dev(synth.activations(k, seed=1, m=m))
@@ -110,3 +146,6 @@ def test_rejections(rf, dev):
     assert acc(P(da), P(w), z, m, 256, k, s) != 0                                # no output
     assert acc(ctypes.c_void_p(da.data_ptr() + 4), P(w), P(d), m, 256, k, s) != 0   # A misaligned
     assert acc(P(da), P(w), P(d), m, 64, k, s) != 0                              # N % 256
+    sw = rf.rf_gemm_q4_k_swiglu_launch
+    assert sw(P(da), P(w), P(w), P(d), m, 64, k, s) != 0                         # N % 128
+    assert sw(P(da), P(w), z, P(d), m, 128, k, s) != 0                           # no up weights
