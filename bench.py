@@ -8,8 +8,11 @@ seeded synthetic GGUF blocks generated in device memory; several distinct
 weight copies are cycled so each step streams from HBM, not from the 256 MB
 Infinity Cache.
 
-The prefill GEMM is reported as an extra object
-("prefill_gemm": TFLOP/s at M = 64..512) beside the headline line.
+Extra objects on the same JSON line: config 0 ("gemv_4096", the single
+Q4_K GEMV), config 3 ("prefill_gemm": TFLOP/s at M = 64..512), config 2
+("decode_stream"), config 4 ("e2e_qwen3_8b") and the CPU baseline.  Every
+timed region is preceded by an untimed clock ramp of about 0.3 s of the
+same launches.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -50,7 +53,7 @@ def parse():
     ap.add_argument("--gemm-pmc", action="store_true", help="only launch the M=512 GEMMs (for rocprofv3 --pmc)")
     ap.add_argument("--no-stream", action="store_true", help="skip the full decode weight stream leg (config 2)")
     ap.add_argument("--stream-tokens", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain copies of known size (PMC traffic calibration)")
     return ap.parse_args()
@@ -128,6 +131,7 @@ def bench_decode(lib, torch, steps, warmup):
     g_dn = capture([dn_call(i % copies) for i in range(steps)])
 
     def timed(g):
+        ramp(torch, g.replay)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -136,9 +140,9 @@ def bench_decode(lib, torch, steps, warmup):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps   # ms per step / per launch
 
-    timed(g_step)   # first replays upload the graphs; not timed
-    timed(g_gu)
-    timed(g_dn)
+    g_step.replay()   # first replays upload the graphs; not timed
+    g_gu.replay()
+    g_dn.replay()
     t0 = time.perf_counter()
     step_ms = timed(g_step)   # the timed region: exactly K steps
     wall = time.perf_counter() - t0
@@ -148,6 +152,63 @@ def bench_decode(lib, torch, steps, warmup):
         "wall": wall, "steps_run": steps, "step_ms": step_ms, "copies": copies,
         "gate_up_ms": gu_ms, "down_ms": dn_ms, "x": x, "h": h, "y": y,
     }
+
+
+def ramp(torch, fn, seconds=0.3):
+    """Untimed clock ramp: repeat fn (a graph replay or a launch loop) for
+    about `seconds` of GPU time before a timed region, so the timed launches
+    run at the clocks a busy GPU settles at (a cold GPU starts lower)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        torch.cuda.synchronize()
+
+
+# BASELINE config 0: one Q4_K GEMV 4096x4096 with the Q8_0 quantisation of x
+# inline (gemv_q4_k_f32_q8_inline_launch), seed 0, as the reference's
+# examples/bench_q4_k_gemv_isolated.rs times it.  Distinct weight copies
+# (>= 4x the Infinity Cache) are cycled so every launch streams from HBM.
+GEMV0_K = GEMV0_N = 4096
+GEMV0_BYTES = GEMV0_N * (GEMV0_K // 256) * Q4K_BYTES + 4 * GEMV0_K + 4 * GEMV0_N   # 9,469,952
+
+
+def bench_gemv_cfg0(lib, torch, launches):
+    from rocmforge_amd import synth
+
+    dev = torch.device("cuda:0")
+    wbytes = GEMV0_N * (GEMV0_K // 256) * Q4K_BYTES
+    copies = -(-4 * MALL_BYTES // wbytes)
+    ws = [synth.torch_weights("q4_k", GEMV0_N, GEMV0_K, seed=c, device=dev) for c in range(copies)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn(GEMV0_K, device=dev, generator=g)
+    y = torch.empty(GEMV0_N, device=dev)
+    fn = lib.gemv_q4_k_f32_q8_inline_launch
+    graph = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(graph, stream=cs):
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(launches):
+                if fn(vp(ws[i % copies]), vp(x), vp(y), GEMV0_K, GEMV0_N, st):
+                    raise RuntimeError("config 0 launch failed")
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    graph.replay()
+    ramp(torch, graph.replay)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    gbs = GEMV0_BYTES / (us * 1e-6) / 1e9
+    return {"workload": "BASELINE config 0: Q4_K GEMV 4096x4096 + Q8_0-inline x, batch 1, seed 0",
+            "launcher": "gemv_q4_k_f32_q8_inline_launch", "bytes_per_launch": GEMV0_BYTES,
+            "weight_copies_cycled": copies, "launches": launches, "us": round(us, 3), "gbs": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 # BASELINE config 2: the full decode weight stream of a Llama-3.1-8B-shaped
@@ -214,7 +275,7 @@ def bench_decode_stream(lib, torch, tokens):
     torch.cuda.current_stream().wait_stream(cs)
     torch.cuda.synchronize()
     graph.replay()
-    torch.cuda.synchronize()
+    ramp(torch, graph.replay)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(tokens):
@@ -257,68 +318,44 @@ def read_traffic():
 
 
 def bench_gemm(lib, torch):
-    """Prefill GEMM TFLOP/s at Llama-3.1-8B FFN shapes, M = 64..512."""
+    """Prefill GEMM TFLOP/s at Llama-3.1-8B FFN shapes, M = 64..512: Q4_K
+    14336x4096 (gate/up) and Q6_K 4096x14336 (down).  Distinct weight copies
+    (>= 4x the Infinity Cache) are cycled so the weights stream from HBM; A
+    (the activations, 0.25-8 MB) is the same for every launch, as the output
+    of the previous layer would be."""
     from rocmforge_amd import synth
 
-    if not hasattr(lib, "wmma_gemm_q4_k_launch"):
-        return None
     dev = torch.device("cuda:0")
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     res = {}
-    shapes = [("q4_k", N_FFN, K_FFN, lib.wmma_gemm_q4_k_launch), ("q6_k", K_FFN, N_FFN, lib.wmma_gemm_q6_k_launch)]
-    for fmt, n, k, fn in shapes:
-        wsets = [synth.torch_weights(fmt, n, k, seed=50 + c, device=dev) for c in range(6)]
+    shapes = [("q4_k", N_FFN, K_FFN, Q4K_BYTES, lib.wmma_gemm_q4_k_launch),
+              ("q6_k", K_FFN, N_FFN, Q6K_BYTES, lib.wmma_gemm_q6_k_launch)]
+    for fmt, n, k, bb, fn in shapes:
+        copies = -(-4 * MALL_BYTES // (n * (k // 256) * bb))
+        wsets = [synth.torch_weights(fmt, n, k, seed=50 + c, device=dev) for c in range(copies)]
         for m in (64, 128, 256, 512):
             a = torch.randn(m, k, device=dev).to(torch.bfloat16).float()
             d = torch.empty(m, n, device=dev)
-            for i in range(5):
-                fn(vp(a), vp(wsets[i % 6]), vp(d), m, n, k, st)
-            iters = 50
+
+            def run(iters):
+                for i in range(iters):
+                    rc = fn(vp(a), vp(wsets[i % copies]), vp(d), m, n, k, st)
+                    if rc:
+                        raise RuntimeError(f"gemm launch failed {rc}")
+
+            ramp(torch, lambda: run(copies))
+            iters = 4 * copies
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for i in range(iters):
-                rc = fn(vp(a), vp(wsets[i % 6]), vp(d), m, n, k, st)
-                if rc:
-                    raise RuntimeError(f"gemm launch failed {rc}")
+            run(iters)
             e1.record()
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1000 / iters
             tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             res[f"{fmt}_{n}x{k}_M{m}"] = {"us": round(us, 2), "tflops": round(tflops, 1),
-                                          "frac_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4)}
+                                          "frac_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+                                          "weight_copies_cycled": copies}
     return res
-
-
-def cpu_baseline(seconds):
-    """The reference CPU algorithm (C port in oracle/) on the same workload:
-    Q4_K x Q8_K AVX2 gate/up on all host threads + silu_fuse, then the scalar
-    Q6_K ffn_down on ONE thread (the reference's rayon split is over batch
-    rows, so a single-token Q6_K GEMV is single-threaded)."""
-    import numpy as np
-
-    from oracle import oracle as O
-    from rocmforge_amd import synth
-
-    threads = min(16, os.cpu_count() or 1)
-    wg = synth.q4_k_weights(N_FFN, K_FFN, seed=1)
-    wu = synth.q4_k_weights(N_FFN, K_FFN, seed=2)
-    wd = synth.q6_k_weights(K_FFN, N_FFN, seed=3)
-    x = synth.activations(K_FFN, seed=0)
-    O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads)        # warm
-    t0 = time.perf_counter()
-    n = 0
-    while True:
-        h = O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads)
-        O.cpu_gemv_q6k(wd, np.ascontiguousarray(h), K_FFN, N_FFN, 1)
-        n += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / n
-    return {
-        "value": round(STEP_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": f"{n} full steps (gate+up {N_FFN}x{K_FFN} Q4_K on {threads} threads + Q6_K down "
-                  f"{K_FFN}x{N_FFN} on 1 thread), {dt * 1e3:.1f} ms/step",
-    }
 
 
 def gemm_pmc(lib, torch):
@@ -336,6 +373,82 @@ def gemm_pmc(lib, torch):
             fn(vp(a), vp(wsets[i % 6]), vp(d), 512, n, k, st)
         torch.cuda.synchronize()
     print(json.dumps({"gemm_pmc": "done"}), flush=True)
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, min_runs, seconds):
+    """Median wall time of fn over at least min_runs calls and about
+    `seconds` (after one untimed call)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(seconds):
+    """The reference CPU algorithm (C port in oracle/) on the bench workloads,
+    on this host's cores (all the CPUs this process may run on):
+      * config 1 step: Q4_K x Q8_K AVX2 gate/up on all threads + silu_fuse,
+        then the scalar Q6_K ffn_down on ONE thread (the reference's rayon
+        split is over batch rows, so a single-token Q6_K GEMV runs on one
+        thread) -- the headline figure;
+      * the same step with the Q6_K GEMV on all threads (labelled variant);
+      * config 0: the Q4_K GEMV 4096x4096;
+      * config 3: the prefill GEMMs (gemm_q4_k_q8_k_avx2, gemm_q6_k_fallback,
+        both parallel over the M rows) at M = 64..512, one call each.
+    The GEMV figures are medians of repeated runs."""
+    from oracle import oracle as O
+    from rocmforge_amd import synth
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    wg = synth.q4_k_weights(N_FFN, K_FFN, seed=1)
+    wu = synth.q4_k_weights(N_FFN, K_FFN, seed=2)
+    wd = synth.q6_k_weights(K_FFN, N_FFN, seed=3)
+    x = synth.activations(K_FFN, seed=0)
+    h = np.ascontiguousarray(O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads))
+    per = seconds / 4
+    t_step, n_step = _median_time(lambda: (O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads),
+                                           O.cpu_gemv_q6k(wd, h, K_FFN, N_FFN, 1)), 5, per)
+    t_step_all, n_all = _median_time(lambda: (O.cpu_gate_up(wg, wu, x, N_FFN, K_FFN, threads),
+                                              O.cpu_gemv_q6k(wd, h, K_FFN, N_FFN, threads)), 5, per / 2)
+    w0 = synth.q4_k_weights(GEMV0_N, GEMV0_K, seed=0)
+    t0_, n0_ = _median_time(lambda: O.cpu_gemv_q4k(w0, x, GEMV0_N, GEMV0_K, threads), 5, per / 4)
+    gemm = {}
+    for fmt, n, k, w in (("q4_k", N_FFN, K_FFN, wg), ("q6_k", K_FFN, N_FFN, wd)):
+        for m in (64, 128, 256, 512):
+            a = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+            t0 = time.perf_counter()
+            O.cpu_gemm(fmt, w, a, m, n, k, threads)
+            dt = time.perf_counter() - t0
+            gemm[f"{fmt}_{n}x{k}_M{m}"] = {"ms": round(dt * 1e3, 1),
+                                           "gflops": round(2.0 * m * n * k / dt / 1e9, 2)}
+    return {
+        "value": round(STEP_BYTES / t_step / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"config 1 step (gate+up {N_FFN}x{K_FFN} Q4_K x Q8_K AVX2 on {threads} threads + Q6_K down "
+                  f"{K_FFN}x{N_FFN} scalar on 1 thread, as the reference runs one token): median of {n_step} "
+                  f"steps = {t_step * 1e3:.1f} ms/step",
+        "cpu_model": _cpu_model(), "nproc": os.cpu_count(), "threads_used": threads,
+        "variant_q6k_all_threads": {"gbs": round(STEP_BYTES / t_step_all / 1e9, 3),
+                                    "ms_per_step": round(t_step_all * 1e3, 2), "runs": n_all},
+        "config0_gemv_4096": {"gbs": round(GEMV0_BYTES / t0_ / 1e9, 3), "us": round(t0_ * 1e6, 1), "runs": n0_},
+        "prefill_gemm": gemm,
+        "note": "C port of the reference CPU path (oracle/cpu_baseline.c); Q4_K via AVX2 maddubs/madd "
+                "(the reference's dispatch uses AVX2 for Q4_K even on AVX-512 hosts); prefill GEMMs timed once "
+                "per M (a single call takes 0.1-10 s)",
+    }
 
 
 def bench_e2e(torch, prompt_len=512, steps=128):
@@ -429,6 +542,7 @@ def main():
         "kernels": {"gate_up_us": round(r["gate_up_ms"] * 1e3, 3), "gate_up_gbs": round(gu_gbs, 1),
                     "q6k_down_us": round(r["down_ms"] * 1e3, 3), "q6k_down_gbs": round(dn_gbs, 1)},
     }
+    out["gemv_4096"] = bench_gemv_cfg0(lib, torch, max(args.steps, 100))
     if not args.no_gemm:
         out["prefill_gemm"] = bench_gemm(lib, torch)
     if not args.no_stream:

@@ -92,7 +92,7 @@ hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* 
                                          float* output, int n_rows, int ncols_dst, hipStream_t stream);
 
 /* ---- Prefill GEMM, dequant-in-register, fp16 MFMA, fp32 accumulate ------
- * hip_kernels/wmma/wmma_gemm_q4_k.hip:506 and wmma_gemm_q6_k.hip:212 (Rust
+ * hip_kernels/wmma/wmma_gemm_q4_k.hip:201 and wmma_gemm_q6_k.hip:212 (Rust
  * decl src/gpu/kernels/wmma.rs:65-83).  NOTE the argument order: input
  * first.  D[M x N] = fp16(A[M x K]) * fp16(dequant W[N x K])^T, fp32 out.
  * M % 64 == 0, N % 64 == 0, K % 256 == 0 (callers pad M to 64 rows). */
@@ -310,7 +310,7 @@ hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const fl
                                           const float* d_k_norm, uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_pos,
                                           const int num_heads, const int num_kv_heads, const int head_dim,
                                           const float eps, const float theta_base, const int neox,
-                                          const float* d_freq_scale, hipStream_t stream);
+                                          const float* d_freq_scale, const float* d_theta, hipStream_t stream);
 /* No counterpart (the reference's prefill takes gpu_rms_norm_batched twice,
  * gpu_rope_heads_batched twice, gpu_kv_write_batched and the fp16
  * conversions, src/gpu/forward.rs prefill path): the same step over the rows
@@ -323,11 +323,13 @@ hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const float* d_k, con
                                          uint16_t* d_v_cache, const int start_pos, const int rows_q, const int rows_kv,
                                          const int num_heads, const int num_kv_heads, const int head_dim,
                                          const int max_seq, const float eps, const float theta_base, const int neox,
-                                         const float* d_freq_scale, hipStream_t stream);
+                                         const float* d_freq_scale, const float* d_theta, hipStream_t stream);
 
 /* hip_kernels/attention.hip:950, :972 -- one query token over seq_len cached
  * positions (fp16 bits): out[h] = softmax(q[h] . K[0..seq_len) * scale) V, GQA head h / (nh / nkv).
- * head_dim 64, 128 or 256. */
+ * head_dim 64, 128 or 256.  Like the reference these take no workspace; they
+ * run one workgroup per query head (the _ws launchers below split the
+ * positions over many workgroups). */
 hipError_t gpu_flash_attn_decode_strided_multi_head(float* d_out, const float* d_q, const uint16_t* d_k_cache,
                                                     const uint16_t* d_v_cache, const int seq_len, const int num_heads,
                                                     const int num_kv_heads, const int head_dim, const float scale,
@@ -336,6 +338,31 @@ hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_out, const fl
                                                           const uint16_t* d_v_cache, const int* d_seq_len,
                                                           const int num_heads, const int num_kv_heads,
                                                           const int head_dim, const float scale, hipStream_t stream);
+
+/* No counterpart: the decode attention with its positions split over up to
+ * 64 workgroups per kv head (all of a GQA group's query heads, <= 8, in one
+ * workgroup) and the partial softmax states merged by a second kernel, in
+ * the caller's workspace d_workspace of workspace_bytes >=
+ * rf_flash_attn_decode_workspace_bytes(num_heads, head_dim) bytes (a smaller
+ * one is rejected).  Same results as the launchers above within fp32
+ * rounding; GQA groups larger than 8 take the one-workgroup path.  Launches
+ * that share a workspace must be stream-ordered. */
+size_t rf_flash_attn_decode_workspace_bytes(const int num_heads, const int head_dim);
+hipError_t rf_flash_attn_decode_ws(float* d_out, const float* d_q, const uint16_t* d_k_cache, const uint16_t* d_v_cache,
+                                   const int seq_len, const int num_heads, const int num_kv_heads, const int head_dim,
+                                   const float scale, float* d_workspace, const size_t workspace_bytes,
+                                   hipStream_t stream);
+hipError_t rf_flash_attn_decode_state_ws(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                         const uint16_t* d_v_cache, const int* d_seq_len, const int num_heads,
+                                         const int num_kv_heads, const int head_dim, const float scale,
+                                         float* d_workspace, const size_t workspace_bytes, hipStream_t stream);
+
+/* No counterpart (the reference computes theta_i in each RoPE launch): fills
+ * the caller's d_theta[head_dim / 2] with theta_i = 1 / base^((float)(2i) /
+ * (float)head_dim) (double pow, rounded once), the values every RoPE here
+ * uses.  The fused launchers' d_theta argument takes such a table (or null:
+ * they then evaluate theta in the kernel, same bits). */
+hipError_t rf_rope_theta_table(float* d_theta, const int head_dim, const float theta_base, hipStream_t stream);
 
 /* No counterpart (the reference launches the per-head norms, the q RoPE and
  * the KV write before gpu_flash_attn_decode_strided_multi_head_state,
@@ -349,7 +376,8 @@ hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, con
                                              uint16_t* d_v_cache, const int* d_state, const int num_heads,
                                              const int num_kv_heads, const int head_dim, const float eps,
                                              const float theta_base, const int neox, const float* d_freq_scale,
-                                             const float scale, hipStream_t stream);
+                                             const float* d_theta, const float scale, float* d_workspace,
+                                             const size_t workspace_bytes, hipStream_t stream);
 
 /* hip_kernels/elementwise.hip:615, :651 -- index of the maximum of d_input[n]
  * (ties: the larger index; NaN never wins); partial buffers hold ceil(n / 1024). */

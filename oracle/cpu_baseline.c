@@ -8,12 +8,12 @@
  *   cb_quantize_q8_k     src/cpu/kernels/q8.rs:19-40 (256-element Q8_K block,
  *                        d = amax/127 (1.0 if amax <= 1e-7), q = round(x/d)
  *                        clamped to +-127, 16 bsums)
- *   cb_dot_q4k_q8k       src/cpu/kernels/gemm_q4k_q8.rs:89-181 (llama.cpp
+ *   cb_dot_q4k_q8k       src/cpu/kernels/gemm_q4k_q8.rs:90-195 (llama.cpp
  *                        AVX2 maddubs/madd block dot, scale unpack via the
  *                        kmask words, min term through bsums)
- *   cb_gemv_q4k_q8k      gemm_q4k_q8.rs:373-404 (quantize x once, rows in
+ *   cb_gemv_q4k_q8k      gemm_q4k_q8.rs:197-241 (quantize x once, rows in
  *                        parallel -- OpenMP stands in for rayon)
- *   cb_gemm_q4k_q8k      gemm_q4k_q8.rs:419-451 (parallel over batch rows)
+ *   cb_gemm_q4k_q8k      gemm_q4k_q8.rs:243-276 (parallel over batch rows)
  *   cb_gemv_q6k          src/cpu/ops.rs:480-572 (scalar dequant-dot; the
  *                        reference parallelises over batch rows only, so a
  *                        single-token GEMV runs on ONE thread; `threads`>1

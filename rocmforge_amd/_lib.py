@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "librocmforge_cdna4.so"
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
+_sz = ctypes.c_size_t
 
 # name -> argtypes (all return hipError_t as int)
 SIGNATURES = {
@@ -55,15 +56,18 @@ SIGNATURES = {
     "gpu_kv_write_rope_state_scaled": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp],
     "gpu_kv_write_batched": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
     "rf_kv_write_batched_on_stream": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
-    "rf_qk_norm_rope_kv_write_rows": [_vp] * 8 + [_i] * 7 + [_f, _f, _i, _vp, _vp],
-    "rf_qk_norm_rope_kv_write_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp, _vp],
+    "rf_qk_norm_rope_kv_write_rows": [_vp] * 8 + [_i] * 7 + [_f, _f, _i, _vp, _vp, _vp],
+    "rf_qk_norm_rope_kv_write_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp, _vp, _vp],
+    "rf_rope_theta_table": [_vp, _i, _f, _vp],
     "gpu_flash_attn_decode_strided_multi_head": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
+    "rf_flash_attn_decode_ws": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp],
+    "rf_flash_attn_decode_state_ws": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp],
     "gpu_argmax_f32_on_stream": [_vp, _vp, _vp, _vp, _i, _vp],
     "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
     "rf_argmax_f32_advance_state_on_stream": [_vp, _vp, _vp, _vp, _i, _vp, _vp],
     "rf_attn_decode_qk_norm_rope_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp,
-                                          _f, _vp],
+                                          _vp, _f, _vp, _sz, _vp],
     "gpu_embed_q4_k_token": [_vp, _vp, _i, _i, _i, _vp],
     "gpu_embed_q4_k_batch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "gpu_add": [_vp, _vp, _vp, _i, _vp],
@@ -101,5 +105,7 @@ def load() -> ctypes.CDLL:
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
     lib.rf_library_version.restype = ctypes.c_char_p
+    lib.rf_flash_attn_decode_workspace_bytes.argtypes = [_i, _i]
+    lib.rf_flash_attn_decode_workspace_bytes.restype = _sz
     _LIB = lib
     return lib

@@ -18,8 +18,6 @@
 //    loads, each wave dequantises its own B operands (the next chunk's,
 //    double buffered) in hand-scheduled slots between its MFMAs; XCD-aware
 //    tile order; split-K with float atomics when the tiles leave CUs idle.
-//  * rf_gemm_qk_v5_kernel: the previous 8-wave design with the same ring
-//    (RF_GEMM_V=5, kept for comparison measurements).
 //  * rf_gemm_qk_v4_kernel: 8 waves, weights loaded per lane (Q6_K with
 //    K % 2048 != 0, whose rows are not 16-byte aligned for the ring).
 //  * rf_gemm_qk_kernel (any M % 64 == 0, N % 64 == 0, K % 256 == 0): the
@@ -31,8 +29,6 @@
 // several weight matrices over one input as column segments of a single
 // launch (rf_gemm_q*_k_segments_launch), and D += product
 // (rf_gemm_q*_k_accumulate_launch, also served by sq).
-#include <stdlib.h>
-
 #include <type_traits>
 
 #include "qk_common.h"
@@ -40,17 +36,9 @@
 
 namespace rf {
 
-// Row-block band of the v7 tile order (RF_GEMM_BAND, default 2), passed to
-// the kernel as an argument.
-static int g_gemm_band = -1;
-static int gemm_band_host() {
-    if (g_gemm_band < 0) {
-        const char* e = getenv("RF_GEMM_BAND");
-        g_gemm_band = e ? atoi(e) : 2;
-        if (g_gemm_band < 1 || g_gemm_band > 8) g_gemm_band = 2;
-    }
-    return g_gemm_band;
-}
+// Row-block band of the v7 tile order (measured best at the Llama-3.1-8B
+// FFN shapes).
+constexpr int kGemmBand = 2;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -614,9 +602,31 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* 
     }
 }
 
-// ── v5: v4 with the weights staged through an LDS ring ───────────────────
-// Per-lane weight loads (32 rows per instruction, 16 B each) saturate the
-// vector L1 long before the MFMAs do.  Here the workgroup loads each
+// Workgroups are dispatched round-robin over the XCDs (b -> XCD b % 8).
+// Returns the virtual index of workgroup b such that XCD x processes the
+// contiguous virtual range [start_x, start_x + count_x): a bijection of
+// [0, total).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+    const int x = b % kXcds, local = b / kXcds;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+    return start + local;
+}
+
+// ── v7: 4 waves (one per SIMD), full K chunk per wave, MFMA/VALU interleave
+// Workgroup = 256 threads over a BM x 256 tile (BM = 32 FM); wave w owns
+// output columns [n0 + 64 w, +64) for all BM rows and both K halves of every
+// chunk, so no cross-wave reduction is needed and each wave has the whole
+// register file of its SIMD (accumulators in AGPRs).  Weights stage through
+// an LDS ring (below); B operands are double buffered so chunk c + 1 is
+// dequantised while the MFMAs of chunk c run, with scheduling hints placing
+// a few VALU operations after every MFMA (the matrix core executes an MFMA
+// for many cycles while the SIMD issues the independent VALU work).
+constexpr int kV7Threads = 256;
+
+// Weight ring.  Per-lane weight loads (32 rows per instruction, 16 B each)
+// saturate the vector L1 long before the MFMAs do.  Here the workgroup loads each
 // super-block of its 256 weight rows with coalesced 16-byte loads (a wave
 // instruction covers 1 KB of consecutive pieces of ~8 rows: whole cache
 // lines), parks them in registers for two chunk iterations, writes them to
@@ -638,255 +648,7 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* 
 //   Schedule: the loads of super-block sb + kDepth are issued in the first
 //   chunk iteration of sb and written to LDS in its third; the slot they
 //   overwrite belonged to sb - 1, finished one barrier earlier.
-template <bool IS_Q6>
-struct RingGeom;
-template <>
-struct RingGeom<false> {
-    static constexpr int kRS = 144, kNPR = 9, kStages = 3, kGroups = 36, kNI = 5;
-};
-template <>
-struct RingGeom<true> {
-    static constexpr int kRS = 240, kNPR = 15, kStages = 2, kGroups = 60, kNI = 8;
-};
-
-template <typename T, bool IS_Q6, int FM, bool SPLIT>
-__global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v5_kernel(const float* __restrict__ A,
-                                                                    const uint8_t* __restrict__ W,
-                                                                    float* __restrict__ D, int M, int N, int K,
-                                                                    int tiles, int chunks_per_split) {
-    using G = RingGeom<IS_Q6>;
-    constexpr int BM = 32 * FM;
-    constexpr int BN = 256;
-    constexpr int A_F4 = BM * kKC / 4 / kV4Threads;   // float4 per thread per chunk
-    constexpr int kStageBytes = BN * G::kRS;
-    constexpr int kDepth = G::kStages - 1;             // super-blocks staged ahead
-    static_assert(G::kGroups * 1024 == kStageBytes && 8 * G::kNI >= G::kGroups && 8 * G::kNI < 2 * G::kGroups,
-                  "load groups cover the stage");
-    static_assert(4 * (FM / 2) * 2 * 16 * 64 * 4 <= G::kStages * kStageBytes, "reduction buffer");
-    __shared__ __align__(16) uint8_t w_ring[G::kStages * kStageBytes];
-    __shared__ __align__(16) _Float16 lds_a[2][BM * kLdsStride];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 3, kh = wave >> 2;
-    const int h = lane >> 5;
-    const int tile = blockIdx.x % tiles;
-    const int split = blockIdx.x / tiles;
-    const int ntiles = N / BN;
-    const int m0 = (tile / ntiles) * BM;
-    const int nt0 = (tile % ntiles) * BN;   // first weight row of the tile
-    const int n0 = nt0 + wn * 64;
-    const int c_begin = split * chunks_per_split;
-    const int c_last = c_begin + chunks_per_split - 1;
-    const int sb_begin = c_begin / 4, sb_last = c_last / 4;
-    const size_t row_bytes = (size_t)(K / kQK) * T::kBytes;
-    const uint8_t* wtile = W + (size_t)nt0 * row_bytes;
-
-    // per-lane staging source offsets (relative to the tile's rows at
-    // super-block 0) and LDS destinations
-    uint32_t goff[G::kNI];
-    uint32_t gdst[G::kNI];
-#pragma unroll
-    for (int t = 0; t < G::kNI; ++t) {
-        int g = wave * G::kNI + t;
-        if (g >= G::kGroups) g -= G::kGroups;
-        const int pc = 64 * g + lane;
-        gdst[t] = 16u * (uint32_t)pc;
-        const int row = pc / G::kNPR;
-        int piece = pc % G::kNPR;
-        if (IS_Q6 && piece == 14) piece = 13;
-        goff[t] = (uint32_t)((size_t)row * row_bytes) + 16u * (uint32_t)piece;
-    }
-    u32x4 wst[G::kNI];
-    auto w_gload = [&](int sb) {
-        sb = min(sb, sb_last);
-        const uint8_t* src = wtile + (IS_Q6 ? (((size_t)sb * kQ6KBytes) & ~(size_t)15) : (size_t)sb * kQ4KBytes);
-#pragma unroll
-        for (int t = 0; t < G::kNI; ++t) wst[t] = *reinterpret_cast<const u32x4*>(src + goff[t]);
-    };
-    auto w_lstore = [&](int slot) {
-        uint8_t* dst = w_ring + slot * kStageBytes;
-#pragma unroll
-        for (int t = 0; t < G::kNI; ++t) *reinterpret_cast<u32x4*>(dst + gdst[t]) = wst[t];
-    };
-
-    const int a_row = tid >> 4;
-    const int a_col = 4 * (tid & 15);
-    const float* a_base = A + (size_t)(m0 + a_row) * K + a_col;
-    float4 a_reg[2][A_F4];
-    auto a_load = [&](float4 (&r)[A_F4], int c) {
-        const float* src = a_base + (size_t)min(c, c_last) * kKC;
-#pragma unroll
-        for (int i = 0; i < A_F4; ++i) r[i] = *reinterpret_cast<const float4*>(src + (size_t)(32 * i) * K);
-    };
-    auto a_store = [&](const float4 (&r)[A_F4], int buf) {
-        _Float16* dst = &lds_a[buf][a_row * kLdsStride + a_col];
-#pragma unroll
-        for (int i = 0; i < A_F4; ++i) {
-            f16x4 hv;
-            hv[0] = (_Float16)r[i].x; hv[1] = (_Float16)r[i].y;
-            hv[2] = (_Float16)r[i].z; hv[3] = (_Float16)r[i].w;
-            *reinterpret_cast<f16x4*>(dst + 32 * i * kLdsStride) = hv;
-        }
-    };
-
-    f32x16 acc[FM][2];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    const int frag = (lane & 31) * kLdsStride + 32 * kh + 16 * h;
-    const int row_lds0 = (wn * 64 + (lane & 31)) * G::kRS;
-    const int row_lds1 = row_lds0 + 32 * G::kRS;
-
-    // iteration I of the 8-chunk group starting at chunk c8 (super-blocks
-    // c8/4 and c8/4+1 in ring slots slot0, slot1; staging targets sd0, sd1)
-    auto iteration = [&](auto it, int c8, int slot0, int slot1, int sd0, int sd1) {
-        constexpr int I = decltype(it)::value;
-        constexpr int P = I & 1, CQ = I & 3;
-        const int c = c8 + I;
-        const int sb = c8 / 4 + (I >> 2);
-        const int slot = (I >> 2) ? slot1 : slot0;
-        __builtin_amdgcn_sched_barrier(0);
-        a_store(a_reg[P ^ 1], P ^ 1);
-        if constexpr (CQ == 2) w_lstore((I >> 2) ? sd1 : sd0);
-        typename T::Hdr hd[2];
-        typename T::Qs qs[2];
-        const uint8_t* st = w_ring + slot * kStageBytes;
-        if constexpr (IS_Q6) {
-            const int shift = 2 * (sb & 7);
-            constexpr int nh = CQ >> 1;
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0) + shift;
-                qs[r].ql = ld16(rb + 64 * nh + 32 * kh + 16 * h);
-                qs[r].qh = ld16(rb + 128 + 32 * nh + 16 * h);
-                qs[r].sc = ld4(rb + 192 + 4 * CQ);
-                hd[r].d = ld_u16(rb + 208);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint8_t* rb = st + (r ? row_lds1 : row_lds0);
-                hd[r].v = *reinterpret_cast<const u32x4*>(rb);
-                qs[r].q = *reinterpret_cast<const u32x4*>(rb + 16 + 32 * CQ + 16 * h);
-            }
-        }
-        f16x8 bq[2][2];
-        T::template dequant<CQ>(hd[0], qs[0], h, kh, bq[0]);
-        T::template dequant<CQ>(hd[1], qs[1], h, kh, bq[1]);
-        a_load(a_reg[P ^ 1], c + 3);
-        if constexpr (CQ == 0) w_gload(sb + kDepth);
-        const _Float16* la = lds_a[P] + frag;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            f16x8 af[FM];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const f16x8*>(la + 32 * i * kLdsStride + 8 * s2);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bq[j][s2], acc[i][j], 0, 0, 0);
-        }
-        lds_barrier();
-    };
-
-    // prologue: super-blocks sb_begin .. sb_begin+kDepth-1 into slots 0..;
-    // A(c0) -> LDS 0; A(c0+1), A(c0+2) in flight
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        w_gload(sb_begin + d);
-        w_lstore(d);
-    }
-    a_load(a_reg[0], c_begin);
-    a_load(a_reg[1], c_begin + 1);
-    a_store(a_reg[0], 0);
-    a_load(a_reg[0], c_begin + 2);
-    lds_barrier();
-
-    int slot0 = 0;   // ring slot of super-block c8/4
-    for (int c8 = c_begin; c8 <= c_last; c8 += 8) {
-        const int slot1 = slot0 + 1 == G::kStages ? 0 : slot0 + 1;
-        const int sd0 = slot0 + kDepth >= G::kStages ? slot0 + kDepth - G::kStages : slot0 + kDepth;
-        const int sd1 = sd0 + 1 == G::kStages ? 0 : sd0 + 1;
-        iteration(std::integral_constant<int, 0>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 1>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 2>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 3>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 4>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 5>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 6>{}, c8, slot0, slot1, sd0, sd1);
-        iteration(std::integral_constant<int, 7>{}, c8, slot0, slot1, sd0, sd1);
-        slot0 = slot1 + 1 == G::kStages ? 0 : slot1 + 1;
-    }
-
-    float* red = reinterpret_cast<float*>(w_ring) + wn * (FM / 2) * 2 * 16 * 64 + lane;
-    auto store = [&](int i, int j, const f32x16& v) {
-        const int col = n0 + 32 * j + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            if constexpr (SPLIT)
-                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
-            else
-                D[(size_t)row * N + col] = v[e];
-        }
-    };
-#pragma unroll
-    for (int round = 0; round < 2; ++round) {
-        const int giver = round == 0 ? 1 : 0;
-        if (kh == giver) {
-#pragma unroll
-            for (int ii = 0; ii < FM / 2; ++ii)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) red[((ii * 2 + j) * 16 + e) * 64] = acc[round * (FM / 2) + ii][j][e];
-        }
-        __syncthreads();
-        if (kh != giver) {
-#pragma unroll
-            for (int ii = 0; ii < FM / 2; ++ii)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    f32x16 v = acc[round * (FM / 2) + ii][j];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) v[e] += red[((ii * 2 + j) * 16 + e) * 64];
-                    store(round * (FM / 2) + ii, j, v);
-                }
-        }
-        __syncthreads();
-    }
-}
-
-// Workgroups are dispatched round-robin over the XCDs (b -> XCD b % 8).
-// Returns the virtual index of workgroup b such that XCD x processes the
-// contiguous virtual range [start_x, start_x + count_x): a bijection of
-// [0, total).
-constexpr int kXcds = 8;
-__device__ __forceinline__ int xcd_remap(int b, int total) {
-    const int x = b % kXcds, local = b / kXcds;
-    const int per = total / kXcds, rem = total % kXcds;
-    const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
-    return start + local;
-}
-
-// ── v7: 4 waves (one per SIMD), full K chunk per wave, MFMA/VALU interleave
-// Workgroup = 256 threads over a BM x 256 tile (BM = 32 FM); wave w owns
-// output columns [n0 + 64 w, +64) for all BM rows and both K halves of every
-// chunk, so no cross-wave reduction is needed and each wave has the whole
-// register file of its SIMD (accumulators in AGPRs).  Weights stage through
-// the same LDS ring as v5; B operands are double buffered so chunk c + 1 is
-// dequantised while the MFMAs of chunk c run, with scheduling hints placing
-// a few VALU operations after every MFMA (the matrix core executes an MFMA
-// for many cycles while the SIMD issues the independent VALU work).
-constexpr int kV7Threads = 256;
-
+//
 // Weight ring of the 256-row tile: one super-block of every row per stage
 // (Q4_K: 144-byte blocks; Q6_K: the 16-byte aligned 240-byte window around
 // the 2-byte aligned block), two stages.  A stage is kGroups KB; each of
@@ -1633,14 +1395,9 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     const int tiles = (M / (32 * FM)) * (N / 256);
     const int nchunks = K / kKC;
     int s = gemm_splits(tiles, nchunks, device_cu_count());
-    if (const char* e = getenv("RF_GEMM_SPLIT")) {   // tuning override, must divide (K/64)/8
-        const int v = atoi(e);
-        if (v >= 1 && (nchunks / 8) % v == 0) s = v;
-    }
     if (sg.pair) s = 1;                              // silu(gate) * up needs the whole sums
-    // v5 (LDS weight ring) unless RF_GEMM_V=4; Q6_K needs 16-byte aligned rows (K % 2048 == 0)
-    const bool v5 = gemm_kernel_version() != 4 && (!IS_Q6 || K % 2048 == 0);
-    const bool v7 = !plain || (v5 && (gemm_kernel_version() == 0 || gemm_kernel_version() == 7));
+    // v7 (LDS weight ring); Q6_K needs 16-byte aligned rows (K % 2048 == 0) for the ring
+    const bool v7 = !plain || !IS_Q6 || K % 2048 == 0;
     if (s > 1) {
         if (!sg.accum) {
             const size_t a4 = (size_t)M * sg.n1 / 4, b4 = (size_t)M * (sg.n2 - sg.n1) / 4,
@@ -1652,20 +1409,14 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
         }
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s, gemm_band_host(), sg);
-        else if (v5)
-            hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s);
+                               w, D, M, N, K, tiles, nchunks / s, kGemmBand, sg);
         else
             hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D,
                                M, N, K, tiles, nchunks / s);
     } else {
         if (v7)
             hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks, gemm_band_host(), sg);
-        else if (v5)
-            hipLaunchKernelGGL((rf_gemm_qk_v5_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks);
+                               D, M, N, K, tiles, nchunks, kGemmBand, sg);
         else
             hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M,
                                N, K, tiles, nchunks);
@@ -1689,8 +1440,7 @@ template <bool IS_Q6>
 static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
                               const GemmSegs& sg) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    const bool plain = sg.n1 == N && sg.n2 == N && !sg.accum && !sg.pair;
-    if (N % 256 == 0 && K % 512 == 0 && (gemm_kernel_version() != 1 || !plain)) {
+    if (N % 256 == 0 && K % 512 == 0) {
         // shared-dequantisation tiles where they come to about one
         // workgroup per CU without a K split: 256 x 256 (M >= 1024 at the
         // Llama FFN shapes, 10 % faster than v7), else 128 x 128 at up to
@@ -1699,7 +1449,7 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long cus = device_cu_count();
         const long sq_tiles = (long)(M / 256) * (N / 256);
         const long sq128_tiles = (long)(M / 128) * (N / 128);
-        const bool sq_ok = gemm_kernel_version() == 0 && sg.n1 == N && sg.n2 == N && !sg.pair;
+        const bool sq_ok = sg.n1 == N && sg.n2 == N && !sg.pair;
         if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
             launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
@@ -1731,7 +1481,7 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
 
 using namespace rf;
 
-// Validation as wmma_gemm_q4_k.hip:513-516 / wmma_gemm_q6_k.hip:220-223,
+// Validation as wmma_gemm_q4_k.hip:207-210 / wmma_gemm_q6_k.hip:220-223,
 // plus 16-byte alignment of A (read as float4) and of Q4_K weights.
 extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, float* output, int M, int N,
                                             int K, hipStream_t stream) {

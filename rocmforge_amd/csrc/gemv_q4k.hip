@@ -23,11 +23,10 @@
 
 #include "qk_common.h"
 
-#ifndef RF_NB
-#define RF_NB 3   // register ring depth of the one-row-per-step GEMV (measured best)
-#endif
 
 namespace rf {
+
+constexpr int kRingDepth = 3;   // register ring depth of the one-row-per-step GEMV (measured best)
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerWg = kThreads / kWave;
@@ -336,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
 // equal contiguous share of the rows), fewer when N is too small to give each
 // wave at least `min_rows` rows.
 static inline int gemv_grid(int N, int min_rows) {
-    const int cap = device_cu_count() * gemv_wg_per_cu(2);
+    const int cap = device_cu_count() * 2;
     const int need = (N + kWavesPerWg * min_rows - 1) / (kWavesPerWg * min_rows);
     return need < cap ? need : cap;
 }
@@ -351,9 +350,9 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     // gate+up 14336x4096 12.9 vs 14.1 us, 6144x4096 5.1 vs 5.45 us,
     // 4096x4096 + residual 4.7 vs 5.1 us, 14336x4096 8.0 vs 8.1 us.
     // a fused RMSNorm needs 256-thread workgroups (its summation order)
-    const int r = qkv.norm_w ? (MODE == kGateUp ? 1 : 2) : gemv_rows_per_step(MODE == kGateUp ? 1 : 2);
-    const int nw = (r == 1 && !qkv.norm_w) ? gemv_waves_per_wg(4) : 4;
-    const int cap = device_cu_count() * gemv_wg_per_cu(1);
+    const int r = MODE == kGateUp ? 1 : 2;
+    constexpr int nw = 4;
+    const int cap = device_cu_count();
     const int need = (N + nw - 1) / nw;
     const int grid = need < cap ? need : cap;
     // result slots per wave: its largest row count
@@ -367,18 +366,9 @@ static hipError_t launch_q8(const void* w0, const void* w1, const float* x, cons
     const size_t lds = q8_lds_bytes(K) + out_bytes;
     auto go = [&](auto one) {
         constexpr bool ONE = decltype(one)::value;
-        if (r == 1 && nw == 16)
-            hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 16, RF_NB, ONE>), dim3(grid), dim3(16 * 64), lds, st, a,
-                               b, x, res, y, K, N, qkv);
-        else if (r == 1 && nw == 8)
-            hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 8, RF_NB, ONE>), dim3(grid), dim3(8 * 64), lds, st, a, b,
-                               x, res, y, K, N, qkv);
-        else if (r == 1)
-            hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 4, RF_NB, ONE>), dim3(grid), dim3(4 * 64), lds, st, a, b,
-                               x, res, y, K, N, qkv);
-        else if (r == 4 && MODE != kGateUp)
-            hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 4, 4, 3, ONE>), dim3(grid), dim3(4 * 64), lds, st, a, b, x,
-                               res, y, K, N, qkv);
+        if (r == 1)
+            hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 1, 4, kRingDepth, ONE>), dim3(grid), dim3(4 * 64), lds, st,
+                               a, b, x, res, y, K, N, qkv);
         else
             hipLaunchKernelGGL((rf_q4k_q8_gemv_kernel<MODE, 2, 4, 3, ONE>), dim3(grid), dim3(4 * 64), lds, st, a, b, x,
                                res, y, K, N, qkv);

@@ -21,11 +21,10 @@
 //    block, x in L2 (K*4 > 64 KB).
 #include "qk_common.h"
 
-#ifndef RF_Q6_NB
-#define RF_Q6_NB 3   // register ring depth (rows in flight + 1) of the K-split GEMV (measured best)
-#endif
 
 namespace rf {
+
+constexpr int kQ6Ring = 3;   // register ring depth (rows in flight + 1) of the K-split GEMV (measured best)
 
 constexpr int kQ6SbPerStep = 16;
 
@@ -476,34 +475,34 @@ static hipError_t launch_q6(const void* weights_q6_k, const float* input, const 
                             int n_rows, int ncols_dst, hipStream_t stream) {
     const uint8_t* w = static_cast<const uint8_t*>(weights_q6_k);
     const int nsb = n_rows / kQK;
-    if (gemv_q6_variant() == 0 && nsb <= 64 && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0) {
+    if (nsb <= 64 && nsb % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0) {
         const int nwk = nsb / 8;
-        const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
+        const int cap = device_cu_count() * (nwk >= 4 ? 1 : 8 / nwk);
         const int grid = ncols_dst < cap ? ncols_dst : cap;
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * 4 * sizeof(float);
         if (lds <= 64 * 1024) {
-            hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
+            hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<kQ6Ring>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
                                residual, output, n_rows, ncols_dst, nullptr, 0.0f);
             return hipGetLastError();
         }
     }
-    if ((gemv_q6_variant() == 0 || gemv_q6_variant() == 2) && nsb <= 64) {
+    if (nsb <= 64) {
         const int nwk = (nsb + 7) / 8;
         // about 8 waves per CU: short K (few slices per workgroup) gets
         // several workgroups per CU
-        const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
+        const int cap = device_cu_count() * (nwk >= 4 ? 1 : 8 / nwk);
         const int grid = ncols_dst < cap ? ncols_dst : cap;
         const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * sizeof(float);
         if (lds <= 64 * 1024) {
-            hipLaunchKernelGGL((rf_q6k_gemv_xreg_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
+            hipLaunchKernelGGL((rf_q6k_gemv_xreg_kernel<kQ6Ring>), dim3(grid), dim3(nwk * 64), lds, stream, w, input,
                                residual, output, n_rows, ncols_dst);
             return hipGetLastError();
         }
     }
-    const int r = gemv_rows_per_step(1);
-    const int nw = (r == 1) ? gemv_waves_per_wg(8) : 4;
+    // one row per wave step, 8 waves per workgroup, one workgroup per CU
+    constexpr int nw = 8;
     const int need = (ncols_dst + nw - 1) / nw;
-    const int cap = device_cu_count() * gemv_wg_per_cu(nw == 8 ? 1 : 2);
+    const int cap = device_cu_count();
     const int grid = need < cap ? need : cap;
     const bool in_lds = (size_t)x_padded_floats(n_rows) * sizeof(float) <= 65536;
     const size_t lds = in_lds ? (size_t)(x_padded_floats(n_rows) + 4) * sizeof(float) : 0;
@@ -511,18 +510,10 @@ static hipError_t launch_q6(const void* weights_q6_k, const float* input, const 
                              (size_t)(n_rows / 16) * 4;   // + x group sums
     if (out_bytes > 64 * 1024) return hipErrorInvalidValue;
     const dim3 blk(nw * 64);
-#define RF_Q6_LAUNCH(RR, L, W) \
-    hipLaunchKernelGGL((rf_q6k_gemv_kernel<RR, L, W, 3>), dim3(grid), blk, lds + out_bytes, stream, w, input, \
+#define RF_Q6_LAUNCH(L) \
+    hipLaunchKernelGGL((rf_q6k_gemv_kernel<1, L, nw, 3>), dim3(grid), blk, lds + out_bytes, stream, w, input, \
                        residual, output, n_rows, ncols_dst)
-    if (r >= 2) {
-        if (in_lds) RF_Q6_LAUNCH(2, true, 4); else RF_Q6_LAUNCH(2, false, 4);
-    } else if (nw == 16) {
-        if (in_lds) RF_Q6_LAUNCH(1, true, 16); else RF_Q6_LAUNCH(1, false, 16);
-    } else if (nw == 8) {
-        if (in_lds) RF_Q6_LAUNCH(1, true, 8); else RF_Q6_LAUNCH(1, false, 8);
-    } else {
-        if (in_lds) RF_Q6_LAUNCH(1, true, 4); else RF_Q6_LAUNCH(1, false, 4);
-    }
+    if (in_lds) RF_Q6_LAUNCH(true); else RF_Q6_LAUNCH(false);
 #undef RF_Q6_LAUNCH
     return hipGetLastError();
 }
@@ -564,11 +555,11 @@ extern "C" hipError_t rf_gemv_q6_k_rmsnorm_launch(const void* weights_q6_k, cons
                                       reinterpret_cast<uintptr_t>(norm_w)) & 15u) != 0)
         return hipErrorInvalidValue;
     const int nwk = nsb / 8;
-    const int cap = device_cu_count() * gemv_wg_per_cu(nwk >= 4 ? 1 : 8 / nwk);
+    const int cap = device_cu_count() * (nwk >= 4 ? 1 : 8 / nwk);
     const int grid = ncols_dst < cap ? ncols_dst : cap;
     const size_t lds = (size_t)((ncols_dst + grid - 1) / grid) * nwk * 4 * sizeof(float);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<RF_Q6_NB>), dim3(grid), dim3(nwk * 64), lds, stream,
+    hipLaunchKernelGGL((rf_q6k_gemv_lin_kernel<kQ6Ring>), dim3(grid), dim3(nwk * 64), lds, stream,
                        static_cast<const uint8_t*>(weights_q6_k), input, nullptr, output, n_rows, ncols_dst, norm_w,
                        eps);
     return hipGetLastError();

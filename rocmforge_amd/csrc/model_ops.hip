@@ -24,10 +24,12 @@
 // as the reference, evaluated in double and rounded once to float (the
 // reference's 1.0f / powf(..) is within an ulp of this), then divided by
 // freq_scale[i] when given; angle = (float)pos * theta_i in fp32.  The
-// values live in a small per-(device, d, base) table made on first use.
+// reference-named launchers evaluate theta_i in the kernel; the fused
+// launchers take an optional caller-owned table of the same values
+// (rf_rope_theta_table fills one), which saves the double-precision pow in
+// every lane.  No launcher allocates, frees or synchronises.
 #include <hip/hip_fp16.h>
 
-#include <mutex>
 
 #include "qk_common.h"
 
@@ -48,20 +50,25 @@ __device__ __forceinline__ float wave_sum_all(float v) {
     return v;
 }
 
-// theta_i from the per-(device, d, base) table (filled once by
-// rf_theta_fill_kernel), divided by freq_scale[i] when given
-__device__ __forceinline__ float rope_theta(int i, const float* __restrict__ tab, const float* freq_scale) {
-    float t = tab[i];
+// theta_i = 1 / base^((float)(2i) / (float)d), evaluated in double and
+// rounded once to float
+__device__ __forceinline__ float theta_exact(int i, int d, float base) {
+    const float e = (float)(2 * i) / (float)d;
+    return (float)(1.0 / pow((double)base, (double)e));
+}
+
+// theta_i from the caller's table when given (the same values), else
+// evaluated here; divided by freq_scale[i] when given
+__device__ __forceinline__ float rope_theta(int i, int d, float base, const float* __restrict__ tab,
+                                            const float* freq_scale) {
+    float t = tab != nullptr ? tab[i] : theta_exact(i, d, base);
     if (freq_scale != nullptr) t /= freq_scale[i];
     return t;
 }
 
 __global__ void rf_theta_fill_kernel(float* tab, int d, float base) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < d / 2) {
-        const float e = (float)(2 * i) / (float)d;
-        tab[i] = (float)(1.0 / pow((double)base, (double)e));
-    }
+    if (i < d / 2) tab[i] = theta_exact(i, d, base);
 }
 
 // (x0, x1) rotated by angle pos * theta
@@ -159,8 +166,7 @@ static hipError_t rms_rows(const float* x, const float* w, float* out, int n, fl
 
 // ---- RoPE over heads (in place) ---------------------------------------------------
 __global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, int pos0, int nh, int d,
-                                     const float* __restrict__ tab, int neox, const float* __restrict__ freq_scale,
-                                     int seq_len) {
+                                     float base, int neox, const float* __restrict__ freq_scale, int seq_len) {
     const int half = d / 2;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     const int s = blockIdx.y;
@@ -171,57 +177,17 @@ __global__ void rf_rope_heads_kernel(float* x, const int* __restrict__ pos_ptr, 
     int i0, i1;
     pair_idx(i, d, neox, &i0, &i1);
     float x0 = row[i0], x1 = row[i1];
-    rope_pair(x0, x1, pos, rope_theta(i, tab, freq_scale));
+    rope_pair(x0, x1, pos, rope_theta(i, d, base, nullptr, freq_scale));
     row[i0] = x0;
     row[i1] = x1;
-}
-
-// theta tables: (d, base) -> device float[d/2], per device, made on first
-// use (so, like the attention workspace, not inside a graph capture: a
-// capturing stream without its table gets an error).
-struct ThetaTab {
-    int dev, d;
-    float base;
-    float* p;
-};
-static ThetaTab g_theta[64];
-static int g_ntheta = 0;
-static std::mutex g_alloc_mutex;     // the theta tables and the attention workspace
-
-static hipError_t theta_table(int d, float base, hipStream_t st, const float** out) {
-    std::lock_guard<std::mutex> lock(g_alloc_mutex);
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    for (int i = 0; i < g_ntheta; ++i)
-        if (g_theta[i].dev == dev && g_theta[i].d == d && g_theta[i].base == base) {
-            *out = g_theta[i].p;
-            return hipSuccess;
-        }
-    if (g_ntheta == 64) return hipErrorOutOfMemory;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-        return hipErrorStreamCaptureUnsupported;
-    float* p = nullptr;
-    e = hipMalloc(&p, (size_t)(d / 2 > 0 ? d / 2 : 1) * sizeof(float));
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(rf_theta_fill_kernel, dim3((d / 2 + 255) / 256 + 1), dim3(256), 0, st, p, d, base);
-    e = hipStreamSynchronize(st);
-    if (e != hipSuccess) return e;
-    g_theta[g_ntheta++] = ThetaTab{dev, d, base, p};
-    *out = p;
-    return hipSuccess;
 }
 
 static hipError_t rope_heads(float* x, const int* pos_ptr, int pos, int nh, int d, float base, int neox,
                              const float* fs, int seq_len, hipStream_t st) {
     if (x == nullptr || nh <= 0 || d <= 0 || (d & 1) || seq_len <= 0) return hipErrorInvalidValue;
     const int pairs = nh * (d / 2);
-    const float* tab = nullptr;
-    const hipError_t e = theta_table(d, base, st, &tab);
-    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rf_rope_heads_kernel, dim3((pairs + 255) / 256, seq_len), dim3(256), 0, st, x, pos_ptr, pos, nh,
-                       d, tab, neox, fs, seq_len);
+                       d, base, neox, fs, seq_len);
     return hipGetLastError();
 }
 
@@ -229,7 +195,7 @@ static hipError_t rope_heads(float* x, const int* pos_ptr, int pos, int nh, int 
 // Cache layout [max_seq][n_kv * d] fp16 per layer; V copied, K rotated.
 __global__ void rf_kv_write_rope_kernel(__half* kc, __half* vc, const float* __restrict__ k,
                                         const float* __restrict__ v, const int* __restrict__ pos_ptr, int pos0,
-                                        int nkv, int d, const float* __restrict__ tab, int neox,
+                                        int nkv, int d, float base, int neox,
                                         const float* __restrict__ freq_scale) {
     const int half = d / 2;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
@@ -241,7 +207,7 @@ __global__ void rf_kv_write_rope_kernel(__half* kc, __half* vc, const float* __r
     const size_t base_in = (size_t)head * d;
     const size_t base_c = (size_t)pos * nkv * d + base_in;
     float x0 = k[base_in + i0], x1 = k[base_in + i1];
-    rope_pair(x0, x1, pos, rope_theta(i, tab, freq_scale));
+    rope_pair(x0, x1, pos, rope_theta(i, d, base, nullptr, freq_scale));
     kc[base_c + i0] = __float2half(x0);
     kc[base_c + i1] = __float2half(x1);
     vc[base_c + i0] = __float2half(v[base_in + i0]);
@@ -268,19 +234,30 @@ __global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* 
 // this function, so they produce the same bits.
 // theta of the 8 pairs a lane rotates, loaded in one go (with the lane's x)
 template <int LPP>
-__device__ __forceinline__ void theta8(const float* __restrict__ tab, int sub, int neox,
+// (from the caller's table when given, else evaluated here)
+__device__ __forceinline__ void theta8(const float* __restrict__ tab, float base, int sub, int neox,
                                        const float* __restrict__ freq_scale, float t[8]) {
     constexpr int D = 8 * LPP;
     int p0;
     if (neox) {
         p0 = sub < LPP / 2 ? 8 * sub : 8 * sub - D / 2;
-        const float4 a = *reinterpret_cast<const float4*>(tab + p0);
-        const float4 b = *reinterpret_cast<const float4*>(tab + p0 + 4);
-        t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w; t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
+        if (tab != nullptr) {
+            const float4 a = *reinterpret_cast<const float4*>(tab + p0);
+            const float4 b = *reinterpret_cast<const float4*>(tab + p0 + 4);
+            t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w; t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t[i] = theta_exact(p0 + i, D, base);
+        }
     } else {
         p0 = 4 * sub;                          // pairs (2i, 2i+1): four per lane, t[i] for i even
-        const float4 a = *reinterpret_cast<const float4*>(tab + p0);
-        t[0] = a.x; t[2] = a.y; t[4] = a.z; t[6] = a.w;
+        if (tab != nullptr) {
+            const float4 a = *reinterpret_cast<const float4*>(tab + p0);
+            t[0] = a.x; t[2] = a.y; t[4] = a.z; t[6] = a.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t[2 * i] = theta_exact(p0 + i, D, base);
+        }
         t[1] = t[3] = t[5] = t[7] = 0.0f;
     }
     if (freq_scale != nullptr) {
@@ -342,7 +319,7 @@ template <int LPP>
 __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     float* q, const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, __half* kc, __half* vc, const int* __restrict__ pos_ptr, int nh, int nkv,
-    float eps, const float* __restrict__ tab, int neox, const float* __restrict__ freq_scale) {
+    float eps, const float* __restrict__ tab, float base, int neox, const float* __restrict__ freq_scale) {
     constexpr int D = 8 * LPP;
     const int lane = threadIdx.x & 63;
     const int hidx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPP) + lane / LPP;
@@ -353,7 +330,7 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     const int pos = *pos_ptr;
     float x[8], th[8];
     load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
-    theta8<LPP>(tab, sub, neox, freq_scale, th);
+    theta8<LPP>(tab, base, sub, neox, freq_scale, th);
     head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
     if (is_q) {
         float* dst = q + (size_t)head * D + 8 * sub;
@@ -376,7 +353,7 @@ template <int LPP>
 __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_rows_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, __half* __restrict__ q16, __half* kc,
-    __half* vc, int pos0, int rows_kv, int nh, int nkv, float eps, const float* __restrict__ tab, int neox,
+    __half* vc, int pos0, int rows_kv, int nh, int nkv, float eps, const float* __restrict__ tab, float base, int neox,
     const float* __restrict__ freq_scale) {
     constexpr int D = 8 * LPP;
     const int lane = threadIdx.x & 63;
@@ -391,7 +368,7 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_rows_kernel(
     const size_t src = (size_t)row * (is_q ? nh : nkv) * D + (size_t)head * D + 8 * sub;
     float x[8], th[8];
     load8((is_q ? q : k) + src, x);
-    theta8<LPP>(tab, sub, neox, freq_scale, th);
+    theta8<LPP>(tab, base, sub, neox, freq_scale, th);
     head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
     if (is_q) {
         store8_f16(q16 + src, x);
@@ -546,6 +523,7 @@ struct QkStep {
     __half* vc;
     float eps;
     const float* tab;
+    float base;
     int neox;
     const float* freq_scale;
 };
@@ -582,7 +560,7 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
     float qv[8], kx[8], vx[8], th[8];
     load8(q + (size_t)head * D + 8 * sub, qv);
-    if constexpr (QK) theta8<LPP>(qk.tab, sub, qk.neox, qk.freq_scale, th);
+    if constexpr (QK) theta8<LPP>(qk.tab, qk.base, sub, qk.neox, qk.freq_scale, th);
     if (owner && wave == 0) {
         load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
         load8(qk.v + (size_t)kvh * D + 8 * sub, vx);
@@ -727,8 +705,10 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
         for (int u = 0; u < 4; ++u) {
             const int s = s0 + u * ngr;
             f[u] = s < S ? fs[s] : 0.0f;
-            v[u] = s < S ? *reinterpret_cast<const float4*>(base + (size_t)s * (D + 4) + 4 * ch)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            // an empty split wrote no acc: its slots hold whatever the
+            // workspace held before, so they are never read
+            v[u] = f[u] > 0.0f ? *reinterpret_cast<const float4*>(base + (size_t)s * (D + 4) + 4 * ch)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -749,56 +729,28 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
     }
 }
 
-// Workspace of the split path: one allocation per device, made on the first
-// call that needs more than it has (so not inside a graph capture: a
-// capturing stream with too small a workspace gets an error instead).
-// Calls that overlap on one device share it and race; the reference's
-// decode runs them in stream order.
-static float* g_attn_ws[64];
-static size_t g_attn_ws_bytes[64];
-
-static hipError_t attn_workspace(size_t bytes, hipStream_t st, float** ws) {
-    std::lock_guard<std::mutex> lock(g_alloc_mutex);
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (g_attn_ws_bytes[dev] < bytes) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return hipErrorStreamCaptureUnsupported;
-        const size_t want = bytes < ((size_t)8 << 20) ? ((size_t)8 << 20) : bytes;
-        float* p = nullptr;
-        e = hipMalloc(&p, want);
-        if (e != hipSuccess) return e;
-        if (g_attn_ws[dev] != nullptr) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_attn_ws[dev]);
-        }
-        g_attn_ws[dev] = p;
-        g_attn_ws_bytes[dev] = want;
-    }
-    *ws = g_attn_ws[dev];
-    return hipSuccess;
-}
+// Workspace of the split path: the (m, l, acc) partials of every head and
+// split, (D + 4) floats each, for at most kMaxSplits splits.  It is the
+// caller's memory (rf_flash_attn_decode_workspace_bytes gives the size);
+// launches that share one workspace must be stream-ordered.
+constexpr int kMaxSplits = 64;
+static size_t attn_ws_bytes(int nh, int d) { return (size_t)nh * kMaxSplits * (d + 4) * sizeof(float); }
 
 static hipError_t attn_decode(float* out, const float* q, const __half* kc, const __half* vc, const int* len_ptr,
-                              int len, int nh, int nkv, int d, float scale, hipStream_t st,
-                              const QkStep* qk = nullptr) {
+                              int len, int nh, int nkv, int d, float scale, float* ws, size_t ws_bytes,
+                              hipStream_t st, const QkStep* qk = nullptr) {
     if (out == nullptr || q == nullptr || kc == nullptr || vc == nullptr) return hipErrorInvalidValue;
     if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || (len_ptr == nullptr && len <= 0)) return hipErrorInvalidValue;
     if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
     const int group = nh / nkv;
-    if (group <= 8) {
+    if (ws != nullptr && ws_bytes < attn_ws_bytes(nh, d)) return hipErrorInvalidValue;
+    if (ws != nullptr && group <= 8) {
         int S = (2 * device_cu_count() + nkv - 1) / nkv;
-        S = S < 1 ? 1 : (S > 64 ? 64 : S);
+        S = S < 1 ? 1 : (S > kMaxSplits ? kMaxSplits : S);
         if (len_ptr == nullptr) {
             const int chunks = (len + kSplitChunk - 1) / kSplitChunk;
             S = chunks < S ? chunks : S;
         }
-        float* ws = nullptr;
-        const hipError_t e = attn_workspace((size_t)nh * S * (d + 4) * sizeof(float), st, &ws);
-        if (e != hipSuccess) return e;
         const dim3 grid(nkv, S), blk(64 * group);
         const QkStep a = qk ? *qk : QkStep{};
 #define RF_SPLIT(LPP)                                                                                                  \
@@ -817,7 +769,7 @@ static hipError_t attn_decode(float* out, const float* q, const __half* kc, cons
         hipLaunchKernelGGL(rf_attn_merge_kernel, dim3(nh), dim3(256), 0, st, ws, out, nh, d, S);
         return hipGetLastError();
     }
-    if (qk) return hipErrorInvalidValue;      // the folded step needs the split path (GQA group <= 8)
+    if (qk) return hipErrorInvalidValue;      // the folded step needs the split path (workspace, GQA group <= 8)
     switch (d) {
     case 64: hipLaunchKernelGGL(rf_attn_decode_kernel<8>, dim3(nh), dim3(256), 0, st, out, q, kc, vc, len_ptr, len, nh,
                                 nkv, scale); break;
@@ -1010,11 +962,8 @@ static hipError_t kv_write_rope(uint16_t* kc, uint16_t* vc, const float* k, cons
     if (kc == nullptr || vc == nullptr || k == nullptr || v == nullptr || nkv <= 0 || d <= 0 || (d & 1))
         return hipErrorInvalidValue;
     const int pairs = nkv * (d / 2);
-    const float* tab = nullptr;
-    const hipError_t e = theta_table(d, base, st, &tab);
-    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rf_kv_write_rope_kernel, grid1(pairs), dim3(256), 0, st, reinterpret_cast<__half*>(kc),
-                       reinterpret_cast<__half*>(vc), k, v, pos_ptr, pos, nkv, d, tab, neox, fs);
+                       reinterpret_cast<__half*>(vc), k, v, pos_ptr, pos, nkv, d, base, neox, fs);
     return hipGetLastError();
 }
 extern "C" hipError_t gpu_kv_write_rope_scaled(uint16_t* d_k_cache, uint16_t* d_v_cache, const float* d_k, const float* d_v,
@@ -1068,20 +1017,22 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_
                                                      uint16_t* d_v_cache, const int* d_pos, const int num_heads,
                                                      const int num_kv_heads, const int head_dim, const float eps,
                                                      const float theta_base, const int neox,
-                                                     const float* d_freq_scale, hipStream_t stream) {
+                                                     const float* d_freq_scale, const float* d_theta,
+                                                     hipStream_t stream) {
     if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_k_cache == nullptr || d_v_cache == nullptr ||
         d_pos == nullptr || num_heads <= 0 || num_kv_heads <= 0)
         return hipErrorInvalidValue;
+    // 8-element vector loads of q/k/v and 16-byte fp16 stores into the caches
+    for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_k_cache,
+                          (const void*)d_v_cache})
+        if (reinterpret_cast<uintptr_t>(p) & 15u) return hipErrorInvalidValue;
     const int heads = num_heads + num_kv_heads;
     __half* kc = reinterpret_cast<__half*>(d_k_cache);
     __half* vc = reinterpret_cast<__half*>(d_v_cache);
-    const float* tab = nullptr;
-    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
-    if (e != hipSuccess) return e;
 #define RF_QKR(LPP)                                                                                                    \
     hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel<LPP>, dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP))),      \
                        dim3(256), 0, stream, d_q, d_k, d_v, d_q_norm, d_k_norm, kc, vc, d_pos, num_heads,         \
-                       num_kv_heads, eps, tab, neox, d_freq_scale)
+                       num_kv_heads, eps, d_theta, theta_base, neox, d_freq_scale)
     switch (head_dim) {
     case 64: RF_QKR(8); break;
     case 128: RF_QKR(16); break;
@@ -1098,25 +1049,24 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const floa
                                                     const int rows_q, const int rows_kv, const int num_heads,
                                                     const int num_kv_heads, const int head_dim, const int max_seq,
                                                     const float eps, const float theta_base, const int neox,
-                                                    const float* d_freq_scale, hipStream_t stream) {
+                                                    const float* d_freq_scale, const float* d_theta,
+                                                    hipStream_t stream) {
     if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_q16 == nullptr || d_k_cache == nullptr ||
         d_v_cache == nullptr || num_heads <= 0 || num_kv_heads <= 0 || start_pos < 0 || rows_q <= 0 ||
         rows_kv < 0 || rows_kv > rows_q || rows_q > 65535 || start_pos + rows_kv > max_seq)
         return hipErrorInvalidValue;
-    for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_q16})
+    for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_q16,
+                          (const void*)d_k_cache, (const void*)d_v_cache})
         if (reinterpret_cast<uintptr_t>(p) & 15u) return hipErrorInvalidValue;
     const int heads = num_heads + num_kv_heads;
     __half* kc = reinterpret_cast<__half*>(d_k_cache);
     __half* vc = reinterpret_cast<__half*>(d_v_cache);
     __half* q16 = reinterpret_cast<__half*>(d_q16);
-    const float* tab = nullptr;
-    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
-    if (e != hipSuccess) return e;
 #define RF_QKR(LPP)                                                                                                    \
     hipLaunchKernelGGL(rf_qk_norm_rope_kv_rows_kernel<LPP>,                                                            \
                        dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP)), rows_q), dim3(256), 0, stream, d_q, d_k, \
-                       d_v, d_q_norm, d_k_norm, q16, kc, vc, start_pos, rows_kv, num_heads, num_kv_heads, eps, tab,   \
-                       neox, d_freq_scale)
+                       d_v, d_q_norm, d_k_norm, q16, kc, vc, start_pos, rows_kv, num_heads, num_kv_heads, eps,        \
+                       d_theta, theta_base, neox, d_freq_scale)
     switch (head_dim) {
     case 64: RF_QKR(8); break;
     case 128: RF_QKR(16); break;
@@ -1128,14 +1078,17 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const floa
 }
 
 // ---- decode attention ----
+// The reference-named launchers take no workspace: they run the
+// one-workgroup-per-head kernel.  The _ws launchers run the split path in
+// the caller's workspace.
 extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head(float* d_out, const float* d_q, const uint16_t* d_k_cache,
                                                                const uint16_t* d_v_cache, const int seq_len,
                                                                const int num_heads, const int num_kv_heads,
                                                                const int head_dim, const float scale,
                                                                hipStream_t stream) {
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
-                       reinterpret_cast<const __half*>(d_v_cache), nullptr, seq_len, num_heads, num_kv_heads, head_dim, scale,
-                       stream);
+                       reinterpret_cast<const __half*>(d_v_cache), nullptr, seq_len, num_heads, num_kv_heads, head_dim,
+                       scale, nullptr, 0, stream);
 }
 extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_out, const float* d_q,
                                                                      const uint16_t* d_k_cache, const uint16_t* d_v_cache,
@@ -1144,8 +1097,34 @@ extern "C" hipError_t gpu_flash_attn_decode_strided_multi_head_state(float* d_ou
                                                                      const float scale, hipStream_t stream) {
     if (d_seq_len == nullptr) return hipErrorInvalidValue;
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
-                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim, scale,
-                       stream);
+                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim,
+                       scale, nullptr, 0, stream);
+}
+
+extern "C" size_t rf_flash_attn_decode_workspace_bytes(const int num_heads, const int head_dim) {
+    if (num_heads <= 0 || head_dim <= 0) return 0;
+    return attn_ws_bytes(num_heads, head_dim);
+}
+
+extern "C" hipError_t rf_flash_attn_decode_ws(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                              const uint16_t* d_v_cache, const int seq_len, const int num_heads,
+                                              const int num_kv_heads, const int head_dim, const float scale,
+                                              float* d_workspace, const size_t workspace_bytes, hipStream_t stream) {
+    if (d_workspace == nullptr) return hipErrorInvalidValue;
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), nullptr, seq_len, num_heads, num_kv_heads, head_dim,
+                       scale, d_workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t rf_flash_attn_decode_state_ws(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                    const uint16_t* d_v_cache, const int* d_seq_len,
+                                                    const int num_heads, const int num_kv_heads, const int head_dim,
+                                                    const float scale, float* d_workspace,
+                                                    const size_t workspace_bytes, hipStream_t stream) {
+    if (d_seq_len == nullptr || d_workspace == nullptr) return hipErrorInvalidValue;
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim,
+                       scale, d_workspace, workspace_bytes, stream);
 }
 
 extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, const float* d_k,
@@ -1154,17 +1133,25 @@ extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const floa
                                                         const int* d_state, const int num_heads,
                                                         const int num_kv_heads, const int head_dim, const float eps,
                                                         const float theta_base, const int neox,
-                                                        const float* d_freq_scale, const float scale,
-                                                        hipStream_t stream) {
-    if (d_k == nullptr || d_v == nullptr || d_state == nullptr) return hipErrorInvalidValue;
-    const float* tab = nullptr;
-    const hipError_t e = theta_table(head_dim, theta_base, stream, &tab);
-    if (e != hipSuccess) return e;
+                                                        const float* d_freq_scale, const float* d_theta,
+                                                        const float scale, float* d_workspace,
+                                                        const size_t workspace_bytes, hipStream_t stream) {
+    if (d_k == nullptr || d_v == nullptr || d_state == nullptr || d_workspace == nullptr) return hipErrorInvalidValue;
     QkStep qk{d_k, d_v, d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
-              eps, tab, neox, d_freq_scale};
+              eps, d_theta, theta_base, neox, d_freq_scale};
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
                        reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
-                       scale, stream, &qk);
+                       scale, d_workspace, workspace_bytes, stream, &qk);
+}
+
+// Caller-owned RoPE table: d_theta[i] = theta_i for i < head_dim / 2 (the
+// values every launcher here uses), for the fused launchers' d_theta.
+extern "C" hipError_t rf_rope_theta_table(float* d_theta, const int head_dim, const float theta_base,
+                                          hipStream_t stream) {
+    if (d_theta == nullptr || head_dim <= 0 || (head_dim & 1)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_theta_fill_kernel, dim3((head_dim / 2 + 255) / 256), dim3(256), 0, stream, d_theta,
+                       head_dim, theta_base);
+    return hipGetLastError();
 }
 
 // ---- argmax ----

@@ -440,21 +440,5 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Device CU count, cached per device (host side).
 int device_cu_count();
-// GEMV workgroups per CU and waves per workgroup (host side).  Each kernel
-// family passes its measured-best default; RF_GEMV_WG_PER_CU / RF_GEMV_NW
-// override them for tuning sweeps.
-int gemv_wg_per_cu(int dflt);
-// Rows per pipeline step of the register GEMVs (each kernel family passes
-// its measured-best default; RF_GEMV_R=1|2|4 overrides it for tuning sweeps).
-int gemv_rows_per_step(int dflt);
-int gemv_waves_per_wg(int dflt);
-// Q6_K GEMV kernel family (0 = K-split register kernel, 1 = row-step kernel).
-int gemv_q6_variant();
-// GEMM kernel selection for tuning comparisons: RF_GEMM_V=1 forces the
-// general 2x2-wave kernel, =4 the register-weight kernel, =5 the 8-wave
-// ring kernel, =7 the one-wave-per-SIMD ring kernel (v7) for every shape;
-// default (0) picks v7, or the 256 x 256 shared-dequantisation kernel where
-// its tiles fill the CUs without a K split.
-int gemm_kernel_version();
 
 }  // namespace rf

@@ -134,6 +134,20 @@ def _chk(rc, what):
         raise ops.HipApiError(rc, what)
 
 
+# The prefill attention kernel (wmma_attention_prefill_gqa_causal_launch) is
+# built for head_dim 128 and its launcher takes no head_dim to check.
+PREFILL_HEAD_DIM = 128
+
+
+def check_prefill_config(cfg) -> None:
+    """Raises ValueError for a model the prefill path cannot run: the
+    prefill attention reads Q/K/V rows of n_heads * 128 / n_kv_heads * 128
+    values, so any other head_dim would be read with the wrong strides."""
+    if cfg.head_dim != PREFILL_HEAD_DIM:
+        raise ValueError(f"prefill needs head_dim {PREFILL_HEAD_DIM} (the prefill attention kernel's); "
+                         f"this model has head_dim {cfg.head_dim}")
+
+
 class Engine:
     """Prefill + greedy decode of one sequence of up to max_seq tokens."""
 
@@ -169,6 +183,13 @@ class Engine:
         self.token = z(1, torch.int32)
         self.state = z(2, torch.int32)      # {pos, seq_len}
         self.scale = 1.0 / math.sqrt(c.head_dim)
+        # RoPE thetas and the split decode attention's workspace: caller-owned
+        # buffers, made here once (the launchers allocate nothing)
+        self.theta = z(max(c.head_dim // 2, 1))
+        ws_bytes = int(self.lib.rf_flash_attn_decode_workspace_bytes(c.n_heads, c.head_dim))
+        self.attn_ws = z((ws_bytes + 3) // 4)
+        self.attn_ws_bytes = ws_bytes
+        _chk(self.lib.rf_rope_theta_table(_p(self.theta), c.head_dim, c.rope_base, self._stream()), "theta table")
         self._graph = None
         self._pf = None
 
@@ -205,17 +226,18 @@ class Engine:
                 _chk(L.rf_attn_decode_qk_norm_rope_state(_p(self.attn), _p(self.q), _p(self.k), _p(self.v),
                                                          _p(lw.q_norm), _p(lw.k_norm), _p(self.kc[i]), _p(self.vc[i]),
                                                          pos_p, c.n_heads, c.n_kv_heads, c.head_dim, c.eps,
-                                                         c.rope_base, int(c.neox), None, self.scale, st),
+                                                         c.rope_base, int(c.neox), None, _p(self.theta), self.scale,
+                                                         _p(self.attn_ws), self.attn_ws_bytes, st),
                      "qk step + attention")
             else:
                 _chk(L.rf_qk_norm_rope_kv_write_state(_p(self.q), _p(self.k), _p(self.v), _p(lw.q_norm),
                                                       _p(lw.k_norm), _p(self.kc[i]), _p(self.vc[i]), pos_p,
                                                       c.n_heads, c.n_kv_heads, c.head_dim, c.eps, c.rope_base,
-                                                      int(c.neox), None, st), "qk_rope_kv")
+                                                      int(c.neox), None, _p(self.theta), st), "qk_rope_kv")
                 t("qk_rope_kv", i)
-                _chk(L.gpu_flash_attn_decode_strided_multi_head_state(_p(self.attn), _p(self.q), _p(self.kc[i]),
-                                                                      _p(self.vc[i]), len_p, c.n_heads, c.n_kv_heads,
-                                                                      c.head_dim, self.scale, st), "attention")
+                _chk(L.rf_flash_attn_decode_state_ws(_p(self.attn), _p(self.q), _p(self.kc[i]), _p(self.vc[i]),
+                                                     len_p, c.n_heads, c.n_kv_heads, c.head_dim, self.scale,
+                                                     _p(self.attn_ws), self.attn_ws_bytes, st), "attention")
             t("attention", i)
             self._residual_gemv(m["attn_output"], self.attn, c.q_size, st)
             t("attn_output", i)
@@ -350,6 +372,7 @@ class Engine:
         it returns."""
         import torch
         L, c = self.lib, self.cfg
+        check_prefill_config(c)
         M = len(tokens)
         if M < 1 or M > self.max_seq:
             raise ValueError("prompt length out of range")
@@ -377,7 +400,7 @@ class Engine:
                 _chk(L.rf_qk_norm_rope_kv_write_rows(_p(b["q"]), _p(b["k"]), _p(b["v"]), _p(lw.q_norm),
                                                      _p(lw.k_norm), _p(b["q16"]), _p(self.kc[i]), _p(self.vc[i]), 0,
                                                      mp, M, c.n_heads, c.n_kv_heads, c.head_dim, self.max_seq, c.eps,
-                                                     c.rope_base, int(c.neox), None, st), "qk rows")
+                                                     c.rope_base, int(c.neox), None, _p(self.theta), st), "qk rows")
                 t("qk_rope_kv", i)
                 k16, v16 = self.kc[i], self.vc[i]
             else:

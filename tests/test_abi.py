@@ -13,7 +13,7 @@ HIP_ERROR_INVALID_VALUE = 1
 
 def header_symbols():
     text = (ROOT / "include" / "rocmforge_cdna4.h").read_text()
-    return sorted(set(re.findall(r"^(?:hipError_t|const char\*|int|void)\s+(\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:hipError_t|const char\*|int|void|size_t)\s+(\w+)\(", text, re.M)))
 
 
 def test_header_declares_reference_launchers():
@@ -61,6 +61,6 @@ def test_fp32_and_q6_reject_shapes(rf, k, n):
 
 @pytest.mark.parametrize("m,n,k", [(0, 64, 256), (65, 64, 256), (64, 96, 256), (64, 64, 320), (64, 64, 0)])
 def test_gemm_rejects_shapes(rf, m, n, k):
-    # wmma_gemm_q4_k.hip:513-516: M % 64, N % 64, K % 256
+    # wmma_gemm_q4_k.hip:207-210: M % 64, N % 64, K % 256
     assert rf.wmma_gemm_q4_k_launch(P, P, P, m, n, k, NUL) == HIP_ERROR_INVALID_VALUE
     assert rf.wmma_gemm_q6_k_launch(P, P, P, m, n, k, NUL) == HIP_ERROR_INVALID_VALUE

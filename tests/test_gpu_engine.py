@@ -312,10 +312,14 @@ def test_qk_rows_rejections(rf, dev):
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     f = rf.rf_qk_norm_rope_kv_write_rows
     ok = (P(z), P(z), P(z), None, None, P(h), P(h), P(h))
-    assert f(*ok, 0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) == 0
+    assert f(*ok, 0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) == 0
     torch.cuda.synchronize()
-    assert f(*ok, 7, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0     # past max_seq
-    assert f(*ok, 0, 2, 3, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0     # more K rows than Q rows
-    assert f(*ok, 0, 2, 2, 2, 1, 96, 8, 1e-6, 1e4, 1, None, s) != 0      # head_dim
+    assert f(*ok, 7, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0     # past max_seq
+    assert f(*ok, 0, 2, 3, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0     # more K rows than Q rows
+    assert f(*ok, 0, 2, 2, 2, 1, 96, 8, 1e-6, 1e4, 1, None, None, s) != 0      # head_dim
     assert f(P(z), P(z), P(z), None, None, ctypes.c_void_p(h.data_ptr() + 2), P(h), P(h),
-             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, s) != 0          # q16 misaligned
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0          # q16 misaligned
+    assert f(P(z), P(z), P(z), None, None, P(h), ctypes.c_void_p(h.data_ptr() + 2), P(h),
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0    # K cache misaligned
+    assert f(P(z), P(z), P(z), None, None, P(h), P(h), ctypes.c_void_p(h.data_ptr() + 8),
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0    # V cache misaligned

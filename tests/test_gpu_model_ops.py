@@ -132,7 +132,8 @@ def test_kv_write_batched(rf, dev):
 
 @pytest.mark.parametrize("with_norm", [True, False])
 @pytest.mark.parametrize("neox", [1, 0])
-def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox):
+@pytest.mark.parametrize("table", [False, True])
+def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox, table):
     # the one-launch Qwen3 step against the oracle, and against the separate launchers
     nh, nkv, d, max_seq, pos = 32, 8, 128, 700, 641
     rng = np.random.default_rng(13 + neox)
@@ -144,8 +145,15 @@ def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox):
     dq, dk, dv, dqn, dkn = (G.to_dev(a) for a in (q, k, v, qn, kn))
     kc, vc = G.empty(max_seq * nkv * d, torch.int16), G.empty(max_seq * nkv * d, torch.int16)
     dpos = G.to_dev(np.array([pos, pos + 1], np.int32))
+    theta = None
+    if table:
+        theta = G.empty(d // 2, torch.float32)
+        G.call(rf.rf_rope_theta_table, G.ptr(theta), d, 1e6)
+        want = np.array([O.rope_theta(i, d, 1e6) for i in range(d // 2)], np.float32)
+        np.testing.assert_array_equal(G.host(theta), want)
     G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn) if with_norm else None,
-           G.ptr(dkn) if with_norm else None, G.ptr(kc), G.ptr(vc), G.ptr(dpos), nh, nkv, d, 1e-6, 1e6, neox, None)
+           G.ptr(dkn) if with_norm else None, G.ptr(kc), G.ptr(vc), G.ptr(dpos), nh, nkv, d, 1e-6, 1e6, neox, None,
+           G.ptr(theta) if table else None)
     qr = O.rms_norm(q, qn, 1e-6, nh) if with_norm else q.astype(np.float64)
     kr = O.rms_norm(k, kn, 1e-6, nkv) if with_norm else k.astype(np.float64)
     _close(G.host(dq), O.rope(qr, 1, nh, d, pos, 1e6, bool(neox)), "fused q")
@@ -188,6 +196,23 @@ def test_attn_decode(rf, dev, seq, nh, nkv, d):
     G.call(rf.gpu_flash_attn_decode_strided_multi_head_state, G.ptr(out2), G.ptr(dq), G.ptr(dkc), G.ptr(dvc),
            G.ptr(dlen), nh, nkv, d, scale)
     np.testing.assert_array_equal(G.host(out2), G.host(out))
+    # the split path in a caller workspace (positions over many workgroups)
+    wsb = int(rf.rf_flash_attn_decode_workspace_bytes(nh, d))
+    assert wsb == nh * 64 * (d + 4) * 4
+    # NaN-filled: splits without positions must not read their stale slots
+    ws = torch.full((wsb // 4,), float("nan"), dtype=torch.float32, device="cuda:0")
+    out3, out4 = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
+    G.call(rf.rf_flash_attn_decode_ws, G.ptr(out3), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), seq, nh, nkv, d, scale,
+           G.ptr(ws), wsb)
+    _close(G.host(out3), ref, f"split attn decode seq {seq} d {d}")
+    G.call(rf.rf_flash_attn_decode_state_ws, G.ptr(out4), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh, nkv, d,
+           scale, G.ptr(ws), wsb)
+    np.testing.assert_array_equal(G.host(out4), G.host(out3))
+    # a workspace below the size the query gives is rejected, and so is none
+    assert rf.rf_flash_attn_decode_ws(G.ptr(out3), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), seq, nh, nkv, d, scale,
+                                      G.ptr(ws), wsb - 4, G.stream()) != 0
+    assert rf.rf_flash_attn_decode_ws(G.ptr(out3), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), seq, nh, nkv, d, scale,
+                                      None, wsb, G.stream()) != 0
 
 
 @pytest.mark.parametrize("n", [1, 1000, 1024, 1025, 151936])
@@ -303,14 +328,16 @@ def test_attention_with_folded_qk_step(rf, dev, seq, nh, nkv, d):
     kc1, vc1, kc2, vc2 = (G.to_dev(cache) for _ in range(4))
     out1, out2 = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
     scale = 1.0 / math.sqrt(d)
+    wsb = int(rf.rf_flash_attn_decode_workspace_bytes(nh, d))
+    ws = G.empty(wsb // 4, torch.float32)
     G.call(rf.rf_attn_decode_qk_norm_rope_state, G.ptr(out1), G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn),
-           G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, scale)
+           G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, scale, G.ptr(ws), wsb)
     np.testing.assert_array_equal(G.host(dq), q)        # the raw q is left as it was
     G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(kc2),
-           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None)
+           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None)
     dlen = G.to_dev(np.array([seq], np.int32))
-    G.call(rf.gpu_flash_attn_decode_strided_multi_head_state, G.ptr(out2), G.ptr(dq), G.ptr(kc2), G.ptr(vc2),
-           G.ptr(dlen), nh, nkv, d, scale)
+    G.call(rf.rf_flash_attn_decode_state_ws, G.ptr(out2), G.ptr(dq), G.ptr(kc2), G.ptr(vc2), G.ptr(dlen), nh, nkv, d,
+           scale, G.ptr(ws), wsb)
     np.testing.assert_array_equal(G.host(out1), G.host(out2))
     np.testing.assert_array_equal(G.host(kc1), G.host(kc2))
     np.testing.assert_array_equal(G.host(vc1), G.host(vc2))
