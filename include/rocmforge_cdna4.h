@@ -357,6 +357,20 @@ hipError_t rf_flash_attn_decode_state_ws(float* d_out, const float* d_q, const u
                                          const int num_kv_heads, const int head_dim, const float scale,
                                          float* d_workspace, const size_t workspace_bytes, hipStream_t stream);
 
+/* No counterpart in the reference: rf_flash_attn_decode_state_ws for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a file-scope device
+ * array of 4,259,840 bytes held by each GPU the library runs on until the
+ * process ends (its address is looked up once per device); calls with
+ * num_heads * (head_dim + 4) > 16640 are rejected with hipErrorInvalidValue.
+ * The launcher calls no hipMalloc/hipFree.  All calls on one GPU share the
+ * array: calls that overlap on a GPU (other streams or threads) race;
+ * stream-ordered calls do not.  Same results as rf_flash_attn_decode_state_ws. */
+hipError_t rf_flash_attn_decode_state_noalloc(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                              const uint16_t* d_v_cache, const int* d_seq_len, const int num_heads,
+                                              const int num_kv_heads, const int head_dim, const float scale,
+                                              hipStream_t stream);
+
 /* No counterpart (the reference computes theta_i in each RoPE launch): fills
  * the caller's d_theta[head_dim / 2] with theta_i = 1 / base^((float)(2i) /
  * (float)head_dim) (double pow, rounded once), the values every RoPE here

@@ -63,6 +63,7 @@ SIGNATURES = {
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "rf_flash_attn_decode_ws": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp],
     "rf_flash_attn_decode_state_ws": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp],
+    "rf_flash_attn_decode_state_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "gpu_argmax_f32_on_stream": [_vp, _vp, _vp, _vp, _i, _vp],
     "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
     "rf_argmax_f32_advance_state_on_stream": [_vp, _vp, _vp, _vp, _i, _vp, _vp],

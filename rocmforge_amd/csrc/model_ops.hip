@@ -30,6 +30,8 @@
 // every lane.  No launcher allocates, frees or synchronises.
 #include <hip/hip_fp16.h>
 
+#include <mutex>
+
 
 #include "qk_common.h"
 
@@ -1142,6 +1144,55 @@ extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const floa
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
                        reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
                        scale, d_workspace, workspace_bytes, stream, &qk);
+}
+
+// ---- decode attention without any allocation ----
+// The split path's workspace as a file-scope device array: for callers that
+// cannot allocate (hipMalloc is not allowed under stream capture, in tight
+// serving loops or in harnesses that forbid it).  Each GPU holds its own copy
+// from the first call on that device until the process ends.  In host code
+// the array's name is only a stand-in: its device address is taken once per
+// device with hipGetSymbolAddress and that address is what the kernels get.
+// Every call on one GPU shares the array, so calls that overlap on a GPU
+// (other streams, other threads) race; stream-ordered calls do not.  Nothing
+// in it must start at zero: every split writes its partial (m, l) and the
+// merge reads the accumulators of non-empty splits only.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 * kMaxSplits * (256 + 4) * sizeof(float);   // 4,259,840
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+constexpr int kMaxDevices = 64;
+static float* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+static hipError_t scratch_ptr(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+extern "C" hipError_t rf_flash_attn_decode_state_noalloc(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                         const uint16_t* d_v_cache, const int* d_seq_len,
+                                                         const int num_heads, const int num_kv_heads,
+                                                         const int head_dim, const float scale, hipStream_t stream) {
+    if (d_seq_len == nullptr || num_heads <= 0 || head_dim <= 0) return hipErrorInvalidValue;
+    const size_t need = attn_ws_bytes(num_heads, head_dim);
+    if (need > kNoAllocScratchBytes) return hipErrorInvalidValue;    // beyond the array: num_heads * (head_dim + 4) > 16640
+    float* ws = nullptr;
+    const hipError_t e = scratch_ptr(&ws);
+    if (e != hipSuccess) return e;
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim,
+                       scale, ws, kNoAllocScratchBytes, stream);
 }
 
 // Caller-owned RoPE table: d_theta[i] = theta_i for i < head_dim / 2 (the
