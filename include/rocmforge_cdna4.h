@@ -101,6 +101,16 @@ hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, f
 hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N, int K,
                                  hipStream_t stream);
 
+/* No counterpart (the reference converts A with __float2half inside its
+ * GEMM, wmma_gemm_q4_k.hip:80-87): the Q4_K GEMM on fp16 activations, for a
+ * caller whose producing kernel already rounded A to fp16 (bit patterns as
+ * uint16_t, row-major [M][K]).  Same operand values as
+ * wmma_gemm_q4_k_launch(fp32 A), so the same products; A is read at half
+ * the bytes and not converted per tile.  M % 64 == 0, N % 128 == 0,
+ * K % 256 == 0, input and weights 16-byte aligned. */
+hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output, int M, int N,
+                                   int K, hipStream_t stream);
+
 /* No counterpart in the reference (its prefill issues one GEMM per weight
  * and adds residuals with gpu_add).  Several weight matrices that share the
  * input and K in one launch: out_i[M x n_i] = fp16(A) * fp16(dequant W_i)^T

@@ -174,6 +174,14 @@ def gemm(fmt: str, a: np.ndarray, w: np.ndarray, m: int, n: int, k: int) -> np.n
     return af @ wf.T
 
 
+def gemm_abs(fmt: str, a: np.ndarray, w: np.ndarray, m: int, n: int, k: int) -> np.ndarray:
+    """|fp16(A)| @ |fp16(dequant W)|^T: per output, the sum of the magnitudes
+    of the products it adds up -- the scale of its fp32 accumulation error."""
+    af = np.abs(round_f16(a).astype(np.float32).reshape(m, k))
+    wf = np.abs(dequant_f16(fmt, w, n, k))
+    return af.astype(np.float64) @ wf.T.astype(np.float64)
+
+
 # ---- CPU timing port ---------------------------------------------------------
 
 def cpu_gemv_q4k(w, x, n, k, threads):

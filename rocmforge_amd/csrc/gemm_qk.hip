@@ -44,6 +44,19 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// fp16 (round to nearest even) of two fp32 values as an instruction of its
+// own.  The reference rounds the fp32 dequant value with __float2half
+// (wmma_gemm_q4_k.hip:137): two roundings, exact value -> fp32 -> fp16.  Left
+// to itself the compiler merges an FMA and its fp16 conversion into one
+// v_fma_mix with an fp16 result, which rounds the exact value once; for Q4_K
+// (d sc q - dmin m) the two differ in about one weight in 10^7.  Q6_K values
+// d sc (q - 32) are exact in fp32, so there one rounding is the same.
+__device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+}
+
 constexpr int kGemmThreads = 256;
 constexpr int kKC = 64;               // K per LDS stage
 constexpr int kLdsStride = kKC + 8;   // halves per LDS row (16-byte pad against bank conflicts)
@@ -85,8 +98,9 @@ __device__ __forceinline__ void q4_stage_dequant(const Q4Stage& s, int c, f16x8 
         for (int b = 0; b < 4; ++b) {
             const uint32_t byte = (w[t] >> (8 * b)) & 0xFFu;
             const int i = 4 * t + b;
-            out0[i >> 3][i & 7] = (_Float16)(ds0 * (float)(byte & 15u) - dm0);
-            out1[i >> 3][i & 7] = (_Float16)(ds1 * (float)(byte >> 4) - dm1);
+            const uint32_t h = cvt_pk_f16(ds0 * (float)(byte & 15u) - dm0, ds1 * (float)(byte >> 4) - dm1);
+            out0[i >> 3][i & 7] = __builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+            out1[i >> 3][i & 7] = __builtin_bit_cast(_Float16, (unsigned short)(h >> 16));
         }
     }
 }
@@ -328,6 +342,13 @@ __device__ __forceinline__ void put4(f16x8& dst, int half, float a, float b, flo
     dst[4 * half + 2] = (_Float16)c;
     dst[4 * half + 3] = (_Float16)d;
 }
+// the same with the fp32 values rounded as the reference rounds them (Q4_K)
+__device__ __forceinline__ void put4_rn(f16x8& dst, int half, float a, float b, float c, float d) {
+    u32x4 v = __builtin_bit_cast(u32x4, dst);
+    v[2 * half] = cvt_pk_f16(a, b);
+    v[2 * half + 1] = cvt_pk_f16(c, d);
+    dst = __builtin_bit_cast(f16x8, v);
+}
 __device__ __forceinline__ float byte_f(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFFu); }
 
 // Q4_K: B operands of one column for the wave's two k16 steps.  Nibbles are
@@ -359,8 +380,8 @@ struct Q4Ops {
         const uint32_t w[4] = {r.q.x & mask, r.q.y & mask, r.q.z & mask, r.q.w & mask};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            put4(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
-                 ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
+            put4_rn(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
+                    ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
     }
     template <int CQ>
     static __device__ __forceinline__ void dequant(const Hdr& hd, const Qs& r, int h, int kh, f16x8 (&b)[2]) {
@@ -373,8 +394,8 @@ struct Q4Ops {
         const uint32_t w[4] = {r.q.x & mask, r.q.y & mask, r.q.z & mask, r.q.w & mask};
 #pragma unroll
         for (int j = 0; j < 4; ++j)   // word j = bytes 4j..4j+3: step j>>1, slots 4*(j&1) + [0,4)
-            put4(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
-                 ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
+            put4_rn(b[j >> 1], j & 1, ds * byte_f(w[j], 0) - dm, ds * byte_f(w[j], 1) - dm,
+                    ds * byte_f(w[j], 2) - dm, ds * byte_f(w[j], 3) - dm);
     }
 };
 
@@ -879,8 +900,12 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
         // instead of one v_cvt_f32_ubyteN
         asm("" : "+v"(q));
         const float a = pa[r][kh], b = pb[r][kh];
-        put4(bq[buf][kh][r][j >> 1], j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b,
-             a * byte_f(q, 3) - b);
+        if constexpr (IS_Q6)
+            put4(bq[buf][kh][r][j >> 1], j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b,
+                 a * byte_f(q, 3) - b);
+        else
+            put4_rn(bq[buf][kh][r][j >> 1], j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b,
+                    a * byte_f(q, 3) - b);
     };
     auto w_dequant_all = [&](auto jj, int buf) {
 #pragma unroll
@@ -1254,7 +1279,11 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
         // opaque to the optimiser: otherwise it folds the mask into per-byte
         // bit-field extracts instead of one v_cvt_f32_ubyteN per weight
         asm("" : "+v"(q));
-        put4(wout, j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b, a * byte_f(q, 3) - b);
+        if constexpr (IS_Q6)
+            put4(wout, j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b, a * byte_f(q, 3) - b);
+        else
+            put4_rn(wout, j & 1, a * byte_f(q, 0) - b, a * byte_f(q, 1) - b, a * byte_f(q, 2) - b,
+                    a * byte_f(q, 3) - b);
         if (p & 1)
             *reinterpret_cast<f16x8*>(&lds_b[buf][wrow * kLdsStride + 32 * kh + 8 * (j >> 1)]) = wout;
     };
@@ -1357,6 +1386,315 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
         }
 }
 
+// ── tall: 256 x 128 tiles, K halves split over wave pairs ────────────────
+// Workgroup = 256 threads over a 256 (M) x 128 (N) tile.  Wave w owns the
+// 64 output columns [n0 + 64 (w >> 1), +64) for all 256 rows, over the K
+// half kh = w & 1 of every 64-wide chunk; the two halves are added through
+// LDS at the end.  Each wave thus issues 32 MFMAs per chunk against 16
+// dequantised weights per lane, so every weight is dequantised once per 256
+// rows of A (v7: once per 128) and its accumulators fill the 256 AGPRs.
+//
+// K order.  Chunk c of a Q4_K row = super-block c / 4, nibble pair p = c % 4:
+// qs byte i of [32p, 32p + 32) holds chunk elements i (low nibble) and
+// 32 + i (high nibble).  Wave half kh, lane half h take the bytes
+// [16 kh + 8 h, +8): k16 step 0 is their 8 low nibbles (k = 16 kh + 8 h + j),
+// step 1 their 8 high nibbles (k = 32 + 16 kh + 8 h + j).  Within each group
+// of 4 consecutive k, A is stored in LDS in the order (0, 2, 1, 3), so that
+// a weight word w (bytes j..j+3) gives the B operand registers directly:
+// (w & 0x000F000F) holds bytes (j, j+2) and ((w >> 8) & 0x000F000F) bytes
+// (j+1, j+3) -- the same permutation of the MFMA k slots on both sides.
+//
+// Dequantisation.  A 16-bit half 0x000q is the fp16 subnormal q * 2^-24 and
+// 0x00q0 is q * 2^-20, both exact; v_fma_mix takes such a half as its fp16
+// source, so the fp32 value D q - M = fma(half, D * 2^24, -M) (or D * 2^20
+// for the high nibbles; D q is exact): one masking operation per two
+// weights, one fma_mix per weight and one v_cvt_pk_f16_f32 per two, the
+// reference's rounding of the fp32 value (D = d * sc, M = dmin * m).
+constexpr int kTallThreads = 256;
+constexpr int kTallBM = 256, kTallBN = 128;
+constexpr int kTallStage = kTallBN * kQ4KBytes;      // one super-block of the tile's 128 rows (18 KB)
+constexpr int kTallGroups = kTallStage / 1024;      // 16-byte lane loads: 18 groups of 64 per stage
+constexpr int kTallNI = (kTallGroups + 3) / 4;      // per wave (the last wave repeats groups 0, 1)
+constexpr int kTallABufs = 3;
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// two weights from one register of masked nibbles (fp16 subnormals): fp32
+// values through v_fma_mix (fp16 source), then one rounding pair to fp16
+__device__ __forceinline__ uint32_t tall_dq2(uint32_t r, float D, float nM) {
+    const f16x2 q = __builtin_bit_cast(f16x2, r);
+    return cvt_pk_f16(__builtin_fmaf((float)q[0], D, nM), __builtin_fmaf((float)q[1], D, nM));
+}
+
+// A16: A is fp16 (the caller rounded it: the same operand values), read
+// 16 bytes a lane and stored to LDS in natural k order; the B operands then
+// take their byte pairs in natural order through v_perm.
+template <bool A16>
+__global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const void* __restrict__ Av,
+                                                                         const uint8_t* __restrict__ W,
+                                                                         float* __restrict__ D, int M, int N, int K,
+                                                                         int accum) {
+    // one LDS block: the weight ring, then three A buffers; after the loop
+    // the first 128 KB carry the K-half exchange
+    __shared__ __align__(16) uint8_t lds[2 * kTallStage + kTallABufs * kTallBM * kLdsStride * 2];
+    uint8_t* ring = lds;
+    _Float16* abuf0 = reinterpret_cast<_Float16*>(lds + 2 * kTallStage);
+    constexpr int kABufHalves = kTallBM * kLdsStride;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wave & 1, wn = wave >> 1;
+    const int h = lane >> 5, col = lane & 31;
+    const int mtiles = (M + kTallBM - 1) / kTallBM;
+    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int m0 = (v % mtiles) * kTallBM;      // the M tiles of one column tile are neighbours
+    const int n0 = (v / mtiles) * kTallBN;
+    const int nchunks = K / kKC;
+    const int nsb = K / kQK;
+    const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+
+    // ---- weight ring: stage = super-block sb of the tile's 128 rows ------
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W + (size_t)n0 * row_bytes);
+    uint32_t goff[kTallNI], gdst[kTallNI];
+#pragma unroll
+    for (int t = 0; t < kTallNI; ++t) {
+        const int g = (wave * kTallNI + t) % kTallGroups;
+        const int pc = 64 * g + lane;                 // 16-byte piece of the stage
+        gdst[t] = 16u * (uint32_t)pc;
+        goff[t] = (uint32_t)(pc / 9) * row_bytes + 16u * (uint32_t)(pc % 9);
+    }
+    u32x4 wst[kTallNI];
+    auto w_gload1 = [&](int t, int sb) {
+#ifdef RF_ABL_NORING
+        if (sb > 0) return;
+#endif
+        wst[t] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, goff[t], (uint32_t)min(sb, nsb - 1) * kQ4KBytes, 0);
+    };
+    auto w_lstore1 = [&](int t, int slot) {
+        *reinterpret_cast<u32x4*>(ring + slot * kTallStage + gdst[t]) = wst[t];
+    };
+
+    // ---- A chunk to LDS.  fp32: 16 float4 per thread, rounded to fp16 and
+    // stored in k order (0 2 1 3) per group of 4; fp16: 8 x 16 bytes per
+    // thread, natural order.  kANI loads per thread per chunk.
+    constexpr int kANI = A16 ? 8 : 16;
+    constexpr int kARowsPerPass = A16 ? 32 : 16;
+    const int a_row = A16 ? (tid >> 3) : (tid >> 4);
+    const int a_col = A16 ? 8 * (tid & 7) : 4 * (tid & 15);
+    constexpr uint32_t kAElt = A16 ? 2u : 4u;
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(static_cast<const uint8_t*>(Av) + (size_t)m0 * K * kAElt);
+    // fp16 A may end inside the tile (M % 256 != 0): rows past M read row M - 1
+    uint32_t a_voff[A16 ? kANI : 1];
+#pragma unroll
+    for (int i = 0; i < (A16 ? kANI : 1); ++i) {
+        const int r = A16 ? min(a_row + kARowsPerPass * i, M - 1 - m0) : a_row;
+        a_voff[i] = (uint32_t)(r * K + a_col) * kAElt;
+    }
+    u32x4 areg[kANI];
+    auto a_load1 = [&](int i, int c) {
+#ifdef RF_ABL_NOA
+        if (c > 2) return;
+#endif
+        const uint32_t so = ((uint32_t)min(c, nchunks - 1) * kKC + (A16 ? 0u : (uint32_t)(kARowsPerPass * i * K))) *
+                            kAElt;
+        areg[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff[A16 ? i : 0], so, 0);
+    };
+    auto a_store1 = [&](int i, int buf) {
+#ifdef RF_ABL_NOAST
+        return;
+#endif
+        _Float16* dst = abuf0 + buf * kABufHalves + (a_row + kARowsPerPass * i) * kLdsStride + a_col;
+        if constexpr (A16) {
+            *reinterpret_cast<u32x4*>(dst) = areg[i];
+        } else {
+            const float4 f = __builtin_bit_cast(float4, areg[i]);
+            f16x4 hv;
+            hv[0] = (_Float16)f.x; hv[1] = (_Float16)f.z;
+            hv[2] = (_Float16)f.y; hv[3] = (_Float16)f.w;
+            *reinterpret_cast<f16x4*>(dst) = hv;
+        }
+    };
+
+    // ---- B: the lane's two weight rows (columns), 8 qs bytes each per chunk
+    const int brow0 = 64 * wn + col;                  // rows brow0 and brow0 + 32 of the tile
+    u32x4 bhdr[2];
+    u32x2 bqs[2];
+    auto b_read = [&](auto cq, int slot) {
+        constexpr int p = decltype(cq)::value;
+        const uint8_t* st = ring + slot * kTallStage;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint8_t* rb = st + (brow0 + 32 * j) * kQ4KBytes;
+            bhdr[j] = *reinterpret_cast<const u32x4*>(rb);
+            bqs[j] = *reinterpret_cast<const u32x2*>(rb + 16 + 32 * p + 16 * kh + 8 * h);
+        }
+    };
+    // bq[buffer][step][col block] = the 8 fp16 weights of one MFMA B operand
+    u32x4 bq[2][2][2];
+    float sD[2][2], sM[2][2];                         // [col block][step]: D * 2^24 (2^20), -M
+    auto b_prep = [&](auto cq, int j) {
+        constexpr int p = decltype(cq)::value;
+        int sc0, mn0, sc1, mn1;
+        q4k_scale_min_pair(bhdr[j].y, bhdr[j].z, bhdr[j].w, p, &sc0, &mn0, &sc1, &mn1);
+        const float d = half_bits_to_float(bhdr[j].x), dmin = half_bits_to_float(bhdr[j].x >> 16);
+        sD[j][0] = d * (float)sc0 * 16777216.0f;
+        sM[j][0] = -(dmin * (float)mn0);
+        sD[j][1] = d * (float)sc1 * 1048576.0f;
+        sM[j][1] = -(dmin * (float)mn1);
+    };
+    // piece q (0..3) of column block j: word q >> 1 of the 8 qs bytes, low
+    // (q even) or shifted (q odd) byte pairs, both steps
+    auto b_piece = [&](int buf, int j, int q) {
+#ifdef RF_ABL_NODQ
+        return;
+#endif
+        uint32_t w = (q >> 1) ? bqs[j].y : bqs[j].x;
+        if constexpr (A16)   // bytes (2q', 2q' + 1) of the word into the two halves: natural k order
+            w = __builtin_amdgcn_perm(0u, w, (q & 1) ? 0x0C030C02u : 0x0C010C00u);
+        else if (q & 1)      // bytes (1, 3): k order 0 2 1 3
+            w >>= 8;
+        bq[buf][0][j][q] = tall_dq2(w & 0x000F000Fu, sD[j][0], sM[j][0]);
+        bq[buf][1][j][q] = tall_dq2(w & 0x00F000F0u, sD[j][1], sM[j][1]);
+    };
+
+    f32x16 acc[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int fa = col * kLdsStride + 16 * kh + 8 * h;   // + 32 step + 32 i rows
+    f16x8 af[2][8];
+    auto frag_ld = [&](int set, int buf, int s, int i) {
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kABufHalves + fa + 32 * i * kLdsStride + 32 * s);
+    };
+
+    // ---- prologue: ring stage 0, A chunks 0 and 1, A regs = chunk 2 ------
+#pragma unroll
+    for (int t = 0; t < kTallNI; ++t) w_gload1(t, 0);
+#pragma unroll
+    for (int t = 0; t < kTallNI; ++t) w_lstore1(t, 0);
+#pragma unroll
+    for (int i = 0; i < kANI; ++i) a_load1(i, 0);
+#pragma unroll
+    for (int i = 0; i < kANI; ++i) {
+        a_store1(i, 0);
+        a_load1(i, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < kANI; ++i) {
+        a_store1(i, 1);
+        a_load1(i, 2);
+    }
+    lds_barrier();
+    b_read(std::integral_constant<int, 0>{}, 0);
+    b_prep(std::integral_constant<int, 0>{}, 0);
+    b_prep(std::integral_constant<int, 0>{}, 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b_piece(0, j, q);
+    b_read(std::integral_constant<int, 1>{}, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) frag_ld(0, 0, 0, i);
+
+    // Chunk c = 4 sb + CQ, A buffer c % 3, ring slot sb % 2.  32 slots, one
+    // MFMA each (slot t = 16 step + 2 i + j), separated by scheduling fences,
+    // each followed by a slice of the side work: the B operands of chunk
+    // c + 1 (raw bytes read at the end of chunk c - 1), the A fragments of the
+    // next step (for step 1: chunk c + 1's first step, from a buffer stored
+    // two chunks ago), A chunk c + 2 to LDS and chunk c + 3 into registers,
+    // the ring (loads of super-block sb + 1 in CQ 0, stored in CQ 2).
+    auto iteration = [&](auto cqc, int sb, int ab) {
+        constexpr int CQ = decltype(cqc)::value;
+        constexpr int P = CQ & 1;                           // bq buffer of this chunk
+        using NEXT = std::integral_constant<int, (CQ + 1) & 3>;
+        using NEXT2 = std::integral_constant<int, (CQ + 2) & 3>;
+        const int c = 4 * sb + CQ;
+        const int slot = sb & 1;
+        const int abn = ab == 2 ? 0 : ab + 1;               // chunk c + 1
+        const int abs2 = abn == 2 ? 0 : abn + 1;            // chunk c + 2
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const f16x8 b0 = __builtin_bit_cast(f16x8, bq[P][s][0]);
+            const f16x8 b1 = __builtin_bit_cast(f16x8, bq[P][s][1]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int t = 16 * s + 2 * i + j;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][i], j ? b1 : b0, acc[i][j], 0, 0, 0);
+                    // next step's fragments: step 1 of this chunk, then step 0 of chunk c + 1
+                    if (j == 0) frag_ld(s ^ 1, s ? abn : ab, s ^ 1, i);
+                    // B operands of chunk c + 1 (its raw bytes were read one chunk ago)
+                    if (t == 2) b_prep(NEXT{}, 0);
+                    if (t >= 3 && t < 7) b_piece(P ^ 1, 0, t - 3);
+                    if (t == 7) b_prep(NEXT{}, 1);
+                    if (t >= 8 && t < 12) b_piece(P ^ 1, 1, t - 8);
+                    // raw bytes of chunk c + 2 (not across the super-block boundary:
+                    // the next stage is stored in CQ 2, read after its barrier)
+                    if (t == 12 && CQ < 2) b_read(NEXT2{}, slot);
+                    if (t == 12 && CQ == 3) b_read(NEXT2{}, slot ^ 1);
+                    // A chunk c + 2 to LDS, registers reloaded with chunk c + 3
+                    if (t >= 14 && t < 14 + kANI) {
+                        a_store1(t - 14, abs2);
+                        a_load1(t - 14, c + 3);
+                    }
+                    if constexpr (CQ == 0) {
+                        if (t >= 24 && t < 24 + kTallNI) w_gload1(t - 24, sb + 1);
+                    }
+                    if constexpr (CQ == 2) {
+                        if (t >= 24 && t < 24 + kTallNI) w_lstore1(t - 24, slot ^ 1);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
+        lds_barrier();
+        // CQ 2: chunk c + 2 is the next super-block's first, stored just now
+        if constexpr (CQ == 2) b_read(NEXT2{}, slot ^ 1);
+    };
+    int ab = 0;                                     // (4 sb) % 3
+    for (int sb = 0; sb < nsb; ++sb) {
+        iteration(std::integral_constant<int, 0>{}, sb, ab);
+        iteration(std::integral_constant<int, 1>{}, sb, ab == 2 ? 0 : ab + 1);
+        iteration(std::integral_constant<int, 2>{}, sb, ab == 0 ? 2 : ab - 1);
+        iteration(std::integral_constant<int, 3>{}, sb, ab);
+        ab = ab == 2 ? 0 : ab + 1;
+    }
+
+    // ---- K halves: wave kh = 1 hands row blocks 0-3 to kh = 0, kh = 0 hands
+    // row blocks 4-7 to kh = 1; each then adds and stores its four blocks ----
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(lds);          // 4 waves x 4 blocks x 2 x 16 x 64 floats = 128 KB
+    const int give = kh ? 0 : 4, keep = kh ? 4 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xch[(((wave * 4 + i) * 2 + j) * 16 + e) * 64 + lane] = acc[give + i][j][e];
+    __syncthreads();
+    const int partner = wave ^ 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ncol = n0 + 64 * wn + 32 * j + col;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float o = xch[(((partner * 4 + i) * 2 + j) * 16 + e) * 64 + lane];
+                // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
+                const float s = kh ? o + acc[keep + i][j][e] : acc[keep + i][j][e] + o;
+                const int row = m0 + 32 * (keep + i) + 8 * (e >> 2) + 4 * h + (e & 3);
+                float* dst = D + (size_t)row * N + ncol;
+                if (A16 && row >= M) continue;
+                *dst = accum ? *dst + s : s;
+            }
+        }
+}
+
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
 // 8-chunk groups) and tiles * S <= CUs (one workgroup per CU; the kernel
 // runs one 512-thread workgroup per CU).  Measured on MI355X at the
@@ -1433,6 +1771,14 @@ static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, 
                        accum);
 }
 
+// 256 x 128 tiles where they come to one round of about a workgroup per CU
+// (Q4_K, M % 256 == 0, N % 128 == 0)
+static bool tall_fits(int M, int N, int K) {
+    if (M % kTallBM || N % kTallBN || K % kQK) return false;
+    const long tiles = (long)(M / kTallBM) * (N / kTallBN), cus = device_cu_count();
+    return 8 * tiles >= 7 * cus && tiles <= cus;
+}
+
 // sg routes column segments / accumulation (v7 and sq only: the callers of
 // a non-trivial sg have checked N % 256 == 0, K % 512 == 0 and, for Q6_K,
 // K % 2048 == 0, and segments never reach sq)
@@ -1450,7 +1796,10 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long sq_tiles = (long)(M / 256) * (N / 256);
         const long sq128_tiles = (long)(M / 128) * (N / 128);
         const bool sq_ok = sg.n1 == N && sg.n2 == N && !sg.pair;
-        if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
+        if (!IS_Q6 && sq_ok && tall_fits(M, N, K))
+            hipLaunchKernelGGL(rf_gemm_q4k_tall_kernel<false>, dim3((M / kTallBM) * (N / kTallBN)), dim3(kTallThreads), 0, st,
+                               A, w, D, M, N, K, sg.accum);
+        else if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
             launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
             launch_sq<IS_Q6, 128, 128>(A, w, D, M, N, K, st, sg.accum);
@@ -1490,6 +1839,23 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
     if ((reinterpret_cast<uintptr_t>(input) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
         return hipErrorInvalidValue;
     return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
+}
+
+// fp16 activations (the caller's rounding of A, e.g. in the kernel that
+// produced them): the same operand values as wmma_gemm_q4_k_launch on fp32
+// A, read at half the bytes and without the per-tile conversion.  M % 64,
+// N % 128, K % 256; M need not fill the 256-row tiles.
+extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output,
+                                              int M, int N, int K, hipStream_t stream) {
+    if (input_f16 == nullptr || weights_q4_k == nullptr || output == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kTallBN) != 0 || (K % kQK) != 0)
+        return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
+        return hipErrorInvalidValue;
+    const int tiles = ((M + kTallBM - 1) / kTallBM) * (N / kTallBN);
+    hipLaunchKernelGGL(rf_gemm_q4k_tall_kernel<true>, dim3(tiles), dim3(kTallThreads), 0, stream, input_f16,
+                       static_cast<const uint8_t*>(weights_q4_k), output, M, N, K, 0);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,

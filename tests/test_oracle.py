@@ -304,11 +304,16 @@ def test_gemm_operands_are_fp16_rounded():
     d = O.gemm("q4_k", a, w, m, n, k)
     want = a.astype(np.float16).astype(np.float64) @ ref.astype(np.float64).T
     np.testing.assert_allclose(d, want, rtol=1e-12, atol=1e-12)
+    # the accumulation scale of the GEMM tolerance: sum of |products|
+    s_abs = O.gemm_abs("q4_k", a, w, m, n, k)
+    want_abs = np.abs(a.astype(np.float16).astype(np.float64)) @ np.abs(ref.astype(np.float64)).T
+    np.testing.assert_allclose(s_abs, want_abs, rtol=1e-12, atol=1e-12)
+    assert (s_abs >= np.abs(d) - 1e-9).all()
 
 
 # ---- CPU timing port ----------------------------------------------------------
 # Its arithmetic is the reference's AVX2 path (src/cpu/kernels/gemm_q4k_q8.rs:
-# 89-181), including two quirks of that port of llama.cpp: the min term keeps
+# 90-195), including two quirks of that port of llama.cpp: the min term keeps
 # only SIMD lane 0 of acc_m (sub-blocks 0 and 1), and acc_m starts at dmin
 # instead of 0.  The model below restates exactly that arithmetic in numpy.
 
