@@ -1398,31 +1398,41 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
 // qs byte i of [32p, 32p + 32) holds chunk elements i (low nibble) and
 // 32 + i (high nibble).  Wave half kh, lane half h take the bytes
 // [16 kh + 8 h, +8): k16 step 0 is their 8 low nibbles (k = 16 kh + 8 h + j),
-// step 1 their 8 high nibbles (k = 32 + 16 kh + 8 h + j).  Within each group
-// of 4 consecutive k, A is stored in LDS in the order (0, 2, 1, 3), so that
-// a weight word w (bytes j..j+3) gives the B operand registers directly:
-// (w & 0x000F000F) holds bytes (j, j+2) and ((w >> 8) & 0x000F000F) bytes
-// (j+1, j+3) -- the same permutation of the MFMA k slots on both sides.
+// step 1 their 8 high nibbles (k = 32 + 16 kh + 8 h + j).
 //
 // Dequantisation.  A 16-bit half 0x000q is the fp16 subnormal q * 2^-24 and
 // 0x00q0 is q * 2^-20, both exact; v_fma_mix takes such a half as its fp16
 // source, so the fp32 value D q - M = fma(half, D * 2^24, -M) (or D * 2^20
-// for the high nibbles; D q is exact): one masking operation per two
-// weights, one fma_mix per weight and one v_cvt_pk_f16_f32 per two, the
-// reference's rounding of the fp32 value (D = d * sc, M = dmin * m).
+// for the high nibbles; D q is exact): per word of 4 bytes one shift and
+// four masks for its 8 weights, one fma_mix per weight and one
+// v_cvt_pk_f16_f32 per two, the reference's rounding of the fp32 value
+// (D = d * sc, M = dmin * m).
 constexpr int kTallThreads = 256;
 constexpr int kTallBM = 256, kTallBN = 128;
 constexpr int kTallStage = kTallBN * kQ4KBytes;      // one super-block of the tile's 128 rows (18 KB)
 constexpr int kTallGroups = kTallStage / 1024;      // 16-byte lane loads: 18 groups of 64 per stage
 constexpr int kTallNI = (kTallGroups + 3) / 4;      // per wave (the last wave repeats groups 0, 1)
 constexpr int kTallABufs = 3;
+// fp16 path: per super-block, a table of the tile rows' sub-block scale terms
+// (D * 2^24 or D * 2^20, -M) built once by the workgroup; 80-byte rows (8
+// float pairs + pad) put 16 consecutive rows on different bank groups
+constexpr int kTabRow = 80;
+constexpr int kTabBytes = kTallBN * kTabRow;
+constexpr int kTallLds32 = 2 * kTallStage + kTallABufs * kTallBM * kLdsStride * 2;
+constexpr int kTallLds16 = 2 * kTallStage + kTallABufs * kTallBM * kKC * 2 + 2 * kTabBytes;
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-// two weights from one register of masked nibbles (fp16 subnormals): fp32
-// values through v_fma_mix (fp16 source), then one rounding pair to fp16
-__device__ __forceinline__ uint32_t tall_dq2(uint32_t r, float D, float nM) {
-    const f16x2 q = __builtin_bit_cast(f16x2, r);
-    return cvt_pk_f16(__builtin_fmaf((float)q[0], D, nM), __builtin_fmaf((float)q[1], D, nM));
+// The four weights of the bytes b0..b3 of w under nibble mask m (low
+// 0x000F000F, high 0x00F000F0), in k order: (w & m) holds (b0, b2) and
+// ((w >> 8) & m) holds (b1, b3) as fp16 subnormals; each goes through
+// v_fma_mix (fp16 source, fp32 value) and the pairs (b0, b1), (b2, b3) are
+// rounded to fp16 together.
+__device__ __forceinline__ uint2 tall_dq4(uint32_t w, uint32_t m, float D, float nM) {
+    const f16x2 e = __builtin_bit_cast(f16x2, w & m);
+    const f16x2 o = __builtin_bit_cast(f16x2, (w >> 8) & m);
+    const float v0 = __builtin_fmaf((float)e[0], D, nM), v2 = __builtin_fmaf((float)e[1], D, nM);
+    const float v1 = __builtin_fmaf((float)o[0], D, nM), v3 = __builtin_fmaf((float)o[1], D, nM);
+    return make_uint2(cvt_pk_f16(v0, v1), cvt_pk_f16(v2, v3));
 }
 
 // A16: A is fp16 (the caller rounded it: the same operand values), read
@@ -1435,10 +1445,16 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
                                                                          int accum) {
     // one LDS block: the weight ring, then three A buffers; after the loop
     // the first 128 KB carry the K-half exchange
-    __shared__ __align__(16) uint8_t lds[2 * kTallStage + kTallABufs * kTallBM * kLdsStride * 2];
+    __shared__ __align__(16) uint8_t lds[A16 ? kTallLds16 : kTallLds32];
     uint8_t* ring = lds;
     _Float16* abuf0 = reinterpret_cast<_Float16*>(lds + 2 * kTallStage);
-    constexpr int kABufHalves = kTallBM * kLdsStride;
+    // fp32 A: rows of kLdsStride halves; fp16 A: rows of 64 halves (128 B)
+    // whose 16-byte pieces are XOR-swizzled by the row (position p of row r
+    // holds k piece p ^ g(r), g(r) = (r & 7) ^ ((r >> 3) & 1): 16 consecutive
+    // rows then fall on 16 different 16-byte bank groups), written by LDS DMA
+    constexpr int kARowHalves = A16 ? kKC : kLdsStride;
+    constexpr int kABufHalves = kTallBM * kARowHalves;
+    uint8_t* tab0 = lds + 2 * kTallStage + kTallABufs * kABufHalves * 2;   // fp16 path only
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1465,96 +1481,137 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
     }
     u32x4 wst[kTallNI];
     auto w_gload1 = [&](int t, int sb) {
-#ifdef RF_ABL_NORING
-        if (sb > 0) return;
-#endif
         wst[t] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, goff[t], (uint32_t)min(sb, nsb - 1) * kQ4KBytes, 0);
     };
     auto w_lstore1 = [&](int t, int slot) {
         *reinterpret_cast<u32x4*>(ring + slot * kTallStage + gdst[t]) = wst[t];
     };
+    // fp16 path: the same pieces by LDS DMA straight into the ring slot
+    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
+    auto w_dma1 = [&](int t, int sb, int slot) {
+        const uint8_t* src = w_tile + (size_t)min(sb, nsb - 1) * kQ4KBytes;
+        const uint32_t dst = ring_lds0 + (uint32_t)slot * kTallStage + gdst[t] - 16u * (uint32_t)lane;
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                     :: "s"(__builtin_amdgcn_readfirstlane(dst)), "v"(goff[t]), "s"(src) : "memory", "m0");
+    };
 
-    // ---- A chunk to LDS.  fp32: 16 float4 per thread, rounded to fp16 and
-    // stored in k order (0 2 1 3) per group of 4; fp16: 8 x 16 bytes per
-    // thread, natural order.  kANI loads per thread per chunk.
+    // ---- A chunk to LDS.  fp32: 16 float4 per thread through registers,
+    // rounded to fp16.  fp16:
+    // LDS DMA, 8 x 1 KB per wave (rows 8 g .. 8 g + 7 of the chunk), no
+    // registers; the kernel waits for it itself (s_waitcnt vmcnt before the
+    // per-chunk barrier) and keeps the compiler unaware of it.
     constexpr int kANI = A16 ? 8 : 16;
-    constexpr int kARowsPerPass = A16 ? 32 : 16;
-    const int a_row = A16 ? (tid >> 3) : (tid >> 4);
-    const int a_col = A16 ? 8 * (tid & 7) : 4 * (tid & 15);
-    constexpr uint32_t kAElt = A16 ? 2u : 4u;
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(static_cast<const uint8_t*>(Av) + (size_t)m0 * K * kAElt);
-    // fp16 A may end inside the tile (M % 256 != 0): rows past M read row M - 1
-    uint32_t a_voff[A16 ? kANI : 1];
+    const int a_row = tid >> 4, a_col = 4 * (tid & 15);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(static_cast<const float*>(Av) + (A16 ? 0 : (size_t)m0 * K));
+    const uint32_t a_voff = (uint32_t)(a_row * K + a_col) * 4u;
+    u32x4 areg[A16 ? 1 : kANI];
+    // fp16: lane L of wave instruction g (rows 8 (4 g' + wave)...) -- global
+    // instruction gi = 8 wave + g covers LDS rows 8 gi + L / 8, piece L % 8
+    uint32_t dma_voff[A16 ? kANI : 1];
+    const uint8_t* a16_base = static_cast<const uint8_t*>(Av) + (size_t)m0 * K * 2;
+    const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
+    if constexpr (A16) {
 #pragma unroll
-    for (int i = 0; i < (A16 ? kANI : 1); ++i) {
-        const int r = A16 ? min(a_row + kARowsPerPass * i, M - 1 - m0) : a_row;
-        a_voff[i] = (uint32_t)(r * K + a_col) * kAElt;
+        for (int g = 0; g < kANI; ++g) {
+            const int r = 8 * (8 * wave + g) + (lane >> 3);
+            const int rc = min(r, M - 1 - m0);          // fp16 A may end inside the tile
+            dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
+        }
     }
-    u32x4 areg[kANI];
     auto a_load1 = [&](int i, int c) {
-#ifdef RF_ABL_NOA
-        if (c > 2) return;
-#endif
-        const uint32_t so = ((uint32_t)min(c, nchunks - 1) * kKC + (A16 ? 0u : (uint32_t)(kARowsPerPass * i * K))) *
-                            kAElt;
-        areg[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff[A16 ? i : 0], so, 0);
+        if constexpr (!A16) {
+            const uint32_t so = ((uint32_t)min(c, nchunks - 1) * kKC + (uint32_t)(16 * i * K)) * 4u;
+            areg[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, so, 0);
+        }
+    };
+    // fp16: the DMA of instruction g of chunk c into buffer buf
+    auto a_dma1 = [&](int g, int c, int buf) {
+        const uint8_t* src = a16_base + (size_t)min(c, nchunks - 1) * kKC * 2;
+        const uint32_t dst = a_lds0 + (uint32_t)(buf * kABufHalves * 2 + (8 * wave + g) * 1024);
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                     :: "s"(dst), "v"(dma_voff[g]), "s"(src) : "memory", "m0");
     };
     auto a_store1 = [&](int i, int buf) {
-#ifdef RF_ABL_NOAST
-        return;
-#endif
-        _Float16* dst = abuf0 + buf * kABufHalves + (a_row + kARowsPerPass * i) * kLdsStride + a_col;
-        if constexpr (A16) {
-            *reinterpret_cast<u32x4*>(dst) = areg[i];
-        } else {
+        if constexpr (!A16) {
+            _Float16* dst = abuf0 + buf * kABufHalves + (a_row + 16 * i) * kARowHalves + a_col;
             const float4 f = __builtin_bit_cast(float4, areg[i]);
             f16x4 hv;
-            hv[0] = (_Float16)f.x; hv[1] = (_Float16)f.z;
-            hv[2] = (_Float16)f.y; hv[3] = (_Float16)f.w;
+            hv[0] = (_Float16)f.x; hv[1] = (_Float16)f.y;
+            hv[2] = (_Float16)f.z; hv[3] = (_Float16)f.w;
             *reinterpret_cast<f16x4*>(dst) = hv;
         }
     };
 
     // ---- B: the lane's two weight rows (columns), 8 qs bytes each per chunk
     const int brow0 = 64 * wn + col;                  // rows brow0 and brow0 + 32 of the tile
-    u32x4 bhdr[2];
-    u32x2 bqs[2];
-    auto b_read = [&](auto cq, int slot) {
+    // raw bytes double buffered by chunk parity R: chunk c + 1 is dequantised
+    // while chunk c + 2's bytes arrive
+    u32x4 bhdr[2][2];
+    u32x2 bqs[2][2];
+    auto b_read = [&](auto cq, int slot, int R) {
         constexpr int p = decltype(cq)::value;
         const uint8_t* st = ring + slot * kTallStage;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const uint8_t* rb = st + (brow0 + 32 * j) * kQ4KBytes;
-            bhdr[j] = *reinterpret_cast<const u32x4*>(rb);
-            bqs[j] = *reinterpret_cast<const u32x2*>(rb + 16 + 32 * p + 16 * kh + 8 * h);
+            if constexpr (!A16) bhdr[R][j] = *reinterpret_cast<const u32x4*>(rb);
+            bqs[R][j] = *reinterpret_cast<const u32x2*>(rb + 16 + 32 * p + 16 * kh + 8 * h);
         }
     };
     // bq[buffer][step][col block] = the 8 fp16 weights of one MFMA B operand
     u32x4 bq[2][2][2];
     float sD[2][2], sM[2][2];                         // [col block][step]: D * 2^24 (2^20), -M
-    auto b_prep = [&](auto cq, int j) {
+    auto b_prep = [&](auto cq, int j, int R) {
         constexpr int p = decltype(cq)::value;
         int sc0, mn0, sc1, mn1;
-        q4k_scale_min_pair(bhdr[j].y, bhdr[j].z, bhdr[j].w, p, &sc0, &mn0, &sc1, &mn1);
-        const float d = half_bits_to_float(bhdr[j].x), dmin = half_bits_to_float(bhdr[j].x >> 16);
+        q4k_scale_min_pair(bhdr[R][j].y, bhdr[R][j].z, bhdr[R][j].w, p, &sc0, &mn0, &sc1, &mn1);
+        const float d = half_bits_to_float(bhdr[R][j].x), dmin = half_bits_to_float(bhdr[R][j].x >> 16);
         sD[j][0] = d * (float)sc0 * 16777216.0f;
         sM[j][0] = -(dmin * (float)mn0);
         sD[j][1] = d * (float)sc1 * 1048576.0f;
         sM[j][1] = -(dmin * (float)mn1);
     };
-    // piece q (0..3) of column block j: word q >> 1 of the 8 qs bytes, low
-    // (q even) or shifted (q odd) byte pairs, both steps
-    auto b_piece = [&](int buf, int j, int q) {
-#ifdef RF_ABL_NODQ
-        return;
-#endif
-        uint32_t w = (q >> 1) ? bqs[j].y : bqs[j].x;
-        if constexpr (A16)   // bytes (2q', 2q' + 1) of the word into the two halves: natural k order
-            w = __builtin_amdgcn_perm(0u, w, (q & 1) ? 0x0C030C02u : 0x0C010C00u);
-        else if (q & 1)      // bytes (1, 3): k order 0 2 1 3
-            w >>= 8;
-        bq[buf][0][j][q] = tall_dq2(w & 0x000F000Fu, sD[j][0], sM[j][0]);
-        bq[buf][1][j][q] = tall_dq2(w & 0x00F000F0u, sD[j][1], sM[j][1]);
+    // fp16 path: the table of super-block slot ts -- thread tid writes row
+    // tid / 2, sub-blocks 4 (tid & 1) .. + 3 (pairs p = 2 (tid & 1), +1)
+    auto tab_build = [&](int ring_slot, int ts) {
+        const int r = tid >> 1, hf = tid & 1;
+        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + ring_slot * kTallStage + r * kQ4KBytes);
+        const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+        // the 6-bit scales and mins of sub-blocks 4 hf .. 4 hf + 3, one per
+        // byte (get_scale_min_k4's layout, word-wide and without branches)
+        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+        const uint32_t scw = hf ? sc_hi : sc_lo, mnw = hf ? mn_hi : mn_lo;
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {      // sub-block 4 hf + i: even -> low nibbles (2^24), odd -> high (2^20)
+            e[2 * i] = d * byte_f(scw, i) * ((i & 1) ? 1048576.0f : 16777216.0f);
+            e[2 * i + 1] = -(dmin * byte_f(mnw, i));
+        }
+        float4* dst = reinterpret_cast<float4*>(tab0 + ts * kTabBytes + r * kTabRow + 32 * hf);
+        dst[0] = make_float4(e[0], e[1], e[2], e[3]);
+        dst[1] = make_float4(e[4], e[5], e[6], e[7]);
+    };
+    // the lane's scale terms of chunk pair p, column block j, from table ts
+    auto tab_read = [&](int ts, int p, int j) {
+        const float4 v = *reinterpret_cast<const float4*>(tab0 + ts * kTabBytes + (brow0 + 32 * j) * kTabRow + 16 * p);
+        sD[j][0] = v.x;
+        sM[j][0] = v.y;
+        sD[j][1] = v.z;
+        sM[j][1] = v.w;
+    };
+    // word wi (bytes 4 wi .. 4 wi + 3, k = 4 wi + 0..3) of column block j:
+    // operand registers 2 wi, 2 wi + 1 of both steps
+    auto b_piece = [&](int buf, int j, int wi, int R) {
+        const uint32_t w = wi ? bqs[R][j].y : bqs[R][j].x;
+        const uint2 lo = tall_dq4(w, 0x000F000Fu, sD[j][0], sM[j][0]);
+        const uint2 hi = tall_dq4(w, 0x00F000F0u, sD[j][1], sM[j][1]);
+        bq[buf][0][j][2 * wi] = lo.x;
+        bq[buf][0][j][2 * wi + 1] = lo.y;
+        bq[buf][1][j][2 * wi] = hi.x;
+        bq[buf][1][j][2 * wi + 1] = hi.y;
     };
 
     f32x16 acc[8][2];
@@ -1565,38 +1622,62 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int fa = col * kLdsStride + 16 * kh + 8 * h;   // + 32 step + 32 i rows
+    // fragment of row block i, step s: row 32 i + col, k piece 4 s + 2 kh + h
+    // (fp16: at position (4 s + 2 kh + h) ^ g(col) of its 128-byte row; rows
+    // 32 i + col have g(32 i + col) = g(col))
+    const int fa = A16 ? col * kARowHalves : col * kARowHalves + 16 * kh + 8 * h;
     f16x8 af[2][8];
     auto frag_ld = [&](int set, int buf, int s, int i) {
-        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kABufHalves + fa + 32 * i * kLdsStride + 32 * s);
+        const int kp = A16 ? 8 * ((4 * s + 2 * kh + h) ^ (col & 7) ^ ((col >> 3) & 1)) : 32 * s;
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kABufHalves + fa + 32 * i * kARowHalves + kp);
     };
 
     // ---- prologue: ring stage 0, A chunks 0 and 1, A regs = chunk 2 ------
+    if constexpr (A16) {
 #pragma unroll
-    for (int t = 0; t < kTallNI; ++t) w_gload1(t, 0);
+        for (int t = 0; t < kTallNI; ++t) w_dma1(t, 0, 0);
+    } else {
 #pragma unroll
-    for (int t = 0; t < kTallNI; ++t) w_lstore1(t, 0);
+        for (int t = 0; t < kTallNI; ++t) w_gload1(t, 0);
 #pragma unroll
-    for (int i = 0; i < kANI; ++i) a_load1(i, 0);
-#pragma unroll
-    for (int i = 0; i < kANI; ++i) {
-        a_store1(i, 0);
-        a_load1(i, 1);
+        for (int t = 0; t < kTallNI; ++t) w_lstore1(t, 0);
     }
+    if constexpr (A16) {
 #pragma unroll
-    for (int i = 0; i < kANI; ++i) {
-        a_store1(i, 1);
-        a_load1(i, 2);
+        for (int g = 0; g < kANI; ++g) a_dma1(g, 0, 0);
+#pragma unroll
+        for (int g = 0; g < kANI; ++g) a_dma1(g, 1, 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+#pragma unroll
+        for (int i = 0; i < kANI; ++i) a_load1(i, 0);
+#pragma unroll
+        for (int i = 0; i < kANI; ++i) {
+            a_store1(i, 0);
+            a_load1(i, 1);
+        }
+#pragma unroll
+        for (int i = 0; i < kANI; ++i) {
+            a_store1(i, 1);
+            a_load1(i, 2);
+        }
     }
     lds_barrier();
-    b_read(std::integral_constant<int, 0>{}, 0);
-    b_prep(std::integral_constant<int, 0>{}, 0);
-    b_prep(std::integral_constant<int, 0>{}, 1);
+    b_read(std::integral_constant<int, 0>{}, 0, 0);
+    if constexpr (A16) {
+        tab_build(0, 0);
+        lds_barrier();
+        tab_read(0, 0, 0);
+        tab_read(0, 0, 1);
+    } else {
+        b_prep(std::integral_constant<int, 0>{}, 0, 0);
+        b_prep(std::integral_constant<int, 0>{}, 1, 0);
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b_piece(0, j, q);
-    b_read(std::integral_constant<int, 1>{}, 0);
+        for (int q = 0; q < 2; ++q) b_piece(0, j, q, 0);
+    b_read(std::integral_constant<int, 1>{}, 0, 1);
 #pragma unroll
     for (int i = 0; i < 8; ++i) frag_ld(0, 0, 0, i);
 
@@ -1628,32 +1709,70 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][i], j ? b1 : b0, acc[i][j], 0, 0, 0);
                     // next step's fragments: step 1 of this chunk, then step 0 of chunk c + 1
                     if (j == 0) frag_ld(s ^ 1, s ? abn : ab, s ^ 1, i);
-                    // B operands of chunk c + 1 (its raw bytes were read one chunk ago)
-                    if (t == 2) b_prep(NEXT{}, 0);
-                    if (t >= 3 && t < 7) b_piece(P ^ 1, 0, t - 3);
-                    if (t == 7) b_prep(NEXT{}, 1);
-                    if (t >= 8 && t < 12) b_piece(P ^ 1, 1, t - 8);
-                    // raw bytes of chunk c + 2 (not across the super-block boundary:
-                    // the next stage is stored in CQ 2, read after its barrier)
-                    if (t == 12 && CQ < 2) b_read(NEXT2{}, slot);
-                    if (t == 12 && CQ == 3) b_read(NEXT2{}, slot ^ 1);
-                    // A chunk c + 2 to LDS, registers reloaded with chunk c + 3
-                    if (t >= 14 && t < 14 + kANI) {
-                        a_store1(t - 14, abs2);
-                        a_load1(t - 14, c + 3);
-                    }
-                    if constexpr (CQ == 0) {
-                        if (t >= 24 && t < 24 + kTallNI) w_gload1(t - 24, sb + 1);
-                    }
-                    if constexpr (CQ == 2) {
-                        if (t >= 24 && t < 24 + kTallNI) w_lstore1(t - 24, slot ^ 1);
+                    if constexpr (A16) {
+                        // A chunk c + 2 by DMA on the even slots of the first half
+                        if (t < 2 * kANI && (t & 1) == 0) a_dma1(t >> 1, c + 2, abs2);
+                        // B operands of chunk c + 1 (raw bytes read one chunk ago):
+                        // ten groups of VALU work, one every third slot, so each
+                        // MFMA has about three VALU operations beside it
+                        // (scale terms from the table of chunk c + 1's super-block)
+                        if (t == 1 || t == 14) tab_read(CQ == 3 ? slot ^ 1 : slot, (CQ + 1) & 3, t == 14);
+                        if (t == 5 || t == 10) b_piece(P ^ 1, 0, t == 10, P ^ 1);
+                        if (t == 20 || t == 25) b_piece(P ^ 1, 1, t == 25, P ^ 1);
+                        // the next super-block's table, from its ring stage (complete
+                        // since CQ 1's barrier), into the slot of super-block sb - 1
+                        if constexpr (CQ == 2) {
+                            if (t == 3) tab_build(slot ^ 1, slot ^ 1);
+                        }
+                        // raw bytes of chunk c + 2: the next super-block's for CQ 2, 3
+                        // (its ring stage is complete after CQ 1's barrier)
+                        if (t == 17) b_read(NEXT2{}, CQ < 2 ? slot : slot ^ 1, P);
+                        // the next super-block's rows into the ring slot super-block
+                        // sb - 1 used (its last read was in CQ 1 of sb - 1)
+                        if constexpr (CQ == 0) {
+                            if (t >= 18 && t < 18 + 2 * kTallNI && (t & 1) == 0) w_dma1((t - 18) >> 1, sb + 1, slot ^ 1);
+                        }
+                    } else {
+                        // B operands of chunk c + 1 (its raw bytes were read one chunk ago)
+                        if (t == 2) b_prep(NEXT{}, 0, P ^ 1);
+                        if (t == 3 || t == 5) b_piece(P ^ 1, 0, t == 5, P ^ 1);
+                        if (t == 7) b_prep(NEXT{}, 1, P ^ 1);
+                        if (t == 8 || t == 10) b_piece(P ^ 1, 1, t == 10, P ^ 1);
+                        // raw bytes of chunk c + 2 (not across the super-block boundary:
+                        // the next stage is stored in CQ 2, read after its barrier)
+                        if (t == 12 && CQ < 2) b_read(NEXT2{}, slot, P);
+                        if (t == 12 && CQ == 3) b_read(NEXT2{}, slot ^ 1, P);
+                        // A chunk c + 2 to LDS, registers reloaded with chunk c + 3
+                        if (t >= 14 && t < 14 + kANI) {
+                            a_store1(t - 14, abs2);
+                            a_load1(t - 14, c + 3);
+                        }
+                        if constexpr (CQ == 0) {
+                            if (t >= 24 && t < 24 + kTallNI) w_gload1(t - 24, sb + 1);
+                        }
+                        if constexpr (CQ == 2) {
+                            if (t >= 9 && t < 9 + kTallNI) w_lstore1(t - 9, slot ^ 1);
+                        }
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
         }
-        lds_barrier();
-        // CQ 2: chunk c + 2 is the next super-block's first, stored just now
-        if constexpr (CQ == 2) b_read(NEXT2{}, slot ^ 1);
+        // fp16: this chunk's A DMA (chunk c + 2) is done before the barrier;
+        // the ring DMA issued after it (CQ 0) may stay in flight one chunk
+        if constexpr (A16) {
+            if constexpr (CQ == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kTallNI) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        // fp16: every LDS access of the chunk except the last 8 fragment reads
+        // (of chunk c + 1, whose buffer is not written before the next
+        // barrier) is complete -- LDS operations complete in order.  fp32:
+        // the A stores interleave with those reads, so all of them.
+        if constexpr (A16)
+            asm volatile("s_waitcnt lgkmcnt(8)\n\ts_barrier" ::: "memory");
+        else
+            lds_barrier();
+        // fp32, CQ 2: chunk c + 2 is the next super-block's first, stored just now
+        if constexpr (!A16 && CQ == 2) b_read(NEXT2{}, slot ^ 1, P);
     };
     int ab = 0;                                     // (4 sb) % 3
     for (int sb = 0; sb < nsb; ++sb) {
@@ -1667,14 +1786,19 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
     // ---- K halves: wave kh = 1 hands row blocks 0-3 to kh = 0, kh = 0 hands
     // row blocks 4-7 to kh = 1; each then adds and stores its four blocks ----
     __syncthreads();
-    float* xch = reinterpret_cast<float*>(lds);          // 4 waves x 4 blocks x 2 x 16 x 64 floats = 128 KB
+    // [wave][block i][col block j][e / 4][lane] of float4: each access is one
+    // contiguous 1 KB per wave (4 waves x 4 x 2 x 4 KB = 128 KB)
+    float4* xch = reinterpret_cast<float4*>(lds);
     const int give = kh ? 0 : 4, keep = kh ? 4 : 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) xch[(((wave * 4 + i) * 2 + j) * 16 + e) * 64 + lane] = acc[give + i][j][e];
+            for (int q = 0; q < 4; ++q)
+                xch[(((wave * 4 + i) * 2 + j) * 4 + q) * 64 + lane] =
+                    make_float4(acc[give + i][j][4 * q], acc[give + i][j][4 * q + 1], acc[give + i][j][4 * q + 2],
+                                acc[give + i][j][4 * q + 3]);
     __syncthreads();
     const int partner = wave ^ 1;
 #pragma unroll
@@ -1683,14 +1807,22 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
         for (int j = 0; j < 2; ++j) {
             const int ncol = n0 + 64 * wn + 32 * j + col;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float o = xch[(((partner * 4 + i) * 2 + j) * 16 + e) * 64 + lane];
-                // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
-                const float s = kh ? o + acc[keep + i][j][e] : acc[keep + i][j][e] + o;
-                const int row = m0 + 32 * (keep + i) + 8 * (e >> 2) + 4 * h + (e & 3);
-                float* dst = D + (size_t)row * N + ncol;
-                if (A16 && row >= M) continue;
-                *dst = accum ? *dst + s : s;
+            for (int q = 0; q < 4; ++q) {
+                const float4 o4 = xch[(((partner * 4 + i) * 2 + j) * 4 + q) * 64 + lane];
+                const float o[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int e = 4 * q + u;
+                    // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
+                    const float sum = kh ? o[u] + acc[keep + i][j][e] : acc[keep + i][j][e] + o[u];
+                    const int row = m0 + 32 * (keep + i) + 8 * q + 4 * h + u;
+                    float* dst = D + (size_t)row * N + ncol;
+                    if (A16 && row >= M) continue;
+                    if (accum)
+                        *dst += sum;
+                    else
+                        *dst = sum;
+                }
             }
         }
 }
