@@ -1386,13 +1386,24 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
         }
 }
 
-// ── tall: 256 x 128 tiles, K halves split over wave pairs ────────────────
+// ── f16a: Q4_K GEMM on fp16 activations, 256 x 128 tiles, K halves on wave
+// pairs (rf_gemm_q4_k_f16_launch) ─────────────────────────────────────────
 // Workgroup = 256 threads over a 256 (M) x 128 (N) tile.  Wave w owns the
 // 64 output columns [n0 + 64 (w >> 1), +64) for all 256 rows, over the K
 // half kh = w & 1 of every 64-wide chunk; the two halves are added through
-// LDS at the end.  Each wave thus issues 32 MFMAs per chunk against 16
+// LDS at the end.  Each wave issues 32 MFMAs per chunk against 16
 // dequantised weights per lane, so every weight is dequantised once per 256
-// rows of A (v7: once per 128) and its accumulators fill the 256 AGPRs.
+// rows of A (the fp32-activation kernels: once per 128) and the
+// accumulators fill the 256 AGPRs.
+//
+// Memory.  A (fp16, as the caller rounded it) and the weight ring arrive by
+// LDS DMA (global_load_lds_dwordx4: no registers, no LDS store
+// instructions), three A chunk buffers and two ring stages.  The DMAs are
+// inline asm the compiler does not see, so the kernel waits for them itself
+// (s_waitcnt vmcnt before the per-chunk barrier).  A's 128-byte rows are
+// XOR-swizzled by 16-byte piece: position p of row r holds k piece
+// p ^ g(r), g(r) = (r & 7) ^ ((r >> 3) & 1), so 16 consecutive rows of a
+// fragment read fall on 16 different bank groups.
 //
 // K order.  Chunk c of a Q4_K row = super-block c / 4, nibble pair p = c % 4:
 // qs byte i of [32p, 32p + 32) holds chunk elements i (low nibble) and
@@ -1406,20 +1417,19 @@ __global__ __launch_bounds__(kSqThreads) void rf_gemm_qk_sq_kernel(const float* 
 // for the high nibbles; D q is exact): per word of 4 bytes one shift and
 // four masks for its 8 weights, one fma_mix per weight and one
 // v_cvt_pk_f16_f32 per two, the reference's rounding of the fp32 value
-// (D = d * sc, M = dmin * m).
-constexpr int kTallThreads = 256;
-constexpr int kTallBM = 256, kTallBN = 128;
-constexpr int kTallStage = kTallBN * kQ4KBytes;      // one super-block of the tile's 128 rows (18 KB)
-constexpr int kTallGroups = kTallStage / 1024;      // 16-byte lane loads: 18 groups of 64 per stage
-constexpr int kTallNI = (kTallGroups + 3) / 4;      // per wave (the last wave repeats groups 0, 1)
-constexpr int kTallABufs = 3;
-// fp16 path: per super-block, a table of the tile rows' sub-block scale terms
-// (D * 2^24 or D * 2^20, -M) built once by the workgroup; 80-byte rows (8
-// float pairs + pad) put 16 consecutive rows on different bank groups
-constexpr int kTabRow = 80;
-constexpr int kTabBytes = kTallBN * kTabRow;
-constexpr int kTallLds32 = 2 * kTallStage + kTallABufs * kTallBM * kLdsStride * 2;
-constexpr int kTallLds16 = 2 * kTallStage + kTallABufs * kTallBM * kKC * 2 + 2 * kTabBytes;
+// (D = d * sc, M = dmin * m).  The per-sub-block terms (D * 2^24 or 2^20,
+// -M) of a super-block are computed once per workgroup into an LDS table.
+constexpr int kF16aThreads = 256;
+constexpr int kF16aBM = 256, kF16aBN = 128;
+constexpr int kF16aStage = kF16aBN * kQ4KBytes;     // one super-block of the tile's 128 rows (18 KB)
+constexpr int kF16aGroups = kF16aStage / 1024;      // 16-byte lane loads: 18 groups of 64 per stage
+constexpr int kF16aNI = (kF16aGroups + 3) / 4;      // per wave (the last wave repeats groups 0, 1)
+constexpr int kF16aABufs = 3;
+constexpr int kF16aANI = 8;                         // A DMA instructions per wave per chunk (1 KB each)
+constexpr int kF16aABuf = kF16aBM * kKC * 2;        // bytes of one A chunk buffer
+constexpr int kTabRow = 80;                         // 8 float pairs + pad: 16 rows on distinct bank groups
+constexpr int kTabBytes = kF16aBN * kTabRow;
+constexpr int kF16aLds = 2 * kF16aStage + kF16aABufs * kF16aABuf + 2 * kTabBytes;   // 152 KB
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // The four weights of the bytes b0..b3 of w under nibble mask m (low
@@ -1427,7 +1437,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // ((w >> 8) & m) holds (b1, b3) as fp16 subnormals; each goes through
 // v_fma_mix (fp16 source, fp32 value) and the pairs (b0, b1), (b2, b3) are
 // rounded to fp16 together.
-__device__ __forceinline__ uint2 tall_dq4(uint32_t w, uint32_t m, float D, float nM) {
+__device__ __forceinline__ uint2 f16a_dq4(uint32_t w, uint32_t m, float D, float nM) {
     const f16x2 e = __builtin_bit_cast(f16x2, w & m);
     const f16x2 o = __builtin_bit_cast(f16x2, (w >> 8) & m);
     const float v0 = __builtin_fmaf((float)e[0], D, nM), v2 = __builtin_fmaf((float)e[1], D, nM);
@@ -1435,148 +1445,86 @@ __device__ __forceinline__ uint2 tall_dq4(uint32_t w, uint32_t m, float D, float
     return make_uint2(cvt_pk_f16(v0, v1), cvt_pk_f16(v2, v3));
 }
 
-// A16: A is fp16 (the caller rounded it: the same operand values), read
-// 16 bytes a lane and stored to LDS in natural k order; the B operands then
-// take their byte pairs in natural order through v_perm.
-template <bool A16>
-__global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const void* __restrict__ Av,
+// 16 bytes a lane from global memory straight into LDS at m0 + 16 lane
+__device__ __forceinline__ void lds_dma16(uint32_t lds_dst, uint32_t voff, const uint8_t* sbase) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(lds_dst), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+
+__global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                          const uint8_t* __restrict__ W,
-                                                                         float* __restrict__ D, int M, int N, int K,
-                                                                         int accum) {
-    // one LDS block: the weight ring, then three A buffers; after the loop
-    // the first 128 KB carry the K-half exchange
-    __shared__ __align__(16) uint8_t lds[A16 ? kTallLds16 : kTallLds32];
+                                                                         float* __restrict__ D, int M, int N, int K) {
+    // one LDS block: ring (2 stages), A (3 buffers), scale tables (2); after
+    // the loop its first 128 KB carry the K-half exchange
+    __shared__ __align__(16) uint8_t lds[kF16aLds];
     uint8_t* ring = lds;
-    _Float16* abuf0 = reinterpret_cast<_Float16*>(lds + 2 * kTallStage);
-    // fp32 A: rows of kLdsStride halves; fp16 A: rows of 64 halves (128 B)
-    // whose 16-byte pieces are XOR-swizzled by the row (position p of row r
-    // holds k piece p ^ g(r), g(r) = (r & 7) ^ ((r >> 3) & 1): 16 consecutive
-    // rows then fall on 16 different 16-byte bank groups), written by LDS DMA
-    constexpr int kARowHalves = A16 ? kKC : kLdsStride;
-    constexpr int kABufHalves = kTallBM * kARowHalves;
-    uint8_t* tab0 = lds + 2 * kTallStage + kTallABufs * kABufHalves * 2;   // fp16 path only
+    uint8_t* abuf0 = lds + 2 * kF16aStage;
+    uint8_t* tab0 = abuf0 + kF16aABufs * kF16aABuf;
+    const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
+    const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kh = wave & 1, wn = wave >> 1;
     const int h = lane >> 5, col = lane & 31;
-    const int mtiles = (M + kTallBM - 1) / kTallBM;
+    const int mtiles = (M + kF16aBM - 1) / kF16aBM;
     const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int m0 = (v % mtiles) * kTallBM;      // the M tiles of one column tile are neighbours
-    const int n0 = (v / mtiles) * kTallBN;
+    const int m0 = (v % mtiles) * kF16aBM;      // the M tiles of one column tile are neighbours
+    const int n0 = (v / mtiles) * kF16aBN;
     const int nchunks = K / kKC;
     const int nsb = K / kQK;
     const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
 
-    // ---- weight ring: stage = super-block sb of the tile's 128 rows ------
-    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W + (size_t)n0 * row_bytes);
-    uint32_t goff[kTallNI], gdst[kTallNI];
+    // ---- weight ring: stage = super-block sb of the tile's 128 rows; group
+    // g of 64 lanes moves 16-byte pieces [64 g, 64 g + 64) (row pc / 9) ------
+    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    uint32_t goff[kF16aNI], gdst[kF16aNI];
 #pragma unroll
-    for (int t = 0; t < kTallNI; ++t) {
-        const int g = (wave * kTallNI + t) % kTallGroups;
-        const int pc = 64 * g + lane;                 // 16-byte piece of the stage
-        gdst[t] = 16u * (uint32_t)pc;
+    for (int t = 0; t < kF16aNI; ++t) {
+        const int g = (wave * kF16aNI + t) % kF16aGroups;
+        const int pc = 64 * g + lane;
+        gdst[t] = 1024u * (uint32_t)g;
         goff[t] = (uint32_t)(pc / 9) * row_bytes + 16u * (uint32_t)(pc % 9);
     }
-    u32x4 wst[kTallNI];
-    auto w_gload1 = [&](int t, int sb) {
-        wst[t] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, goff[t], (uint32_t)min(sb, nsb - 1) * kQ4KBytes, 0);
-    };
-    auto w_lstore1 = [&](int t, int slot) {
-        *reinterpret_cast<u32x4*>(ring + slot * kTallStage + gdst[t]) = wst[t];
-    };
-    // fp16 path: the same pieces by LDS DMA straight into the ring slot
-    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
-    const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
     auto w_dma1 = [&](int t, int sb, int slot) {
-        const uint8_t* src = w_tile + (size_t)min(sb, nsb - 1) * kQ4KBytes;
-        const uint32_t dst = ring_lds0 + (uint32_t)slot * kTallStage + gdst[t] - 16u * (uint32_t)lane;
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                     :: "s"(__builtin_amdgcn_readfirstlane(dst)), "v"(goff[t]), "s"(src) : "memory", "m0");
+        lds_dma16(__builtin_amdgcn_readfirstlane(ring_lds0 + (uint32_t)slot * kF16aStage + gdst[t]), goff[t],
+                  w_tile + (size_t)min(sb, nsb - 1) * kQ4KBytes);
     };
 
-    // ---- A chunk to LDS.  fp32: 16 float4 per thread through registers,
-    // rounded to fp16.  fp16:
-    // LDS DMA, 8 x 1 KB per wave (rows 8 g .. 8 g + 7 of the chunk), no
-    // registers; the kernel waits for it itself (s_waitcnt vmcnt before the
-    // per-chunk barrier) and keeps the compiler unaware of it.
-    constexpr int kANI = A16 ? 8 : 16;
-    const int a_row = tid >> 4, a_col = 4 * (tid & 15);
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(static_cast<const float*>(Av) + (A16 ? 0 : (size_t)m0 * K));
-    const uint32_t a_voff = (uint32_t)(a_row * K + a_col) * 4u;
-    u32x4 areg[A16 ? 1 : kANI];
-    // fp16: lane L of wave instruction g (rows 8 (4 g' + wave)...) -- global
-    // instruction gi = 8 wave + g covers LDS rows 8 gi + L / 8, piece L % 8
-    uint32_t dma_voff[A16 ? kANI : 1];
-    const uint8_t* a16_base = static_cast<const uint8_t*>(Av) + (size_t)m0 * K * 2;
-    const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
-    if constexpr (A16) {
+    // ---- A: instruction gi = 8 wave + g covers rows 8 gi + L / 8 of the chunk,
+    // position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row M - 1 --
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    uint32_t dma_voff[kF16aANI];
 #pragma unroll
-        for (int g = 0; g < kANI; ++g) {
-            const int r = 8 * (8 * wave + g) + (lane >> 3);
-            const int rc = min(r, M - 1 - m0);          // fp16 A may end inside the tile
-            dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
-        }
+    for (int g = 0; g < kF16aANI; ++g) {
+        const int r = 8 * (8 * wave + g) + (lane >> 3);
+        const int rc = min(r, M - 1 - m0);
+        dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
     }
-    auto a_load1 = [&](int i, int c) {
-        if constexpr (!A16) {
-            const uint32_t so = ((uint32_t)min(c, nchunks - 1) * kKC + (uint32_t)(16 * i * K)) * 4u;
-            areg[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, so, 0);
-        }
-    };
-    // fp16: the DMA of instruction g of chunk c into buffer buf
     auto a_dma1 = [&](int g, int c, int buf) {
-        const uint8_t* src = a16_base + (size_t)min(c, nchunks - 1) * kKC * 2;
-        const uint32_t dst = a_lds0 + (uint32_t)(buf * kABufHalves * 2 + (8 * wave + g) * 1024);
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                     :: "s"(dst), "v"(dma_voff[g]), "s"(src) : "memory", "m0");
-    };
-    auto a_store1 = [&](int i, int buf) {
-        if constexpr (!A16) {
-            _Float16* dst = abuf0 + buf * kABufHalves + (a_row + 16 * i) * kARowHalves + a_col;
-            const float4 f = __builtin_bit_cast(float4, areg[i]);
-            f16x4 hv;
-            hv[0] = (_Float16)f.x; hv[1] = (_Float16)f.y;
-            hv[2] = (_Float16)f.z; hv[3] = (_Float16)f.w;
-            *reinterpret_cast<f16x4*>(dst) = hv;
-        }
+        lds_dma16(a_lds0 + (uint32_t)(buf * kF16aABuf + (8 * wave + g) * 1024), dma_voff[g],
+                  a_tile + (size_t)min(c, nchunks - 1) * kKC * 2);
     };
 
-    // ---- B: the lane's two weight rows (columns), 8 qs bytes each per chunk
+    // ---- B: the lane's two weight rows (columns), 8 qs bytes each per chunk,
+    // double buffered by chunk parity R (chunk c + 1 is dequantised while the
+    // bytes of chunk c + 2 arrive) ---------------------------------------------
     const int brow0 = 64 * wn + col;                  // rows brow0 and brow0 + 32 of the tile
-    // raw bytes double buffered by chunk parity R: chunk c + 1 is dequantised
-    // while chunk c + 2's bytes arrive
-    u32x4 bhdr[2][2];
     u32x2 bqs[2][2];
     auto b_read = [&](auto cq, int slot, int R) {
         constexpr int p = decltype(cq)::value;
-        const uint8_t* st = ring + slot * kTallStage;
+        const uint8_t* st = ring + slot * kF16aStage;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint8_t* rb = st + (brow0 + 32 * j) * kQ4KBytes;
-            if constexpr (!A16) bhdr[R][j] = *reinterpret_cast<const u32x4*>(rb);
-            bqs[R][j] = *reinterpret_cast<const u32x2*>(rb + 16 + 32 * p + 16 * kh + 8 * h);
-        }
+        for (int j = 0; j < 2; ++j)
+            bqs[R][j] = *reinterpret_cast<const u32x2*>(st + (brow0 + 32 * j) * kQ4KBytes + 16 + 32 * p + 16 * kh +
+                                                        8 * h);
     };
-    // bq[buffer][step][col block] = the 8 fp16 weights of one MFMA B operand
-    u32x4 bq[2][2][2];
-    float sD[2][2], sM[2][2];                         // [col block][step]: D * 2^24 (2^20), -M
-    auto b_prep = [&](auto cq, int j, int R) {
-        constexpr int p = decltype(cq)::value;
-        int sc0, mn0, sc1, mn1;
-        q4k_scale_min_pair(bhdr[R][j].y, bhdr[R][j].z, bhdr[R][j].w, p, &sc0, &mn0, &sc1, &mn1);
-        const float d = half_bits_to_float(bhdr[R][j].x), dmin = half_bits_to_float(bhdr[R][j].x >> 16);
-        sD[j][0] = d * (float)sc0 * 16777216.0f;
-        sM[j][0] = -(dmin * (float)mn0);
-        sD[j][1] = d * (float)sc1 * 1048576.0f;
-        sM[j][1] = -(dmin * (float)mn1);
-    };
-    // fp16 path: the table of super-block slot ts -- thread tid writes row
-    // tid / 2, sub-blocks 4 (tid & 1) .. + 3 (pairs p = 2 (tid & 1), +1)
+    // scale table of super-block slot ts: thread tid writes row tid / 2,
+    // sub-blocks 4 (tid & 1) .. + 3 as (D * 2^24 or D * 2^20, -M) pairs
     auto tab_build = [&](int ring_slot, int ts) {
         const int r = tid >> 1, hf = tid & 1;
-        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + ring_slot * kTallStage + r * kQ4KBytes);
+        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + ring_slot * kF16aStage + r * kQ4KBytes);
         const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
         // the 6-bit scales and mins of sub-blocks 4 hf .. 4 hf + 3, one per
         // byte (get_scale_min_k4's layout, word-wide and without branches)
@@ -1594,20 +1542,22 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
         dst[0] = make_float4(e[0], e[1], e[2], e[3]);
         dst[1] = make_float4(e[4], e[5], e[6], e[7]);
     };
-    // the lane's scale terms of chunk pair p, column block j, from table ts
+    float sD[2][2], sM[2][2];                         // [col block][step]
     auto tab_read = [&](int ts, int p, int j) {
-        const float4 v = *reinterpret_cast<const float4*>(tab0 + ts * kTabBytes + (brow0 + 32 * j) * kTabRow + 16 * p);
-        sD[j][0] = v.x;
-        sM[j][0] = v.y;
-        sD[j][1] = v.z;
-        sM[j][1] = v.w;
+        const float4 t = *reinterpret_cast<const float4*>(tab0 + ts * kTabBytes + (brow0 + 32 * j) * kTabRow + 16 * p);
+        sD[j][0] = t.x;
+        sM[j][0] = t.y;
+        sD[j][1] = t.z;
+        sM[j][1] = t.w;
     };
-    // word wi (bytes 4 wi .. 4 wi + 3, k = 4 wi + 0..3) of column block j:
-    // operand registers 2 wi, 2 wi + 1 of both steps
+    // bq[buffer][step][col block] = the 8 fp16 weights of one MFMA B operand;
+    // word wi (bytes 4 wi .. 4 wi + 3) of column block j fills registers
+    // 2 wi, 2 wi + 1 of both steps
+    u32x4 bq[2][2][2];
     auto b_piece = [&](int buf, int j, int wi, int R) {
         const uint32_t w = wi ? bqs[R][j].y : bqs[R][j].x;
-        const uint2 lo = tall_dq4(w, 0x000F000Fu, sD[j][0], sM[j][0]);
-        const uint2 hi = tall_dq4(w, 0x00F000F0u, sD[j][1], sM[j][1]);
+        const uint2 lo = f16a_dq4(w, 0x000F000Fu, sD[j][0], sM[j][0]);
+        const uint2 hi = f16a_dq4(w, 0x00F000F0u, sD[j][1], sM[j][1]);
         bq[buf][0][j][2 * wi] = lo.x;
         bq[buf][0][j][2 * wi + 1] = lo.y;
         bq[buf][1][j][2 * wi] = hi.x;
@@ -1622,57 +1572,29 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // fragment of row block i, step s: row 32 i + col, k piece 4 s + 2 kh + h
-    // (fp16: at position (4 s + 2 kh + h) ^ g(col) of its 128-byte row; rows
-    // 32 i + col have g(32 i + col) = g(col))
-    const int fa = A16 ? col * kARowHalves : col * kARowHalves + 16 * kh + 8 * h;
+    // fragment of row block i, step s: row 32 i + col, k piece 4 s + 2 kh + h,
+    // at position (4 s + 2 kh + h) ^ g(col) of its row (g(32 i + col) = g(col))
+    const int gcol = (col & 7) ^ ((col >> 3) & 1);
     f16x8 af[2][8];
     auto frag_ld = [&](int set, int buf, int s, int i) {
-        const int kp = A16 ? 8 * ((4 * s + 2 * kh + h) ^ (col & 7) ^ ((col >> 3) & 1)) : 32 * s;
-        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kABufHalves + fa + 32 * i * kARowHalves + kp);
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kF16aABuf + (32 * i + col) * 128 +
+                                                     16 * ((4 * s + 2 * kh + h) ^ gcol));
     };
 
-    // ---- prologue: ring stage 0, A chunks 0 and 1, A regs = chunk 2 ------
-    if constexpr (A16) {
+    // ---- prologue: ring stage 0 and A chunks 0, 1; table 0; chunk 0's B ----
 #pragma unroll
-        for (int t = 0; t < kTallNI; ++t) w_dma1(t, 0, 0);
-    } else {
+    for (int t = 0; t < kF16aNI; ++t) w_dma1(t, 0, 0);
 #pragma unroll
-        for (int t = 0; t < kTallNI; ++t) w_gload1(t, 0);
+    for (int g = 0; g < kF16aANI; ++g) a_dma1(g, 0, 0);
 #pragma unroll
-        for (int t = 0; t < kTallNI; ++t) w_lstore1(t, 0);
-    }
-    if constexpr (A16) {
-#pragma unroll
-        for (int g = 0; g < kANI; ++g) a_dma1(g, 0, 0);
-#pragma unroll
-        for (int g = 0; g < kANI; ++g) a_dma1(g, 1, 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else {
-#pragma unroll
-        for (int i = 0; i < kANI; ++i) a_load1(i, 0);
-#pragma unroll
-        for (int i = 0; i < kANI; ++i) {
-            a_store1(i, 0);
-            a_load1(i, 1);
-        }
-#pragma unroll
-        for (int i = 0; i < kANI; ++i) {
-            a_store1(i, 1);
-            a_load1(i, 2);
-        }
-    }
+    for (int g = 0; g < kF16aANI; ++g) a_dma1(g, 1, 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     b_read(std::integral_constant<int, 0>{}, 0, 0);
-    if constexpr (A16) {
-        tab_build(0, 0);
-        lds_barrier();
-        tab_read(0, 0, 0);
-        tab_read(0, 0, 1);
-    } else {
-        b_prep(std::integral_constant<int, 0>{}, 0, 0);
-        b_prep(std::integral_constant<int, 0>{}, 1, 0);
-    }
+    tab_build(0, 0);
+    lds_barrier();
+    tab_read(0, 0, 0);
+    tab_read(0, 0, 1);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1683,16 +1605,16 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
 
     // Chunk c = 4 sb + CQ, A buffer c % 3, ring slot sb % 2.  32 slots, one
     // MFMA each (slot t = 16 step + 2 i + j), separated by scheduling fences,
-    // each followed by a slice of the side work: the B operands of chunk
-    // c + 1 (raw bytes read at the end of chunk c - 1), the A fragments of the
-    // next step (for step 1: chunk c + 1's first step, from a buffer stored
-    // two chunks ago), A chunk c + 2 to LDS and chunk c + 3 into registers,
-    // the ring (loads of super-block sb + 1 in CQ 0, stored in CQ 2).
+    // each followed by a slice of the side work: the A fragments of the next
+    // step (for step 1: chunk c + 1's first, from a buffer complete since the
+    // last barrier); A chunk c + 2 by DMA into the buffer chunk c - 1 used;
+    // the B operands of chunk c + 1 (raw bytes read one chunk ago, scale
+    // terms from its super-block's table) and the raw bytes of chunk c + 2;
+    // in CQ 0 the ring DMA of super-block sb + 1 (complete after CQ 1's
+    // barrier) and in CQ 2 its scale table.
     auto iteration = [&](auto cqc, int sb, int ab) {
         constexpr int CQ = decltype(cqc)::value;
         constexpr int P = CQ & 1;                           // bq buffer of this chunk
-        using NEXT = std::integral_constant<int, (CQ + 1) & 3>;
-        using NEXT2 = std::integral_constant<int, (CQ + 2) & 3>;
         const int c = 4 * sb + CQ;
         const int slot = sb & 1;
         const int abn = ab == 2 ? 0 : ab + 1;               // chunk c + 1
@@ -1707,72 +1629,32 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
                 for (int j = 0; j < 2; ++j) {
                     const int t = 16 * s + 2 * i + j;
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][i], j ? b1 : b0, acc[i][j], 0, 0, 0);
-                    // next step's fragments: step 1 of this chunk, then step 0 of chunk c + 1
                     if (j == 0) frag_ld(s ^ 1, s ? abn : ab, s ^ 1, i);
-                    if constexpr (A16) {
-                        // A chunk c + 2 by DMA on the even slots of the first half
-                        if (t < 2 * kANI && (t & 1) == 0) a_dma1(t >> 1, c + 2, abs2);
-                        // B operands of chunk c + 1 (raw bytes read one chunk ago):
-                        // ten groups of VALU work, one every third slot, so each
-                        // MFMA has about three VALU operations beside it
-                        // (scale terms from the table of chunk c + 1's super-block)
-                        if (t == 1 || t == 14) tab_read(CQ == 3 ? slot ^ 1 : slot, (CQ + 1) & 3, t == 14);
-                        if (t == 5 || t == 10) b_piece(P ^ 1, 0, t == 10, P ^ 1);
-                        if (t == 20 || t == 25) b_piece(P ^ 1, 1, t == 25, P ^ 1);
-                        // the next super-block's table, from its ring stage (complete
-                        // since CQ 1's barrier), into the slot of super-block sb - 1
-                        if constexpr (CQ == 2) {
-                            if (t == 3) tab_build(slot ^ 1, slot ^ 1);
-                        }
-                        // raw bytes of chunk c + 2: the next super-block's for CQ 2, 3
-                        // (its ring stage is complete after CQ 1's barrier)
-                        if (t == 17) b_read(NEXT2{}, CQ < 2 ? slot : slot ^ 1, P);
-                        // the next super-block's rows into the ring slot super-block
-                        // sb - 1 used (its last read was in CQ 1 of sb - 1)
-                        if constexpr (CQ == 0) {
-                            if (t >= 18 && t < 18 + 2 * kTallNI && (t & 1) == 0) w_dma1((t - 18) >> 1, sb + 1, slot ^ 1);
-                        }
-                    } else {
-                        // B operands of chunk c + 1 (its raw bytes were read one chunk ago)
-                        if (t == 2) b_prep(NEXT{}, 0, P ^ 1);
-                        if (t == 3 || t == 5) b_piece(P ^ 1, 0, t == 5, P ^ 1);
-                        if (t == 7) b_prep(NEXT{}, 1, P ^ 1);
-                        if (t == 8 || t == 10) b_piece(P ^ 1, 1, t == 10, P ^ 1);
-                        // raw bytes of chunk c + 2 (not across the super-block boundary:
-                        // the next stage is stored in CQ 2, read after its barrier)
-                        if (t == 12 && CQ < 2) b_read(NEXT2{}, slot, P);
-                        if (t == 12 && CQ == 3) b_read(NEXT2{}, slot ^ 1, P);
-                        // A chunk c + 2 to LDS, registers reloaded with chunk c + 3
-                        if (t >= 14 && t < 14 + kANI) {
-                            a_store1(t - 14, abs2);
-                            a_load1(t - 14, c + 3);
-                        }
-                        if constexpr (CQ == 0) {
-                            if (t >= 24 && t < 24 + kTallNI) w_gload1(t - 24, sb + 1);
-                        }
-                        if constexpr (CQ == 2) {
-                            if (t >= 9 && t < 9 + kTallNI) w_lstore1(t - 9, slot ^ 1);
-                        }
+                    if (t < 2 * kF16aANI && (t & 1) == 0) a_dma1(t >> 1, c + 2, abs2);
+                    if (t == 1 || t == 14) tab_read(CQ == 3 ? slot ^ 1 : slot, (CQ + 1) & 3, t == 14);
+                    if (t == 5 || t == 10) b_piece(P ^ 1, 0, t == 10, P ^ 1);
+                    if (t == 20 || t == 25) b_piece(P ^ 1, 1, t == 25, P ^ 1);
+                    if constexpr (CQ == 2) {
+                        if (t == 3) tab_build(slot ^ 1, slot ^ 1);
+                    }
+                    if (t == 17) b_read(std::integral_constant<int, (CQ + 2) & 3>{}, CQ < 2 ? slot : slot ^ 1, P);
+                    if constexpr (CQ == 0) {
+                        // into the slot super-block sb - 1 used (last read in its CQ 1)
+                        if (t >= 18 && t < 18 + 2 * kF16aNI && (t & 1) == 0) w_dma1((t - 18) >> 1, sb + 1, slot ^ 1);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
         }
-        // fp16: this chunk's A DMA (chunk c + 2) is done before the barrier;
-        // the ring DMA issued after it (CQ 0) may stay in flight one chunk
-        if constexpr (A16) {
-            if constexpr (CQ == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kTallNI) : "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        // fp16: every LDS access of the chunk except the last 8 fragment reads
-        // (of chunk c + 1, whose buffer is not written before the next
-        // barrier) is complete -- LDS operations complete in order.  fp32:
-        // the A stores interleave with those reads, so all of them.
-        if constexpr (A16)
-            asm volatile("s_waitcnt lgkmcnt(8)\n\ts_barrier" ::: "memory");
+        // this chunk's A DMA (chunk c + 2) is complete before the barrier; the
+        // ring DMA issued after it (CQ 0) may stay in flight one more chunk
+        if constexpr (CQ == 0)
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kF16aNI) : "memory");
         else
-            lds_barrier();
-        // fp32, CQ 2: chunk c + 2 is the next super-block's first, stored just now
-        if constexpr (!A16 && CQ == 2) b_read(NEXT2{}, slot ^ 1, P);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // every LDS access of the chunk except the last 8 fragment reads (of
+        // chunk c + 1, whose buffer is not written before the next barrier) is
+        // complete -- LDS operations complete in order
+        asm volatile("s_waitcnt lgkmcnt(8)\n\ts_barrier" ::: "memory");
     };
     int ab = 0;                                     // (4 sb) % 3
     for (int sb = 0; sb < nsb; ++sb) {
@@ -1784,47 +1666,67 @@ __global__ __launch_bounds__(kTallThreads) void rf_gemm_q4k_tall_kernel(const vo
     }
 
     // ---- K halves: wave kh = 1 hands row blocks 0-3 to kh = 0, kh = 0 hands
-    // row blocks 4-7 to kh = 1; each then adds and stores its four blocks ----
-    __syncthreads();
+    // row blocks 4-7 to kh = 1; each then adds and stores its four blocks.
     // [wave][block i][col block j][e / 4][lane] of float4: each access is one
-    // contiguous 1 KB per wave (4 waves x 4 x 2 x 4 KB = 128 KB)
-    float4* xch = reinterpret_cast<float4*>(lds);
-    const int give = kh ? 0 : 4, keep = kh ? 4 : 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                xch[(((wave * 4 + i) * 2 + j) * 4 + q) * 64 + lane] =
-                    make_float4(acc[give + i][j][4 * q], acc[give + i][j][4 * q + 1], acc[give + i][j][4 * q + 2],
-                                acc[give + i][j][4 * q + 3]);
+    // contiguous 1 KB per wave (4 waves x 4 x 2 x 4 KB = 128 KB) -------------
+    // (acc indexed by compile-time constants only: one branch per wave half,
+    // the barrier between the halves outside them)
     __syncthreads();
-    const int partner = wave ^ 1;
+    float4* xch = reinterpret_cast<float4*>(lds);
+    auto give_half = [&](auto khc) {
+        constexpr int give = decltype(khc)::value ? 0 : 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int ncol = n0 + 64 * wn + 32 * j + col;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 o4 = xch[(((partner * 4 + i) * 2 + j) * 4 + q) * 64 + lane];
-                const float o[4] = {o4.x, o4.y, o4.z, o4.w};
+                for (int q = 0; q < 4; ++q)
+                    xch[(((wave * 4 + i) * 2 + j) * 4 + q) * 64 + lane] =
+                        make_float4(acc[give + i][j][4 * q], acc[give + i][j][4 * q + 1],
+                                    acc[give + i][j][4 * q + 2], acc[give + i][j][4 * q + 3]);
+    };
+    auto keep_half = [&](auto khc, auto fullc) {
+        constexpr int KH = decltype(khc)::value;
+        constexpr bool FULL = decltype(fullc)::value;     // all 256 rows of the tile below M
+        constexpr int keep = KH ? 4 : 0;
+        const int partner = wave ^ 1;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int e = 4 * q + u;
-                    // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
-                    const float sum = kh ? o[u] + acc[keep + i][j][e] : acc[keep + i][j][e] + o[u];
-                    const int row = m0 + 32 * (keep + i) + 8 * q + 4 * h + u;
-                    float* dst = D + (size_t)row * N + ncol;
-                    if (A16 && row >= M) continue;
-                    if (accum)
-                        *dst += sum;
-                    else
-                        *dst = sum;
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int ncol = n0 + 64 * wn + 32 * j + col;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 o4 = xch[(((partner * 4 + i) * 2 + j) * 4 + q) * 64 + lane];
+                    const float o[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int row = m0 + 32 * (keep + i) + 8 * q + 4 * h + u;
+                        if (!FULL && row >= M) continue;
+                        // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
+                        const float a = acc[keep + i][j][4 * q + u];
+                        D[(size_t)row * N + ncol] = KH ? o[u] + a : a + o[u];
+                    }
                 }
             }
-        }
+    };
+    if (kh)
+        give_half(std::integral_constant<int, 1>{});
+    else
+        give_half(std::integral_constant<int, 0>{});
+    __syncthreads();
+    const bool full = m0 + kF16aBM <= M;
+    if (kh) {
+        if (full)
+            keep_half(std::integral_constant<int, 1>{}, std::true_type{});
+        else
+            keep_half(std::integral_constant<int, 1>{}, std::false_type{});
+    } else {
+        if (full)
+            keep_half(std::integral_constant<int, 0>{}, std::true_type{});
+        else
+            keep_half(std::integral_constant<int, 0>{}, std::false_type{});
+    }
 }
 
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
@@ -1903,14 +1805,6 @@ static void launch_sq(const float* A, const uint8_t* w, float* D, int M, int N, 
                        accum);
 }
 
-// 256 x 128 tiles where they come to one round of about a workgroup per CU
-// (Q4_K, M % 256 == 0, N % 128 == 0)
-static bool tall_fits(int M, int N, int K) {
-    if (M % kTallBM || N % kTallBN || K % kQK) return false;
-    const long tiles = (long)(M / kTallBM) * (N / kTallBN), cus = device_cu_count();
-    return 8 * tiles >= 7 * cus && tiles <= cus;
-}
-
 // sg routes column segments / accumulation (v7 and sq only: the callers of
 // a non-trivial sg have checked N % 256 == 0, K % 512 == 0 and, for Q6_K,
 // K % 2048 == 0, and segments never reach sq)
@@ -1928,10 +1822,7 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
         const long sq_tiles = (long)(M / 256) * (N / 256);
         const long sq128_tiles = (long)(M / 128) * (N / 128);
         const bool sq_ok = sg.n1 == N && sg.n2 == N && !sg.pair;
-        if (!IS_Q6 && sq_ok && tall_fits(M, N, K))
-            hipLaunchKernelGGL(rf_gemm_q4k_tall_kernel<false>, dim3((M / kTallBM) * (N / kTallBN)), dim3(kTallThreads), 0, st,
-                               A, w, D, M, N, K, sg.accum);
-        else if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
+        if (sq_ok && M % 256 == 0 && 8 * sq_tiles >= 7 * cus)
             launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
             launch_sq<IS_Q6, 128, 128>(A, w, D, M, N, K, st, sg.accum);
@@ -1980,13 +1871,13 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
 extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output,
                                               int M, int N, int K, hipStream_t stream) {
     if (input_f16 == nullptr || weights_q4_k == nullptr || output == nullptr) return hipErrorInvalidValue;
-    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kTallBN) != 0 || (K % kQK) != 0)
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kF16aBN) != 0 || (K % kQK) != 0)
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
         return hipErrorInvalidValue;
-    const int tiles = ((M + kTallBM - 1) / kTallBM) * (N / kTallBN);
-    hipLaunchKernelGGL(rf_gemm_q4k_tall_kernel<true>, dim3(tiles), dim3(kTallThreads), 0, stream, input_f16,
-                       static_cast<const uint8_t*>(weights_q4_k), output, M, N, K, 0);
+    const int tiles = ((M + kF16aBM - 1) / kF16aBM) * (N / kF16aBN);
+    hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16,
+                       static_cast<const uint8_t*>(weights_q4_k), output, M, N, K);
     return hipGetLastError();
 }
 

@@ -108,8 +108,8 @@ def test_gemm_llama_ffn_shapes(rf, dev, fmt, n, k, m):
 
 
 @pytest.mark.parametrize("fmt,m,n,k", [
-    ("q4_k", 512, 14336, 512),   # 256 x 128 tiles with the K halves on wave pairs (224 tiles)
-    ("q4_k", 256, 28672, 768),   # the same kernel with one row of tiles, three super-blocks
+    ("q4_k", 512, 14336, 512),   # ring tiles, 128 rows
+    ("q4_k", 256, 28672, 768),   # ring tiles, 128 rows, three super-blocks
     ("q4_k", 128, 512, 2048),    # ring tiles with split-K
     ("q6_k", 512, 4096, 2048),   # ring tiles, 128 rows
 ])
@@ -153,8 +153,8 @@ def test_gemm_q4k_fp16_activations_identity(rf, dev):
 
 
 @pytest.mark.parametrize("fmt,n,k,m,a16", [
-    ("q4_k", 14336, 4096, 512, False),   # 256 x 128 tiles, K halves on wave pairs
-    ("q4_k", 14336, 4096, 512, True),    # the same on fp16 activations
+    ("q4_k", 14336, 4096, 512, False),   # ring tiles, 128 rows
+    ("q4_k", 14336, 4096, 512, True),    # fp16 activations: 256 x 128 tiles, K halves on wave pairs
     ("q4_k", 14336, 4096, 128, False),   # ring tiles of 64 rows, split-K
     ("q6_k", 4096, 14336, 512, False),   # ring tiles of 128 rows
 ])
