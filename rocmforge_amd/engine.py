@@ -90,10 +90,12 @@ def weights_from_gguf(f, device="cuda:0") -> Weights:
     return Weights(mw.token_emb, mw.output_norm, mw.lm_head, layers)
 
 
-def synthetic_weights(cfg: ModelConfig, seed: int = 0, device="cuda:0") -> Weights:
+def synthetic_weights(cfg: ModelConfig, seed: int = 0, device="cuda:0", signed: bool = False) -> Weights:
     """Seeded random weights of the configuration in the Q4_K_M type mix
     (Q6_K attn_v / ffn_down on the layers gguf.q4_k_m_uses_q6_k picks and
-    Q6_K output.weight), generated in device memory."""
+    Q6_K output.weight), generated in device memory.  signed: Q4_K blocks of
+    random sign (synth.torch_weights), which keeps the activations of a deep
+    stack in range."""
     import torch
 
     from . import synth
@@ -105,7 +107,7 @@ def synthetic_weights(cfg: ModelConfig, seed: int = 0, device="cuda:0") -> Weigh
     def mat(n, k, q6=False):
         s[0] += 1
         fmt = "q6_k" if q6 else "q4_k"
-        w = synth.torch_weights(fmt, n, k, seed=s[0], device=device).reshape(-1)
+        w = synth.torch_weights(fmt, n, k, seed=s[0], device=device, signed=signed).reshape(-1)
         return w, WeightMeta(GgmlType.Q6_K if q6 else GgmlType.Q4_K, [k, n])
 
     def norm(n):

@@ -60,8 +60,14 @@ def weights(fmt: str, n: int, k: int, seed: int = 0) -> np.ndarray:
 
 # ---- device-side generator (torch) -----------------------------------------
 
-def torch_weights(fmt: str, n: int, k: int, seed: int, device="cuda"):
-    """Same distributions, generated in device memory (uint8 [n, row_bytes])."""
+def torch_weights(fmt: str, n: int, k: int, seed: int, device="cuda", signed: bool = False):
+    """Same distributions, generated in device memory (uint8 [n, row_bytes]).
+
+    signed: negate half the Q4_K super-blocks at random (the sign bit of both
+    d and dmin, so w -> -w block by block).  The plain distribution has a
+    positive mean per weight (d sc q - dmin m with q, sc, m uniform), which a
+    deep stack of such matrices amplifies until the hidden state is one
+    common-mode vector; signed blocks have mean zero across a row."""
     import torch
 
     g = torch.Generator(device=device)
@@ -77,6 +83,10 @@ def torch_weights(fmt: str, n: int, k: int, seed: int, device="cuda"):
     if fmt == "q4_k":
         blk[:, 0:2] = f16(nb)
         blk[:, 2:4] = f16(nb)
+        if signed:
+            neg = torch.randint(0, 2, (nb,), dtype=torch.uint8, device=device, generator=g) * 0x80
+            blk[:, 1] |= neg
+            blk[:, 3] |= neg
     else:
         sc = torch.randint(-32, 32, (nb, 16), dtype=torch.int8, device=device, generator=g)
         blk[:, 192:208] = sc.view(torch.uint8)

@@ -46,7 +46,7 @@ def _gemv(wm, x, n, k):
 
 @pytest.fixture(scope="module")
 def weights(dev):
-    return E.synthetic_weights(CFG, seed=3)
+    return E.synthetic_weights(CFG, seed=3, signed=True)
 
 
 @pytest.fixture(scope="module")
@@ -55,9 +55,12 @@ def eng(weights):
     return E.Engine(CFG, weights, max_seq=256, fuse_norm=False)
 
 
-def test_decode_step_per_operation(eng):
-    c, w = CFG, eng.w
-    prompt = [5, 77, 1023, 9, 2047, 300, 12]
+def _check_decode_steps(eng, prompt, steps=3, layers=None):
+    """Prefill the prompt, then run decode steps with a trace that checks
+    every operation of the layers in `layers` (all if None), the embedding,
+    the output norm, the LM head and the argmax against the oracle applied to
+    the GPU's own inputs of that operation."""
+    c, w = eng.cfg, eng.w
     eng.prefill(prompt)
     snap = {}
     errs = []
@@ -68,7 +71,9 @@ def test_decode_step_per_operation(eng):
     def trace(name, layer):
         torch.cuda.synchronize()
         pos = int(_h(eng.state)[0])
-        if name == "embed":
+        if layers is not None and layer >= 0 and layer not in layers and name != "embed":
+            pass
+        elif name == "embed":
             tok = int(snap["token"][0])
             ref = O.q4k_dequant(_h(w.token_emb[0]).reshape(c.vocab, -1)[tok], c.hidden // 256)
             errs.append((name, _rel(_h(eng.hidden), ref), 1e-6))
@@ -104,6 +109,7 @@ def test_decode_step_per_operation(eng):
             m = w.layers[layer].mats
             ref = O.silu_mul(_gemv(m["ffn_gate"], snap["normed"], c.ff, c.hidden).astype(np.float32),
                              _gemv(m["ffn_up"], snap["normed"], c.ff, c.hidden).astype(np.float32))
+            assert np.abs(ref).max() > 1e-3, f"gate_up {layer}: vanishing activations, a vacuous check"
             errs.append((f"gate_up {layer}", _rel(_h(eng.act), ref), 1e-5))
         elif name == "lm_head":
             errs.append(("lm_head", _rel(_h(eng.logits), _gemv(w.lm_head, snap["normed"], c.vocab, c.hidden)), 1e-5))
@@ -112,13 +118,43 @@ def test_decode_step_per_operation(eng):
             assert list(_h(eng.state)) == [snap["pos"] + 1, snap["pos"] + 2]
         snap.update(keep("hidden", "normed", "q", "k", "v", "attn", "act"))
 
-    for _ in range(3):
+    for _ in range(steps):
         snap.update(keep("token"))
         snap["pos"] = int(_h(eng.state)[0])
         eng.decode_launches(trace)
     for what, err, bar in errs:
         print(f"{what}: {err:.2e}", flush=True)
         assert err <= bar, f"{what}: {err:.2e} > {bar}"
+    return [what for what, _, _ in errs]
+
+
+def test_decode_step_per_operation(eng):
+    _check_decode_steps(eng, [5, 77, 1023, 9, 2047, 300, 12])
+
+
+def test_decode_step_qwen3_8b_shape(dev):
+    # Qwen3-8B at full size (36 layers, hidden 4096, ff 12288, 32/8 heads,
+    # vocab 151936, Q4_K_M type mix): every operation of layer 0, of the
+    # first all-Q4_K layer, of the first mid-stack layer with Q6_K attn_v /
+    # ffn_down, of the last layer, and the LM head, over two decode steps
+    # after a 9-token prefill
+    from rocmforge_amd.gguf import q4_k_m_uses_q6_k
+    cfg = E.ModelConfig.qwen3_8b()
+    q4 = next(i for i in range(cfg.n_layers) if not q4_k_m_uses_q6_k(i, cfg.n_layers))
+    q6 = next(i for i in range(q4, cfg.n_layers) if q4_k_m_uses_q6_k(i, cfg.n_layers))
+    last = cfg.n_layers - 1
+    e = E.Engine(cfg, E.synthetic_weights(cfg, seed=8, signed=True), max_seq=64, fuse_norm=False)
+    for lay, t in ((0, GgmlType.Q6_K), (q4, GgmlType.Q4_K), (q6, GgmlType.Q6_K)):
+        assert e.w.layers[lay].mats["ffn_down"][1].wtype == t
+        assert e.w.layers[lay].mats["attn_v"][1].wtype == t
+    checked = _check_decode_steps(e, [1, 151935, 4096, 77, 12288, 3, 99999, 5, 42], steps=2,
+                                  layers={0, q4, q6, last})
+    for lay in (0, q4, q6, last):
+        for op in ("attn_q", "attention", "attn_output", "gate_up", "ffn_down"):
+            assert f"{op} {lay}" in checked
+    assert "lm_head" in checked
+    del e
+    torch.cuda.empty_cache()
 
 
 def _snapshot(eng):
@@ -211,6 +247,29 @@ def test_prefill_stages(eng):
             prod = O.gemm(fmt, seen["att"], _h(wm[0]).reshape(c.hidden, -1), M, c.hidden, c.q_size)
             x = _h(b["x"]).reshape(-1, c.hidden)[:M]
             assert _rel(x.astype(np.float64) - seen["x_pre"], prod) <= 2e-3
+            seen["x_att"] = x.copy()
+        elif name == "gate_up":
+            # silu(xn Wg^T) * (xn Wu^T) on the ffn-normalised rows
+            xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
+            assert _rel(xn, O.rms_norm(seen["x_att"], _h(w.layers[0].ffn_norm), c.eps, M)) <= 1e-5
+            m = w.layers[0].mats
+            prods = []
+            for mat in ("ffn_gate", "ffn_up"):
+                wm = m[mat]
+                fmt = "q4_k" if wm[1].wtype == GgmlType.Q4_K else "q6_k"
+                prods.append(O.gemm(fmt, xn, _h(wm[0]).reshape(c.ff, -1), M, c.ff, c.hidden))
+            g, u = prods
+            ref = g / (1.0 + np.exp(-g)) * u
+            got = _h(b["g"]).reshape(-1, c.ff)[:M]
+            assert _rel(got, ref) <= 4e-3
+            seen["act"] = got.copy()
+        elif name == "ffn_down":
+            wm = w.layers[0].mats["ffn_down"]
+            fmt = "q4_k" if wm[1].wtype == GgmlType.Q4_K else "q6_k"
+            prod = O.gemm(fmt, seen["act"], _h(wm[0]).reshape(c.hidden, -1), M, c.hidden, c.ff)
+            x = _h(b["x"]).reshape(-1, c.hidden)[:M]
+            assert _rel(x.astype(np.float64) - seen["x_att"], prod) <= 2e-3
+            seen["ffn_checked"] = True
         elif name == "lm_head":
             xl = _h(b["x"]).reshape(-1, c.hidden)[M - 1]
             nl = O.rms_norm(xl, _h(w.output_norm), c.eps)
@@ -219,6 +278,7 @@ def test_prefill_stages(eng):
             assert int(_h(eng.token)[0]) == O.argmax(_h(eng.logits))
 
     tok = eng.prefill(prompt, trace)
+    assert seen.get("ffn_checked")
     assert list(_h(eng.state)) == [M, M + 1]
     assert 0 <= tok < c.vocab
     assert len(eng.decode(3)) == 3

@@ -95,6 +95,9 @@ def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k, split):
     ("q4_k", 64, 256, 1024),       # 64-row tiles (no K split even where one would pay)
     ("q4_k", 512, 1536, 2048),
     ("q6_k", 128, 256, 2048),
+    ("q6_k", 64, 256, 2048),       # Q6_K, 64-row tiles
+    ("q4_k", 512, 12288, 4096),    # Qwen3-8B gate/up at full size
+    ("q6_k", 256, 12288, 4096),    # the same shape in Q6_K
 ])
 def test_swiglu_pairs(rf, dev, fmt, m, n, k):
     # out = silu(A Wg^T) * (A Wu^T): the products within the GEMM bar of the

@@ -164,6 +164,24 @@ def test_q6k_gemv_residual_in_place(rf, dev, k, n):
     _check(got, O.gemv_q6k(w, x, k, n) + r.astype(np.float64), f"q6 residual {n}x{k}")
 
 
+@pytest.mark.parametrize("n", [128256, 151936])
+def test_q6k_gemv_lm_head(rf, dev, n):
+    # the LM heads of Llama-3.1-8B (128256 x 4096) and Qwen3-8B (151936 x
+    # 4096) at full size, every row against the oracle, and the argmax the
+    # decode step takes from them
+    k = 4096
+    w = synth.q6_k_weights(n, k, seed=n)
+    x = synth.activations(k, seed=n + 1)
+    dw, dx = G.to_dev(w), G.to_dev(x)
+    y = G.empty(n, torch.float32)
+    G.call(rf.gemv_q6_k_f32_launch, G.ptr(dw), G.ptr(dx), G.ptr(y), k, n)
+    got, ref = G.host(y), O.gemv_q6k(w, x, k, n)
+    _check(got, ref, f"q6 lm_head {n}x{k}")
+    top = np.sort(ref)[-2:]
+    if top[1] - top[0] > 1e-4 * abs(top[1]):     # a clear maximum: the same token
+        assert int(np.argmax(got)) == int(np.argmax(ref))
+
+
 def test_q6k_unaligned_blocks(rf, dev):
     # K = 768 gives 630-byte rows: blocks start at every even offset mod 16
     k, n = 768, 40
