@@ -231,17 +231,49 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
     return d;
 }
 
-// 16 weights of one scale group (four dwords of 6-bit values) against 16 x.
-__device__ __forceinline__ float q6_dot16(const uint32_t v[4], const float* xv) {
-    float t = 0.0f;
+// 16 weights of one scale group (four dwords of 6-bit values) against 16 x,
+// the x held pre-scaled by 2^24 (exact), for each of a lane's two runs.  Each 6-bit value is spread into a
+// 16-bit half, where it reads as the fp16 subnormal q * 2^-24 (exact), and
+// v_fma_mix takes that half as its fp16 operand: fma(q * 2^-24, x * 2^24, t)
+// has the product q * x and the rounding of fma((float)q, x, t), so one
+// instruction per weight does what a byte convert and an FMA did.
+// The two runs of a lane (v0 against x0, v1 against x1) as two chains
+// advanced alternately: a v_fma_mix that reads the previous one's result
+// waits a cycle, the other chain's instruction fills it.
+__device__ __forceinline__ void q6_dot16x2(const uint32_t v0[4], const float* x0, const uint32_t v1[4],
+                                           const float* x1, float& t0, float& t1) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    t0 = 0.0f;
+    t1 = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        t += (float)(v[k] & 0xFFu) * xv[4 * k + 0];
-        t += (float)((v[k] >> 8) & 0xFFu) * xv[4 * k + 1];
-        t += (float)((v[k] >> 16) & 0xFFu) * xv[4 * k + 2];
-        t += (float)(v[k] >> 24) * xv[4 * k + 3];
+        // v_perm_b32 selector bytes: 0-3 pick a byte of v, 0x0C a zero
+        const h2 e0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, v0[k], 0x0C020C00u));   // bytes 0, 2
+        const h2 o0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, v0[k], 0x0C030C01u));   // bytes 1, 3
+        const h2 e1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, v1[k], 0x0C020C00u));
+        const h2 o1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, v1[k], 0x0C030C01u));
+        t0 = __builtin_fmaf((float)e0[0], x0[4 * k + 0], t0);
+        t1 = __builtin_fmaf((float)e1[0], x1[4 * k + 0], t1);
+        t0 = __builtin_fmaf((float)o0[0], x0[4 * k + 1], t0);
+        t1 = __builtin_fmaf((float)o1[0], x1[4 * k + 1], t1);
+        t0 = __builtin_fmaf((float)e0[1], x0[4 * k + 2], t0);
+        t1 = __builtin_fmaf((float)e1[1], x1[4 * k + 2], t1);
+        t0 = __builtin_fmaf((float)o0[1], x0[4 * k + 3], t0);
+        t1 = __builtin_fmaf((float)o1[1], x1[4 * k + 3], t1);
     }
-    return t;
+}
+
+// x sums of the two runs (before scaling), then x * 2^24 for q6_dot16x2
+__device__ __forceinline__ void q6_x_prep(float (&xr)[2][16], float (&xs)[2]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += xr[r][i];
+        xs[r] = t;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xr[r][i] *= 16777216.0f;
+    }
 }
 
 
@@ -307,21 +339,15 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_xreg_kernel(const uint8_t* __
             v0[t] = (L[t] & 0x0F0F0F0Fu) | (((Q[t] >> qsh) & 0x03030303u) << 4);
             v1[t] = ((L[t] >> 4) & 0x0F0F0F0Fu) | (((Q[t] >> (qsh + 4)) & 0x03030303u) << 4);
         }
-        float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
-        acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
+        float t0, t1;
+        q6_dot16x2(v0, xr[0], v1, xr[1], t0, t1);
+        float acc = s0 * (t0 - 32.0f * xs[0]);
+        acc += s1 * (t1 - 32.0f * xs[1]);
         const float tot = wave_sum(live ? acc : 0.0f);
         if (lane == 0) part[j * nwk + wave] = tot;
     };
     Q6Lane ring[NB];
-    ring_pipeline<NB>(nrows, ring, load, process, [&]() {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            float t = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) t += xr[r][i];
-            xs[r] = t;
-        }
-    });
+    ring_pipeline<NB>(nrows, ring, load, process, [&]() { q6_x_prep(xr, xs); });
     __syncthreads();
     for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
         float t = 0.0f;
@@ -440,23 +466,17 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
             v0[t] = bfi(0x0F0F0F0Fu, L[t], hm << 4);
             v1[t] = bfi(0x0F0F0F0Fu, L[t] >> 4, hm);
         }
-        float acc = s0 * (q6_dot16(v0, xr[0]) - 32.0f * xs[0]);
-        acc += s1 * (q6_dot16(v1, xr[1]) - 32.0f * xs[1]);
+        float t0, t1;
+        q6_dot16x2(v0, xr[0], v1, xr[1], t0, t1);
+        float acc = s0 * (t0 - 32.0f * xs[0]);
+        acc += s1 * (t1 - 32.0f * xs[1]);
         // the four 16-lane row sums go to LDS (no cross-row broadcast and
         // no read-lane per row); the final pass adds them in fixed order
         const float r16 = row16_sum(acc);
         if ((lane & 15) == 0) part[(j * nwk + wave) * 4 + (lane >> 4)] = r16;
     };
     Q6Seg ring[NB];
-    ring_pipeline<NB>(nrows, ring, load, process, [&]() {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            float t = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) t += xr[r][i];
-            xs[r] = t;
-        }
-    });
+    ring_pipeline<NB>(nrows, ring, load, process, [&]() { q6_x_prep(xr, xs); });
     __syncthreads();
     for (int j = threadIdx.x; j < nrows; j += blockDim.x) {
         float t = 0.0f;
