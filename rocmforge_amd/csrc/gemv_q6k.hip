@@ -419,8 +419,11 @@ __global__ __launch_bounds__(512) void rf_q6k_gemv_lin_kernel(const uint8_t* __r
     const int c1 = min(64 + lane, 104);   // chunks 105..127 re-read chunk 104 (same line), written to the spare area
     auto load = [&](Q6Seg& u, int j) {
         const uint8_t* src = wseg + (size_t)(nrows ? g + min(j, nrows - 1) * G : 0) * row_bytes;
-        u.a = *reinterpret_cast<const u32x4*>(src + 16 * lane);
-        u.b = *reinterpret_cast<const u32x4*>(src + 16 * c1);
+        // nontemporal: each byte is read once; measured 6 % faster than
+        // plain loads for the 4096 x 14336 ffn_down (no line is shared
+        // between load instructions here, unlike the Q4_K unit loads)
+        u.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16 * lane));
+        u.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16 * c1));
     };
     // Aligned LDS reads.  Block b of the stage starts at byte 210b, which
     // is 0 or 2 past a dword boundary (a3); each 16-byte field is read as the
