@@ -355,15 +355,16 @@ def bench_gemm(lib, torch):
             res[f"{fmt}_{n}x{k}_M{m}"] = {"us": round(us, 2), "tflops": round(tflops, 1),
                                           "frac_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
                                           "weight_copies_cycled": copies}
-            if fmt == "q4_k" and m >= 256:
+            if m >= 256:
                 # the same GEMM on activations the caller already rounded to fp16
-                # (rf_gemm_q4_k_f16_launch): identical operands, A read at half the
+                # (rf_gemm_q*_k_f16_launch): identical operands, A read at half the
                 # bytes by LDS DMA
                 a16 = a.half()
+                fn16 = lib.rf_gemm_q4_k_f16_launch if fmt == "q4_k" else lib.rf_gemm_q6_k_f16_launch
 
                 def run16(iters):
                     for i in range(iters):
-                        rc = lib.rf_gemm_q4_k_f16_launch(vp(a16), vp(wsets[i % copies]), vp(d), m, n, k, st)
+                        rc = fn16(vp(a16), vp(wsets[i % copies]), vp(d), m, n, k, st)
                         if rc:
                             raise RuntimeError(f"gemm launch failed {rc}")
 
@@ -377,13 +378,13 @@ def bench_gemm(lib, torch):
                 res[f"{fmt}_{n}x{k}_M{m}_fp16_activations"] = {
                     "us": round(us, 2), "tflops": round(tflops, 1),
                     "frac_fp16_peak": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4),
-                    "launcher": "rf_gemm_q4_k_f16_launch", "weight_copies_cycled": copies}
+                    "launcher": fn16.__name__, "weight_copies_cycled": copies}
     return res
 
 
 def gemm_pmc(lib, torch):
-    """Ten untimed launches of each M = 512 prefill GEMM (Q4_K 14336x4096 on
-    fp32 and on fp16 activations, Q6_K 4096x14336), for counter collection
+    """Ten untimed launches of each M = 512 prefill GEMM (Q4_K 14336x4096 and
+    Q6_K 4096x14336, each on fp32 and on fp16 activations), for counter collection
     under rocprofv3 --pmc."""
     from rocmforge_amd import synth
     dev = torch.device("cuda:0")
@@ -395,10 +396,10 @@ def gemm_pmc(lib, torch):
         d = torch.empty(512, n, device=dev)
         for i in range(10):
             fn(vp(a), vp(wsets[i % 6]), vp(d), 512, n, k, st)
-        if fmt == "q4_k":
-            a16 = a.half()
-            for i in range(10):
-                lib.rf_gemm_q4_k_f16_launch(vp(a16), vp(wsets[i % 6]), vp(d), 512, n, k, st)
+        a16 = a.half()
+        fn16 = lib.rf_gemm_q4_k_f16_launch if fmt == "q4_k" else lib.rf_gemm_q6_k_f16_launch
+        for i in range(10):
+            fn16(vp(a16), vp(wsets[i % 6]), vp(d), 512, n, k, st)
         torch.cuda.synchronize()
     print(json.dumps({"gemm_pmc": "done"}), flush=True)
 

@@ -111,6 +111,16 @@ hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, f
 hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output, int M, int N,
                                    int K, hipStream_t stream);
 
+/* No counterpart (the reference converts A with __float2half inside its
+ * GEMM, wmma_gemm_q6_k.hip:93-100): the Q6_K GEMM on fp16 activations, same
+ * contract as rf_gemm_q4_k_f16_launch -- the operand values of
+ * wmma_gemm_q6_k_launch(fp32 A).  128 x 64 tiles with K split over the
+ * waves of a workgroup: meant for M >= 256 at N = 4096 (one tile per CU at
+ * M = 512).  M % 64 == 0, N % 64 == 0, K % 2048 == 0, input and weights
+ * 16-byte aligned. */
+hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
+                                   int K, hipStream_t stream);
+
 /* No counterpart in the reference (its prefill issues one GEMM per weight
  * and adds residuals with gpu_add).  Several weight matrices that share the
  * input and K in one launch: out_i[M x n_i] = fp16(A) * fp16(dequant W_i)^T

@@ -1729,6 +1729,313 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
     }
 }
 
+// ── q6a: Q6_K GEMM on fp16 activations, 128 x 64 tiles, K slices on waves
+// (rf_gemm_q6_k_f16_launch) ───────────────────────────────────────────────
+// Workgroup = 512 threads (two waves per SIMD) over a 128 (M) x 64 (N) tile:
+// at the Llama-3.1-8B down projection (N = 4096) and M = 512 that is 256
+// workgroups, one per CU, with no split of K across workgroups.  Wave
+// w = 4 cg + ks takes k [16 ks, 16 ks + 16) of every 64-wide chunk for the
+// 128 rows and the 32 columns [32 cg, +32) of the tile (4 MFMAs per chunk),
+// so each weight is dequantised once per workgroup; the four K-slice
+// partials of a column group are added through LDS at the end, in ks order.
+// The second wave on each SIMD issues its dequantisation while the first
+// one's MFMAs run.
+//
+// K order.  Chunk c of a Q6_K row covers k [64 c, 64 c + 64) of super-block
+// c / 4; its 16-group g = 4 (c % 4) + ks holds the elements 128 n + 32 q + l,
+// n = g >> 3, q = (g >> 1) & 3, l in [16 (g & 1), +16): low 4 bits in ql byte
+// 64 n + 32 (q & 1) + l (low nibble for q < 2, high for q >= 2), high 2 bits
+// at bit 2 q of qh byte 32 n + l, sub-block scale sc[g].  Lane half h takes
+// l + 8 h .. l + 8 h + 7: 8 ql bytes and 8 qh bytes of its weight row, the
+// same bytes for chunks 2 n and 2 n + 1 of a super-block.
+//
+// Weights.  Q6_K blocks (210 bytes) start 2-byte aligned.  The ring stage of
+// super-block sb holds, per tile row, the 224-byte 16-byte aligned window
+// that starts at floor16(sb * 210) (the block at byte 2 sb % 16 of it), in a
+// 240-byte LDS row (60 dwords: the 32 rows of a read fall on 8 banks, 4-way),
+// loaded by 16-byte LDS DMA (16 instructions per stage: the DMA costs per
+// instruction, not per byte).  Three stages: super-block
+// sb + 2 loads while sb is used.  K % 2048 == 0 keeps the last window of a
+// row inside it.  A arrives as in rf_gemm_q4k_f16a_kernel
+// (16-byte LDS DMA, XOR-swizzled 128-byte rows), seven chunk buffers deep:
+// a DMA gets four chunks to land.
+//
+// Dequantisation.  The 6-bit values of four weights are assembled in the
+// bytes of a word (the qh field moved to bits 4-5 by one rotate), spread to
+// fp16 subnormal halves q * 2^-24 by v_perm, and fma_mix(q * 2^-24,
+// s * 2^24, -32 s) = s (q - 32) is exact in fp32 (s = d sc has at most 19
+// significant bits), so its fp16 rounding in the same instruction is the
+// reference's value __float2half(d * sc * (q - 32)).
+constexpr int kQ6aThreads = 512;
+constexpr int kQ6aBM = 128, kQ6aBN = 64;
+constexpr int kQ6aRowB = 240;                         // ring bytes per weight row (14 pieces + 1 padding)
+constexpr int kQ6aRingInstr = 16;                     // 16-byte DMAs per stage
+constexpr int kQ6aStage = kQ6aRingInstr * 1024;       // 16384 B
+constexpr int kQ6aRS = 3;                             // ring stages
+constexpr int kQ6aABufs = 7;                          // DMA of chunk c + 6 issued in chunk c
+constexpr int kQ6aLag = kQ6aABufs - 3;                // chunks a DMA may stay in flight
+constexpr int kQ6aABuf = kQ6aBM * kKC * 2;            // 16 KB
+constexpr int kQ6aLdsLoop = kQ6aRS * kQ6aStage + kQ6aABufs * kQ6aABuf;   // 163,840 B
+constexpr int kQ6aLdsXch = 8 * 3 * 4096;              // 98,304 B: three row blocks of each wave's partial
+constexpr int kQ6aLds = kQ6aLdsLoop > kQ6aLdsXch ? kQ6aLdsLoop : kQ6aLdsXch;
+
+// The 4 fp16 weights s (q - 32) of the 6-bit values in the bytes of qb, in
+// byte order, as two packed words.
+__device__ __forceinline__ u32x2 q6a_dq4(uint32_t qb, float S24, float nO) {
+    const f16x2 e = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(qb, qb, 0x0C020C00u));
+    const f16x2 o = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(qb, qb, 0x0C030C01u));
+    f16x2 lo, hi;
+    lo[0] = (_Float16)__builtin_fmaf((float)e[0], S24, nO);
+    lo[1] = (_Float16)__builtin_fmaf((float)o[0], S24, nO);
+    hi[0] = (_Float16)__builtin_fmaf((float)e[1], S24, nO);
+    hi[1] = (_Float16)__builtin_fmaf((float)o[1], S24, nO);
+    return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
+
+__global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint8_t* __restrict__ W,
+                                                                        float* __restrict__ D, int M, int N, int K) {
+    __shared__ __align__(16) uint8_t lds[kQ6aLds];
+    uint8_t* ring = lds;
+    uint8_t* abuf0 = lds + kQ6aRS * kQ6aStage;
+    const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
+    const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = wave & 3, cg = wave >> 2;
+    const int h = lane >> 5, col = lane & 31;
+    const int mtiles = (M + kQ6aBM - 1) / kQ6aBM;
+    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int m0 = (v % mtiles) * kQ6aBM;      // the M tiles of one column tile are neighbours
+    const int n0 = (v / mtiles) * kQ6aBN;
+    const int nchunks = K / kKC;
+    const int nsb = K / kQK;
+    const uint32_t row_bytes = (uint32_t)nsb * kQ6KBytes;
+
+    // ---- weight ring: DMA instruction ii = wave + 8 t moves the 16-byte
+    // pieces [64 ii, 64 ii + 64) of the stage (row i / 15, piece i % 15 of the
+    // row's window; piece 14 and the last 64 pieces are padding and repeat
+    // piece 13) ----------------------------------------------------------------
+    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    constexpr int kRPW = kQ6aRingInstr / 8;   // 2 per wave per super-block
+    uint32_t roff[kRPW];
+#pragma unroll
+    for (int t = 0; t < kRPW; ++t) {
+        const int i = 64 * (wave + 8 * t) + lane;
+        const int r = min(i / 15, 63), pc = i < 960 ? min(i % 15, 13) : 13;
+        roff[t] = (uint32_t)r * row_bytes + 16u * (uint32_t)pc;
+    }
+    auto w_dma1 = [&](int t, int sb, int slot) {
+        const int s = min(sb, nsb - 1);
+        lds_dma16(ring_lds0 + (uint32_t)slot * kQ6aStage + 1024u * (uint32_t)(wave + 8 * t), roff[t],
+                  w_tile + (size_t)((s * kQ6KBytes) & ~15));
+    };
+
+    // ---- A: instruction gi = 2 wave + g covers rows 8 gi + L / 8 of the chunk,
+    // position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row M - 1 --
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    uint32_t dma_voff[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int r = 8 * (2 * wave + g) + (lane >> 3);
+        const int rc = min(r, M - 1 - m0);
+        dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
+    }
+    auto a_dma1 = [&](int g, int c, int buf) {
+        lds_dma16(a_lds0 + (uint32_t)(buf * kQ6aABuf + (2 * wave + g) * 1024), dma_voff[g],
+                  a_tile + (size_t)min(c, nchunks - 1) * kKC * 2);
+    };
+
+    // ---- B: the lane's weight row (column 32 cg + col) in the ring stage of
+    // its super-block (block at byte 2 sb % 16 of the row): raw ql / qh words
+    // of half n (dword reads, shifted into place for odd super-blocks), the
+    // per-super-block factors d * 2^24 and -32 d, and the chunk's sub-block
+    // scale -------------------------------------------------------------------
+    const int brow = 32 * cg + col;
+    uint32_t rql[2], rqh[2];
+    auto raw_read = [&](int n, int sb) {
+        const int off = (2 * sb) & 15;
+        const uint8_t* rowp = ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB;
+        const int oql = off + 64 * n + 16 * ks + 8 * h;
+        const int oqh = off + 128 + 32 * n + 16 * (ks & 1) + 8 * h;
+        const uint32_t* pl = reinterpret_cast<const uint32_t*>(rowp + (oql & ~3));
+        const uint32_t* ph = reinterpret_cast<const uint32_t*>(rowp + (oqh & ~3));
+        if (sb & 1) {
+            const uint32_t l0 = pl[0], l1 = pl[1], l2 = pl[2];
+            const uint32_t h0 = ph[0], h1 = ph[1], h2 = ph[2];
+            rql[0] = __builtin_amdgcn_alignbit(l1, l0, 16);
+            rql[1] = __builtin_amdgcn_alignbit(l2, l1, 16);
+            rqh[0] = __builtin_amdgcn_alignbit(h1, h0, 16);
+            rqh[1] = __builtin_amdgcn_alignbit(h2, h1, 16);
+        } else {
+            rql[0] = pl[0];
+            rql[1] = pl[1];
+            rqh[0] = ph[0];
+            rqh[1] = ph[1];
+        }
+    };
+    float d24 = 0.0f, dm32 = 0.0f;
+    int scb = 0;
+    auto d_read = [&](int sb) {
+        const int off = (2 * sb) & 15;
+        const float d = half_bits_to_float(
+            *reinterpret_cast<const uint16_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 208));
+        d24 = d * 16777216.0f;
+        dm32 = -32.0f * d;
+    };
+    auto sc_read = [&](int cq, int sb) {
+        const int off = (2 * sb) & 15;
+        scb = *reinterpret_cast<const int8_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 192 +
+                                               4 * cq + ks);
+    };
+    // qh field 2q of each byte to bits 4-5: rotate right by (2q - 4) mod 32
+    const uint32_t rot0 = (uint32_t)(2 * (ks >> 1) + 28) & 31u;   // q = ks >> 1 (chunks 0, 2)
+    const uint32_t rot1 = (uint32_t)(2 * (ks >> 1)) & 31u;        // q = 2 + (ks >> 1) (chunks 1, 3)
+    u32x4 bq[2];                          // [chunk parity]
+    auto b_dequant = [&](int t, int P) {
+        const float sc = (float)scb;
+        const float S24 = d24 * sc, nO = dm32 * sc;
+        const uint32_t rot = t ? rot1 : rot0;
+        u32x2 r[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t lo = t ? (rql[i] >> 4) : rql[i];
+            const uint32_t qb = (lo & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(rqh[i], rqh[i], rot) & 0x30303030u);
+            r[i] = q6a_dq4(qb, S24, nO);
+        }
+        bq[P] = u32x4{r[0].x, r[0].y, r[1].x, r[1].y};
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+    // fragment of row block i: row 32 i + col, k piece 2 ks + h at position
+    // (2 ks + h) ^ g(col) of its row
+    const int gcol = (col & 7) ^ ((col >> 3) & 1);
+    f16x8 af[2][4];
+    auto frag_ld = [&](int set, int buf, int i) {
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kQ6aABuf + (32 * i + col) * 128 +
+                                                     16 * ((2 * ks + h) ^ gcol));
+    };
+
+    // ---- prologue: ring stages 0, 1; A chunks 0 .. 5; chunk 0's operands ----
+#pragma unroll
+    for (int t = 0; t < kRPW; ++t) w_dma1(t, 0, 0);
+#pragma unroll
+    for (int t = 0; t < kRPW; ++t) w_dma1(t, 1, 1);
+#pragma unroll
+    for (int c = 0; c < kQ6aABufs - 1; ++c)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) a_dma1(g, c, c);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    raw_read(0, 0);
+    d_read(0);
+    sc_read(0, 0);
+    b_dequant(0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) frag_ld(0, 0, i);
+
+    // Chunk c = 4 sb + CQ uses A buffer c % 7 and ring stage sb % 3.  Its 4
+    // MFMA slots carry: the A fragments of chunk c + 1, the A DMA of chunk
+    // c + 6 (into the buffer chunk c - 1 used), in CQ 0 the ring DMA of
+    // super-block sb + 2 (into the stage sb - 1 used), and the B operands of
+    // chunk c + 1 (raw bytes of half n read in the chunk before 2 n).  At the
+    // end every DMA issued up to chunk c - 4 is complete (vmcnt = the 4 x 2 A
+    // and 2 ring DMAs of the last four chunks), then one barrier: a ring DMA
+    // lands by the end of chunk 4 sb + 4, before the stage's first read in
+    // chunk 4 sb + 7.
+    int ab = 0;                                     // c % 7
+    auto iteration = [&](auto cqc, int sb) {
+        constexpr int CQ = decltype(cqc)::value;
+        constexpr int P = CQ & 1;
+        constexpr int NQ = (CQ + 1) & 3;            // chunk c + 1 within its super-block
+        const int c = 4 * sb + CQ;
+        const int sbn = CQ == 3 ? sb + 1 : sb;
+        const int abn = ab == kQ6aABufs - 1 ? 0 : ab + 1;       // chunk c + 1
+        const int abp = ab == 0 ? kQ6aABufs - 1 : ab - 1;       // chunk c - 1 (= c + 6)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[P][i], __builtin_bit_cast(f16x8, bq[P]), acc[i], 0, 0,
+                                                            0);
+            if (i == 0) {
+                // every LDS read of chunk c + 1 right after the first MFMA
+                if constexpr ((NQ & 1) == 0) raw_read(NQ >> 1, sbn);
+                if constexpr (NQ == 0) d_read(sbn);
+                sc_read(NQ, sbn);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) frag_ld(P ^ 1, abn, r);
+            }
+            if (i < 2) a_dma1(i, c + kQ6aABufs - 1, abp);
+            if constexpr (CQ == 0) {
+                if (i < kRPW) w_dma1(i, sb + 2, (sb + 2) % kQ6aRS);
+            }
+            if (i == 3) b_dequant(NQ & 1, P ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kQ6aLag + kRPW) : "memory");
+        lds_barrier();
+        ab = abn;
+    };
+    for (int sb = 0; sb < nsb; ++sb) {
+        iteration(std::integral_constant<int, 0>{}, sb);
+        iteration(std::integral_constant<int, 1>{}, sb);
+        iteration(std::integral_constant<int, 2>{}, sb);
+        iteration(std::integral_constant<int, 3>{}, sb);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- K slices: wave (ks, cg) keeps row block ks and hands the other three
+    // to the waves of its column group; [src wave][slot 0..2][e / 4][lane] of
+    // float4 (each access one contiguous 1 KB per wave) -----------------------
+    __syncthreads();
+    float4* xch = reinterpret_cast<float4*>(lds);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i == ks) continue;
+        const int slot = i < ks ? i : i - 1;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            xch[((wave * 3 + slot) * 4 + q) * 64 + lane] =
+                make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
+    }
+    __syncthreads();
+    // block ks of the column group: partials of ks' = 0..3 added in that order
+    f32x16 own = acc[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (i == ks) own = acc[i];
+    const int ncol = n0 + 32 * cg + col;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int src = 0; src < 4; ++src) {
+            float4 p;
+            if (src == ks) {
+                p = make_float4(own[4 * q], own[4 * q + 1], own[4 * q + 2], own[4 * q + 3]);
+            } else {
+                const int slot = ks < src ? ks : ks - 1;
+                p = xch[(((4 * cg + src) * 3 + slot) * 4 + q) * 64 + lane];
+            }
+            s[0] += p.x;
+            s[1] += p.y;
+            s[2] += p.z;
+            s[3] += p.w;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
+            if (row < M) D[(size_t)row * N + ncol] = s[u];
+        }
+    }
+}
+
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
 // 8-chunk groups) and tiles * S <= CUs (one workgroup per CU; the kernel
 // runs one 512-thread workgroup per CU).  Measured on MI355X at the
@@ -1878,6 +2185,21 @@ extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const v
     const int tiles = ((M + kF16aBM - 1) / kF16aBM) * (N / kF16aBN);
     hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16,
                        static_cast<const uint8_t*>(weights_q4_k), output, M, N, K);
+    return hipGetLastError();
+}
+
+// Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,
+// K % 2048 (weight rows 16-byte aligned); A and the weights 16-byte aligned.
+extern "C" hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output,
+                                              int M, int N, int K, hipStream_t stream) {
+    if (input_f16 == nullptr || weights_q6_k == nullptr || output == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ6aBN) != 0 || (K % 2048) != 0)
+        return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 15u))
+        return hipErrorInvalidValue;
+    const int tiles = ((M + kQ6aBM - 1) / kQ6aBM) * (N / kQ6aBN);
+    hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel, dim3(tiles), dim3(kQ6aThreads), 0, stream, input_f16,
+                       static_cast<const uint8_t*>(weights_q6_k), output, M, N, K);
     return hipGetLastError();
 }
 

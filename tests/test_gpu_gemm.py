@@ -10,6 +10,8 @@ by up to K * 2^-24 * S; the MFMA sums measure below 1e-5 * S), so outputs that
 cancel to near zero are judged against the size of what cancelled.  The
 operands themselves are pinned bit for bit by the identity tests below.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -139,6 +141,33 @@ def test_gemm_q4k_fp16_activations(rf, dev, m, n, k):
     _check(G.host(d).reshape(m, n), "q4_k", a, w, m, n, k, f"fp16-A q4_k M={m} {n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 14336), (256, 4096, 14336), (64, 4096, 14336), (192, 1024, 2048),
+                                   (576, 128, 4096), (128, 64, 2048)])
+def test_gemm_q6k_fp16_activations(rf, dev, m, n, k):
+    # rf_gemm_q6_k_f16_launch: the operands of wmma_gemm_q6_k_launch on fp32 A
+    # rounded to fp16 by the caller; M = 192 and 576 leave a partial 128-row tile
+    a = torch.from_numpy(synth.activations(k, seed=m + 13, m=m)).to(torch.bfloat16).float().numpy()
+    w = synth.weights("q6_k", n, k, seed=k + 9)
+    da, dw = G.to_dev(a.astype(np.float16).view(np.int16)), G.to_dev(w)
+    d = G.empty(m * n, torch.float32)
+    G.call(rf.rf_gemm_q6_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
+    _check(G.host(d).reshape(m, n), "q6_k", a, w, m, n, k, f"fp16-A q6_k M={m} {n}x{k}")
+
+
+def test_gemm_q6k_fp16_rejections(rf, dev):
+    d = G.empty(64 * 64, torch.float32)
+    a = G.to_dev(np.zeros((64, 4096), np.int16))
+    w = G.to_dev(synth.weights("q6_k", 64, 4096, seed=1))
+    f = rf.rf_gemm_q6_k_f16_launch
+    s = G.stream()
+    assert f(G.ptr(a), G.ptr(w), G.ptr(d), 64, 64, 1024, s) != 0       # K % 2048
+    assert f(G.ptr(a), G.ptr(w), G.ptr(d), 64, 32, 4096, s) != 0       # N % 64
+    assert f(G.ptr(a), G.ptr(w), G.ptr(d), 96, 64, 4096, s) != 0       # M % 64
+    assert f(ctypes.c_void_p(a.data_ptr() + 2), G.ptr(w), G.ptr(d), 64, 64, 4096, s) != 0   # A alignment
+    assert f(G.ptr(a), ctypes.c_void_p(w.data_ptr() + 4), G.ptr(d), 64, 64, 4096, s) != 0   # weight alignment
+    assert f(None, G.ptr(w), G.ptr(d), 64, 64, 4096, s) != 0
+
+
 def test_gemm_q4k_fp16_activations_identity(rf, dev):
     # A = [I | 0] in fp16: D[r, c] = dequantised W[c, r] bit for bit (the
     # natural-order B operands of the fp16 path)
@@ -157,6 +186,7 @@ def test_gemm_q4k_fp16_activations_identity(rf, dev):
     ("q4_k", 14336, 4096, 512, True),    # fp16 activations: 256 x 128 tiles, K halves on wave pairs
     ("q4_k", 14336, 4096, 128, False),   # ring tiles of 64 rows, split-K
     ("q6_k", 4096, 14336, 512, False),   # ring tiles of 128 rows
+    ("q6_k", 4096, 14336, 512, True),    # fp16 activations: 128 x 64 tiles, K slices on waves
 ])
 def test_gemm_every_weight_at_full_size(rf, dev, fmt, n, k, m, a16):
     # A = I over successive m-column windows of K: D = W^T window by window,
@@ -172,7 +202,8 @@ def test_gemm_every_weight_at_full_size(rf, dev, fmt, n, k, m, a16):
         a = np.zeros((m, k), np.float16 if a16 else np.float32)
         a[np.arange(m), b * m + np.arange(m)] = 1.0
         if a16:
-            G.call(rf.rf_gemm_q4_k_f16_launch, G.ptr(G.to_dev(a.view(np.int16))), G.ptr(dw), G.ptr(d), m, n, k)
+            fn = rf.rf_gemm_q4_k_f16_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_f16_launch
+            G.call(fn, G.ptr(G.to_dev(a.view(np.int16))), G.ptr(dw), G.ptr(d), m, n, k)
         else:
             fn = rf.wmma_gemm_q4_k_launch if fmt == "q4_k" else rf.wmma_gemm_q6_k_launch
             G.call(fn, G.ptr(G.to_dev(a)), G.ptr(dw), G.ptr(d), m, n, k)
