@@ -120,6 +120,13 @@ hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weight
  * 16-byte aligned. */
 hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
                                    int K, hipStream_t stream);
+/* No counterpart: inout[M x N] += the product of rf_gemm_q6_k_f16_launch (the
+ * reference's prefill adds residuals with gpu_add).  Each output is read and
+ * written once after its fp32 sum, so the result is inout + that launch's
+ * output bit for bit.  Same shape rules.  Used for the FFN down projection of
+ * a prefill, into the residual stream. */
+hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
+                                              int M, int N, int K, hipStream_t stream);
 
 /* No counterpart in the reference (its prefill issues one GEMM per weight
  * and adds residuals with gpu_add).  Several weight matrices that share the
@@ -150,6 +157,15 @@ hipError_t rf_gemm_q4_k_swiglu_launch(const float* input, const void* w_gate, co
                                       int N, int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out, int M,
                                       int N, int K, hipStream_t stream);
+/* The same paired launches with the output rounded to fp16 (round to nearest
+ * even, bit patterns as uint16_t): out_f16[M x N] = __float2half(silu(gate) *
+ * up) of the fp32 launchers' values -- the operand values the reference's
+ * down-projection GEMM makes from fp32 with __float2half, ready for
+ * rf_gemm_q6_k_f16_accumulate_launch. */
+hipError_t rf_gemm_q4_k_swiglu_f16_launch(const float* input, const void* w_gate, const void* w_up, uint16_t* out_f16,
+                                          int M, int N, int K, hipStream_t stream);
+hipError_t rf_gemm_q6_k_swiglu_f16_launch(const float* input, const void* w_gate, const void* w_up, uint16_t* out_f16,
+                                          int M, int N, int K, hipStream_t stream);
 
 /* ---- Host dispatch (routing of the arms above) --------------------------
  * C counterparts of ROCmForge's src/gpu/ops.rs routing for the Q4_K / Q6_K

@@ -31,12 +31,15 @@ SIGNATURES = {
     "wmma_gemm_q6_k_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q4_k_f16_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_f16_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q6_k_f16_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q4_k_segments_launch": [_vp] * 7 + [_i] * 5 + [_vp],
     "rf_gemm_q6_k_segments_launch": [_vp] * 7 + [_i] * 5 + [_vp],
     "rf_gemm_q4_k_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q4_k_swiglu_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_swiglu_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q4_k_swiglu_f16_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q6_k_swiglu_f16_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemv_q4_k_q8_rmsnorm_launch": [_vp, _vp, _vp, _f, _vp, _i, _i, _vp],
     "rf_gemv_gate_up_q4_k_q8_rmsnorm_launch": [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _vp],
     "rf_gemv_qkv_q4_k_q8_rmsnorm_launch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i,

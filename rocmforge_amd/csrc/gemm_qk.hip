@@ -691,7 +691,8 @@ struct RingGeom7 {
 // adds).  pair != 0 (one segment, no K split): the N columns are N/2 gate
 // rows (W) and N/2 up rows (w1) taken 128 at a time -- tile j covers gate
 // rows [128j, +128) on waves 0-1 and the same up rows on waves 2-3 -- and
-// D[M x N/2] = silu(gate) * up.
+// D[M x N/2] = silu(gate) * up; pair == 2 stores that fp32 value rounded to
+// fp16 (round to nearest even) into D read as an array of halves.
 struct GemmSegs {
     const uint8_t* w1;
     const uint8_t* w2;
@@ -1102,7 +1103,11 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
                         const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                         const float g = acc[i][j][e];
                         const float u = xch[(wave * NE + (i * FN + j) * 16 + e) * 64 + lane];
-                        D[(size_t)row * ldo + col] = g / (1.0f + expf(-g)) * u;
+                        const float v = g / (1.0f + expf(-g)) * u;
+                        if (segs.pair == 2)
+                            reinterpret_cast<_Float16*>(D)[(size_t)row * ldo + col] = (_Float16)v;
+                        else
+                            D[(size_t)row * ldo + col] = v;
                     }
                 }
         }
@@ -1792,6 +1797,7 @@ __device__ __forceinline__ u32x2 q6a_dq4(uint32_t qb, float S24, float nO) {
     return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
+template <bool ACC>
 __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ W,
                                                                         float* __restrict__ D, int M, int N, int K) {
@@ -2031,7 +2037,10 @@ __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uin
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
-            if (row < M) D[(size_t)row * N + ncol] = s[u];
+            if (row < M) {
+                float* o = D + (size_t)row * N + ncol;
+                *o = ACC ? *o + s[u] : s[u];
+            }
         }
     }
 }
@@ -2190,17 +2199,30 @@ extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const v
 
 // Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,
 // K % 2048 (weight rows 16-byte aligned); A and the weights 16-byte aligned.
-extern "C" hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output,
-                                              int M, int N, int K, hipStream_t stream) {
+template <bool ACC>
+static hipError_t gemm_q6_f16(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
+                              int K, hipStream_t stream) {
     if (input_f16 == nullptr || weights_q6_k == nullptr || output == nullptr) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ6aBN) != 0 || (K % 2048) != 0)
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 15u))
         return hipErrorInvalidValue;
     const int tiles = ((M + kQ6aBM - 1) / kQ6aBM) * (N / kQ6aBN);
-    hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel, dim3(tiles), dim3(kQ6aThreads), 0, stream, input_f16,
+    hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<ACC>, dim3(tiles), dim3(kQ6aThreads), 0, stream, input_f16,
                        static_cast<const uint8_t*>(weights_q6_k), output, M, N, K);
     return hipGetLastError();
+}
+
+extern "C" hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output,
+                                              int M, int N, int K, hipStream_t stream) {
+    return gemm_q6_f16<false>(input_f16, weights_q6_k, output, M, N, K, stream);
+}
+
+// inout[M x N] += fp16(A) * fp16(dequant W)^T: each output read and written
+// once, after its fp32 sum (no K split: reproducible bit for bit).
+extern "C" hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k,
+                                                         float* inout, int M, int N, int K, hipStream_t stream) {
+    return gemm_q6_f16<true>(input_f16, weights_q6_k, inout, M, N, K, stream);
 }
 
 extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,
@@ -2276,24 +2298,37 @@ extern "C" hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const v
 }
 
 template <bool IS_Q6>
-static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, float* D, int M, int N, int K,
-                              hipStream_t st) {
+static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, void* D, int M, int N, int K,
+                              hipStream_t st, bool f16_out) {
     if (!seg_shape_ok<IS_Q6>(A, M, K) || !wg || !wu || !D || N <= 0 || N % 128 || !aligned16(D))
         return hipErrorInvalidValue;
     const uintptr_t wal = IS_Q6 ? 1u : 15u;
     if ((reinterpret_cast<uintptr_t>(wg) & wal) || (reinterpret_cast<uintptr_t>(wu) & wal)) return hipErrorInvalidValue;
     GemmSegs sg = single_seg(2 * N);
     sg.w1 = static_cast<const uint8_t*>(wu);
-    sg.pair = 1;
-    return launch_gemm<IS_Q6>(A, wg, D, M, 2 * N, K, st, sg);
+    sg.pair = f16_out ? 2 : 1;
+    return launch_gemm<IS_Q6>(A, wg, static_cast<float*>(D), M, 2 * N, K, st, sg);
 }
 
 extern "C" hipError_t rf_gemm_q4_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out,
                                                  int M, int N, int K, hipStream_t stream) {
-    return gemm_swiglu<false>(input, w_gate, w_up, out, M, N, K, stream);
+    return gemm_swiglu<false>(input, w_gate, w_up, out, M, N, K, stream, false);
 }
 
 extern "C" hipError_t rf_gemm_q6_k_swiglu_launch(const float* input, const void* w_gate, const void* w_up, float* out,
                                                  int M, int N, int K, hipStream_t stream) {
-    return gemm_swiglu<true>(input, w_gate, w_up, out, M, N, K, stream);
+    return gemm_swiglu<true>(input, w_gate, w_up, out, M, N, K, stream, false);
+}
+
+// The paired gate/up GEMM with its SwiGLU output rounded to fp16 (the
+// operand the next GEMM's fp16 path reads): out_f16[M x N] holds
+// __float2half(silu(gate) * up) of the fp32 launcher's values.
+extern "C" hipError_t rf_gemm_q4_k_swiglu_f16_launch(const float* input, const void* w_gate, const void* w_up,
+                                                     uint16_t* out_f16, int M, int N, int K, hipStream_t stream) {
+    return gemm_swiglu<false>(input, w_gate, w_up, out_f16, M, N, K, stream, true);
+}
+
+extern "C" hipError_t rf_gemm_q6_k_swiglu_f16_launch(const float* input, const void* w_gate, const void* w_up,
+                                                     uint16_t* out_f16, int M, int N, int K, hipStream_t stream) {
+    return gemm_swiglu<true>(input, w_gate, w_up, out_f16, M, N, K, stream, true);
 }

@@ -194,6 +194,7 @@ class Engine:
         _chk(self.lib.rf_rope_theta_table(_p(self.theta), c.head_dim, c.rope_base, self._stream()), "theta table")
         self._graph = None
         self._pf = None
+        self._act16 = False      # the last prefill layer's SwiGLU output went to the fp16 buffer
 
     # ---- decode ---------------------------------------------------------------------------
     def _stream(self):
@@ -365,7 +366,7 @@ class Engine:
                     "k": z(mp * c.kv_size), "v": z(mp * c.kv_size), "q16": z(mp * c.q_size, torch.int16),
                     "k16": z(mp * c.kv_size, torch.int16), "v16": z(mp * c.kv_size, torch.int16),
                     "att": z(mp * c.q_size), "tmp": z(mp * c.hidden), "g": z(mp * c.ff), "u": z(mp * c.ff),
-                    "ids": z(mp, torch.int32)}
+                    "g16": z(mp * c.ff, torch.int16), "ids": z(mp, torch.int32)}
         return self._pf
 
     def prefill(self, tokens, trace=None) -> int:
@@ -438,7 +439,15 @@ class Engine:
             _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp, st),
                  "norm")
             gt, ut = m["ffn_gate"][1].wtype, m["ffn_up"][1].wtype
-            if gt == ut and c.ff % 128 == 0 and self._fusable(gt, 256, c.hidden):
+            pair = gt == ut and c.ff % 128 == 0 and self._fusable(gt, 256, c.hidden)
+            # a Q6_K down projection reads the SwiGLU output as fp16 (the operand its
+            # fp32 launcher would round it to) through the 128 x 64-tile kernel
+            self._act16 = pair and self._down_f16(m["ffn_down"][1].wtype)
+            if self._act16:
+                fn = L.rf_gemm_q4_k_swiglu_f16_launch if gt == GgmlType.Q4_K else L.rf_gemm_q6_k_swiglu_f16_launch
+                _chk(fn(_p(b["xn"]), _p(m["ffn_gate"][0]), _p(m["ffn_up"][0]), _p(b["g16"]), mp, c.ff, c.hidden,
+                        st), "gemm swiglu f16")
+            elif pair:
                 # gate and up in one launch, SwiGLU in its epilogue
                 fn = L.rf_gemm_q4_k_swiglu_launch if gt == GgmlType.Q4_K else L.rf_gemm_q6_k_swiglu_launch
                 _chk(fn(_p(b["xn"]), _p(m["ffn_gate"][0]), _p(m["ffn_up"][0]), _p(b["g"]), mp, c.ff, c.hidden, st),
@@ -448,7 +457,11 @@ class Engine:
                 self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
                 _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             t("gate_up", i)
-            self._gemm_residual(m["ffn_down"], b["g"], b["x"], b["tmp"], c.hidden, c.ff, M, st)
+            if self._act16:
+                _chk(L.rf_gemm_q6_k_f16_accumulate_launch(_p(b["g16"]), _p(m["ffn_down"][0]), _p(b["x"]), mp,
+                                                          c.hidden, c.ff, st), "gemm f16 accumulate")
+            else:
+                self._gemm_residual(m["ffn_down"], b["g"], b["x"], b["tmp"], c.hidden, c.ff, M, st)
             t("ffn_down", i)
         last = ctypes.c_void_p(b["x"].data_ptr() + 4 * (M - 1) * c.hidden)
         _chk(L.gpu_rms_norm(last, _p(self.w.output_norm), _p(self.normed), c.hidden, c.eps, st), "norm")
@@ -460,6 +473,12 @@ class Engine:
         t("lm_head", -1)
         torch.cuda.synchronize()
         return int(self.token.item())
+
+    def _down_f16(self, wtype):
+        """The FFN down projection on fp16 activations: Q6_K with K = ff a
+        multiple of 2048 and N = hidden of 64 (rf_gemm_q6_k_f16_accumulate_launch)."""
+        c = self.cfg
+        return self.fuse_gemm and wtype == GgmlType.Q6_K and c.ff % 2048 == 0 and c.hidden % 64 == 0
 
     def _fusable(self, wtype, n, k):
         return (self.fuse_gemm and wtype in (GgmlType.Q4_K, GgmlType.Q6_K) and n % 256 == 0

@@ -207,23 +207,24 @@ def test_fused_norm_decode_equals_separate(weights, eng):
         assert np.array_equal(_h(a), _h(b))
 
 
-def test_prefill_stages(eng):
-    c, w = CFG, eng.w
+def _check_prefill_stages(eng, lay):
+    # every stage of layer `lay`, the embedding and the LM head against the oracle
+    c, w = eng.cfg, eng.w
     prompt = [int(t) for t in np.random.default_rng(1).integers(0, c.vocab, 100)]
     M = len(prompt)
     seen = {}
 
     def trace(name, layer):
         torch.cuda.synchronize()
-        if layer not in (0, -1):
+        if layer not in (lay, -1):
             return
         b = eng._pf
-        if name == "embed":
-            seen["x0"] = _h(b["x"]).reshape(-1, c.hidden)[:M].copy()
-        elif name == "qkv":
+        if name == "qkv":
+            # x is the layer's input until the O product is added
+            x_in = _h(b["x"]).reshape(-1, c.hidden)[:M]
             xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
-            assert _rel(xn, O.rms_norm(seen["x0"], _h(w.layers[0].attn_norm), c.eps, M)) <= 1e-5
-            m = w.layers[0].mats
+            assert _rel(xn, O.rms_norm(x_in, _h(w.layers[lay].attn_norm), c.eps, M)) <= 1e-5
+            m = w.layers[lay].mats
             for buf, mat, n in (("q", "attn_q", c.q_size), ("k", "attn_k", c.kv_size), ("v", "attn_v", c.kv_size)):
                 wm = m[mat]
                 fmt = "q4_k" if wm[1].wtype == GgmlType.Q4_K else "q6_k"
@@ -237,12 +238,12 @@ def test_prefill_stages(eng):
             ref = O.attn_prefill_f16(q, k, v, M, c.n_heads, c.n_kv_heads, c.head_dim, eng.scale)
             got = _h(b["att"]).reshape(-1, c.q_size)[:M]
             assert _rel(got, ref) <= 2e-3
-            kc = _h(eng.kc[0]).view(np.uint16).reshape(-1, c.kv_size)[:M]
+            kc = _h(eng.kc[lay]).view(np.uint16).reshape(-1, c.kv_size)[:M]
             assert np.array_equal(kc, k.astype(np.float16).view(np.uint16))
             seen["x_pre"], seen["att"] = _h(b["x"]).reshape(-1, c.hidden)[:M].copy(), got.copy()
         elif name == "attn_output":
             # the O product added into the residual stream (one accumulating GEMM)
-            wm = w.layers[0].mats["attn_output"]
+            wm = w.layers[lay].mats["attn_output"]
             fmt = "q4_k" if wm[1].wtype == GgmlType.Q4_K else "q6_k"
             prod = O.gemm(fmt, seen["att"], _h(wm[0]).reshape(c.hidden, -1), M, c.hidden, c.q_size)
             x = _h(b["x"]).reshape(-1, c.hidden)[:M]
@@ -251,8 +252,8 @@ def test_prefill_stages(eng):
         elif name == "gate_up":
             # silu(xn Wg^T) * (xn Wu^T) on the ffn-normalised rows
             xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
-            assert _rel(xn, O.rms_norm(seen["x_att"], _h(w.layers[0].ffn_norm), c.eps, M)) <= 1e-5
-            m = w.layers[0].mats
+            assert _rel(xn, O.rms_norm(seen["x_att"], _h(w.layers[lay].ffn_norm), c.eps, M)) <= 1e-5
+            m = w.layers[lay].mats
             prods = []
             for mat in ("ffn_gate", "ffn_up"):
                 wm = m[mat]
@@ -260,11 +261,13 @@ def test_prefill_stages(eng):
                 prods.append(O.gemm(fmt, xn, _h(wm[0]).reshape(c.ff, -1), M, c.ff, c.hidden))
             g, u = prods
             ref = g / (1.0 + np.exp(-g)) * u
-            got = _h(b["g"]).reshape(-1, c.ff)[:M]
+            # (fp16 when the down projection reads it so: one more rounding)
+            got = (_h(b["g16"]).view(np.float16) if eng._act16 else _h(b["g"])).reshape(-1, c.ff)[:M]
             assert _rel(got, ref) <= 4e-3
+            seen["act16"] = eng._act16
             seen["act"] = got.copy()
         elif name == "ffn_down":
-            wm = w.layers[0].mats["ffn_down"]
+            wm = w.layers[lay].mats["ffn_down"]
             fmt = "q4_k" if wm[1].wtype == GgmlType.Q4_K else "q6_k"
             prod = O.gemm(fmt, seen["act"], _h(wm[0]).reshape(c.hidden, -1), M, c.hidden, c.ff)
             x = _h(b["x"]).reshape(-1, c.hidden)[:M]
@@ -282,6 +285,20 @@ def test_prefill_stages(eng):
     assert list(_h(eng.state)) == [M, M + 1]
     assert 0 <= tok < c.vocab
     assert len(eng.decode(3)) == 3
+    return seen
+
+
+def test_prefill_stages(eng):
+    assert not _check_prefill_stages(eng, 0)["act16"]
+
+
+def test_prefill_stages_f16_down(dev):
+    # ff % 2048 == 0 and a Q6_K down projection (layer 2 of 3 under the Q4_K_M
+    # rule): SwiGLU to fp16, the fp16-activation down GEMM into the residual
+    cfg = E.ModelConfig(n_layers=3, hidden=512, ff=2048, n_heads=4, n_kv_heads=2, head_dim=128, vocab=2048)
+    e = E.Engine(cfg, E.synthetic_weights(cfg, seed=12, signed=True), max_seq=256, fuse_norm=False)
+    assert e.w.layers[2].mats["ffn_down"][1].wtype == GgmlType.Q6_K
+    assert _check_prefill_stages(e, 2)["act16"]
 
 
 def test_gguf_model_decodes_like_memory_weights(dev, tmp_path):

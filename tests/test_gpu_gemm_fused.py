@@ -128,6 +128,44 @@ def test_swiglu_pairs(rf, dev, fmt, m, n, k):
     assert np.allclose(got, sil, rtol=1e-5, atol=1e-6 * np.abs(sil).max())
 
 
+@pytest.mark.parametrize("fmt,m,n,k", [("q4_k", 512, 12288, 4096), ("q4_k", 64, 256, 1024), ("q6_k", 128, 256, 2048)])
+def test_swiglu_pairs_f16_out(rf, dev, fmt, m, n, k):
+    # rf_gemm_q*_k_swiglu_f16_launch: the fp32 launcher's values rounded to
+    # fp16 (nearest even), bit for bit
+    a = synth.activations(k, seed=m + n + 3, m=m)
+    wg = synth.weights(fmt, n, k, seed=31)
+    wu = synth.weights(fmt, n, k, seed=32)
+    da, dg, du = G.to_dev(a), G.to_dev(wg), G.to_dev(wu)
+    d32 = G.empty(m * n, torch.float32)
+    d16 = G.empty(m * n, torch.int16)
+    f32 = rf.rf_gemm_q4_k_swiglu_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_swiglu_launch
+    f16 = rf.rf_gemm_q4_k_swiglu_f16_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_swiglu_f16_launch
+    G.call(f32, G.ptr(da), G.ptr(dg), G.ptr(du), G.ptr(d32), m, n, k)
+    G.call(f16, G.ptr(da), G.ptr(dg), G.ptr(du), G.ptr(d16), m, n, k)
+    want = G.host(d32).astype(np.float16)
+    got = G.host(d16).view(np.float16)
+    np.testing.assert_array_equal(got.view(np.int16), want.view(np.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 12288), (192, 128, 2048)])
+def test_q6k_f16_accumulate(rf, dev, m, n, k):
+    # inout += product: bit for bit the plain fp16-activation launch plus the
+    # old contents (one fp32 add per output), and within the GEMM bar of the
+    # oracle; M = 192 leaves a partial 128-row tile whose rows past M stay put
+    a = torch.from_numpy(synth.activations(k, seed=m + 17, m=m)).to(torch.bfloat16).float().numpy()
+    w = synth.weights("q6_k", n, k, seed=k + 3)
+    da, dw = G.to_dev(a.astype(np.float16).view(np.int16)), G.to_dev(w)
+    r = synth.activations(n, seed=5, m=m + 64)
+    dr = G.to_dev(r)
+    G.call(rf.rf_gemm_q6_k_f16_accumulate_launch, G.ptr(da), G.ptr(dw), G.ptr(dr), m, n, k)
+    d = G.empty(m * n, torch.float32)
+    G.call(rf.rf_gemm_q6_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
+    got = G.host(dr).reshape(m + 64, n)
+    np.testing.assert_array_equal(got[:m], r[:m] + G.host(d).reshape(m, n))
+    np.testing.assert_array_equal(got[m:], r[m:])
+    _check(got[:m], O.gemm("q6_k", a, w, m, n, k), f"q6_k f16 accumulate {m}x{n}x{k}", base=r[:m])
+
+
 def test_rejections(rf, dev):
     m, k = 64, 512
     da = G.to_dev(synth.activations(k, seed=1, m=m))
