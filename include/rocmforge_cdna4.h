@@ -289,6 +289,12 @@ hipError_t gpu_rms_norm_batched(const float* d_x, const float* d_weight, float* 
                                 const int seq_len);
 hipError_t gpu_rms_norm_batched_on_stream(const float* d_x, const float* d_weight, float* d_out, const int n,
                                           const float eps, const int seq_len, hipStream_t stream);
+/* No counterpart: the batched norm with its output rounded to fp16 (round to
+ * nearest even, bit patterns as uint16_t) -- the operand values a prefill
+ * GEMM on fp16 activations (rf_gemm_q4_k_f16_launch) reads, identical to the
+ * fp32 GEMM's own __float2half of gpu_rms_norm_batched_on_stream's output. */
+hipError_t rf_rms_norm_batched_f16_on_stream(const float* d_x, const float* d_weight, uint16_t* d_out_f16,
+                                             const int n, const float eps, const int seq_len, hipStream_t stream);
 
 /* hip_kernels/rope.hip:293-420 -- RoPE over [num_heads][head_dim] in place;
  * neox != 0: pairs (i, i + d/2), else (2i, 2i + 1); freq_scale divides theta_i. */
@@ -458,6 +464,9 @@ hipError_t convert_f32_to_f16(const float* input, void* output, int n, hipStream
  * src/gpu/forward.rs:1133-1143): out = silu(gate) * up. */
 hipError_t rf_silu_mul_on_stream(const float* d_gate, const float* d_up, float* d_out, const int n,
                                  hipStream_t stream);
+/* No counterpart: the same with the result rounded to fp16 (nearest even). */
+hipError_t rf_silu_mul_f16_on_stream(const float* d_gate, const float* d_up, uint16_t* d_out_f16, const int n,
+                                     hipStream_t stream);
 
 /* hip_kernels/wmma/wmma_attention_prefill.hip:711 -- causal (or full) GQA
  * attention over seq_len % 64 == 0 rows: Q [seq][nq*128], K, V [seq][nkv*128]

@@ -48,6 +48,7 @@ SIGNATURES = {
     "gpu_rms_norm": [_vp, _vp, _vp, _i, _f, _vp],
     "gpu_rms_norm_batched": [_vp, _vp, _vp, _i, _f, _i],
     "gpu_rms_norm_batched_on_stream": [_vp, _vp, _vp, _i, _f, _i, _vp],
+    "rf_rms_norm_batched_f16_on_stream": [_vp, _vp, _vp, _i, _f, _i, _vp],
     "gpu_rope_heads": [_vp, _i, _i, _i, _f, _i, _vp],
     "gpu_rope_heads_scaled": [_vp, _i, _i, _i, _f, _i, _vp, _vp],
     "gpu_rope_heads_state": [_vp, _vp, _i, _i, _f, _i, _vp],
@@ -80,6 +81,7 @@ SIGNATURES = {
     "gpu_mul_on_stream": [_vp, _vp, _vp, _i, _vp],
     "gpu_silu_on_stream": [_vp, _vp, _i, _vp],
     "rf_silu_mul_on_stream": [_vp, _vp, _vp, _i, _vp],
+    "rf_silu_mul_f16_on_stream": [_vp, _vp, _vp, _i, _vp],
     "gpu_increment_decode_state_on_stream": [_vp, _vp],
     "convert_f32_to_f16": [_vp, _vp, _i, _vp],
     "wmma_attention_prefill_gqa_causal_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],

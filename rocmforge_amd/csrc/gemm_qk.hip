@@ -1105,7 +1105,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
                         const float u = xch[(wave * NE + (i * FN + j) * 16 + e) * 64 + lane];
                         const float v = g / (1.0f + expf(-g)) * u;
                         if (segs.pair == 2)
-                            reinterpret_cast<_Float16*>(D)[(size_t)row * ldo + col] = (_Float16)v;
+                            reinterpret_cast<uint16_t*>(D)[(size_t)row * ldo + col] = f16_bits_rn(v);
                         else
                             D[(size_t)row * ldo + col] = v;
                     }

@@ -33,6 +33,8 @@
 #include <mutex>
 
 
+#include <type_traits>
+
 #include "qk_common.h"
 
 namespace rf {
@@ -99,13 +101,16 @@ __device__ __forceinline__ void pair_idx(int p, int d, int neox, int* i0, int* i
 // Single vectors and long rows: one 256-thread workgroup per row.  Short
 // batched rows (n <= 512, the per-head norms): one wave per row, four rows
 // per workgroup.
+// OUT = float, or __half (the fp32 value rounded to nearest even: the
+// operand a GEMM on fp16 activations reads)
+template <typename OUT>
 __global__ __launch_bounds__(256) void rf_rms_norm_long_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                               float* out, int n, float eps, int rows) {
+                                                               OUT* out, int n, float eps, int rows) {
     __shared__ float red[4];
     const int r = blockIdx.x;
     if (r >= rows) return;
     const float* xr = x + (size_t)r * n;
-    float* orow = out + (size_t)r * n;
+    OUT* orow = out + (size_t)r * n;
     // the canonical summation order (rms_inv_canonical) whenever the row is
     // float4-addressable: the GEMVs with a fused norm use the same order
     const bool v4 = (n & 7) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow) |
@@ -124,11 +129,25 @@ __global__ __launch_bounds__(256) void rf_rms_norm_long_kernel(const float* __re
         for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
             const float4 a = reinterpret_cast<const float4*>(xr)[i];
             const float4 g = reinterpret_cast<const float4*>(w)[i];
-            reinterpret_cast<float4*>(orow)[i] = make_float4((a.x * inv) * g.x, (a.y * inv) * g.y, (a.z * inv) * g.z,
-                                                             (a.w * inv) * g.w);
+            const float4 o = make_float4((a.x * inv) * g.x, (a.y * inv) * g.y, (a.z * inv) * g.z, (a.w * inv) * g.w);
+            if constexpr (std::is_same<OUT, float>::value) {
+                reinterpret_cast<float4*>(orow)[i] = o;
+            } else {
+                uint16_t* o16 = reinterpret_cast<uint16_t*>(orow);
+                o16[4 * i] = f16_bits_rn(o.x);
+                o16[4 * i + 1] = f16_bits_rn(o.y);
+                o16[4 * i + 2] = f16_bits_rn(o.z);
+                o16[4 * i + 3] = f16_bits_rn(o.w);
+            }
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = (xr[i] * inv) * w[i];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float o = (xr[i] * inv) * w[i];
+            if constexpr (std::is_same<OUT, float>::value)
+                orow[i] = o;
+            else
+                reinterpret_cast<uint16_t*>(orow)[i] = f16_bits_rn(o);
+        }
     }
 }
 
@@ -162,7 +181,7 @@ static hipError_t rms_rows(const float* x, const float* w, float* out, int n, fl
     if (n <= 512 && rows > 1)
         hipLaunchKernelGGL(rf_rms_norm_short_kernel, dim3((rows + 3) / 4), dim3(256), 0, st, x, w, out, n, eps, rows);
     else
-        hipLaunchKernelGGL(rf_rms_norm_long_kernel, dim3(rows), dim3(256), 0, st, x, w, out, n, eps, rows);
+        hipLaunchKernelGGL(rf_rms_norm_long_kernel<float>, dim3(rows), dim3(256), 0, st, x, w, out, n, eps, rows);
     return hipGetLastError();
 }
 
@@ -889,6 +908,10 @@ __global__ void rf_silu_mul_kernel(const float* __restrict__ g, const float* __r
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = silu_f(g[i]) * u[i];
 }
+__global__ void rf_silu_mul_f16_kernel(const float* __restrict__ g, const float* __restrict__ u, __half* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) reinterpret_cast<uint16_t*>(out)[i] = f16_bits_rn(silu_f(g[i]) * u[i]);
+}
 __global__ void rf_f32_to_f16_kernel(const float* __restrict__ x, __half* out, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = __float2half(x[i]);
@@ -920,6 +943,16 @@ extern "C" hipError_t gpu_rms_norm_batched_on_stream(const float* d_x, const flo
 extern "C" hipError_t gpu_rms_norm_batched(const float* d_x, const float* d_weight, float* d_out, const int n,
                                            const float eps, const int seq_len) {
     return rms_rows(d_x, d_weight, d_out, n, eps, seq_len, nullptr);
+}
+// fp16 output: __float2half of gpu_rms_norm_batched_on_stream's values
+extern "C" hipError_t rf_rms_norm_batched_f16_on_stream(const float* d_x, const float* d_weight, uint16_t* d_out_f16,
+                                                        const int n, const float eps, const int seq_len,
+                                                        hipStream_t stream) {
+    if (d_x == nullptr || d_weight == nullptr || d_out_f16 == nullptr || n <= 0 || seq_len <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_rms_norm_long_kernel<__half>, dim3(seq_len), dim3(256), 0, stream, d_x, d_weight,
+                       reinterpret_cast<__half*>(d_out_f16), n, eps, seq_len);
+    return hipGetLastError();
 }
 
 // ---- RoPE ----
@@ -1278,6 +1311,14 @@ extern "C" hipError_t rf_silu_mul_on_stream(const float* d_gate, const float* d_
                                             hipStream_t stream) {
     if (d_gate == nullptr || d_up == nullptr || d_out == nullptr || n <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rf_silu_mul_kernel, grid1(n), dim3(256), 0, stream, d_gate, d_up, d_out, n);
+    return hipGetLastError();
+}
+// fp16 output: __float2half of rf_silu_mul_on_stream's values
+extern "C" hipError_t rf_silu_mul_f16_on_stream(const float* d_gate, const float* d_up, uint16_t* d_out_f16,
+                                                const int n, hipStream_t stream) {
+    if (d_gate == nullptr || d_up == nullptr || d_out_f16 == nullptr || n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_silu_mul_f16_kernel, grid1(n), dim3(256), 0, stream, d_gate, d_up,
+                       reinterpret_cast<__half*>(d_out_f16), n);
     return hipGetLastError();
 }
 extern "C" hipError_t convert_f32_to_f16(const float* input, void* output, int n, hipStream_t stream) {

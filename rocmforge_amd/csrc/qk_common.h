@@ -430,6 +430,16 @@ __device__ __forceinline__ float q4k_q8_combine(float acc, float xd, float d, fl
     return acc + xd * (d * (float)sc * (float)dot - dmin * (float)mn * (float)qsum);
 }
 
+// fp16 bits (round to nearest even) of an fp32 value, as an instruction of
+// its own: left to itself the compiler folds a preceding multiply or FMA into
+// one v_fma_mix with an fp16 result, which rounds the exact product once
+// instead of the fp32 value (a different half for a few values in 10^5).
+__device__ __forceinline__ uint16_t f16_bits_rn(float v) {
+    uint32_t r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(v));
+    return (uint16_t)r;
+}
+
 // Workgroup barrier that does not wait for outstanding global loads
 // (__syncthreads() implies a fence, i.e. vmcnt(0), which would drain the
 // loads a pipeline keeps in flight across the barrier).  LDS writes of this

@@ -154,7 +154,7 @@ class Engine:
     """Prefill + greedy decode of one sequence of up to max_seq tokens."""
 
     def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0",
-                 fuse_norm: bool = True, fold_qk: bool = False, fuse_gemm: bool = True):
+                 fuse_norm: bool = True, fold_qk: bool = False, fuse_gemm: bool = True, ffn_f16: bool = True):
         """fuse_norm: decode with the RMSNorms folded into the GEMVs that
         consume them, the per-head Q/K step into the attention and the state
         advance into the argmax (same bits as the separate launches);
@@ -164,7 +164,10 @@ class Engine:
         fuse_gemm: prefill projections that share an input in one segmented
         GEMM launch, and the O / FFN-down products added straight into the
         residual stream (same per-element products; the sums of a K split
-        land in another order)."""
+        land in another order);
+        ffn_f16: (with fuse_gemm) a Q4_K gate/up prefill on fp16 activations:
+        the FFN norm rounded to fp16 feeds two 256 x 128-tile GEMMs and the
+        SwiGLU (the same operand values as the fp32 launchers)."""
         import torch
         self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
         self.fuse_norm = fuse_norm
@@ -195,6 +198,8 @@ class Engine:
         self._graph = None
         self._pf = None
         self._act16 = False      # the last prefill layer's SwiGLU output went to the fp16 buffer
+        self.ffn_f16 = ffn_f16
+        self._ffn16 = False      # the last prefill layer ran gate/up on the fp16 norm
 
     # ---- decode ---------------------------------------------------------------------------
     def _stream(self):
@@ -366,7 +371,8 @@ class Engine:
                     "k": z(mp * c.kv_size), "v": z(mp * c.kv_size), "q16": z(mp * c.q_size, torch.int16),
                     "k16": z(mp * c.kv_size, torch.int16), "v16": z(mp * c.kv_size, torch.int16),
                     "att": z(mp * c.q_size), "tmp": z(mp * c.hidden), "g": z(mp * c.ff), "u": z(mp * c.ff),
-                    "g16": z(mp * c.ff, torch.int16), "ids": z(mp, torch.int32)}
+                    "g16": z(mp * c.ff, torch.int16), "xn16": z(mp * c.hidden, torch.int16),
+                    "ids": z(mp, torch.int32)}
         return self._pf
 
     def prefill(self, tokens, trace=None) -> int:
@@ -436,14 +442,31 @@ class Engine:
             t("attention", i)
             self._gemm_residual(m["attn_output"], b["att"], b["x"], b["tmp"], c.hidden, c.q_size, M, st)
             t("attn_output", i)
-            _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp, st),
-                 "norm")
             gt, ut = m["ffn_gate"][1].wtype, m["ffn_up"][1].wtype
+            gu16 = (self.fuse_gemm and self.ffn_f16 and gt == ut == GgmlType.Q4_K and c.ff % 128 == 0
+                    and c.hidden % 256 == 0)
+            if gu16:
+                _chk(L.rf_rms_norm_batched_f16_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn16"]), c.hidden, c.eps,
+                                                         mp, st), "norm f16")
+            else:
+                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.ffn_norm), _p(b["xn"]), c.hidden, c.eps, mp,
+                                                      st), "norm")
+            self._ffn16 = gu16
             pair = gt == ut and c.ff % 128 == 0 and self._fusable(gt, 256, c.hidden)
             # a Q6_K down projection reads the SwiGLU output as fp16 (the operand its
             # fp32 launcher would round it to) through the 128 x 64-tile kernel
-            self._act16 = pair and self._down_f16(m["ffn_down"][1].wtype)
-            if self._act16:
+            self._act16 = (pair or gu16) and self._down_f16(m["ffn_down"][1].wtype)
+            if gu16:
+                # gate and up as two GEMMs on the fp16 norm (256 x 128 tiles: one round
+                # of CUs each at 512 x 12288), then the SwiGLU
+                for mat, out in (("ffn_gate", "g"), ("ffn_up", "u")):
+                    _chk(L.rf_gemm_q4_k_f16_launch(_p(b["xn16"]), _p(m[mat][0]), _p(b[out]), mp, c.ff, c.hidden, st),
+                         "gemm f16")
+                if self._act16:
+                    _chk(L.rf_silu_mul_f16_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g16"]), mp * c.ff, st), "swiglu f16")
+                else:
+                    _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
+            elif self._act16:
                 fn = L.rf_gemm_q4_k_swiglu_f16_launch if gt == GgmlType.Q4_K else L.rf_gemm_q6_k_swiglu_f16_launch
                 _chk(fn(_p(b["xn"]), _p(m["ffn_gate"][0]), _p(m["ffn_up"][0]), _p(b["g16"]), mp, c.ff, c.hidden,
                         st), "gemm swiglu f16")

@@ -250,9 +250,14 @@ def _check_prefill_stages(eng, lay):
             assert _rel(x.astype(np.float64) - seen["x_pre"], prod) <= 2e-3
             seen["x_att"] = x.copy()
         elif name == "gate_up":
-            # silu(xn Wg^T) * (xn Wu^T) on the ffn-normalised rows
-            xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
-            assert _rel(xn, O.rms_norm(seen["x_att"], _h(w.layers[lay].ffn_norm), c.eps, M)) <= 1e-5
+            # silu(xn Wg^T) * (xn Wu^T) on the ffn-normalised rows (fp16 rows where the
+            # gate/up GEMMs read fp16 activations: one rounding of the same values)
+            if eng._ffn16:
+                xn = _h(b["xn16"]).view(np.float16).reshape(-1, c.hidden)[:M].astype(np.float32)
+            else:
+                xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
+            ref_n = O.rms_norm(seen["x_att"], _h(w.layers[lay].ffn_norm), c.eps, M)
+            assert _rel(xn, ref_n) <= (5e-4 if eng._ffn16 else 1e-5)
             m = w.layers[lay].mats
             prods = []
             for mat in ("ffn_gate", "ffn_up"):
@@ -265,6 +270,7 @@ def _check_prefill_stages(eng, lay):
             got = (_h(b["g16"]).view(np.float16) if eng._act16 else _h(b["g"])).reshape(-1, c.ff)[:M]
             assert _rel(got, ref) <= 4e-3
             seen["act16"] = eng._act16
+            seen["ffn16"] = eng._ffn16
             seen["act"] = got.copy()
         elif name == "ffn_down":
             wm = w.layers[lay].mats["ffn_down"]
@@ -289,7 +295,16 @@ def _check_prefill_stages(eng, lay):
 
 
 def test_prefill_stages(eng):
-    assert not _check_prefill_stages(eng, 0)["act16"]
+    # (hidden 512, ff 1024: gate/up on the fp16 norm, a fp32 SwiGLU into a Q4_K down)
+    seen = _check_prefill_stages(eng, 0)
+    assert seen["ffn16"] and not seen["act16"]
+
+
+def test_prefill_stages_fp32_ffn(weights):
+    # the paired gate/up GEMM with SwiGLU in its epilogue, on the fp32 norm
+    e = E.Engine(CFG, weights, max_seq=256, fuse_norm=False, ffn_f16=False)
+    seen = _check_prefill_stages(e, 0)
+    assert not seen["ffn16"] and not seen["act16"]
 
 
 def test_prefill_stages_f16_down(dev):

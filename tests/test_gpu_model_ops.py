@@ -478,3 +478,24 @@ def test_against_reference_layer_kernels(rf, dev):
 def _rel_err(a, b):
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     return np.abs(a - b).max() / np.abs(b).max()
+
+
+def test_rms_norm_and_swiglu_f16_outputs(rf, dev):
+    # the fp16-output forms are __float2half of the fp32 launchers' values, bit for bit
+    rows, n = 70, 4096
+    x = np.random.default_rng(3).standard_normal((rows, n)).astype(np.float32)
+    wt = np.random.default_rng(4).standard_normal(n).astype(np.float32)
+    dx, dw = G.to_dev(x), G.to_dev(wt)
+    d32 = G.empty(rows * n, torch.float32)
+    d16 = G.empty(rows * n, torch.int16)
+    G.call(rf.gpu_rms_norm_batched_on_stream, G.ptr(dx), G.ptr(dw), G.ptr(d32), n, 1e-6, rows)
+    G.call(rf.rf_rms_norm_batched_f16_on_stream, G.ptr(dx), G.ptr(dw), G.ptr(d16), n, 1e-6, rows)
+    np.testing.assert_array_equal(G.host(d16), G.host(d32).astype(np.float16).view(np.int16))
+    g = np.random.default_rng(5).standard_normal(rows * n).astype(np.float32) * 4
+    u = np.random.default_rng(6).standard_normal(rows * n).astype(np.float32)
+    dg, du = G.to_dev(g), G.to_dev(u)
+    G.call(rf.rf_silu_mul_on_stream, G.ptr(dg), G.ptr(du), G.ptr(d32), rows * n)
+    G.call(rf.rf_silu_mul_f16_on_stream, G.ptr(dg), G.ptr(du), G.ptr(d16), rows * n)
+    np.testing.assert_array_equal(G.host(d16), G.host(d32).astype(np.float16).view(np.int16))
+    assert rf.rf_rms_norm_batched_f16_on_stream(None, G.ptr(dw), G.ptr(d16), n, 1e-6, rows, G.stream()) != 0
+    assert rf.rf_silu_mul_f16_on_stream(G.ptr(dg), G.ptr(du), None, 8, G.stream()) != 0
