@@ -1349,7 +1349,15 @@ extern "C" hipError_t gpu_increment_decode_state_on_stream(int* d_state, hipStre
 // lane ^ 32, alpha is a per-lane scale of the O^T accumulators, and the
 // accumulator values of P feed the B operand of O^T = V^T P^T directly --
 // the key order they come in is matched by the order the V^T operand is
-// read in.
+// read in.  exp(x - m) is evaluated as 2^(x log2 e - m log2 e) (one
+// v_exp_f32; within a few fp32 ulps of expf, P is rounded to fp16 anyway),
+// the causal mask is applied only on the tiles that reach past a wave's
+// first query, and O is rescaled only when some lane's maximum moved.  The
+// V^T tile's key index is XOR-swizzled by 4 (dim / 8): the 16 threads that
+// write one key's dims (rows 8 apart) then hit different banks, and every
+// group of 4 keys an operand read takes stays contiguous.  The kernel is
+// compiled with MFMA results in VGPRs (the rescale touches every
+// accumulator each tile).
 namespace rf {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -1359,7 +1367,8 @@ constexpr int kAttD = 128;
 constexpr int kKStr = kAttD + 8;     // K tile row stride (halves)
 constexpr int kVStr = 64 + 8;        // V^T tile row stride (halves)
 
-__global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
+template <int NWQ>
+__global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
                                                               const _Float16* __restrict__ K,
                                                               const _Float16* __restrict__ V, float* __restrict__ O,
                                                               int seq, int nq, int nkv, int causal, float scale) {
@@ -1368,7 +1377,7 @@ __global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int head = blockIdx.y;
     const int kvh = head / (nq / nkv);
-    const int qb = blockIdx.x * 128;
+    const int qb = blockIdx.x * 32 * NWQ;
     const int q0 = qb + 32 * wave;
     const int hi = lane >> 5, col = lane & 31;
     const size_t qrow = (size_t)nq * kAttD, kvrow = (size_t)nkv * kAttD;
@@ -1391,8 +1400,9 @@ __global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __
         for (int e = 0; e < 16; ++e) o[b][e] = 0.0f;
     float m = kNegMax, l = 0.0f;
     const int query = q0 + col;
+    const float scale2 = scale * 1.4426950408889634f;   // log2 e
 
-    const int wg_last_q = min(qb + 127, seq - 1);
+    const int wg_last_q = min(qb + 32 * NWQ - 1, seq - 1);
     const int ntiles = causal ? wg_last_q / 64 + 1 : seq / 64;
     const int wave_tiles = causal ? (q0 + 31) / 64 + 1 : seq / 64;
     for (int t = 0; t < ntiles; ++t) {
@@ -1400,14 +1410,17 @@ __global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __
         __syncthreads();   // previous tile's reads done
         // K tile: 64 keys x 128 dims, 16-byte chunks; V tile transposed
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i;          // 0..1023
+        for (int i = 0; i < 16 / NWQ; ++i) {
+            const int c = tid + 64 * NWQ * i;     // 0..1023
             const int key = c >> 4, d8 = (c & 15) * 8;
             const h8 kv = *reinterpret_cast<const h8*>(K + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
             *reinterpret_cast<h8*>(&ks[key * kKStr + d8]) = kv;
             const h8 vv = *reinterpret_cast<const h8*>(V + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
+            // transposed, keys XOR-swizzled by 4 (d / 8): the 16 threads of a key
+            // write rows 8 apart, which the swizzle spreads over the banks
+            const int sw = 4 * (c & 15);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vt[(d8 + j) * kVStr + key] = vv[j];
+            for (int j = 0; j < 8; ++j) vt[(d8 + j) * kVStr + (key ^ sw)] = vv[j];
         }
         __syncthreads();
         if (!active || t >= wave_tiles) continue;
@@ -1424,38 +1437,47 @@ __global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __
                 s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks_], s[b], 0, 0, 0);
             }
         }
-        // scale, mask, tile max
+        // scale (in the log2 domain: exp(x - m) = 2^(x log2 e - m log2 e), one
+        // v_exp_f32 each), mask (only a tile that reaches past the wave's first
+        // query holds keys to mask), tile max
         float tmax = kNegMax;
+        const bool diag = causal && t0 + 63 > q0;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int key = t0 + 32 * b + 8 * (e >> 2) + 4 * hi + (e & 3);
-                float v = s[b][e] * scale;
-                if (causal && key > query) v = kNegMax;
+                float v = s[b][e] * scale2;
+                if (diag) {
+                    const int key = t0 + 32 * b + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    if (key > query) v = kNegMax;
+                }
                 s[b][e] = v;
                 tmax = fmaxf(tmax, v);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float m_new = fmaxf(m, tmax);
-        const float alpha = expf(m - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
         float rs = 0.0f;
         h8 p[4];   // B operands, k-step j = (block j / 2, keys 16 (j % 2) ..)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float ex = expf(s[b][e] - m_new);
+                const float ex = __builtin_amdgcn_exp2f(s[b][e] - m_new);
                 rs += ex;
                 p[2 * b + (e >> 3)][e & 7] = (_Float16)ex;
             }
         rs += __shfl_xor(rs, 32);
         l = l * alpha + rs;
         m = m_new;
+        // rescale O only where some lane's maximum moved (alpha == 1 elsewhere:
+        // multiplying by it changes nothing)
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+            for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) o[b][e] *= alpha;
+                for (int e = 0; e < 16; ++e) o[b][e] *= alpha;
+        }
         // O^T += V^T P^T: A operand lane (dim = 32 bd + col) keys of k-step j in
         // the accumulator order: 32 (j/2) + 16 (j%2) + 4 hi + {0..3, 8..11}
 #pragma unroll
@@ -1463,10 +1485,13 @@ __global__ __launch_bounds__(256) void rf_attn_prefill_kernel(const _Float16* __
             const int kb = 32 * (j >> 1) + 16 * (j & 1) + 4 * hi;
 #pragma unroll
             for (int bd = 0; bd < 4; ++bd) {
-                const _Float16* vr = &vt[(32 * bd + col) * kVStr + kb];
+                // row d = 32 bd + col, keys kb .. kb + 3 and kb + 8 .. kb + 11 under
+                // the row's swizzle 4 (d / 8) (a multiple of 4: groups stay whole)
+                const int sw = 4 * ((4 * bd + (col >> 3)) & 15);
+                const _Float16* vrow = &vt[(32 * bd + col) * kVStr];
                 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                const h4 lo = *reinterpret_cast<const h4*>(vr);
-                const h4 hi4 = *reinterpret_cast<const h4*>(vr + 8);
+                const h4 lo = *reinterpret_cast<const h4*>(vrow + (kb ^ sw));
+                const h4 hi4 = *reinterpret_cast<const h4*>(vrow + ((kb + 8) ^ sw));
                 const h8 a = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 o[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[j], o[bd], 0, 0, 0);
             }
@@ -1491,7 +1516,8 @@ extern "C" hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, co
     if (seq_len <= 0 || seq_len % 64 != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) & 15u)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rf::rf_attn_prefill_kernel, dim3((seq_len + 127) / 128, num_q_heads), dim3(256), 0, stream,
+    // four waves (128 queries) per workgroup: measured faster than two
+    hipLaunchKernelGGL(rf::rf_attn_prefill_kernel<4>, dim3((seq_len + 127) / 128, num_q_heads), dim3(256), 0, stream,
                        static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
                        static_cast<const _Float16*>(V), O, seq_len, num_q_heads, num_kv_heads, causal, scale);
     return hipGetLastError();
