@@ -106,8 +106,10 @@ hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, f
  * caller whose producing kernel already rounded A to fp16 (bit patterns as
  * uint16_t, row-major [M][K]).  Same operand values as
  * wmma_gemm_q4_k_launch(fp32 A), so the same products; A is read at half
- * the bytes and not converted per tile.  M % 64 == 0, N % 128 == 0,
- * K % 256 == 0, input and weights 16-byte aligned. */
+ * the bytes and not converted per tile.  256 x 128 tiles where they fill
+ * three quarters of the CUs (M = 512 at N = 14336), else 64- or 128-row x
+ * 64-column tiles with K split over the waves of a workgroup.  M % 64 == 0,
+ * N % 64 == 0, K % 256 == 0, input and weights 16-byte aligned. */
 hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output, int M, int N,
                                    int K, hipStream_t stream);
 
@@ -125,6 +127,12 @@ hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weight
  * written once after its fp32 sum, so the result is inout + that launch's
  * output bit for bit.  Same shape rules.  Used for the FFN down projection of
  * a prefill, into the residual stream. */
+/* No counterpart: inout[M x N] += the product of rf_gemm_q4_k_f16_launch, each
+ * output read and written once after its fp32 sum (inout + that product bit
+ * for bit).  M % 64 == 0, N % 64 == 0, K % 256 == 0, input and weights 16-byte
+ * aligned.  Used for the O and FFN-down projections of a prefill. */
+hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q4_k, float* inout,
+                                              int M, int N, int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
 
@@ -475,6 +483,13 @@ hipError_t rf_silu_mul_f16_on_stream(const float* d_gate, const float* d_up, uin
 hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K, const void* V, float* O,
                                                     int seq_len, int num_q_heads, int num_kv_heads, int causal,
                                                     float scale, hipStream_t stream);
+/* No counterpart: the same attention with O rounded to fp16 (round to nearest
+ * even, bits as uint16_t) -- the operand an O projection on fp16 activations
+ * (rf_gemm_q4_k_f16_accumulate_launch) reads, __float2half of the fp32
+ * launcher's output. */
+hipError_t rf_attention_prefill_gqa_causal_f16_launch(const void* Q, const void* K, const void* V, uint16_t* O_f16,
+                                                      int seq_len, int num_q_heads, int num_kv_heads, int causal,
+                                                      float scale, hipStream_t stream);
 
 /* ---- GEMVs with the RMSNorm of their input fused in (no counterpart) ----
  * out = W * rmsnorm(input, norm_w, eps), bit-identical to gpu_rms_norm into a

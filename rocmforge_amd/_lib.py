@@ -32,6 +32,7 @@ SIGNATURES = {
     "rf_gemm_q4_k_f16_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_f16_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_f16_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q4_k_f16_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q4_k_segments_launch": [_vp] * 7 + [_i] * 5 + [_vp],
     "rf_gemm_q6_k_segments_launch": [_vp] * 7 + [_i] * 5 + [_vp],
     "rf_gemm_q4_k_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
@@ -85,6 +86,7 @@ SIGNATURES = {
     "gpu_increment_decode_state_on_stream": [_vp, _vp],
     "convert_f32_to_f16": [_vp, _vp, _i, _vp],
     "wmma_attention_prefill_gqa_causal_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
+    "rf_attention_prefill_gqa_causal_f16_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],
     "rf_q4_k_q8_int_dots_launch": [_vp, _vp, _vp, _i, _i, _vp],
 }

@@ -2045,6 +2045,238 @@ __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uin
     }
 }
 
+// ── q4s: Q4_K GEMM on fp16 activations, 32 FMR x 64 tiles, K slices on waves
+// (rf_gemm_q4_k_f16_launch where the 256 x 128 tiles leave CUs idle) ───────
+// The layout of rf_gemm_q6k_f16a_kernel for Q4_K weights: eight waves, wave
+// w = 4 cg + ks takes k [16 ks, +16) of every 64-wide chunk for the tile's
+// rows (FMR row blocks of 32) and the 32 columns of group cg; the four
+// K-slice partials of an output block are added through LDS in ks order,
+// each output written once.  Chunk c covers nibble pair p = c % 4 of
+// super-block c / 4: slice ks holds the low (ks < 2) or high nibbles of qs
+// bytes 32 p + 16 (ks & 1) .. + 15, lane half h bytes + 8 h .. + 7, of
+// sub-block 2 p + (ks >> 1).  The ring stage of a super-block holds its
+// 144-byte blocks of the tile's 64 weight rows (16-byte aligned: plain
+// LDS DMA, 16 instructions of which 9 carry the stage); each lane takes its
+// row's four (d sc 2^24 or 2^20, -dmin m) pairs from the header once per
+// super-block and dequantises as rf_gemm_q4k_f16a_kernel does (nibbles as
+// fp16 subnormals into v_fma_mix, the fp32 value rounded to fp16 after).
+constexpr int kQ4sThreads = 512;
+constexpr int kQ4sBN = 64;
+constexpr int kQ4sStage = 16 * 1024;                  // 64 rows x 144 B (+ padding DMAs)
+constexpr int kQ4sRS = 3;
+constexpr int kQ4sABufs = 7;
+constexpr int kQ4sLag = kQ4sABufs - 3;
+
+template <int FMR>
+struct Q4sGeom {
+    static constexpr int kBM = 32 * FMR;
+    static constexpr int kABuf = kBM * kKC * 2;       // FMR x 4 KB
+    static constexpr int kAPW = FMR / 2;              // A DMAs per wave per chunk (1 KB each)
+    static constexpr int kLdsLoop = kQ4sRS * kQ4sStage + kQ4sABufs * kABuf;
+    static constexpr int kLdsXch = 8 * FMR * 4096;    // every wave's partial tile
+    static constexpr int kLds = kLdsLoop > kLdsXch ? kLdsLoop : kLdsXch;
+};
+
+template <int FMR, bool ACC>
+__global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint8_t* __restrict__ W,
+                                                                        float* __restrict__ D, int M, int N, int K) {
+    using G = Q4sGeom<FMR>;
+    __shared__ __align__(16) uint8_t lds[G::kLds];
+    uint8_t* ring = lds;
+    uint8_t* abuf0 = lds + kQ4sRS * kQ4sStage;
+    const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
+    const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = wave & 3, cg = wave >> 2;
+    const int h = lane >> 5, col = lane & 31;
+    const int mtiles = (M + G::kBM - 1) / G::kBM;
+    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int m0 = (v % mtiles) * G::kBM;      // the M tiles of one column tile are neighbours
+    const int n0 = (v / mtiles) * kQ4sBN;
+    const int nchunks = K / kKC;
+    const int nsb = K / kQK;
+    const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+
+    // ---- weight ring: DMA instruction ii = wave + 8 t moves 16-byte pieces
+    // [64 ii, 64 ii + 64) of the stage (row i / 9, piece i % 9; pieces past
+    // the 576 of the stage repeat the last one) ------------------------------
+    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    uint32_t roff[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int i = 64 * (wave + 8 * t) + lane;
+        roff[t] = i < 576 ? (uint32_t)(i / 9) * row_bytes + 16u * (uint32_t)(i % 9) : 63u * row_bytes + 128u;
+    }
+    auto w_dma1 = [&](int t, int sb, int slot) {
+        lds_dma16(ring_lds0 + (uint32_t)slot * kQ4sStage + 1024u * (uint32_t)(wave + 8 * t), roff[t],
+                  w_tile + (size_t)min(sb, nsb - 1) * kQ4KBytes);
+    };
+
+    // ---- A: instruction gi = kAPW wave + g covers rows 8 gi + L / 8 of the
+    // chunk, position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row
+    // M - 1 ---------------------------------------------------------------------
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    uint32_t dma_voff[G::kAPW];
+#pragma unroll
+    for (int g = 0; g < G::kAPW; ++g) {
+        const int r = 8 * (G::kAPW * wave + g) + (lane >> 3);
+        const int rc = min(r, M - 1 - m0);
+        dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
+    }
+    auto a_dma1 = [&](int g, int c, int buf) {
+        lds_dma16(a_lds0 + (uint32_t)(buf * G::kABuf + (G::kAPW * wave + g) * 1024), dma_voff[g],
+                  a_tile + (size_t)min(c, nchunks - 1) * kKC * 2);
+    };
+
+    // ---- B: the lane's weight row (column 32 cg + col) in the ring stage ------
+    const int brow = 32 * cg + col;
+    const int hf = ks >> 1;                     // high nibbles (odd sub-block) for ks >= 2
+    const uint32_t nmask = hf ? 0x00F000F0u : 0x000F000Fu;
+    const float nfac = hf ? 1048576.0f : 16777216.0f;
+    float sD[4], sM[4];                         // per chunk p of the super-block: (d sc 2^x, -dmin m)
+    auto hdr_read = [&](int sb) {
+        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + (sb % kQ4sRS) * kQ4sStage + brow * kQ4KBytes);
+        const float d = half_bits_to_float(hd.x) * nfac, dmin = half_bits_to_float(hd.x >> 16);
+        // get_scale_min_k4 for sub-blocks hf, 2 + hf (bytes of the low words)
+        // and 4 + hf, 6 + hf (high words), word-wide without branches
+        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t scw = p < 2 ? sc_lo : sc_hi, mnw = p < 2 ? mn_lo : mn_hi;
+            const int byte = 2 * (p & 1) + hf;
+            sD[p] = d * (float)((scw >> (8 * byte)) & 0xFFu);
+            sM[p] = -(dmin * (float)((mnw >> (8 * byte)) & 0xFFu));
+        }
+    };
+    u32x2 rqs;
+    auto qs_read = [&](int p, int sb) {
+        rqs = *reinterpret_cast<const u32x2*>(ring + (sb % kQ4sRS) * kQ4sStage + brow * kQ4KBytes + 16 + 32 * p +
+                                               16 * (ks & 1) + 8 * h);
+    };
+    u32x4 bq[2];                          // [chunk parity]
+    auto b_dequant = [&](int p, int P) {
+        // hdr_read folded 2^24 (low nibbles) or 2^20 (high: 16 q) into d
+        const uint2 a = f16a_dq4(rqs.x, nmask, sD[p], sM[p]);
+        const uint2 b = f16a_dq4(rqs.y, nmask, sD[p], sM[p]);
+        bq[P] = u32x4{a.x, a.y, b.x, b.y};
+    };
+
+    f32x16 acc[FMR];
+#pragma unroll
+    for (int i = 0; i < FMR; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+    const int gcol = (col & 7) ^ ((col >> 3) & 1);
+    f16x8 af[2][FMR];
+    auto frag_ld = [&](int set, int buf, int i) {
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * G::kABuf + (32 * i + col) * 128 +
+                                                     16 * ((2 * ks + h) ^ gcol));
+    };
+
+    // ---- prologue: ring stages 0, 1; A chunks 0 .. 5; chunk 0's operands ----
+#pragma unroll
+    for (int t = 0; t < 2; ++t) w_dma1(t, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) w_dma1(t, 1, 1);
+#pragma unroll
+    for (int c = 0; c < kQ4sABufs - 1; ++c)
+#pragma unroll
+        for (int g = 0; g < G::kAPW; ++g) a_dma1(g, c, c);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    hdr_read(0);
+    qs_read(0, 0);
+    b_dequant(0, 0);
+#pragma unroll
+    for (int i = 0; i < FMR; ++i) frag_ld(0, 0, i);
+
+    // Chunk c = 4 sb + CQ: A buffer c % 7, ring stage sb % 3.  After the
+    // first MFMA every LDS read of chunk c + 1 (its fragments, qs bytes and,
+    // entering a new super-block, its header); the A DMA of chunk c + 6;
+    // in CQ 0 the ring DMA of super-block sb + 2; the B operands of chunk
+    // c + 1 after the last MFMA.  At the end every DMA issued up to chunk
+    // c - 4 is complete, then one barrier.
+    int ab = 0;
+    auto iteration = [&](auto cqc, int sb) {
+        constexpr int CQ = decltype(cqc)::value;
+        constexpr int P = CQ & 1;
+        constexpr int NQ = (CQ + 1) & 3;
+        const int c = 4 * sb + CQ;
+        const int sbn = CQ == 3 ? sb + 1 : sb;
+        const int abn = ab == kQ4sABufs - 1 ? 0 : ab + 1;
+        const int abp = ab == 0 ? kQ4sABufs - 1 : ab - 1;
+#pragma unroll
+        for (int i = 0; i < FMR; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[P][i], __builtin_bit_cast(f16x8, bq[P]), acc[i], 0, 0,
+                                                            0);
+            if (i == 0) {
+                if constexpr (NQ == 0) hdr_read(sbn);
+                qs_read(NQ, sbn);
+#pragma unroll
+                for (int r = 0; r < FMR; ++r) frag_ld(P ^ 1, abn, r);
+            }
+            if (i < G::kAPW) a_dma1(i, c + kQ4sABufs - 1, abp);
+            if constexpr (CQ == 0) {
+                if (i < 2) w_dma1(i, sb + 2, (sb + 2) % kQ4sRS);
+            }
+            if (i == FMR - 1) b_dequant(NQ, P ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(G::kAPW * kQ4sLag + 2) : "memory");
+        lds_barrier();
+        ab = abn;
+    };
+    for (int sb = 0; sb < nsb; ++sb) {
+        iteration(std::integral_constant<int, 0>{}, sb);
+        iteration(std::integral_constant<int, 1>{}, sb);
+        iteration(std::integral_constant<int, 2>{}, sb);
+        iteration(std::integral_constant<int, 3>{}, sb);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- K slices: every wave parks its FMR row blocks in LDS
+    // ([wave][row block][e / 4][lane] of float4); wave (ks, cg), ks < FMR, adds
+    // row block ks of column group cg over ks' = 0..3 in that order ----------
+    __syncthreads();
+    float4* xch = reinterpret_cast<float4*>(lds);
+#pragma unroll
+    for (int i = 0; i < FMR; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            xch[((wave * FMR + i) * 4 + q) * 64 + lane] =
+                make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
+    __syncthreads();
+    if (ks >= FMR) return;
+    const int ncol = n0 + 32 * cg + col;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int src = 0; src < 4; ++src) {
+            const float4 p = xch[(((4 * cg + src) * FMR + ks) * 4 + q) * 64 + lane];
+            s[0] += p.x;
+            s[1] += p.y;
+            s[2] += p.z;
+            s[3] += p.w;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
+            if (row < M) {
+                float* o = D + (size_t)row * N + ncol;
+                *o = ACC ? *o + s[u] : s[u];
+            }
+        }
+    }
+}
+
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
 // 8-chunk groups) and tiles * S <= CUs (one workgroup per CU; the kernel
 // runs one 512-thread workgroup per CU).  Measured on MI355X at the
@@ -2180,6 +2412,26 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
     return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
 }
 
+// Q4_K on fp16 activations: 256 x 128 tiles (rf_gemm_q4k_f16a_kernel) where
+// they fill at least three quarters of the CUs, else the eight-wave
+// K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64) or 128.
+template <bool ACC>
+static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
+    int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
+    if (pick == 0) {
+        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, D, M, N, K);
+    } else if (pick == 2) {
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(((M + 63) / 64) * (N / kQ4sBN)), dim3(kQ4sThreads),
+                           0, st, A, w, D, M, N, K);
+    } else {
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, ACC>), dim3(((M + 127) / 128) * (N / kQ4sBN)),
+                           dim3(kQ4sThreads), 0, st, A, w, D, M, N, K);
+    }
+    return hipGetLastError();
+}
+
 // fp16 activations (the caller's rounding of A, e.g. in the kernel that
 // produced them): the same operand values as wmma_gemm_q4_k_launch on fp32
 // A, read at half the bytes and without the per-tile conversion.  M % 64,
@@ -2187,14 +2439,11 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
 extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output,
                                               int M, int N, int K, hipStream_t stream) {
     if (input_f16 == nullptr || weights_q4_k == nullptr || output == nullptr) return hipErrorInvalidValue;
-    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kF16aBN) != 0 || (K % kQK) != 0)
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
         return hipErrorInvalidValue;
-    const int tiles = ((M + kF16aBM - 1) / kF16aBM) * (N / kF16aBN);
-    hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16,
-                       static_cast<const uint8_t*>(weights_q4_k), output, M, N, K);
-    return hipGetLastError();
+    return gemm_q4_f16<false>(input_f16, weights_q4_k, output, M, N, K, stream);
 }
 
 // Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,
@@ -2223,6 +2472,18 @@ extern "C" hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const v
 extern "C" hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k,
                                                          float* inout, int M, int N, int K, hipStream_t stream) {
     return gemm_q6_f16<true>(input_f16, weights_q6_k, inout, M, N, K, stream);
+}
+
+// inout[M x N] += the product of rf_gemm_q4_k_f16_launch, on the K-sliced
+// tiles (each output read and written once after its fp32 sum).
+extern "C" hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q4_k,
+                                                         float* inout, int M, int N, int K, hipStream_t stream) {
+    if (input_f16 == nullptr || weights_q4_k == nullptr || inout == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
+        return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
+        return hipErrorInvalidValue;
+    return gemm_q4_f16<true>(input_f16, weights_q4_k, inout, M, N, K, stream);
 }
 
 extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,

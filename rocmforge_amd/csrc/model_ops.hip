@@ -1367,10 +1367,12 @@ constexpr int kAttD = 128;
 constexpr int kKStr = kAttD + 8;     // K tile row stride (halves)
 constexpr int kVStr = 64 + 8;        // V^T tile row stride (halves)
 
-template <int NWQ>
+// OUT = float, or uint16_t: fp16 bits of the fp32 output (round to nearest
+// even), the operand a GEMM on fp16 activations reads
+template <int NWQ, typename OUT>
 __global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
                                                               const _Float16* __restrict__ K,
-                                                              const _Float16* __restrict__ V, float* __restrict__ O,
+                                                              const _Float16* __restrict__ V, OUT* __restrict__ O,
                                                               int seq, int nq, int nkv, int causal, float scale) {
     __shared__ __align__(16) _Float16 ks[64 * kKStr];
     __shared__ __align__(16) _Float16 vt[kAttD * kVStr];
@@ -1499,26 +1501,47 @@ __global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float1
     }
     if (!active) return;
     const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
-    float* orow = O + (size_t)query * qrow + (size_t)head * kAttD;
+    OUT* orow = O + (size_t)query * qrow + (size_t)head * kAttD;
 #pragma unroll
     for (int bd = 0; bd < 4; ++bd)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) orow[32 * bd + 8 * (e >> 2) + 4 * hi + (e & 3)] = o[bd][e] * inv_l;
+        for (int e = 0; e < 16; ++e) {
+            const float r = o[bd][e] * inv_l;
+            if constexpr (std::is_same<OUT, float>::value)
+                orow[32 * bd + 8 * (e >> 2) + 4 * hi + (e & 3)] = r;
+            else
+                orow[32 * bd + 8 * (e >> 2) + 4 * hi + (e & 3)] = f16_bits_rn(r);
+        }
 }
 
 }  // namespace rf
 
-extern "C" hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K, const void* V, float* O,
-                                                               int seq_len, int num_q_heads, int num_kv_heads,
-                                                               int causal, float scale, hipStream_t stream) {
+template <typename OUT>
+static hipError_t attn_prefill(const void* Q, const void* K, const void* V, OUT* O, int seq_len, int num_q_heads,
+                               int num_kv_heads, int causal, float scale, hipStream_t stream) {
     if (Q == nullptr || K == nullptr || V == nullptr || O == nullptr) return hipErrorInvalidValue;
     if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return hipErrorInvalidValue;
     if (seq_len <= 0 || seq_len % 64 != 0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(V)) & 15u)
         return hipErrorInvalidValue;
     // four waves (128 queries) per workgroup: measured faster than two
-    hipLaunchKernelGGL(rf::rf_attn_prefill_kernel<4>, dim3((seq_len + 127) / 128, num_q_heads), dim3(256), 0, stream,
-                       static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+    hipLaunchKernelGGL((rf::rf_attn_prefill_kernel<4, OUT>), dim3((seq_len + 127) / 128, num_q_heads), dim3(256), 0,
+                       stream, static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
                        static_cast<const _Float16*>(V), O, seq_len, num_q_heads, num_kv_heads, causal, scale);
     return hipGetLastError();
+}
+
+extern "C" hipError_t wmma_attention_prefill_gqa_causal_launch(const void* Q, const void* K, const void* V, float* O,
+                                                               int seq_len, int num_q_heads, int num_kv_heads,
+                                                               int causal, float scale, hipStream_t stream) {
+    return attn_prefill(Q, K, V, O, seq_len, num_q_heads, num_kv_heads, causal, scale, stream);
+}
+
+// The same with the output rounded to fp16 (bits as uint16_t): the operand of
+// an O projection on fp16 activations, __float2half of the fp32 launcher's.
+extern "C" hipError_t rf_attention_prefill_gqa_causal_f16_launch(const void* Q, const void* K, const void* V,
+                                                                 uint16_t* O_f16, int seq_len, int num_q_heads,
+                                                                 int num_kv_heads, int causal, float scale,
+                                                                 hipStream_t stream) {
+    return attn_prefill(Q, K, V, O_f16, seq_len, num_q_heads, num_kv_heads, causal, scale, stream);
 }

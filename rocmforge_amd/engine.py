@@ -200,6 +200,7 @@ class Engine:
         self._act16 = False      # the last prefill layer's SwiGLU output went to the fp16 buffer
         self.ffn_f16 = ffn_f16
         self._ffn16 = False      # the last prefill layer ran gate/up on the fp16 norm
+        self._att16 = False      # the last prefill layer's attention output went to the fp16 buffer
 
     # ---- decode ---------------------------------------------------------------------------
     def _stream(self):
@@ -372,6 +373,7 @@ class Engine:
                     "k16": z(mp * c.kv_size, torch.int16), "v16": z(mp * c.kv_size, torch.int16),
                     "att": z(mp * c.q_size), "tmp": z(mp * c.hidden), "g": z(mp * c.ff), "u": z(mp * c.ff),
                     "g16": z(mp * c.ff, torch.int16), "xn16": z(mp * c.hidden, torch.int16),
+                    "att16": z(mp * c.q_size, torch.int16),
                     "ids": z(mp, torch.int32)}
         return self._pf
 
@@ -436,11 +438,24 @@ class Engine:
                     for src, dst in (("k", "k16"), ("v", "v16")):
                         _chk(L.convert_f32_to_f16(_p(b[src]), _p(b[dst]), mp * c.kv_size, st), "to f16")
                     k16, v16 = b["k16"], b["v16"]
-            _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(k16), _p(v16), _p(b["att"]),
-                                                           mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
-                 "attention")
+            # a Q4_K O projection reads the attention output as fp16 (the operand its
+            # fp32 launcher would round it to) through the K-sliced 128 x 64 tiles
+            self._att16 = (self.fuse_gemm and self.ffn_f16 and m["attn_output"][1].wtype == GgmlType.Q4_K
+                           and c.hidden % 64 == 0 and c.q_size % 256 == 0)
+            if self._att16:
+                _chk(L.rf_attention_prefill_gqa_causal_f16_launch(_p(b["q16"]), _p(k16), _p(v16), _p(b["att16"]),
+                                                                  mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
+                     "attention f16")
+            else:
+                _chk(L.wmma_attention_prefill_gqa_causal_launch(_p(b["q16"]), _p(k16), _p(v16), _p(b["att"]),
+                                                               mp, c.n_heads, c.n_kv_heads, 1, self.scale, st),
+                     "attention")
             t("attention", i)
-            self._gemm_residual(m["attn_output"], b["att"], b["x"], b["tmp"], c.hidden, c.q_size, M, st)
+            if self._att16:
+                _chk(L.rf_gemm_q4_k_f16_accumulate_launch(_p(b["att16"]), _p(m["attn_output"][0]), _p(b["x"]), mp,
+                                                          c.hidden, c.q_size, st), "gemm f16 accumulate")
+            else:
+                self._gemm_residual(m["attn_output"], b["att"], b["x"], b["tmp"], c.hidden, c.q_size, M, st)
             t("attn_output", i)
             gt, ut = m["ffn_gate"][1].wtype, m["ffn_up"][1].wtype
             gu16 = (self.fuse_gemm and self.ffn_f16 and gt == ut == GgmlType.Q4_K and c.ff % 128 == 0
@@ -481,8 +496,10 @@ class Engine:
                 _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             t("gate_up", i)
             if self._act16:
-                _chk(L.rf_gemm_q6_k_f16_accumulate_launch(_p(b["g16"]), _p(m["ffn_down"][0]), _p(b["x"]), mp,
-                                                          c.hidden, c.ff, st), "gemm f16 accumulate")
+                fn = (L.rf_gemm_q6_k_f16_accumulate_launch if m["ffn_down"][1].wtype == GgmlType.Q6_K
+                      else L.rf_gemm_q4_k_f16_accumulate_launch)
+                _chk(fn(_p(b["g16"]), _p(m["ffn_down"][0]), _p(b["x"]), mp, c.hidden, c.ff, st),
+                     "gemm f16 accumulate")
             else:
                 self._gemm_residual(m["ffn_down"], b["g"], b["x"], b["tmp"], c.hidden, c.ff, M, st)
             t("ffn_down", i)
@@ -499,9 +516,15 @@ class Engine:
 
     def _down_f16(self, wtype):
         """The FFN down projection on fp16 activations: Q6_K with K = ff a
-        multiple of 2048 and N = hidden of 64 (rf_gemm_q6_k_f16_accumulate_launch)."""
+        multiple of 2048 (rf_gemm_q6_k_f16_accumulate_launch), or Q4_K with
+        the fp16 FFN path (rf_gemm_q4_k_f16_accumulate_launch); N = hidden a
+        multiple of 64."""
         c = self.cfg
-        return self.fuse_gemm and wtype == GgmlType.Q6_K and c.ff % 2048 == 0 and c.hidden % 64 == 0
+        if not self.fuse_gemm or c.hidden % 64:
+            return False
+        if wtype == GgmlType.Q6_K:
+            return c.ff % 2048 == 0
+        return self.ffn_f16 and wtype == GgmlType.Q4_K and c.ff % 256 == 0
 
     def _fusable(self, wtype, n, k):
         return (self.fuse_gemm and wtype in (GgmlType.Q4_K, GgmlType.Q6_K) and n % 256 == 0

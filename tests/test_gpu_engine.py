@@ -236,8 +236,11 @@ def _check_prefill_stages(eng, lay):
             k = _h(b["k"]).reshape(-1, c.kv_size)[:M]
             v = _h(b["v"]).reshape(-1, c.kv_size)[:M]
             ref = O.attn_prefill_f16(q, k, v, M, c.n_heads, c.n_kv_heads, c.head_dim, eng.scale)
-            got = _h(b["att"]).reshape(-1, c.q_size)[:M]
+            # (fp16 where the O projection reads fp16 activations: one more rounding)
+            got = (_h(b["att16"]).view(np.float16).astype(np.float32) if eng._att16
+                   else _h(b["att"])).reshape(-1, c.q_size)[:M]
             assert _rel(got, ref) <= 2e-3
+            seen["att16"] = eng._att16
             kc = _h(eng.kc[lay]).view(np.uint16).reshape(-1, c.kv_size)[:M]
             assert np.array_equal(kc, k.astype(np.float16).view(np.uint16))
             seen["x_pre"], seen["att"] = _h(b["x"]).reshape(-1, c.hidden)[:M].copy(), got.copy()
@@ -295,16 +298,17 @@ def _check_prefill_stages(eng, lay):
 
 
 def test_prefill_stages(eng):
-    # (hidden 512, ff 1024: gate/up on the fp16 norm, a fp32 SwiGLU into a Q4_K down)
+    # (hidden 512, ff 1024: fp16 attention output into the Q4_K O projection,
+    # gate/up on the fp16 norm, a fp16 SwiGLU into the Q4_K down projection)
     seen = _check_prefill_stages(eng, 0)
-    assert seen["ffn16"] and not seen["act16"]
+    assert seen["ffn16"] and seen["act16"] and seen["att16"]
 
 
 def test_prefill_stages_fp32_ffn(weights):
     # the paired gate/up GEMM with SwiGLU in its epilogue, on the fp32 norm
     e = E.Engine(CFG, weights, max_seq=256, fuse_norm=False, ffn_f16=False)
     seen = _check_prefill_stages(e, 0)
-    assert not seen["ffn16"] and not seen["act16"]
+    assert not seen["ffn16"] and not seen["act16"] and not seen["att16"]
 
 
 def test_prefill_stages_f16_down(dev):

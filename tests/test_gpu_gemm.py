@@ -128,8 +128,11 @@ def test_gemm_identity_random_weights(rf, dev, fmt, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 14336, 4096), (256, 14336, 4096), (64, 14336, 4096), (128, 4096, 4096),
-                                   (576, 6144, 4096), (320, 256, 1024)])
+                                   (576, 6144, 4096), (320, 256, 1024), (128, 14336, 4096), (512, 4096, 4096),
+                                   (512, 4096, 12288), (192, 192, 512), (64, 64, 256)])
 def test_gemm_q4k_fp16_activations(rf, dev, m, n, k):
+    # 256 x 128 tiles at 512 x 14336; elsewhere the K-sliced 64 / 128-row tiles
+    # (M <= 64 / above), including partial row tiles and N = 64, 192
     # rf_gemm_q4_k_f16_launch on A rounded to fp16 by the caller: the operands
     # of wmma_gemm_q4_k_launch on fp32 A, so the same oracle and bar
     a = torch.from_numpy(synth.activations(k, seed=m + 11, m=m)).to(torch.bfloat16).float().numpy()
@@ -152,6 +155,29 @@ def test_gemm_q6k_fp16_activations(rf, dev, m, n, k):
     d = G.empty(m * n, torch.float32)
     G.call(rf.rf_gemm_q6_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
     _check(G.host(d).reshape(m, n), "q6_k", a, w, m, n, k, f"fp16-A q6_k M={m} {n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (64, 128, 512), (192, 64, 1024)])
+def test_gemm_q4k_fp16_accumulate(rf, dev, m, n, k):
+    # inout += product: bit for bit the plain launch's sums plus the old
+    # contents (the K-sliced tiles serve both; rows past M stay put)
+    a = torch.from_numpy(synth.activations(k, seed=m + 23, m=m)).to(torch.bfloat16).float().numpy()
+    w = synth.q4_k_weights(n, k, seed=k + 7)
+    da, dw = G.to_dev(a.astype(np.float16).view(np.int16)), G.to_dev(w)
+    r = synth.activations(n, seed=9, m=m + 64)
+    dr = G.to_dev(r)
+    G.call(rf.rf_gemm_q4_k_f16_accumulate_launch, G.ptr(da), G.ptr(dw), G.ptr(dr), m, n, k)
+    got = G.host(dr).reshape(m + 64, n)
+    np.testing.assert_array_equal(got[m:], r[m:])
+    ref = O.gemm("q4_k", a, w, m, n, k)
+    err = np.abs(got[:m].astype(np.float64) - r[:m] - ref)
+    tol = 2e-3 * np.abs(ref) + 1e-5 * np.abs(ref).max() + 1e-6 * np.abs(r[:m])
+    assert (err <= tol).all(), f"q4_k f16 accumulate {m}x{n}x{k}: worst {(err / tol).max():.3f}"
+    if m * n <= 64 * 4096:
+        # where the plain launch takes the same K-sliced tiles, bit for bit
+        d = G.empty(m * n, torch.float32)
+        G.call(rf.rf_gemm_q4_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
+        np.testing.assert_array_equal(got[:m], r[:m] + G.host(d).reshape(m, n))
 
 
 def test_gemm_q6k_fp16_rejections(rf, dev):

@@ -499,3 +499,22 @@ def test_rms_norm_and_swiglu_f16_outputs(rf, dev):
     np.testing.assert_array_equal(G.host(d16), G.host(d32).astype(np.float16).view(np.int16))
     assert rf.rf_rms_norm_batched_f16_on_stream(None, G.ptr(dw), G.ptr(d16), n, 1e-6, rows, G.stream()) != 0
     assert rf.rf_silu_mul_f16_on_stream(G.ptr(dg), G.ptr(du), None, 8, G.stream()) != 0
+
+
+def test_attention_prefill_f16_output(rf, dev):
+    # rf_attention_prefill_gqa_causal_f16_launch: __float2half of the fp32
+    # launcher's output, bit for bit
+    seq, nq, nkv, d = 192, 8, 2, 128
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((seq, nq * d)).astype(np.float16)
+    k = rng.standard_normal((seq, nkv * d)).astype(np.float16)
+    v = rng.standard_normal((seq, nkv * d)).astype(np.float16)
+    dq, dk, dv = (G.to_dev(t.view(np.int16)) for t in (q, k, v))
+    o32 = G.empty(seq * nq * d, torch.float32)
+    o16 = G.empty(seq * nq * d, torch.int16)
+    for causal in (1, 0):
+        G.call(rf.wmma_attention_prefill_gqa_causal_launch, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(o32), seq, nq, nkv,
+               causal, 0.088)
+        G.call(rf.rf_attention_prefill_gqa_causal_f16_launch, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(o16), seq, nq,
+               nkv, causal, 0.088)
+        np.testing.assert_array_equal(G.host(o16), G.host(o32).astype(np.float16).view(np.int16))
