@@ -509,6 +509,17 @@ hipError_t rf_gemv_qkv_q4_k_q8_rmsnorm_launch(const void* w_q, const void* w_k, 
                                               float* out_v, int n_rows, int n_q, int n_kv, hipStream_t stream);
 hipError_t rf_gemv_q6_k_rmsnorm_launch(const void* weights_q6_k, const float* input, const float* norm_w, float eps,
                                        float* output, int n_rows, int ncols_dst, hipStream_t stream);
+/* Q4_K Q and K with a Q6_K V (Q4_K_M layers whose attn_v is Q6_K), the
+ * RMSNorm folded in, one launch: out_q / out_k as rf_gemv_q4_k_q8_rmsnorm_launch
+ * and out_v as rf_gemv_q6_k_rmsnorm_launch would give them (same bits), plus
+ * the optional biases.  The reference runs a norm and three GEMVs
+ * (src/gpu/ops.rs:851-853, src/gpu/forward.rs:2349-2359).  K (n_rows) in
+ * {2048, 4096, 8192}; weights, input and norm_w 16-byte aligned. */
+hipError_t rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch(const void* w_q, const void* w_k, const void* w_v_q6_k,
+                                                  const float* bias_q, const float* bias_k, const float* bias_v,
+                                                  const float* input, const float* norm_w, float eps, float* out_q,
+                                                  float* out_k, float* out_v, int n_rows, int n_q, int n_kv,
+                                                  hipStream_t stream);
 
 /* ---- Parity probes (no reference counterpart) ---------------------------
  * Expose the intermediate integers of the Q8-inline path so tests can check

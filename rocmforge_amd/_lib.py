@@ -46,6 +46,8 @@ SIGNATURES = {
     "rf_gemv_qkv_q4_k_q8_rmsnorm_launch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i,
                                            _vp],
     "rf_gemv_q6_k_rmsnorm_launch": [_vp, _vp, _vp, _f, _vp, _i, _i, _vp],
+    "rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _i,
+                                               _i, _vp],
     "gpu_rms_norm": [_vp, _vp, _vp, _i, _f, _vp],
     "gpu_rms_norm_batched": [_vp, _vp, _vp, _i, _f, _i],
     "gpu_rms_norm_batched_on_stream": [_vp, _vp, _vp, _i, _f, _i, _vp],

@@ -21,7 +21,7 @@
 //    the CU count so a large N re-uses each workgroup's quantised vector.
 #include <type_traits>
 
-#include "qk_common.h"
+#include "q6k_lin.h"
 
 
 namespace rf {
@@ -46,25 +46,28 @@ struct QkvArgs {
     int n_q, n_kv;
     const float* norm_w;   // RMSNorm weights applied to x first (any mode), or null
     float eps;
+    int no_v;              // Q and K only (the V projection runs elsewhere)
 };
 
 // Waves per matrix: [0, nw[0]) on Q, then nw[1] on K, nw[2] on V (each >= 1;
-// nwaves >= 3).  Host and device compute the same split.
+// nwaves >= 3), or with no_v nw[2] = 0 (nwaves >= 2).  Host and device
+// compute the same split.
 struct QkvSplit {
     int nw[3];
 };
-__host__ __device__ inline QkvSplit qkv_split(int nwaves, int n_q, int n_kv) {
-    const long n = (long)n_q + 2L * n_kv;
+__host__ __device__ inline QkvSplit qkv_split(int nwaves, int n_q, int n_kv, int no_v = 0) {
+    const int nm = no_v ? 2 : 3;
+    const long n = (long)n_q + (long)(nm - 1) * n_kv;
     int q = (int)(((long)nwaves * n_q + n / 2) / n);
-    q = q < 1 ? 1 : (q > nwaves - 2 ? nwaves - 2 : q);
-    const int k = (nwaves - q) / 2;
+    q = q < 1 ? 1 : (q > nwaves - (nm - 1) ? nwaves - (nm - 1) : q);
+    const int k = no_v ? nwaves - q : (nwaves - q) / 2;
     return QkvSplit{{q, k, nwaves - q - k}};
 }
 // Largest number of rows one wave owns (its LDS result slots).
 __host__ __device__ inline int qkv_max_rows(const QkvSplit& sp, int n_q, int n_kv) {
     const int a = (n_q + sp.nw[0] - 1) / sp.nw[0];
     const int b = (n_kv + sp.nw[1] - 1) / sp.nw[1];
-    const int c = (n_kv + sp.nw[2] - 1) / sp.nw[2];
+    const int c = sp.nw[2] ? (n_kv + sp.nw[2] - 1) / sp.nw[2] : 0;
     return a > b ? (a > c ? a : c) : (b > c ? b : c);
 }
 
@@ -99,13 +102,12 @@ __device__ __forceinline__ float q4k_q8_unit_dot(const Q4KUnit& u, int p, const 
 
 // ONE: K <= 4096 (a row group is one pipeline step), so the step -> (row
 // group, K slice) split needs no division and every step ends a group.
-template <int MODE, int R, int NW, int NB, bool ONE = false>
-__global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
-                                                                   const uint8_t* __restrict__ w1,
-                                                                   const float* __restrict__ x,
-                                                                   const float* residual, float* y, int K, int N,
-                                                                   QkvArgs qkv) {
-    extern __shared__ __align__(16) uint8_t smem[];
+// Workgroup bid of nblk (the kernel below passes blockIdx.x, gridDim.x);
+// smem is the dynamic LDS block.
+template <int MODE, int R, int NW, int NB, bool ONE>
+__device__ __forceinline__ void q4k_q8_gemv_wg(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                               const float* __restrict__ x, const float* residual, float* y, int K,
+                                               int N, const QkvArgs& qkv, int bid, int nblk, uint8_t* smem) {
     const Q8Lds q8 = q8_lds_carve(smem, K);
     constexpr int M = (MODE == kGateUp) ? 2 : 1;
 
@@ -115,19 +117,19 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
     const int p = lane & 3;
     const int nsb = K / kQK;
     const size_t row_bytes = (size_t)nsb * kQ4KBytes;
-    const int nwaves = gridDim.x * NW;
+    const int nwaves = nblk * NW;
     // Rows are dealt out round-robin: global wave gw owns rows gw, gw+nwaves,
     // ...  All waves of the grid then stream neighbouring rows at the same
     // time, which keeps the open DRAM pages few (measured: an interleaved
     // read of 64 MB runs ~12% faster than per-wave contiguous stretches).
-    const int gw = blockIdx.x * NW + wave;
+    const int gw = bid * NW + wave;
     int rstride = nwaves, rfirst = gw, nrows_of = N, max_rows = (N + nwaves - 1) / nwaves;
     const uint8_t* wm = w0;
     float* ym = y;
     const float* bm = nullptr;
     if constexpr (MODE == kQkv) {
         // this wave's matrix and its rank among the waves on that matrix
-        const QkvSplit sp = qkv_split(nwaves, qkv.n_q, qkv.n_kv);
+        const QkvSplit sp = qkv_split(nwaves, qkv.n_q, qkv.n_kv, qkv.no_v);
         // (selects, not indexing: a runtime index into the argument arrays
         // would put them in scratch memory)
         const int m = gw < sp.nw[0] ? 0 : (gw < sp.nw[0] + sp.nw[1] ? 1 : 2);
@@ -235,6 +237,53 @@ __global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* 
             y[row] = g / (1.0f + expf(-g)) * sum4(4 * (M * j + 1));
         }
     }
+}
+
+template <int MODE, int R, int NW, int NB, bool ONE = false>
+__global__ __launch_bounds__(NW * 64) void rf_q4k_q8_gemv_kernel(const uint8_t* __restrict__ w0,
+                                                                   const uint8_t* __restrict__ w1,
+                                                                   const float* __restrict__ x,
+                                                                   const float* residual, float* y, int K, int N,
+                                                                   QkvArgs qkv) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    q4k_q8_gemv_wg<MODE, R, NW, NB, ONE>(w0, w1, x, residual, y, K, N, qkv, blockIdx.x, gridDim.x, smem);
+}
+
+// Q4_K Q and K with a Q6_K V, RMSNorm folded in, one launch: workgroups
+// [0, gv) are teams of the K-split Q6_K GEMV (q6k_lin.h: 4 / nwk teams of
+// nwk = K / 2048 waves each, team t of the grid taking V rows t, t + teams,
+// ..), the rest run the fused Q8-inline Q/K GEMV over Q and K.  Each output
+// has the bits of its own launcher (rf_gemv_q4_k_q8_rmsnorm_launch,
+// rf_gemv_q6_k_rmsnorm_launch).  LDS: the larger of the two layouts.
+struct Q6VArgs {
+    const uint8_t* w;
+    const float* bias;
+    float* y;
+    int n;      // V rows
+    int gv;     // workgroups on V
+};
+
+template <bool ONE>
+__global__ __launch_bounds__(256) void rf_qkv_q4k_q6v_kernel(const float* __restrict__ x, int K, QkvArgs qkv,
+                                                             Q6VArgs v) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if ((int)blockIdx.x < v.gv) {
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+        const int nwk = K / 2048;
+        const int tpw = 4 / nwk;                          // teams per workgroup
+        const int team = wave / nwk;
+        __shared__ float red[4];
+        const float inv = rms_inv_canonical(x, K, qkv.eps, red);
+        const int G = v.gv * tpw;
+        const int g = (int)blockIdx.x * tpw + team;
+        const int rows = (v.n + G - 1) / G;
+        float* part = reinterpret_cast<float*>(smem + 4 * 2048) + team * rows * nwk * 4;
+        q6_lin_team<kQ6Ring>(v.w, x, v.bias, v.y, K, v.n, qkv.norm_w, inv, g, G, wave % nwk, nwk,
+                                smem + wave * 2048, part);
+        return;
+    }
+    q4k_q8_gemv_wg<kQkv, 2, 4, 3, ONE>(qkv.w[0], nullptr, x, nullptr, nullptr, K, qkv.n_q + qkv.n_kv, qkv,
+                                        (int)blockIdx.x - v.gv, (int)gridDim.x - v.gv, smem);
 }
 
 // ── FP32-activation family (q4_k_gemv.hip) ───────────────────────────────
@@ -586,6 +635,63 @@ extern "C" hipError_t rf_gemv_qkv_q4_k_q8_rmsnorm_launch(const void* w_q, const 
     a.norm_w = norm_w;
     a.eps = eps;
     return launch_q8<kQkv>(w_q, nullptr, input, nullptr, nullptr, n_rows, n_q + 2 * n_kv, stream, a);
+}
+
+// Q4_K Q and K with a Q6_K V (the Q4_K_M attention input of the layers
+// whose attn_v is Q6_K), RMSNorm folded in, one launch; each output has the
+// bits of its own normalising launcher.  No counterpart in the reference
+// (three GEMV launches after a norm, src/gpu/ops.rs:851-853).  K (n_rows) in
+// {2048, 4096, 8192}; weights, input and norm_w 16-byte aligned.
+constexpr int kQkvVRowsPerTeam = 2;     // V rows per Q6_K team
+
+extern "C" hipError_t rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch(const void* w_q, const void* w_k, const void* w_v_q6_k,
+                                                             const float* bias_q, const float* bias_k,
+                                                             const float* bias_v, const float* input,
+                                                             const float* norm_w, float eps, float* out_q,
+                                                             float* out_k, float* out_v, int n_rows, int n_q,
+                                                             int n_kv, hipStream_t stream) {
+    if (n_rows <= 0 || n_q <= 0 || n_kv <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows))
+        return hipErrorInvalidValue;
+    const int nsb = n_rows / kQK;
+    if (nsb % 8 != 0 || nsb / 8 > 4 || 4 % (nsb / 8) != 0) return hipErrorInvalidValue;
+    if (w_q == nullptr || w_k == nullptr || w_v_q6_k == nullptr) return hipErrorInvalidValue;
+    if (out_q == nullptr || out_k == nullptr || out_v == nullptr) return hipErrorInvalidValue;
+    if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v_q6_k) || !norm_args_ok(input, norm_w))
+        return hipErrorInvalidValue;
+    if ((long)n_q + (long)n_kv > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    QkvArgs a{};
+    a.w[0] = static_cast<const uint8_t*>(w_q);
+    a.w[1] = static_cast<const uint8_t*>(w_k);
+    a.bias[0] = bias_q;
+    a.bias[1] = bias_k;
+    a.y[0] = out_q;
+    a.y[1] = out_k;
+    a.n_q = n_q;
+    a.n_kv = n_kv;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.no_v = 1;
+    // Q/K workgroups as launch_q8: four waves, two rows per lane step, at
+    // most one workgroup per CU
+    const int cap = device_cu_count();
+    const int nqk = n_q + n_kv;
+    const int gq = (nqk + 3) / 4 < cap ? (nqk + 3) / 4 : cap;
+    const size_t wave_rows = (size_t)qkv_max_rows(qkv_split(gq * 4, n_q, n_kv, 1), n_q, n_kv);
+    const size_t lds_q = q8_lds_bytes(n_rows) + 4 * wave_rows * 4 * sizeof(float);
+    // Q6_K teams of nwk waves, kQkvVRowsPerTeam rows each
+    const int nwk = nsb / 8, tpw = 4 / nwk;
+    const int teams = (n_kv + kQkvVRowsPerTeam - 1) / kQkvVRowsPerTeam;
+    const int gv = (teams + tpw - 1) / tpw;
+    const size_t v_rows = (size_t)(n_kv + gv * tpw - 1) / (gv * tpw);
+    const size_t lds_v = 4 * 2048 + (size_t)tpw * v_rows * nwk * 4 * sizeof(float);
+    const size_t lds = lds_q > lds_v ? lds_q : lds_v;
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    const Q6VArgs v{static_cast<const uint8_t*>(w_v_q6_k), bias_v, out_v, n_kv, gv};
+    if (nsb <= kSbPerStep)
+        hipLaunchKernelGGL(rf_qkv_q4k_q6v_kernel<true>, dim3(gv + gq), dim3(256), lds, stream, input, n_rows, a, v);
+    else
+        hipLaunchKernelGGL(rf_qkv_q4k_q6v_kernel<false>, dim3(gv + gq), dim3(256), lds, stream, input, n_rows, a, v);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t gemv_q4_k_f32_launch(const void* weights_q4_k, const float* input, float* output, int n_rows,

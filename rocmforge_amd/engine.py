@@ -286,8 +286,9 @@ class Engine:
         return (k // 256) % 8 == 0 and k <= 16384
 
     def _qkv_normed(self, m, norm_w, st):
-        """q, k, v = W rmsnorm(hidden): one launch when all three are Q4_K,
-        else one normalising GEMV per matrix."""
+        """q, k, v = W rmsnorm(hidden): one launch when all three are Q4_K
+        or Q/K are Q4_K and V is Q6_K, else one normalising GEMV per
+        matrix."""
         L, c = self.lib, self.cfg
         mats = [m["attn_q"], m["attn_k"], m["attn_v"]]
         outs = [(self.q, c.q_size), (self.k, c.kv_size), (self.v, c.kv_size)]
@@ -296,6 +297,13 @@ class Engine:
                                                       None, _p(self.hidden), _p(norm_w), c.eps, _p(self.q),
                                                       _p(self.k), _p(self.v), c.hidden, c.q_size, c.kv_size, st),
                  "qkv+norm")
+            return
+        if ([mt[1].wtype for mt in mats] == [GgmlType.Q4_K, GgmlType.Q4_K, GgmlType.Q6_K]
+                and c.hidden in (2048, 4096, 8192)):
+            _chk(L.rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch(_p(mats[0][0]), _p(mats[1][0]), _p(mats[2][0]), None, None,
+                                                          None, _p(self.hidden), _p(norm_w), c.eps, _p(self.q),
+                                                          _p(self.k), _p(self.v), c.hidden, c.q_size, c.kv_size, st),
+                 "qkv+norm (q6_k v)")
             return
         for (w, meta), (out, n) in zip(mats, outs):
             if meta.wtype == GgmlType.Q4_K:

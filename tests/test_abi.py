@@ -64,3 +64,20 @@ def test_gemm_rejects_shapes(rf, m, n, k):
     # wmma_gemm_q4_k.hip:207-210: M % 64, N % 64, K % 256
     assert rf.wmma_gemm_q4_k_launch(P, P, P, m, n, k, NUL) == HIP_ERROR_INVALID_VALUE
     assert rf.wmma_gemm_q6_k_launch(P, P, P, m, n, k, NUL) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("k", [0, 1024, 3072, 6144, 16384, 300])
+def test_qkv_q6v_rejects_shapes(rf, k):
+    # K in {2048, 4096, 8192}: whole Q6_K teams of K / 2048 waves in a workgroup
+    assert rf.rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch(P, P, P, NUL, NUL, NUL, P, P, 1e-6, P, P, P, k, 64, 16,
+                                                     NUL) == HIP_ERROR_INVALID_VALUE
+
+
+def test_qkv_q6v_rejects_pointers(rf):
+    f = rf.rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch
+    assert f(P, P, NUL, NUL, NUL, NUL, P, P, 1e-6, P, P, P, 4096, 64, 16, NUL) == HIP_ERROR_INVALID_VALUE
+    assert f(P, P, P, NUL, NUL, NUL, P, NUL, 1e-6, P, P, P, 4096, 64, 16, NUL) == HIP_ERROR_INVALID_VALUE
+    assert f(P, P, P, NUL, NUL, NUL, P, P, 1e-6, P, P, NUL, 4096, 64, 16, NUL) == HIP_ERROR_INVALID_VALUE
+    assert f(P, P, ctypes.c_void_p(0x100002), NUL, NUL, NUL, P, P, 1e-6, P, P, P, 4096, 64, 16,
+             NUL) == HIP_ERROR_INVALID_VALUE
+    assert f(P, P, P, NUL, NUL, NUL, P, P, 1e-6, P, P, P, 4096, 0, 16, NUL) == HIP_ERROR_INVALID_VALUE

@@ -275,3 +275,40 @@ def test_rmsnorm_fused_gemvs_equal_two_launches(rf, dev, k, n):
         G.call(rf.gemv_q6_k_f32_launch, G.ptr(w6), G.ptr(normed), G.ptr(a6), k, n)
         G.call(rf.rf_gemv_q6_k_rmsnorm_launch, G.ptr(w6), G.ptr(dx), G.ptr(dg), 1e-6, G.ptr(b6), k, n)
         np.testing.assert_array_equal(G.host(a6), G.host(b6))
+
+
+@pytest.mark.parametrize("k,nq,nkv,bias", [(4096, 4096, 1024, False), (4096, 4096, 1000, True),
+                                           (2048, 2048, 512, True), (8192, 1024, 256, False)])
+def test_qkv_q4k_q6v_equals_separate_launches(rf, dev, k, nq, nkv, bias):
+    # Q4_K Q/K with a Q6_K V in one launch: Q and K bit for bit as the
+    # all-Q4_K fused launch, V as the normalising Q6_K GEMV (plus bias: the
+    # residual launcher on the normalised x), V also against the oracle
+    rng = np.random.default_rng(k + nkv)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    dx, dg = G.to_dev(x), G.to_dev(g)
+    wq, wk = G.to_dev(synth.q4_k_weights(nq, k, seed=11)), G.to_dev(synth.q4_k_weights(nkv, k, seed=12))
+    wv4 = G.to_dev(synth.q4_k_weights(nkv, k, seed=13))
+    wv6h = synth.q6_k_weights(nkv, k, seed=14)
+    wv6 = G.to_dev(wv6h)
+    bs = [G.to_dev(synth.activations(m, seed=20 + i)) if bias else None for i, m in enumerate((nq, nkv, nkv))]
+    bp = [G.ptr(b) if b is not None else None for b in bs]
+    ref = [G.empty(m, torch.float32) for m in (nq, nkv, nkv)]
+    out = [G.empty(m, torch.float32) for m in (nq, nkv, nkv)]
+    G.call(rf.rf_gemv_qkv_q4_k_q8_rmsnorm_launch, G.ptr(wq), G.ptr(wk), G.ptr(wv4), *bp, G.ptr(dx), G.ptr(dg), 1e-6,
+           *[G.ptr(o) for o in ref], k, nq, nkv)
+    G.call(rf.rf_gemv_qkv_q4_k_q6_k_v_rmsnorm_launch, G.ptr(wq), G.ptr(wk), G.ptr(wv6), *bp, G.ptr(dx), G.ptr(dg),
+           1e-6, *[G.ptr(o) for o in out], k, nq, nkv)
+    np.testing.assert_array_equal(G.host(out[0]), G.host(ref[0]))
+    np.testing.assert_array_equal(G.host(out[1]), G.host(ref[1]))
+    v_ref = G.empty(nkv, torch.float32)
+    if bias:
+        normed = G.empty(k, torch.float32)
+        G.call(rf.gpu_rms_norm, G.ptr(dx), G.ptr(dg), G.ptr(normed), k, 1e-6)
+        G.call(rf.gemv_q6_k_f32_residual_launch, G.ptr(wv6), G.ptr(normed), G.ptr(bs[2]), G.ptr(v_ref), k, nkv)
+    else:
+        G.call(rf.rf_gemv_q6_k_rmsnorm_launch, G.ptr(wv6), G.ptr(dx), G.ptr(dg), 1e-6, G.ptr(v_ref), k, nkv)
+    np.testing.assert_array_equal(G.host(out[2]), G.host(v_ref))
+    xn = O.rms_norm(x, g, 1e-6)
+    v_or = O.gemv_q6k(wv6h, xn, k, nkv) + (G.host(bs[2]) if bias else 0.0)
+    _check(G.host(out[2]), v_or, f"q6_k v {nkv}x{k}")
