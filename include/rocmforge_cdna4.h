@@ -133,6 +133,16 @@ hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weight
  * aligned.  Used for the O and FFN-down projections of a prefill. */
 hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q4_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
+/* Up to three weight matrices over one fp16 input as column segments of one
+ * launch, each Q4_K (type 12) or Q6_K (type 14, GGML type ids):
+ * out_s[M x n_s] = the product of rf_gemm_q4_k_f16_launch /
+ * rf_gemm_q6_k_f16_launch on 128 x 64 tiles (each output written once).  The
+ * prefill Q/K/V of a layer of any type mix (the reference runs three GEMMs,
+ * src/gpu/forward.rs:2327).  M % 64, n_s % 64 (n1, n2 may be 0), K % 256
+ * (K % 2048 with a Q6_K segment); input, weights and outputs 16-byte aligned. */
+hipError_t rf_gemm_qk_f16_segments_launch(const uint16_t* input_f16, const void* w0, const void* w1, const void* w2,
+                                          int type0, int type1, int type2, float* out0, float* out1, float* out2,
+                                          int M, int n0, int n1, int n2, int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
 

@@ -1797,11 +1797,10 @@ __device__ __forceinline__ u32x2 q6a_dq4(uint32_t qb, float S24, float nO) {
     return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
+// Tile v of the launch (after the XCD remap); lds: the kLds-byte LDS block.
 template <bool ACC>
-__global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
-                                                                        const uint8_t* __restrict__ W,
-                                                                        float* __restrict__ D, int M, int N, int K) {
-    __shared__ __align__(16) uint8_t lds[kQ6aLds];
+__device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
+                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds) {
     uint8_t* ring = lds;
     uint8_t* abuf0 = lds + kQ6aRS * kQ6aStage;
     const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
@@ -1813,7 +1812,6 @@ __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uin
     const int ks = wave & 3, cg = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
     const int mtiles = (M + kQ6aBM - 1) / kQ6aBM;
-    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (v % mtiles) * kQ6aBM;      // the M tiles of one column tile are neighbours
     const int n0 = (v / mtiles) * kQ6aBN;
     const int nchunks = K / kKC;
@@ -2045,6 +2043,14 @@ __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uin
     }
 }
 
+template <bool ACC>
+__global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint8_t* __restrict__ W,
+                                                                        float* __restrict__ D, int M, int N, int K) {
+    __shared__ __align__(16) uint8_t lds[kQ6aLds];
+    q6a_wg<ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds);
+}
+
 // ── q4s: Q4_K GEMM on fp16 activations, 32 FMR x 64 tiles, K slices on waves
 // (rf_gemm_q4_k_f16_launch where the 256 x 128 tiles leave CUs idle) ───────
 // The layout of rf_gemm_q6k_f16a_kernel for Q4_K weights: eight waves, wave
@@ -2077,12 +2083,11 @@ struct Q4sGeom {
     static constexpr int kLds = kLdsLoop > kLdsXch ? kLdsLoop : kLdsXch;
 };
 
+// Tile v of the launch (after the XCD remap); lds: the kLds-byte LDS block.
 template <int FMR, bool ACC>
-__global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uint16_t* __restrict__ A,
-                                                                        const uint8_t* __restrict__ W,
-                                                                        float* __restrict__ D, int M, int N, int K) {
+__device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
+                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds) {
     using G = Q4sGeom<FMR>;
-    __shared__ __align__(16) uint8_t lds[G::kLds];
     uint8_t* ring = lds;
     uint8_t* abuf0 = lds + kQ4sRS * kQ4sStage;
     const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
@@ -2094,7 +2099,6 @@ __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uin
     const int ks = wave & 3, cg = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
     const int mtiles = (M + G::kBM - 1) / G::kBM;
-    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (v % mtiles) * G::kBM;      // the M tiles of one column tile are neighbours
     const int n0 = (v / mtiles) * kQ4sBN;
     const int nchunks = K / kKC;
@@ -2275,6 +2279,47 @@ __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uin
             }
         }
     }
+}
+
+template <int FMR, bool ACC>
+__global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint8_t* __restrict__ W,
+                                                                        float* __restrict__ D, int M, int N, int K) {
+    __shared__ __align__(16) uint8_t lds[Q4sGeom<FMR>::kLds];
+    q4s_wg<FMR, ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds);
+}
+
+// Column segments on fp16 activations: up to three weight matrices (each
+// Q4_K or Q6_K) over one input, each with its own output, in one launch of
+// 128 x 64 tiles -- the K-sliced Q4_K tiles (q4s_wg) and the Q6_K tiles
+// (q6a_wg) share the tile shape, the 512 threads and the LDS size.  Tile v
+// (after the XCD remap) belongs to the segment whose tile range holds it;
+// each output is written once (no K split).
+struct F16Segs {
+    const uint8_t* w[3];
+    float* d[3];
+    int n[3];
+    int q6[3];
+    int tiles[3];      // M tiles x column tiles of each segment
+};
+static_assert(kQ6aBM == 128 && kQ6aBN == kQ4sBN && kQ6aThreads == kQ4sThreads, "q6a and q4s tiles differ");
+constexpr int kF16SegLds = kQ6aLds > Q4sGeom<4>::kLds ? kQ6aLds : Q4sGeom<4>::kLds;
+
+__global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uint16_t* __restrict__ A, int M, int K,
+                                                                        F16Segs sg) {
+    __shared__ __align__(16) uint8_t lds[kF16SegLds];
+    int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    // segment selection by selects (no runtime index into the argument)
+    const int s = v < sg.tiles[0] ? 0 : (v < sg.tiles[0] + sg.tiles[1] ? 1 : 2);
+    v -= s == 0 ? 0 : (s == 1 ? sg.tiles[0] : sg.tiles[0] + sg.tiles[1]);
+    const uint8_t* w = s == 0 ? sg.w[0] : (s == 1 ? sg.w[1] : sg.w[2]);
+    float* d = s == 0 ? sg.d[0] : (s == 1 ? sg.d[1] : sg.d[2]);
+    const int n = s == 0 ? sg.n[0] : (s == 1 ? sg.n[1] : sg.n[2]);
+    const int q6 = s == 0 ? sg.q6[0] : (s == 1 ? sg.q6[1] : sg.q6[2]);
+    if (q6)
+        q6a_wg<false>(A, w, d, M, n, K, v, lds);
+    else
+        q4s_wg<4, false>(A, w, d, M, n, K, v, lds);
 }
 
 // Split count: the largest S with S | (K/64)/8 (each split a whole number of
@@ -2546,6 +2591,46 @@ extern "C" hipError_t rf_gemm_q6_k_segments_launch(const float* input, const voi
                                                    float* out0, float* out1, float* out2, int M, int n0, int n1,
                                                    int n2, int K, hipStream_t stream) {
     return gemm_segments<true>(input, w0, w1, w2, out0, out1, out2, M, n0, n1, n2, K, stream);
+}
+
+// Up to three weight matrices over one fp16 input as column segments of one
+// launch (rf_gemm_f16_segs_kernel), each Q4_K (type 12) or Q6_K (type 14):
+// out_s[M x n_s] = fp16(A) * fp16(dequant W_s)^T, the products of
+// rf_gemm_q4_k_f16_launch / rf_gemm_q6_k_f16_launch on 128 x 64 tiles.  The
+// prefill Q/K/V of a layer whatever its type mix.  M % 64, n_s % 64 (n1, n2
+// may be 0: fewer segments), K % 256 (K % 2048 with a Q6_K segment); input,
+// weights and outputs 16-byte aligned.
+extern "C" hipError_t rf_gemm_qk_f16_segments_launch(const uint16_t* input_f16, const void* w0, const void* w1,
+                                                     const void* w2, int type0, int type1, int type2, float* out0,
+                                                     float* out1, float* out2, int M, int n0, int n1, int n2, int K,
+                                                     hipStream_t stream) {
+    constexpr int kQ4KType = 12, kQ6KType = 14;
+    if (input_f16 == nullptr || !aligned16(input_f16) || M <= 0 || M % 64 || K <= 0 || K % kQK)
+        return hipErrorInvalidValue;
+    if (n0 <= 0 || n1 < 0 || n2 < 0 || (n1 == 0 && n2 > 0)) return hipErrorInvalidValue;
+    F16Segs sg{};
+    const void* ws[3] = {w0, w1, w2};
+    float* ds[3] = {out0, out1, out2};
+    const int ns[3] = {n0, n1, n2}, ts[3] = {type0, type1, type2};
+    const int mtiles = (M + 127) / 128;
+    long total = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (ns[i] == 0) continue;
+        if (ns[i] % kQ4sBN || ws[i] == nullptr || ds[i] == nullptr || !aligned16(ws[i]) || !aligned16(ds[i]))
+            return hipErrorInvalidValue;
+        if (ts[i] != kQ4KType && ts[i] != kQ6KType) return hipErrorInvalidValue;
+        if (ts[i] == kQ6KType && K % 2048) return hipErrorInvalidValue;
+        sg.w[i] = static_cast<const uint8_t*>(ws[i]);
+        sg.d[i] = ds[i];
+        sg.n[i] = ns[i];
+        sg.q6[i] = ts[i] == kQ6KType;
+        sg.tiles[i] = mtiles * (ns[i] / kQ4sBN);
+        total += sg.tiles[i];
+    }
+    if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_gemm_f16_segs_kernel, dim3((unsigned)total), dim3(kQ4sThreads), 0, stream, input_f16, M, K,
+                       sg);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const void* weights_q4_k, float* inout,

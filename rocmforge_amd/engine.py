@@ -201,6 +201,7 @@ class Engine:
         self.ffn_f16 = ffn_f16
         self._ffn16 = False      # the last prefill layer ran gate/up on the fp16 norm
         self._att16 = False      # the last prefill layer's attention output went to the fp16 buffer
+        self._qkv16 = False      # the last prefill layer ran Q/K/V on the fp16 attention norm
 
     # ---- decode ---------------------------------------------------------------------------
     def _stream(self):
@@ -407,10 +408,24 @@ class Engine:
         t("embed", -1)
         for i, lw in enumerate(self.w.layers):
             m = lw.mats
-            _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn"]), c.hidden, c.eps, mp,
-                                                  st), "norm")
-            self._gemm_group([(m["attn_q"], b["q"], c.q_size), (m["attn_k"], b["k"], c.kv_size),
-                              (m["attn_v"], b["v"], c.kv_size)], b["xn"], c.hidden, M, st)
+            qkv = [(m["attn_q"], b["q"], c.q_size), (m["attn_k"], b["k"], c.kv_size),
+                   (m["attn_v"], b["v"], c.kv_size)]
+            types = [wm[1].wtype for wm, _, _ in qkv]
+            # Q/K/V on the attention norm rounded to fp16 (the operand values the fp32
+            # launchers round it to): one launch of 128 x 64 tiles whatever the type mix
+            self._qkv16 = (self.fuse_gemm and self.ffn_f16 and all(ty in (GgmlType.Q4_K, GgmlType.Q6_K) for ty in types)
+                           and c.q_size % 64 == 0 and c.kv_size % 64 == 0
+                           and c.hidden % (2048 if GgmlType.Q6_K in types else 256) == 0)
+            if self._qkv16:
+                _chk(L.rf_rms_norm_batched_f16_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn16"]), c.hidden, c.eps,
+                                                         mp, st), "norm f16")
+                _chk(L.rf_gemm_qk_f16_segments_launch(_p(b["xn16"]), *[_p(wm[0]) for wm, _, _ in qkv],
+                                                      *[int(ty) for ty in types], *[_p(o) for _, o, _ in qkv], mp,
+                                                      c.q_size, c.kv_size, c.kv_size, c.hidden, st), "qkv f16")
+            else:
+                _chk(L.gpu_rms_norm_batched_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn"]), c.hidden, c.eps, mp,
+                                                      st), "norm")
+                self._gemm_group(qkv, b["xn"], c.hidden, M, st)
             t("qkv", i)
             if self.fuse_norm and c.head_dim in (64, 128, 256) and mp <= self.max_seq:
                 # per-head norms, RoPE, the KV-cache rows and fp16 Q in one launch (the

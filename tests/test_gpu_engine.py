@@ -222,8 +222,13 @@ def _check_prefill_stages(eng, lay):
         if name == "qkv":
             # x is the layer's input until the O product is added
             x_in = _h(b["x"]).reshape(-1, c.hidden)[:M]
-            xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
-            assert _rel(xn, O.rms_norm(x_in, _h(w.layers[lay].attn_norm), c.eps, M)) <= 1e-5
+            # (fp16 rows where Q/K/V read fp16 activations: one rounding of the same values)
+            if eng._qkv16:
+                xn = _h(b["xn16"]).view(np.float16).reshape(-1, c.hidden)[:M].astype(np.float32)
+            else:
+                xn = _h(b["xn"]).reshape(-1, c.hidden)[:M]
+            assert _rel(xn, O.rms_norm(x_in, _h(w.layers[lay].attn_norm), c.eps, M)) <= (5e-4 if eng._qkv16 else 1e-5)
+            seen["qkv16"] = eng._qkv16
             m = w.layers[lay].mats
             for buf, mat, n in (("q", "attn_q", c.q_size), ("k", "attn_k", c.kv_size), ("v", "attn_v", c.kv_size)):
                 wm = m[mat]
@@ -302,13 +307,26 @@ def test_prefill_stages(eng):
     # gate/up on the fp16 norm, a fp16 SwiGLU into the Q4_K down projection)
     seen = _check_prefill_stages(eng, 0)
     assert seen["ffn16"] and seen["act16"] and seen["att16"]
+    # (hidden 512 keeps a Q6_K V off the fp16 segments: its tiles need K % 2048)
+    assert seen["qkv16"] == (eng.w.layers[0].mats["attn_v"][1].wtype == GgmlType.Q4_K)
 
 
 def test_prefill_stages_fp32_ffn(weights):
     # the paired gate/up GEMM with SwiGLU in its epilogue, on the fp32 norm
     e = E.Engine(CFG, weights, max_seq=256, fuse_norm=False, ffn_f16=False)
     seen = _check_prefill_stages(e, 0)
-    assert not seen["ffn16"] and not seen["act16"] and not seen["att16"]
+    assert not seen["ffn16"] and not seen["act16"] and not seen["att16"] and not seen["qkv16"]
+
+
+def test_prefill_stages_qkv16_q6v(dev):
+    # hidden 2048: the Q6_K V of layer 2 (of 3, Q4_K_M rule) joins Q and K in
+    # the fp16-activation segment launch
+    cfg = E.ModelConfig(n_layers=3, hidden=2048, ff=2048, n_heads=16, n_kv_heads=4, head_dim=128, vocab=2048)
+    e = E.Engine(cfg, E.synthetic_weights(cfg, seed=13, signed=True), max_seq=256, fuse_norm=False)
+    assert e.w.layers[2].mats["attn_v"][1].wtype == GgmlType.Q6_K
+    assert _check_prefill_stages(e, 2)["qkv16"]
+    del e
+    torch.cuda.empty_cache()
 
 
 def test_prefill_stages_f16_down(dev):

@@ -190,3 +190,55 @@ def test_rejections(rf, dev):
     sw = rf.rf_gemm_q4_k_swiglu_launch
     assert sw(P(da), P(w), P(w), P(d), m, 64, k, s) != 0                         # N % 128
     assert sw(P(da), P(w), z, P(d), m, 128, k, s) != 0                           # no up weights
+
+
+# (M, [(type, width)], K): Q4_K / Q6_K mixes of the prefill Q/K/V
+@pytest.mark.parametrize("m,segs,k", [
+    (512, [("q4_k", 4096), ("q4_k", 1024), ("q6_k", 1024)], 4096),    # Qwen3-8B layer with a Q6_K V
+    (320, [("q4_k", 512), ("q4_k", 128), ("q4_k", 128)], 2048),       # all Q4_K, partial 128-row tile
+    (64, [("q6_k", 192), ("q4_k", 64)], 2048),                        # two segments, one 64-row M tile
+])
+def test_f16_segments_mixed_types(rf, dev, m, segs, k):
+    # each segment bit for bit its own fp16-activation launcher on the same
+    # 128 x 64 tiles (Q4_K: the accumulating launcher onto zeros, whose
+    # K-sliced tiles add the same partials in the same order; Q6_K: the plain
+    # launcher), and within the GEMM bar of the oracle
+    a = torch.from_numpy(synth.activations(k, seed=m + 3, m=m)).to(torch.bfloat16).float().numpy()
+    da = G.to_dev(a.astype(np.float16).view(np.int16))
+    ws = [synth.weights(f, n, k, seed=30 + i) for i, (f, n) in enumerate(segs)]
+    dws = [G.to_dev(w) for w in ws]
+    ds = [G.empty(m * n, torch.float32).fill_(float("nan")) for _, n in segs]
+    z = ctypes.c_void_p(0)
+    types = [12 if f == "q4_k" else 14 for f, _ in segs] + [12] * (3 - len(segs))
+    G.call(rf.rf_gemm_qk_f16_segments_launch, G.ptr(da), *([G.ptr(t) for t in dws] + [z] * (3 - len(segs))), *types,
+           *([G.ptr(t) for t in ds] + [z] * (3 - len(segs))), m, *([n for _, n in segs] + [0] * (3 - len(segs))), k)
+    for i, ((f, n), w, dw, d) in enumerate(zip(segs, ws, dws, ds)):
+        got = G.host(d).reshape(m, n)
+        if f == "q4_k":
+            ref = G.empty(m * n, torch.float32).zero_()
+            G.call(rf.rf_gemm_q4_k_f16_accumulate_launch, G.ptr(da), G.ptr(dw), G.ptr(ref), m, n, k)
+        else:
+            ref = G.empty(m * n, torch.float32)
+            G.call(rf.rf_gemm_q6_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(ref), m, n, k)
+        np.testing.assert_array_equal(got, G.host(ref).reshape(m, n))
+        _check(got, O.gemm(f, a, w, m, n, k), f"f16 segment {i} {f} {m}x{n}x{k}")
+
+
+def test_f16_segments_rejections(rf, dev):
+    m, k = 64, 2048
+    da = G.to_dev(np.zeros(m * k, np.int16))
+    w = G.to_dev(synth.weights("q4_k", 64, k, seed=1))
+    d = G.empty(m * 64, torch.float32)
+    s = G.stream()
+    z = ctypes.c_void_p(0)
+    P = G.ptr
+    f = rf.rf_gemm_qk_f16_segments_launch
+    assert f(P(da), P(w), z, z, 12, 12, 12, P(d), z, z, m, 64, 0, 0, k, s) == 0
+    torch.cuda.synchronize()
+    assert f(P(da), P(w), z, z, 13, 12, 12, P(d), z, z, m, 64, 0, 0, k, s) != 0       # not Q4_K / Q6_K
+    assert f(P(da), P(w), z, z, 14, 12, 12, P(d), z, z, m, 64, 0, 0, 1024, s) != 0    # Q6_K needs K % 2048
+    assert f(P(da), P(w), z, z, 12, 12, 12, P(d), z, z, m, 96, 0, 0, k, s) != 0       # width % 64
+    assert f(P(da), P(w), z, P(w), 12, 12, 12, P(d), z, P(d), m, 64, 0, 64, k, s) != 0  # third without second
+    assert f(P(da), P(w), P(w), z, 12, 12, 12, P(d), z, z, m, 64, 64, 0, k, s) != 0     # segment without output
+    assert f(P(da), P(w), z, z, 12, 12, 12, P(d), z, z, 96, 64, 0, 0, k, s) != 0      # M % 64
+    assert f(ctypes.c_void_p(da.data_ptr() + 2), P(w), z, z, 12, 12, 12, P(d), z, z, m, 64, 0, 0, k, s) != 0
