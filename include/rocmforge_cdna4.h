@@ -143,6 +143,14 @@ hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f16, const v
 hipError_t rf_gemm_qk_f16_segments_launch(const uint16_t* input_f16, const void* w0, const void* w1, const void* w2,
                                           int type0, int type1, int type2, float* out0, float* out1, float* out2,
                                           int M, int n0, int n1, int n2, int K, hipStream_t stream);
+/* Gate and up on fp16 activations in one launch, SwiGLU in the epilogue:
+ * out[M x N] = silu(A Wg^T) * (A Wu^T) as fp32, or rounded to fp16 when
+ * out_f16 != 0 -- the values of two rf_gemm_q4_k_f16_launch calls followed
+ * by rf_silu_mul(_f16)_on_stream.  The reference runs two GEMMs and a SwiGLU
+ * kernel (src/gpu/forward.rs:2327).  M % 64, N % 64, K % 256; input and
+ * weights 16-byte aligned. */
+hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void* w_gate, const void* w_up, void* out,
+                                          int out_f16, int M, int N, int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
 

@@ -1456,8 +1456,16 @@ __device__ __forceinline__ void lds_dma16(uint32_t lds_dst, uint32_t voff, const
                  :: "s"(lds_dst), "v"(voff), "s"(sbase) : "memory", "m0");
 }
 
+// PAIR (gate and up in one tile, SwiGLU in the epilogue): the tile's 128
+// weight rows are gate rows [n0, n0 + 64) of W (waves 0-1) and the same up
+// rows of W1 (waves 2-3), n0 = 64 per column tile; after the K halves are
+// added the gate waves hand their sums to the up waves through LDS, which
+// store silu(gate) * up into D[M x N] (N = the gate/up row count) as fp32
+// (PAIR 1) or rounded to fp16 (PAIR 2, D read as halves).
+template <int PAIR>
 __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                          const uint8_t* __restrict__ W,
+                                                                         const uint8_t* __restrict__ W1,
                                                                          float* __restrict__ D, int M, int N, int K) {
     // one LDS block: ring (2 stages), A (3 buffers), scale tables (2); after
     // the loop its first 128 KB carry the K-half exchange
@@ -1476,25 +1484,29 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
     const int mtiles = (M + kF16aBM - 1) / kF16aBM;
     const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int m0 = (v % mtiles) * kF16aBM;      // the M tiles of one column tile are neighbours
-    const int n0 = (v / mtiles) * kF16aBN;
+    const int n0 = (v / mtiles) * (PAIR ? kF16aBN / 2 : kF16aBN);
     const int nchunks = K / kKC;
     const int nsb = K / kQK;
     const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
 
     // ---- weight ring: stage = super-block sb of the tile's 128 rows; group
-    // g of 64 lanes moves 16-byte pieces [64 g, 64 g + 64) (row pc / 9) ------
+    // g of 64 lanes moves 16-byte pieces [64 g, 64 g + 64) (row pc / 9; with
+    // PAIR groups 0-8 hold the 64 gate rows, 9-17 the 64 up rows) -------------
     const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    const uint8_t* w1_tile = PAIR ? W1 + (size_t)n0 * row_bytes : w_tile;
     uint32_t goff[kF16aNI], gdst[kF16aNI];
+    bool gup[kF16aNI];
 #pragma unroll
     for (int t = 0; t < kF16aNI; ++t) {
         const int g = (wave * kF16aNI + t) % kF16aGroups;
         const int pc = 64 * g + lane;
         gdst[t] = 1024u * (uint32_t)g;
-        goff[t] = (uint32_t)(pc / 9) * row_bytes + 16u * (uint32_t)(pc % 9);
+        gup[t] = PAIR && g >= kF16aGroups / 2;
+        goff[t] = (uint32_t)(pc / 9 - (gup[t] ? kF16aBN / 2 : 0)) * row_bytes + 16u * (uint32_t)(pc % 9);
     }
     auto w_dma1 = [&](int t, int sb, int slot) {
         lds_dma16(__builtin_amdgcn_readfirstlane(ring_lds0 + (uint32_t)slot * kF16aStage + gdst[t]), goff[t],
-                  w_tile + (size_t)min(sb, nsb - 1) * kQ4KBytes);
+                  (gup[t] ? w1_tile : w_tile) + (size_t)min(sb, nsb - 1) * kQ4KBytes);
     };
 
     // ---- A: instruction gi = 8 wave + g covers rows 8 gi + L / 8 of the chunk,
@@ -1721,6 +1733,72 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
         give_half(std::integral_constant<int, 0>{});
     __syncthreads();
     const bool full = m0 + kF16aBM <= M;
+    if constexpr (PAIR) {
+        // per wave half (its own code path to the end, so the accumulators
+        // are never merged across branches): the K halves added into acc
+        // (kh 0 + kh 1, the order above), the gate waves' sums to LDS at
+        // [kh][block i][j][q][lane], the up waves store silu(gate) * up
+        auto pair_tail = [&](auto khc) {
+            constexpr int KH = decltype(khc)::value;
+            constexpr int keep = KH ? 4 : 0;
+            const int partner = wave ^ 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 o4 = xch[(((partner * 4 + i) * 2 + j) * 4 + q) * 64 + lane];
+                        const float o[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const float a = acc[keep + i][j][4 * q + u];
+                            acc[keep + i][j][4 * q + u] = KH ? o[u] + a : a + o[u];
+                        }
+                    }
+            __syncthreads();
+            if (wn == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            xch[(((KH * 4 + i) * 2 + j) * 4 + q) * 64 + lane] =
+                                make_float4(acc[keep + i][j][4 * q], acc[keep + i][j][4 * q + 1],
+                                            acc[keep + i][j][4 * q + 2], acc[keep + i][j][4 * q + 3]);
+            }
+            __syncthreads();
+            if (wn == 0) return;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int ncol = n0 + 32 * j + col;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 g4 = xch[(((KH * 4 + i) * 2 + j) * 4 + q) * 64 + lane];
+                        const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int row = m0 + 32 * (keep + i) + 8 * q + 4 * h + u;
+                            if (row >= M) continue;
+                            const float gg = gv[u];
+                            const float r = gg / (1.0f + expf(-gg)) * acc[keep + i][j][4 * q + u];
+                            if constexpr (PAIR == 2)
+                                reinterpret_cast<uint16_t*>(D)[(size_t)row * N + ncol] = f16_bits_rn(r);
+                            else
+                                D[(size_t)row * N + ncol] = r;
+                        }
+                    }
+                }
+        };
+        if (kh)
+            pair_tail(std::integral_constant<int, 1>{});
+        else
+            pair_tail(std::integral_constant<int, 0>{});
+        return;
+    }
     if (kh) {
         if (full)
             keep_half(std::integral_constant<int, 1>{}, std::true_type{});
@@ -2466,7 +2544,8 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
     if (pick == 0) {
-        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, D, M, N, K);
+        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D, M,
+                           N, K);
     } else if (pick == 2) {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(((M + 63) / 64) * (N / kQ4sBN)), dim3(kQ4sThreads),
                            0, st, A, w, D, M, N, K);
@@ -2489,6 +2568,31 @@ extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const v
     if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
         return hipErrorInvalidValue;
     return gemm_q4_f16<false>(input_f16, weights_q4_k, output, M, N, K, stream);
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Gate and up on fp16 activations in one launch, SwiGLU in the epilogue
+// (rf_gemm_q4k_f16a_kernel<1 or 2>: 256 x 128 tiles of 64 gate and the same
+// 64 up rows): out[M x N] = silu(A Wg^T) * (A Wu^T), fp32 or rounded to fp16
+// (out_f16), the values of rf_gemm_q4_k_f16_launch twice and
+// rf_silu_mul(_f16)_on_stream.  M % 64, N % 64, K % 256; input and weights
+// 16-byte aligned.
+extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void* w_gate, const void* w_up,
+                                                     void* out, int out_f16, int M, int N, int K, hipStream_t stream) {
+    if (input_f16 == nullptr || w_gate == nullptr || w_up == nullptr || out == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(input_f16) || !aligned16(w_gate) || !aligned16(w_up)) return hipErrorInvalidValue;
+    const unsigned tiles = (unsigned)(((M + kF16aBM - 1) / kF16aBM) * (N / 64));
+    const uint8_t* wg = static_cast<const uint8_t*>(w_gate);
+    const uint8_t* wu = static_cast<const uint8_t*>(w_up);
+    if (out_f16)
+        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<2>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
+                           static_cast<float*>(out), M, N, K);
+    else
+        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<1>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
+                           static_cast<float*>(out), M, N, K);
+    return hipGetLastError();
 }
 
 // Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,
@@ -2548,8 +2652,6 @@ static bool seg_shape_ok(const float* A, int M, int K) {
     if (M <= 0 || K <= 0 || M % 64 || K % (IS_Q6 ? 2048 : 512)) return false;
     return (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
 }
-
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <bool IS_Q6>
 static hipError_t gemm_segments(const float* A, const void* w0, const void* w1, const void* w2, float* d0,

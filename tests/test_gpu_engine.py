@@ -207,10 +207,10 @@ def test_fused_norm_decode_equals_separate(weights, eng):
         assert np.array_equal(_h(a), _h(b))
 
 
-def _check_prefill_stages(eng, lay):
+def _check_prefill_stages(eng, lay, n_prompt=100):
     # every stage of layer `lay`, the embedding and the LM head against the oracle
     c, w = eng.cfg, eng.w
-    prompt = [int(t) for t in np.random.default_rng(1).integers(0, c.vocab, 100)]
+    prompt = [int(t) for t in np.random.default_rng(1).integers(0, c.vocab, n_prompt)]
     M = len(prompt)
     seen = {}
 
@@ -309,6 +309,14 @@ def test_prefill_stages(eng):
     assert seen["ffn16"] and seen["act16"] and seen["att16"]
     # (hidden 512 keeps a Q6_K V off the fp16 segments: its tiles need K % 2048)
     assert seen["qkv16"] == (eng.w.layers[0].mats["attn_v"][1].wtype == GgmlType.Q4_K)
+
+
+def test_prefill_stages_paired_f16_gate_up(eng):
+    # a 200-token prompt (256 padded rows): gate and up as one paired fp16 launch
+    # with SwiGLU in its epilogue
+    assert eng._pair16(256) and not eng._pair16(128)
+    seen = _check_prefill_stages(eng, 0, n_prompt=200)
+    assert seen["ffn16"] and seen["act16"]
 
 
 def test_prefill_stages_fp32_ffn(weights):

@@ -242,3 +242,55 @@ def test_f16_segments_rejections(rf, dev):
     assert f(P(da), P(w), P(w), z, 12, 12, 12, P(d), z, z, m, 64, 64, 0, k, s) != 0     # segment without output
     assert f(P(da), P(w), z, z, 12, 12, 12, P(d), z, z, 96, 64, 0, 0, k, s) != 0      # M % 64
     assert f(ctypes.c_void_p(da.data_ptr() + 2), P(w), z, z, 12, 12, 12, P(d), z, z, m, 64, 0, 0, k, s) != 0
+
+
+@pytest.mark.parametrize("m,n,k,f16", [(512, 12288, 4096, True), (512, 12288, 4096, False), (320, 192, 1024, True),
+                                       (64, 64, 256, False)])
+def test_q4k_f16_swiglu(rf, dev, m, n, k, f16):
+    # gate and up in one launch with SwiGLU in the epilogue: at 512 x 12288
+    # (the 256 x 128 tiles the plain launcher takes there too) bit for bit two
+    # fp16-activation GEMMs and the SwiGLU kernel; every shape within the bar
+    # of the oracle's silu(gate) * up (plus the fp16 rounding of the output)
+    a = torch.from_numpy(synth.activations(k, seed=m + 9, m=m)).to(torch.bfloat16).float().numpy()
+    da = G.to_dev(a.astype(np.float16).view(np.int16))
+    wg, wu = synth.weights("q4_k", n, k, seed=41), synth.weights("q4_k", n, k, seed=42)
+    dwg, dwu = G.to_dev(wg), G.to_dev(wu)
+    out = G.empty(m * n, torch.int16 if f16 else torch.float32)
+    G.call(rf.rf_gemm_q4_k_f16_swiglu_launch, G.ptr(da), G.ptr(dwg), G.ptr(dwu), G.ptr(out), int(f16), m, n, k)
+    got = G.host(out).view(np.float16).astype(np.float32) if f16 else G.host(out)
+    got = got.reshape(m, n)
+    if m == 512:
+        g, u = G.empty(m * n, torch.float32), G.empty(m * n, torch.float32)
+        G.call(rf.rf_gemm_q4_k_f16_launch, G.ptr(da), G.ptr(dwg), G.ptr(g), m, n, k)
+        G.call(rf.rf_gemm_q4_k_f16_launch, G.ptr(da), G.ptr(dwu), G.ptr(u), m, n, k)
+        ref = G.empty(m * n, torch.int16 if f16 else torch.float32)
+        if f16:
+            G.call(rf.rf_silu_mul_f16_on_stream, G.ptr(g), G.ptr(u), G.ptr(ref), m * n)
+            np.testing.assert_array_equal(G.host(out), G.host(ref))
+        else:
+            G.call(rf.rf_silu_mul_on_stream, G.ptr(g), G.ptr(u), G.ptr(ref), m * n)
+            np.testing.assert_array_equal(G.host(out), G.host(ref))
+    gr, ur = O.gemm("q4_k", a, wg, m, n, k), O.gemm("q4_k", a, wu, m, n, k)
+    ref = gr / (1.0 + np.exp(-gr)) * ur
+    scale = np.abs(ref).max()
+    err = np.abs(got.astype(np.float64) - ref)
+    tol = (4e-3 if f16 else 2e-3) * np.abs(ref) + 1e-4 * scale
+    print(f"q4_k f16 swiglu {m}x{n}x{k}: worst={(err / tol).max():.3f}", flush=True)
+    assert (err / tol).max() <= 1.0
+
+
+def test_q4k_f16_swiglu_rejections(rf, dev):
+    m, k = 64, 256
+    da = G.to_dev(np.zeros(m * k, np.int16))
+    w = G.to_dev(synth.weights("q4_k", 64, k, seed=1))
+    d = G.empty(m * 64, torch.float32)
+    s = G.stream()
+    z = ctypes.c_void_p(0)
+    P = G.ptr
+    f = rf.rf_gemm_q4_k_f16_swiglu_launch
+    assert f(P(da), P(w), P(w), P(d), 0, m, 64, k, s) == 0
+    torch.cuda.synchronize()
+    assert f(P(da), P(w), z, P(d), 0, m, 64, k, s) != 0          # no up weights
+    assert f(P(da), P(w), P(w), P(d), 0, m, 96, k, s) != 0       # N % 64
+    assert f(P(da), P(w), P(w), P(d), 0, 32, 64, k, s) != 0      # M % 64
+    assert f(P(da), P(w), P(w), P(d), 0, m, 64, 320, s) != 0     # K % 256
