@@ -290,11 +290,14 @@ __device__ __forceinline__ void theta8(const float* __restrict__ tab, float base
     }
 }
 
+// norm: the head is normalised with the weights gv (the lane's 8, loaded by
+// the caller together with its other operands: a load here would wait for
+// every load issued before it)
 template <int LPP>
-__device__ __forceinline__ void head_norm_rope(float v[8], int sub, const float* __restrict__ g, float eps, int pos,
+__device__ __forceinline__ void head_norm_rope(float v[8], int sub, bool norm, const float gv[8], float eps, int pos,
                                                const float t[8], int neox) {
     constexpr int D = 8 * LPP;
-    if (g != nullptr) {
+    if (norm) {
         float ss = v[0] * v[0];
 #pragma unroll
         for (int i = 1; i < 8; ++i) ss = __fmaf_rn(v[i], v[i], ss);
@@ -302,7 +305,7 @@ __device__ __forceinline__ void head_norm_rope(float v[8], int sub, const float*
         for (int o = 1; o < LPP; o <<= 1) ss += __shfl_xor(ss, o);
         const float inv = rsqrtf(ss / (float)D + eps);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * g[8 * sub + i];
+        for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * gv[i];
     }
     if (neox) {
         const bool lo = sub < LPP / 2;
@@ -348,11 +351,16 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     if (hidx >= nh + nkv) return;            // whole LPP-lane groups leave together
     const bool is_q = hidx < nh;
     const int head = is_q ? hidx : hidx - nh;
+    // every load first (one memory round trip): the head, its norm weights,
+    // the V head to copy, the position and the angles
     const int pos = *pos_ptr;
-    float x[8], th[8];
+    const float* g = is_q ? q_norm : k_norm;
+    float x[8], th[8], gv[8], vv[8];
     load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
+    if (g != nullptr) load8(g + 8 * sub, gv);
+    if (!is_q) load8(v + (size_t)head * D + 8 * sub, vv);
     theta8<LPP>(tab, base, sub, neox, freq_scale, th);
-    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
+    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, pos, th, neox);
     if (is_q) {
         float* dst = q + (size_t)head * D + 8 * sub;
         *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
@@ -360,8 +368,6 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     } else {
         const size_t c = (size_t)pos * nkv * D + (size_t)head * D + 8 * sub;
         store8_f16(kc + c, x);
-        float vv[8];
-        load8(v + (size_t)head * D + 8 * sub, vv);
         store8_f16(vc + c, vv);
     }
 }
@@ -387,17 +393,18 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_rows_kernel(
     const int head = is_q ? hidx : hidx - nh;
     const int pos = pos0 + row;
     const size_t src = (size_t)row * (is_q ? nh : nkv) * D + (size_t)head * D + 8 * sub;
-    float x[8], th[8];
+    const float* g = is_q ? q_norm : k_norm;
+    float x[8], th[8], gv[8], vv[8];
     load8((is_q ? q : k) + src, x);
+    if (g != nullptr) load8(g + 8 * sub, gv);
+    if (!is_q) load8(v + src, vv);
     theta8<LPP>(tab, base, sub, neox, freq_scale, th);
-    head_norm_rope<LPP>(x, sub, is_q ? q_norm : k_norm, eps, pos, th, neox);
+    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, pos, th, neox);
     if (is_q) {
         store8_f16(q16 + src, x);
     } else {
         const size_t c = (size_t)pos * nkv * D + (size_t)head * D + 8 * sub;
         store8_f16(kc + c, x);
-        float vv[8];
-        load8(v + src, vv);
         store8_f16(vc + c, vv);
     }
 }
@@ -579,12 +586,16 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     const int pos = seq - 1;
     const bool owner = QK && split == (pos / kSplitChunk) % S;   // workgroup-uniform
     // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
-    float qv[8], kx[8], vx[8], th[8];
+    float qv[8], kx[8], vx[8], th[8], gq[8], gk[8];
     load8(q + (size_t)head * D + 8 * sub, qv);
-    if constexpr (QK) theta8<LPP>(qk.tab, qk.base, sub, qk.neox, qk.freq_scale, th);
+    if constexpr (QK) {
+        if (qk.q_norm != nullptr) load8(qk.q_norm + 8 * sub, gq);
+        theta8<LPP>(qk.tab, qk.base, sub, qk.neox, qk.freq_scale, th);
+    }
     if (owner && wave == 0) {
         load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
         load8(qk.v + (size_t)kvh * D + 8 * sub, vx);
+        if (qk.k_norm != nullptr) load8(qk.k_norm + 8 * sub, gk);
     }
     float m = kNegMax, l = 0.0f, acc[8];
 #pragma unroll
@@ -600,10 +611,10 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
         }
         if constexpr (QK) {
             if (c0 == split * kSplitChunk) {     // first chunk: the per-head step, while the loads fly
-                head_norm_rope<LPP>(qv, sub, qk.q_norm, qk.eps, pos, th, qk.neox);
+                head_norm_rope<LPP>(qv, sub, qk.q_norm != nullptr, gq, qk.eps, pos, th, qk.neox);
                 if (owner) {
                     if (wave == 0) {
-                        head_norm_rope<LPP>(kx, sub, qk.k_norm, qk.eps, pos, th, qk.neox);
+                        head_norm_rope<LPP>(kx, sub, qk.k_norm != nullptr, gk, qk.eps, pos, th, qk.neox);
                         if (grp == 0) {
                             const size_t c = (size_t)pos * row + (size_t)kvh * D + 8 * sub;
                             store8_f16(qk.kc + c, kx);
