@@ -207,6 +207,32 @@ def test_fused_norm_decode_equals_separate(weights, eng):
         assert np.array_equal(_h(a), _h(b))
 
 
+def test_mixed_qkv_decode_graph_equals_unfused(dev):
+    # hidden 2048: the Q6_K attn_v layer of the Q4_K_M mix takes the one-launch
+    # Q4_K Q/K + Q6_K V GEMV; captured decode replays equal eager steps and
+    # the unfused engine (norm, three GEMVs) bit for bit
+    cfg = E.ModelConfig(n_layers=3, hidden=2048, ff=2048, n_heads=16, n_kv_heads=4, head_dim=128, vocab=2048)
+    w = E.synthetic_weights(cfg, seed=21, signed=True)
+    assert [lw.mats["attn_v"][1].wtype for lw in w.layers].count(GgmlType.Q6_K) >= 1
+    fused = E.Engine(cfg, w, max_seq=128)
+    plain = E.Engine(cfg, w, max_seq=128, fuse_norm=False)
+    fused.prefill(list(range(3, 40)))
+    snap = _snapshot(fused)
+    toks = fused.decode(5, graph=True)
+    logits = _h(fused.logits).copy()
+    caches = [_h(t).copy() for t in fused.kc + fused.vc]
+    _restore(fused, snap)
+    assert fused.decode(5, graph=False) == toks
+    assert np.array_equal(_h(fused.logits), logits)
+    _restore(plain, snap)
+    assert plain.decode(5, graph=False) == toks
+    assert np.array_equal(_h(plain.logits), logits)
+    for a, b in zip(caches, plain.kc + plain.vc):
+        assert np.array_equal(a, _h(b))
+    del fused, plain
+    torch.cuda.empty_cache()
+
+
 def _check_prefill_stages(eng, lay, n_prompt=100):
     # every stage of layer `lay`, the embedding and the LM head against the oracle
     c, w = eng.cfg, eng.w
