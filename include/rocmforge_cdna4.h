@@ -378,20 +378,23 @@ hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_k, const fl
                                           const float* d_k_norm, uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_pos,
                                           const int num_heads, const int num_kv_heads, const int head_dim,
                                           const float eps, const float theta_base, const int neox,
-                                          const float* d_freq_scale, const float* d_theta, hipStream_t stream);
+                                          const float* d_freq_scale, const float* d_theta, const float* d_cos_sin,
+                                          hipStream_t stream);
 /* No counterpart (the reference's prefill takes gpu_rms_norm_batched twice,
  * gpu_rope_heads_batched twice, gpu_kv_write_batched and the fp16
  * conversions, src/gpu/forward.rs prefill path): the same step over the rows
  * of a prompt, row r at position start_pos + r.  Query rows [0, rows_q) are
  * written as fp16 to d_q16 ([row][num_heads * head_dim]); key/value rows
  * [0, rows_kv) go to the caches at start_pos + r (start_pos + rows_kv <=
- * max_seq).  d_q, d_k, d_v and d_q16 16-byte aligned; rows_q <= 65535. */
+ * max_seq).  d_q, d_k, d_v and d_q16 16-byte aligned; rows_q <= 65535.
+ * With d_cos_sin (below) start_pos + rows_q <= max_seq as well. */
 hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const float* d_k, const float* d_v, const float* d_q_norm,
                                          const float* d_k_norm, uint16_t* d_q16, uint16_t* d_k_cache,
                                          uint16_t* d_v_cache, const int start_pos, const int rows_q, const int rows_kv,
                                          const int num_heads, const int num_kv_heads, const int head_dim,
                                          const int max_seq, const float eps, const float theta_base, const int neox,
-                                         const float* d_freq_scale, const float* d_theta, hipStream_t stream);
+                                         const float* d_freq_scale, const float* d_theta, const float* d_cos_sin,
+                                         hipStream_t stream);
 
 /* hip_kernels/attention.hip:950, :972 -- one query token over seq_len cached
  * positions (fp16 bits): out[h] = softmax(q[h] . K[0..seq_len) * scale) V, GQA head h / (nh / nkv).
@@ -446,6 +449,17 @@ hipError_t rf_flash_attn_decode_state_noalloc(float* d_out, const float* d_q, co
  * they then evaluate theta in the kernel, same bits). */
 hipError_t rf_rope_theta_table(float* d_theta, const int head_dim, const float theta_base, hipStream_t stream);
 
+/* No counterpart (the reference evaluates cosf / sinf in each RoPE launch):
+ * fills the caller's d_cos_sin[positions][head_dim / 2][2] with the cosine
+ * and sine of pos * theta_i, theta_i as the fused launchers take it (from
+ * d_theta when given, else evaluated; divided by d_freq_scale[i] when given).
+ * The fused launchers' d_cos_sin argument (16-byte aligned, or null) takes
+ * such a table, built with their theta_base / d_theta / d_freq_scale and
+ * covering every position they are called at, in place of evaluating cosf /
+ * sinf: the same values, so the same bits. */
+hipError_t rf_rope_cos_sin_table(float* d_cos_sin, const int positions, const int head_dim, const float theta_base,
+                                 const float* d_theta, const float* d_freq_scale, hipStream_t stream);
+
 /* No counterpart (the reference launches the per-head norms, the q RoPE and
  * the KV write before gpu_flash_attn_decode_strided_multi_head_state,
  * src/gpu/forward.rs:2384-2440): the same step folded into the decode
@@ -458,7 +472,8 @@ hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, con
                                              uint16_t* d_v_cache, const int* d_state, const int num_heads,
                                              const int num_kv_heads, const int head_dim, const float eps,
                                              const float theta_base, const int neox, const float* d_freq_scale,
-                                             const float* d_theta, const float scale, float* d_workspace,
+                                             const float* d_theta, const float* d_cos_sin, const float scale,
+                                             float* d_workspace,
                                              const size_t workspace_bytes, hipStream_t stream);
 
 /* hip_kernels/elementwise.hip:615, :651 -- index of the maximum of d_input[n]

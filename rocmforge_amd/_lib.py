@@ -67,9 +67,10 @@ SIGNATURES = {
     "gpu_kv_write_rope_state_scaled": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp],
     "gpu_kv_write_batched": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
     "rf_kv_write_batched_on_stream": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
-    "rf_qk_norm_rope_kv_write_rows": [_vp] * 8 + [_i] * 7 + [_f, _f, _i, _vp, _vp, _vp],
-    "rf_qk_norm_rope_kv_write_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp, _vp, _vp],
+    "rf_qk_norm_rope_kv_write_rows": [_vp] * 8 + [_i] * 7 + [_f, _f, _i, _vp, _vp, _vp, _vp],
+    "rf_qk_norm_rope_kv_write_state": [_vp] * 8 + [_i, _i, _i, _f, _f, _i, _vp, _vp, _vp, _vp],
     "rf_rope_theta_table": [_vp, _i, _f, _vp],
+    "rf_rope_cos_sin_table": [_vp, _i, _i, _f, _vp, _vp, _vp],
     "gpu_flash_attn_decode_strided_multi_head": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "rf_flash_attn_decode_ws": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp],
@@ -79,7 +80,7 @@ SIGNATURES = {
     "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
     "rf_argmax_f32_advance_state_on_stream": [_vp, _vp, _vp, _vp, _i, _vp, _vp],
     "rf_attn_decode_qk_norm_rope_state": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _vp,
-                                          _vp, _f, _vp, _sz, _vp],
+                                          _vp, _vp, _f, _vp, _sz, _vp],
     "gpu_embed_q4_k_token": [_vp, _vp, _i, _i, _i, _vp],
     "gpu_embed_q4_k_batch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "gpu_add": [_vp, _vp, _vp, _i, _vp],

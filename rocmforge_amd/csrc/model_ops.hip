@@ -75,14 +75,34 @@ __global__ void rf_theta_fill_kernel(float* tab, int d, float base) {
     if (i < d / 2) tab[i] = theta_exact(i, d, base);
 }
 
+// (x0, x1) rotated by the angle with cosine c and sine s.  The roundings
+// are spelled out (one product rounded, the other fused) so that every
+// kernel here rotates to the same bits, whatever contraction the compiler
+// would pick where c and s come from
+__device__ __forceinline__ void rope_cs(float& x0, float& x1, float c, float s) {
+    const float y0 = __fmaf_rn(x0, c, -__fmul_rn(x1, s));
+    const float y1 = __fmaf_rn(x0, s, __fmul_rn(x1, c));
+    x0 = y0;
+    x1 = y1;
+}
+
 // (x0, x1) rotated by angle pos * theta
 __device__ __forceinline__ void rope_pair(float& x0, float& x1, int pos, float theta) {
     const float a = (float)pos * theta;
-    const float c = cosf(a), s = sinf(a);
-    const float y0 = x0 * c - x1 * s;
-    const float y1 = x0 * s + x1 * c;
-    x0 = y0;
-    x1 = y1;
+    rope_cs(x0, x1, cosf(a), sinf(a));
+}
+
+// cs[pos][i] = (cos, sin) of pos * theta_i, theta_i as rope_theta (from the
+// table when given, divided by freq_scale[i] when given): the values rope_pair evaluates, so a kernel
+// that reads them rotates to the same bits without cosf / sinf
+__global__ void rf_rope_cos_sin_kernel(float2* __restrict__ cs, int positions, int d, float base,
+                                       const float* __restrict__ tab, const float* __restrict__ freq_scale) {
+    const int half = d / 2;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)positions * half) return;
+    const int pos = (int)(idx / half), i = (int)(idx % half);
+    const float a = (float)pos * rope_theta(i, d, base, nullptr, freq_scale);
+    cs[idx] = make_float2(cosf(a), sinf(a));
 }
 
 // element indices of pair p of a head: NeoX pairs (p, p + d/2), classic (2p, 2p + 1)
@@ -252,50 +272,62 @@ __global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* 
 // LPP lanes by an xor butterfly; NeoX pairs (i, i + D/2) sit in lanes sub
 // and sub + LPP/2 (one xor shuffle), classic pairs (2i, 2i+1) in one lane.
 // Both the standalone step and the attention with the step folded in use
-// this function, so they produce the same bits.
-// theta of the 8 pairs a lane rotates, loaded in one go (with the lane's x)
+// head_norm_rope below, so they produce the same bits.
+// RoPE angles: a head's D / 2 pairs all turn by pos * theta_i, the same for
+// every head of a position, so each wave takes the cos / sin of the D / 2
+// angles once into its own LDS slice (lane l: pairs l, l + 64) and every
+// lane reads its pairs from there.  The values are cosf / sinf of the angle
+// rope_pair takes (theta_i from the caller's table when given, divided by
+// freq_scale[i] when given), or the same values from a rf_rope_cos_sin_kernel
+// table row: the rotations match the per-element RoPE launchers bit for bit.
 template <int LPP>
-// (from the caller's table when given, else evaluated here)
-__device__ __forceinline__ void theta8(const float* __restrict__ tab, float base, int sub, int neox,
-                                       const float* __restrict__ freq_scale, float t[8]) {
-    constexpr int D = 8 * LPP;
-    int p0;
-    if (neox) {
-        p0 = sub < LPP / 2 ? 8 * sub : 8 * sub - D / 2;
-        if (tab != nullptr) {
-            const float4 a = *reinterpret_cast<const float4*>(tab + p0);
-            const float4 b = *reinterpret_cast<const float4*>(tab + p0 + 4);
-            t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w; t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
-        } else {
+__device__ __forceinline__ void wave_cos_sin(float2* w, const float2* __restrict__ cs_row,
+                                             const float* __restrict__ tab, float base,
+                                             const float* __restrict__ freq_scale, int pos, int lane) {
+    constexpr int H = 4 * LPP;   // D / 2
 #pragma unroll
-            for (int i = 0; i < 8; ++i) t[i] = theta_exact(p0 + i, D, base);
-        }
-    } else {
-        p0 = 4 * sub;                          // pairs (2i, 2i+1): four per lane, t[i] for i even
-        if (tab != nullptr) {
-            const float4 a = *reinterpret_cast<const float4*>(tab + p0);
-            t[0] = a.x; t[2] = a.y; t[4] = a.z; t[6] = a.w;
+    for (int i = lane; i < H; i += 64) {
+        float2 c;
+        if (cs_row != nullptr) {
+            c = cs_row[i];
         } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) t[2 * i] = theta_exact(p0 + i, D, base);
+            const float a = (float)pos * rope_theta(i, 8 * LPP, base, tab, freq_scale);
+            c = make_float2(cosf(a), sinf(a));
         }
-        t[1] = t[3] = t[5] = t[7] = 0.0f;
+        w[i] = c;
     }
-    if (freq_scale != nullptr) {
+    // the slice is the wave's own: a wave-scope fence orders the writes
+    // before the other lanes' reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The lane's (cos, sin) pairs from a wave_cos_sin slice: NeoX pairs (i,
+// i + D/2) for i in [p0, p0 + 8), p0 = 8 sub mod D/2 (lanes sub and
+// sub + LPP/2 hold the two halves); classic pairs (2i, 2i+1) for i in
+// [4 sub, 4 sub + 4)
+template <int LPP>
+__device__ __forceinline__ void cs8(const float2* w, int sub, int neox, float2 c[8]) {
+    constexpr int D = 8 * LPP;
+    const int p0 = neox ? (sub < LPP / 2 ? 8 * sub : 8 * sub - D / 2) : 4 * sub;
+    const float4* r = reinterpret_cast<const float4*>(w + p0);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int p = neox ? p0 + i : p0 + i / 2;
-            if (neox || (i & 1) == 0) t[i] /= freq_scale[p];
+    for (int k = 0; k < 4; ++k) {
+        if (neox || k < 2) {
+            const float4 a = r[k];
+            c[2 * k] = make_float2(a.x, a.y);
+            c[2 * k + 1] = make_float2(a.z, a.w);
         }
     }
 }
 
 // norm: the head is normalised with the weights gv (the lane's 8, loaded by
 // the caller together with its other operands: a load here would wait for
-// every load issued before it)
+// every load issued before it); then rotated by the lane's cos / sin pairs c
 template <int LPP>
-__device__ __forceinline__ void head_norm_rope(float v[8], int sub, bool norm, const float gv[8], float eps, int pos,
-                                               const float t[8], int neox) {
+__device__ __forceinline__ void head_norm_rope(float v[8], int sub, bool norm, const float gv[8], float eps,
+                                               const float2 c[8], int neox) {
     constexpr int D = 8 * LPP;
     if (norm) {
         float ss = v[0] * v[0];
@@ -313,12 +345,12 @@ __device__ __forceinline__ void head_norm_rope(float v[8], int sub, bool norm, c
         for (int i = 0; i < 8; ++i) {
             const float other = __shfl_xor(v[i], LPP / 2);
             float x0 = lo ? v[i] : other, x1 = lo ? other : v[i];
-            rope_pair(x0, x1, pos, t[i]);
+            rope_cs(x0, x1, c[i].x, c[i].y);
             v[i] = lo ? x0 : x1;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) rope_pair(v[i], v[i + 1], pos, t[i]);
+        for (int i = 0; i < 8; i += 2) rope_cs(v[i], v[i + 1], c[i / 2].x, c[i / 2].y);
     }
 }
 
@@ -343,24 +375,32 @@ template <int LPP>
 __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_kernel(
     float* q, const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, __half* kc, __half* vc, const int* __restrict__ pos_ptr, int nh, int nkv,
-    float eps, const float* __restrict__ tab, float base, int neox, const float* __restrict__ freq_scale) {
+    float eps, const float* __restrict__ tab, float base, int neox, const float* __restrict__ freq_scale,
+    const float2* __restrict__ cs) {
     constexpr int D = 8 * LPP;
-    const int lane = threadIdx.x & 63;
-    const int hidx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPP) + lane / LPP;
+    __shared__ __align__(16) float2 lcs[4][D / 2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hidx = (blockIdx.x * 4 + wave) * (64 / LPP) + lane / LPP;
     const int sub = lane % LPP;
-    if (hidx >= nh + nkv) return;            // whole LPP-lane groups leave together
+    const bool live = hidx < nh + nkv;
     const bool is_q = hidx < nh;
     const int head = is_q ? hidx : hidx - nh;
     // every load first (one memory round trip): the head, its norm weights,
-    // the V head to copy, the position and the angles
+    // the V head to copy and the position; the wave's cos / sin meanwhile
     const int pos = *pos_ptr;
     const float* g = is_q ? q_norm : k_norm;
-    float x[8], th[8], gv[8], vv[8];
-    load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
-    if (g != nullptr) load8(g + 8 * sub, gv);
-    if (!is_q) load8(v + (size_t)head * D + 8 * sub, vv);
-    theta8<LPP>(tab, base, sub, neox, freq_scale, th);
-    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, pos, th, neox);
+    float x[8], gv[8], vv[8];
+    float2 cv[8];
+    if (live) {
+        load8((is_q ? q : k) + (size_t)head * D + 8 * sub, x);
+        if (g != nullptr) load8(g + 8 * sub, gv);
+        if (!is_q) load8(v + (size_t)head * D + 8 * sub, vv);
+    }
+    wave_cos_sin<LPP>(lcs[wave], cs != nullptr ? cs + (size_t)pos * (D / 2) : nullptr, tab, base, freq_scale, pos,
+                      lane);
+    if (!live) return;                       // whole LPP-lane groups leave together
+    cs8<LPP>(lcs[wave], sub, neox, cv);
+    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, cv, neox);
     if (is_q) {
         float* dst = q + (size_t)head * D + 8 * sub;
         *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
@@ -381,25 +421,31 @@ __global__ __launch_bounds__(256) void rf_qk_norm_rope_kv_rows_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm, __half* __restrict__ q16, __half* kc,
     __half* vc, int pos0, int rows_kv, int nh, int nkv, float eps, const float* __restrict__ tab, float base, int neox,
-    const float* __restrict__ freq_scale) {
+    const float* __restrict__ freq_scale, const float2* __restrict__ cs) {
     constexpr int D = 8 * LPP;
-    const int lane = threadIdx.x & 63;
-    const int hidx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPP) + lane / LPP;
+    __shared__ __align__(16) float2 lcs[4][D / 2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hidx = (blockIdx.x * 4 + wave) * (64 / LPP) + lane / LPP;
     const int sub = lane % LPP;
     const int row = blockIdx.y;
-    if (hidx >= nh + nkv) return;            // whole LPP-lane groups leave together
     const bool is_q = hidx < nh;
-    if (!is_q && row >= rows_kv) return;
+    const bool live = hidx < nh + nkv && (is_q || row < rows_kv);
     const int head = is_q ? hidx : hidx - nh;
     const int pos = pos0 + row;
     const size_t src = (size_t)row * (is_q ? nh : nkv) * D + (size_t)head * D + 8 * sub;
     const float* g = is_q ? q_norm : k_norm;
-    float x[8], th[8], gv[8], vv[8];
-    load8((is_q ? q : k) + src, x);
-    if (g != nullptr) load8(g + 8 * sub, gv);
-    if (!is_q) load8(v + src, vv);
-    theta8<LPP>(tab, base, sub, neox, freq_scale, th);
-    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, pos, th, neox);
+    float x[8], gv[8], vv[8];
+    float2 cv[8];
+    if (live) {
+        load8((is_q ? q : k) + src, x);
+        if (g != nullptr) load8(g + 8 * sub, gv);
+        if (!is_q) load8(v + src, vv);
+    }
+    wave_cos_sin<LPP>(lcs[wave], cs != nullptr ? cs + (size_t)pos * (D / 2) : nullptr, tab, base, freq_scale, pos,
+                      lane);
+    if (!live) return;                       // whole LPP-lane groups leave together
+    cs8<LPP>(lcs[wave], sub, neox, cv);
+    head_norm_rope<LPP>(x, sub, g != nullptr, gv, eps, cv, neox);
     if (is_q) {
         store8_f16(q16 + src, x);
     } else {
@@ -554,6 +600,7 @@ struct QkStep {
     float base;
     int neox;
     const float* freq_scale;
+    const float2* cs;      // cos / sin table (rf_rope_cos_sin_kernel), or null
 };
 
 template <int LPP, bool QK>
@@ -567,6 +614,7 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     constexpr int PPW = 64 / LPP;
     constexpr int NI = kSplitChunk / PPW;       // load instructions per chunk (K and V each)
     __shared__ u32x4 new_kv[2][LPP];            // QK: the new position's fp16 K and V row of this kv head
+    __shared__ __align__(16) float2 lcs[QK ? 8 : 1][QK ? D / 2 : 2];   // QK: each wave's cos / sin
     const int seq = len_ptr ? *len_ptr : len0;
     const int kvh = blockIdx.x, split = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -586,11 +634,14 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     const int pos = seq - 1;
     const bool owner = QK && split == (pos / kSplitChunk) % S;   // workgroup-uniform
     // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
-    float qv[8], kx[8], vx[8], th[8], gq[8], gk[8];
+    float qv[8], kx[8], vx[8], gq[8], gk[8];
+    float2 cv[8];
     load8(q + (size_t)head * D + 8 * sub, qv);
     if constexpr (QK) {
         if (qk.q_norm != nullptr) load8(qk.q_norm + 8 * sub, gq);
-        theta8<LPP>(qk.tab, qk.base, sub, qk.neox, qk.freq_scale, th);
+        wave_cos_sin<LPP>(lcs[wave], qk.cs != nullptr ? qk.cs + (size_t)pos * (D / 2) : nullptr, qk.tab, qk.base,
+                          qk.freq_scale, pos, lane);
+        cs8<LPP>(lcs[wave], sub, qk.neox, cv);
     }
     if (owner && wave == 0) {
         load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
@@ -611,10 +662,10 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
         }
         if constexpr (QK) {
             if (c0 == split * kSplitChunk) {     // first chunk: the per-head step, while the loads fly
-                head_norm_rope<LPP>(qv, sub, qk.q_norm != nullptr, gq, qk.eps, pos, th, qk.neox);
+                head_norm_rope<LPP>(qv, sub, qk.q_norm != nullptr, gq, qk.eps, cv, qk.neox);
                 if (owner) {
                     if (wave == 0) {
-                        head_norm_rope<LPP>(kx, sub, qk.k_norm != nullptr, gk, qk.eps, pos, th, qk.neox);
+                        head_norm_rope<LPP>(kx, sub, qk.k_norm != nullptr, gk, qk.eps, cv, qk.neox);
                         if (grp == 0) {
                             const size_t c = (size_t)pos * row + (size_t)kvh * D + 8 * sub;
                             store8_f16(qk.kc + c, kx);
@@ -1064,10 +1115,11 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_
                                                      const int num_kv_heads, const int head_dim, const float eps,
                                                      const float theta_base, const int neox,
                                                      const float* d_freq_scale, const float* d_theta,
-                                                     hipStream_t stream) {
+                                                     const float* d_cos_sin, hipStream_t stream) {
     if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_k_cache == nullptr || d_v_cache == nullptr ||
         d_pos == nullptr || num_heads <= 0 || num_kv_heads <= 0)
         return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(d_cos_sin) & 15u) return hipErrorInvalidValue;
     // 8-element vector loads of q/k/v and 16-byte fp16 stores into the caches
     for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_k_cache,
                           (const void*)d_v_cache})
@@ -1078,7 +1130,8 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_state(float* d_q, const float* d_
 #define RF_QKR(LPP)                                                                                                    \
     hipLaunchKernelGGL(rf_qk_norm_rope_kv_kernel<LPP>, dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP))),      \
                        dim3(256), 0, stream, d_q, d_k, d_v, d_q_norm, d_k_norm, kc, vc, d_pos, num_heads,         \
-                       num_kv_heads, eps, d_theta, theta_base, neox, d_freq_scale)
+                       num_kv_heads, eps, d_theta, theta_base, neox, d_freq_scale,                              \
+                       reinterpret_cast<const float2*>(d_cos_sin))
     switch (head_dim) {
     case 64: RF_QKR(8); break;
     case 128: RF_QKR(16); break;
@@ -1096,10 +1149,13 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const floa
                                                     const int num_kv_heads, const int head_dim, const int max_seq,
                                                     const float eps, const float theta_base, const int neox,
                                                     const float* d_freq_scale, const float* d_theta,
-                                                    hipStream_t stream) {
+                                                    const float* d_cos_sin, hipStream_t stream) {
     if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_q16 == nullptr || d_k_cache == nullptr ||
         d_v_cache == nullptr || num_heads <= 0 || num_kv_heads <= 0 || start_pos < 0 || rows_q <= 0 ||
         rows_kv < 0 || rows_kv > rows_q || rows_q > 65535 || start_pos + rows_kv > max_seq)
+        return hipErrorInvalidValue;
+    // the cos / sin table holds max_seq positions
+    if (d_cos_sin != nullptr && ((reinterpret_cast<uintptr_t>(d_cos_sin) & 15u) || start_pos + rows_q > max_seq))
         return hipErrorInvalidValue;
     for (const void* p : {(const void*)d_q, (const void*)d_k, (const void*)d_v, (const void*)d_q16,
                           (const void*)d_k_cache, (const void*)d_v_cache})
@@ -1112,7 +1168,7 @@ extern "C" hipError_t rf_qk_norm_rope_kv_write_rows(const float* d_q, const floa
     hipLaunchKernelGGL(rf_qk_norm_rope_kv_rows_kernel<LPP>,                                                            \
                        dim3((heads + 4 * (64 / LPP) - 1) / (4 * (64 / LPP)), rows_q), dim3(256), 0, stream, d_q, d_k, \
                        d_v, d_q_norm, d_k_norm, q16, kc, vc, start_pos, rows_kv, num_heads, num_kv_heads, eps,        \
-                       d_theta, theta_base, neox, d_freq_scale)
+                       d_theta, theta_base, neox, d_freq_scale, reinterpret_cast<const float2*>(d_cos_sin))
     switch (head_dim) {
     case 64: RF_QKR(8); break;
     case 128: RF_QKR(16); break;
@@ -1180,11 +1236,12 @@ extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const floa
                                                         const int num_kv_heads, const int head_dim, const float eps,
                                                         const float theta_base, const int neox,
                                                         const float* d_freq_scale, const float* d_theta,
-                                                        const float scale, float* d_workspace,
+                                                        const float* d_cos_sin, const float scale, float* d_workspace,
                                                         const size_t workspace_bytes, hipStream_t stream) {
     if (d_k == nullptr || d_v == nullptr || d_state == nullptr || d_workspace == nullptr) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(d_cos_sin) & 15u) return hipErrorInvalidValue;
     QkStep qk{d_k, d_v, d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
-              eps, d_theta, theta_base, neox, d_freq_scale};
+              eps, d_theta, theta_base, neox, d_freq_scale, reinterpret_cast<const float2*>(d_cos_sin)};
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
                        reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
                        scale, d_workspace, workspace_bytes, stream, &qk);
@@ -1246,6 +1303,22 @@ extern "C" hipError_t rf_rope_theta_table(float* d_theta, const int head_dim, co
     if (d_theta == nullptr || head_dim <= 0 || (head_dim & 1)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rf_theta_fill_kernel, dim3((head_dim / 2 + 255) / 256), dim3(256), 0, stream, d_theta,
                        head_dim, theta_base);
+    return hipGetLastError();
+}
+
+// Caller-owned RoPE cos / sin table: d_cos_sin[2 * (pos * head_dim / 2 + i)
+// + {0, 1}] = cos / sin of pos * theta_i for pos < positions, theta_i as the
+// fused launchers evaluate it (d_theta when given, divided by d_freq_scale[i]
+// when given).  The fused launchers' d_cos_sin takes it in place of cosf /
+// sinf: the same values, so the same results.
+extern "C" hipError_t rf_rope_cos_sin_table(float* d_cos_sin, const int positions, const int head_dim,
+                                            const float theta_base, const float* d_theta, const float* d_freq_scale,
+                                            hipStream_t stream) {
+    if (d_cos_sin == nullptr || positions <= 0 || head_dim <= 0 || (head_dim & 1)) return hipErrorInvalidValue;
+    const long n = (long)positions * (head_dim / 2);
+    if (n > (1L << 30)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_rope_cos_sin_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<float2*>(d_cos_sin), positions, head_dim, theta_base, d_theta, d_freq_scale);
     return hipGetLastError();
 }
 

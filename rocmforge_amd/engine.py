@@ -154,25 +154,30 @@ class Engine:
     """Prefill + greedy decode of one sequence of up to max_seq tokens."""
 
     def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0",
-                 fuse_norm: bool = True, fold_qk: bool = False, fuse_gemm: bool = True, ffn_f16: bool = True):
+                 fuse_norm: bool = True, fold_qk: bool = True, fuse_gemm: bool = True, ffn_f16: bool = True,
+                 rope_table: bool = True):
         """fuse_norm: decode with the RMSNorms folded into the GEMVs that
         consume them, the per-head Q/K step into the attention and the state
         advance into the argmax (same bits as the separate launches);
         fold_qk: the per-head Q/K step folded into the attention (with
-        fuse_norm; off by default: measured on MI355X at the Qwen3-8B shape
-        it is 2.28 ms/token against 2.20 with the separate step);
+        fuse_norm; same bits; measured on MI355X at the Qwen3-8B shape
+        1.83 ms/token against 1.89 with the separate step);
         fuse_gemm: prefill projections that share an input in one segmented
         GEMM launch, and the O / FFN-down products added straight into the
         residual stream (same per-element products; the sums of a K split
         land in another order);
         ffn_f16: (with fuse_gemm) a Q4_K gate/up prefill on fp16 activations:
         the FFN norm rounded to fp16 feeds two 256 x 128-tile GEMMs and the
-        SwiGLU (the same operand values as the fp32 launchers)."""
+        SwiGLU (the same operand values as the fp32 launchers);
+        rope_table: the fused Q/K launchers read cos / sin of every
+        position's RoPE angles from a table made here once (the values their
+        cosf / sinf would give, so the same bits)."""
         import torch
         self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
         self.fuse_norm = fuse_norm
         self.fold_qk = fold_qk and fuse_norm
         self.fuse_gemm = fuse_gemm
+        self.rope_table = rope_table
         self.lib = _lib.load()
         ops._lib()
         f32, i16 = torch.float32, torch.int16
@@ -195,6 +200,11 @@ class Engine:
         self.attn_ws = z((ws_bytes + 3) // 4)
         self.attn_ws_bytes = ws_bytes
         _chk(self.lib.rf_rope_theta_table(_p(self.theta), c.head_dim, c.rope_base, self._stream()), "theta table")
+        self.cos_sin = None
+        if rope_table and c.head_dim % 2 == 0:
+            self.cos_sin = z(max_seq * c.head_dim)      # [pos][head_dim / 2] (cos, sin) pairs
+            _chk(self.lib.rf_rope_cos_sin_table(_p(self.cos_sin), max_seq, c.head_dim, c.rope_base, _p(self.theta),
+                                                None, self._stream()), "cos / sin table")
         self._graph = None
         self._pf = None
         self._act16 = False      # the last prefill layer's SwiGLU output went to the fp16 buffer
@@ -236,14 +246,16 @@ class Engine:
                 _chk(L.rf_attn_decode_qk_norm_rope_state(_p(self.attn), _p(self.q), _p(self.k), _p(self.v),
                                                          _p(lw.q_norm), _p(lw.k_norm), _p(self.kc[i]), _p(self.vc[i]),
                                                          pos_p, c.n_heads, c.n_kv_heads, c.head_dim, c.eps,
-                                                         c.rope_base, int(c.neox), None, _p(self.theta), self.scale,
+                                                         c.rope_base, int(c.neox), None, _p(self.theta),
+                                                         _p(self.cos_sin), self.scale,
                                                          _p(self.attn_ws), self.attn_ws_bytes, st),
                      "qk step + attention")
             else:
                 _chk(L.rf_qk_norm_rope_kv_write_state(_p(self.q), _p(self.k), _p(self.v), _p(lw.q_norm),
                                                       _p(lw.k_norm), _p(self.kc[i]), _p(self.vc[i]), pos_p,
                                                       c.n_heads, c.n_kv_heads, c.head_dim, c.eps, c.rope_base,
-                                                      int(c.neox), None, _p(self.theta), st), "qk_rope_kv")
+                                                      int(c.neox), None, _p(self.theta), _p(self.cos_sin), st),
+                     "qk_rope_kv")
                 t("qk_rope_kv", i)
                 _chk(L.rf_flash_attn_decode_state_ws(_p(self.attn), _p(self.q), _p(self.kc[i]), _p(self.vc[i]),
                                                      len_p, c.n_heads, c.n_kv_heads, c.head_dim, self.scale,
@@ -434,7 +446,8 @@ class Engine:
                 _chk(L.rf_qk_norm_rope_kv_write_rows(_p(b["q"]), _p(b["k"]), _p(b["v"]), _p(lw.q_norm),
                                                      _p(lw.k_norm), _p(b["q16"]), _p(self.kc[i]), _p(self.vc[i]), 0,
                                                      mp, M, c.n_heads, c.n_kv_heads, c.head_dim, self.max_seq, c.eps,
-                                                     c.rope_base, int(c.neox), None, _p(self.theta), st), "qk rows")
+                                                     c.rope_base, int(c.neox), None, _p(self.theta),
+                                                     _p(self.cos_sin), st), "qk rows")
                 t("qk_rope_kv", i)
                 k16, v16 = self.kc[i], self.vc[i]
             else:

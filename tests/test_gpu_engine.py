@@ -191,7 +191,7 @@ def test_graph_replays_eager_steps(eng):
 def test_fused_norm_decode_equals_separate(weights, eng):
     # the RMSNorm folded into the QKV / gate-up / LM-head GEMVs gives the same
     # bits; every engine decodes from the same prefilled state
-    fused = E.Engine(CFG, weights, max_seq=256)
+    fused = E.Engine(CFG, weights, max_seq=256, fold_qk=False)
     folded = E.Engine(CFG, weights, max_seq=256, fold_qk=True)
     prompt = list(range(7, 47))
     eng.prefill(prompt)
@@ -460,14 +460,14 @@ def test_qk_rows_rejections(rf, dev):
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     f = rf.rf_qk_norm_rope_kv_write_rows
     ok = (P(z), P(z), P(z), None, None, P(h), P(h), P(h))
-    assert f(*ok, 0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) == 0
+    assert f(*ok, 0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) == 0
     torch.cuda.synchronize()
-    assert f(*ok, 7, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0     # past max_seq
-    assert f(*ok, 0, 2, 3, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0     # more K rows than Q rows
-    assert f(*ok, 0, 2, 2, 2, 1, 96, 8, 1e-6, 1e4, 1, None, None, s) != 0      # head_dim
+    assert f(*ok, 7, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) != 0     # past max_seq
+    assert f(*ok, 0, 2, 3, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) != 0     # more K rows than Q rows
+    assert f(*ok, 0, 2, 2, 2, 1, 96, 8, 1e-6, 1e4, 1, None, None, None, s) != 0      # head_dim
     assert f(P(z), P(z), P(z), None, None, ctypes.c_void_p(h.data_ptr() + 2), P(h), P(h),
-             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0          # q16 misaligned
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) != 0          # q16 misaligned
     assert f(P(z), P(z), P(z), None, None, P(h), ctypes.c_void_p(h.data_ptr() + 2), P(h),
-             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0    # K cache misaligned
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) != 0    # K cache misaligned
     assert f(P(z), P(z), P(z), None, None, P(h), P(h), ctypes.c_void_p(h.data_ptr() + 8),
-             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, s) != 0    # V cache misaligned
+             0, 2, 2, 2, 1, 128, 8, 1e-6, 1e4, 1, None, None, None, s) != 0    # V cache misaligned

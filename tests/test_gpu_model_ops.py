@@ -153,7 +153,7 @@ def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox, table):
         np.testing.assert_array_equal(G.host(theta), want)
     G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn) if with_norm else None,
            G.ptr(dkn) if with_norm else None, G.ptr(kc), G.ptr(vc), G.ptr(dpos), nh, nkv, d, 1e-6, 1e6, neox, None,
-           G.ptr(theta) if table else None)
+           G.ptr(theta) if table else None, None)
     qr = O.rms_norm(q, qn, 1e-6, nh) if with_norm else q.astype(np.float64)
     kr = O.rms_norm(k, kn, 1e-6, nkv) if with_norm else k.astype(np.float64)
     _close(G.host(dq), O.rope(qr, 1, nh, d, pos, 1e6, bool(neox)), "fused q")
@@ -170,6 +170,8 @@ def test_fused_qk_norm_rope_kv(rf, dev, with_norm, neox, table):
     G.call(rf.gpu_rope_heads_state, G.ptr(dq2), G.ptr(dpos), nh, d, 1e6, neox)
     G.call(rf.gpu_kv_write_rope_state, G.ptr(kc2), G.ptr(vc2), G.ptr(dk2), G.ptr(dv), G.ptr(dpos), nkv, d, 1e6, neox)
     a, b = G.host(dq), G.host(dq2)
+    if not with_norm:       # the same rotation, so the same bits
+        np.testing.assert_array_equal(a, b)
     assert np.abs(a - b).max() <= 4 * np.spacing(np.abs(b).max())
     kc2_h = G.host(kc2).view(np.uint16).reshape(max_seq, -1)
     assert (np.abs(kc_h[pos].view(np.float16).astype(np.float64) - kc2_h[pos].view(np.float16).astype(np.float64))
@@ -331,10 +333,10 @@ def test_attention_with_folded_qk_step(rf, dev, seq, nh, nkv, d):
     wsb = int(rf.rf_flash_attn_decode_workspace_bytes(nh, d))
     ws = G.empty(wsb // 4, torch.float32)
     G.call(rf.rf_attn_decode_qk_norm_rope_state, G.ptr(out1), G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn),
-           G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, scale, G.ptr(ws), wsb)
+           G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, None, scale, G.ptr(ws), wsb)
     np.testing.assert_array_equal(G.host(dq), q)        # the raw q is left as it was
     G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(kc2),
-           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None)
+           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, None)
     dlen = G.to_dev(np.array([seq], np.int32))
     G.call(rf.rf_flash_attn_decode_state_ws, G.ptr(out2), G.ptr(dq), G.ptr(kc2), G.ptr(vc2), G.ptr(dlen), nh, nkv, d,
            scale, G.ptr(ws), wsb)
@@ -346,6 +348,86 @@ def test_attention_with_folded_qk_step(rf, dev, seq, nh, nkv, d):
     ref = O.attn_decode(qr.astype(np.float32), G.host(kc1).view(np.uint16), G.host(vc1).view(np.uint16), seq, nh,
                         nkv, d, scale)
     _close(G.host(out1), ref, f"attention with qk step seq {seq}")
+
+
+@pytest.mark.parametrize("d,neox,scaled", [(128, 1, False), (128, 0, False), (64, 1, True), (256, 0, True),
+                                           (256, 1, False)])
+def test_rope_cos_sin_table_same_bits(rf, dev, d, neox, scaled):
+    # the cos / sin table replaces cosf / sinf in the three fused Q/K launchers:
+    # same values, so the outputs and caches must match the trig path bit for bit
+    nh, nkv, max_seq, base = 16, 4, 300, 1e6
+    rng = np.random.default_rng(d + neox)
+    fs = G.to_dev((1 + rng.random(d // 2)).astype(np.float32)) if scaled else None
+    theta = G.empty(d // 2, torch.float32)
+    G.call(rf.rf_rope_theta_table, G.ptr(theta), d, base)
+    cs = G.empty(max_seq * d, torch.float32)
+    G.call(rf.rf_rope_cos_sin_table, G.ptr(cs), max_seq, d, base, G.ptr(theta), G.ptr(fs) if scaled else None)
+    # the table against double-precision cos / sin of the same float angle
+    th = G.host(theta).astype(np.float32)
+    if scaled:
+        th = (th / G.host(fs)).astype(np.float32)
+    ang = (np.arange(max_seq, dtype=np.float32)[:, None] * th[None, :]).astype(np.float64)
+    tab = G.host(cs).reshape(max_seq, d // 2, 2)
+    assert np.abs(tab[..., 0] - np.cos(ang)).max() <= 4e-7
+    assert np.abs(tab[..., 1] - np.sin(ang)).max() <= 4e-7
+    fsp = G.ptr(fs) if scaled else None
+    qn, kn = ((1 + 0.1 * rng.standard_normal(d)).astype(np.float32) for _ in range(2))
+    dqn, dkn = G.to_dev(qn), G.to_dev(kn)
+    # decode step at a late position
+    pos = max_seq - 3
+    q = (rng.standard_normal(nh * d) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * d) * 3).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    dk, dv = G.to_dev(k), G.to_dev(v)
+    st = G.to_dev(np.array([pos, pos + 1], np.int32))
+    outs = []
+    for table in (None, G.ptr(cs)):
+        dq = G.to_dev(q)
+        kc, vc = G.empty(max_seq * nkv * d, torch.int16).zero_(), G.empty(max_seq * nkv * d, torch.int16).zero_()
+        G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(kc),
+               G.ptr(vc), G.ptr(st), nh, nkv, d, 1e-6, base, neox, fsp, G.ptr(theta), table)
+        outs.append((G.host(dq), G.host(kc)))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    # the step folded into the attention
+    wsb = int(rf.rf_flash_attn_decode_workspace_bytes(nh, d))
+    ws = G.empty(wsb // 4, torch.float32)
+    cache = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.int16)
+    outs = []
+    for table in (None, G.ptr(cs)):
+        dq = G.to_dev(q)
+        kc, vc = G.to_dev(cache), G.to_dev(cache)
+        out = G.empty(nh * d, torch.float32)
+        G.call(rf.rf_attn_decode_qk_norm_rope_state, G.ptr(out), G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn),
+               G.ptr(dkn), G.ptr(kc), G.ptr(vc), G.ptr(st), nh, nkv, d, 1e-6, base, neox, fsp, G.ptr(theta), table,
+               1.0 / math.sqrt(d), G.ptr(ws), wsb)
+        outs.append((G.host(out), G.host(kc)))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    # the prompt rows: 37 query rows from position 200, 30 of them with K/V rows
+    start, rq, rkv = 200, 37, 30
+    qr = (rng.standard_normal(rq * nh * d) * 3).astype(np.float32)
+    kr = (rng.standard_normal(rq * nkv * d) * 3).astype(np.float32)
+    vr = rng.standard_normal(rq * nkv * d).astype(np.float32)
+    dq, dk, dv = G.to_dev(qr), G.to_dev(kr), G.to_dev(vr)
+    outs = []
+    for table in (None, G.ptr(cs)):
+        q16 = G.empty(rq * nh * d, torch.int16)
+        kc, vc = G.empty(max_seq * nkv * d, torch.int16).zero_(), G.empty(max_seq * nkv * d, torch.int16).zero_()
+        G.call(rf.rf_qk_norm_rope_kv_write_rows, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(q16),
+               G.ptr(kc), G.ptr(vc), start, rq, rkv, nh, nkv, d, max_seq, 1e-6, base, neox, fsp, G.ptr(theta), table)
+        outs.append((G.host(q16), G.host(kc), G.host(vc)))
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    # the table covers max_seq positions: query rows past it are rejected
+    s0 = G.stream()
+    assert rf.rf_qk_norm_rope_kv_write_rows(G.ptr(dq), G.ptr(dk), G.ptr(dv), None, None, G.ptr(q16), G.ptr(kc),
+                                            G.ptr(vc), max_seq - 10, 20, 5, nh, nkv, d, max_seq, 1e-6, base, neox,
+                                            fsp, None, G.ptr(cs), s0) != 0
+    assert rf.rf_qk_norm_rope_kv_write_rows(G.ptr(dq), G.ptr(dk), G.ptr(dv), None, None, G.ptr(q16), G.ptr(kc),
+                                            G.ptr(vc), max_seq - 10, 20, 5, nh, nkv, d, max_seq, 1e-6, base, neox,
+                                            fsp, None, None, s0) == 0
+    torch.cuda.synchronize()
 
 
 def test_argmax_advances_state(rf, dev):
