@@ -151,6 +151,15 @@ hipError_t rf_gemm_qk_f16_segments_launch(const uint16_t* input_f16, const void*
  * weights 16-byte aligned. */
 hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void* w_gate, const void* w_up, void* out,
                                           int out_f16, int M, int N, int K, hipStream_t stream);
+/* The up projection of a SwiGLU on fp16 activations with the gate product
+ * gate[M x N] (fp32, e.g. from rf_gemm_q4_k_f16_launch on the gate weights)
+ * already computed: out_f16[M x N] = fp16(silu(gate) * (A Wu^T)), the
+ * values of rf_gemm_q4_k_f16_launch on w_up followed by
+ * rf_silu_mul_f16_on_stream, with the SwiGLU in the GEMM's store (the
+ * reference runs the GEMM and a SwiGLU kernel, src/gpu/forward.rs:2327).
+ * Shapes as rf_gemm_q4_k_f16_launch; gate must not overlap out_f16. */
+hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f16, const void* w_up, const float* gate,
+                                             uint16_t* out_f16, int M, int N, int K, hipStream_t stream);
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
 

@@ -1461,12 +1461,16 @@ __device__ __forceinline__ void lds_dma16(uint32_t lds_dst, uint32_t voff, const
 // rows of W1 (waves 2-3), n0 = 64 per column tile; after the K halves are
 // added the gate waves hand their sums to the up waves through LDS, which
 // store silu(gate) * up into D[M x N] (N = the gate/up row count) as fp32
-// (PAIR 1) or rounded to fp16 (PAIR 2, D read as halves).
-template <int PAIR>
+// (PAIR 1) or rounded to fp16 (PAIR 2, D read as halves).  PAIR 3: a plain
+// tile whose store is the up projection of a SwiGLU, fp16 silu(G) * sum
+// with the gate product G [M x N] read back.
+template <int PAIR_ARG>
 __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                          const uint8_t* __restrict__ W,
                                                                          const uint8_t* __restrict__ W1,
-                                                                         float* __restrict__ D, int M, int N, int K) {
+                                                                         float* __restrict__ D, int M, int N, int K,
+                                                                         const float* __restrict__ G) {
+    constexpr int PAIR = PAIR_ARG == 3 ? 0 : PAIR_ARG;      // 3: a plain tile, gated store
     // one LDS block: ring (2 stages), A (3 buffers), scale tables (2); after
     // the loop its first 128 KB carry the K-half exchange
     __shared__ __align__(16) uint8_t lds[kF16aLds];
@@ -1722,7 +1726,14 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
                         if (!FULL && row >= M) continue;
                         // kh 0 + kh 1 in a fixed order (either wave forms the same sum)
                         const float a = acc[keep + i][j][4 * q + u];
-                        D[(size_t)row * N + ncol] = KH ? o[u] + a : a + o[u];
+                        const float sum = KH ? o[u] + a : a + o[u];
+                        const size_t e = (size_t)row * N + ncol;
+                        if constexpr (PAIR_ARG == 3) {      // up projection of a SwiGLU: fp16 silu(gate) * up
+                            const float gg = G[e];
+                            reinterpret_cast<uint16_t*>(D)[e] = f16_bits_rn(gg / (1.0f + expf(-gg)) * sum);
+                        } else {
+                            D[e] = sum;
+                        }
                     }
                 }
             }
@@ -2164,7 +2175,8 @@ struct Q4sGeom {
 // Tile v of the launch (after the XCD remap); lds: the kLds-byte LDS block.
 template <int FMR, bool ACC>
 __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds) {
+                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds,
+                                       const float* __restrict__ gate = nullptr) {
     using G = Q4sGeom<FMR>;
     uint8_t* ring = lds;
     uint8_t* abuf0 = lds + kQ4sRS * kQ4sStage;
@@ -2352,8 +2364,14 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
         for (int u = 0; u < 4; ++u) {
             const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
             if (row < M) {
-                float* o = D + (size_t)row * N + ncol;
-                *o = ACC ? *o + s[u] : s[u];
+                const size_t e = (size_t)row * N + ncol;
+                if (!ACC && gate != nullptr) {   // up projection of a SwiGLU: fp16 silu(gate) * up
+                    const float gg = gate[e];
+                    reinterpret_cast<uint16_t*>(D)[e] = f16_bits_rn(gg / (1.0f + expf(-gg)) * s[u]);
+                } else {
+                    float* o = D + e;
+                    *o = ACC ? *o + s[u] : s[u];
+                }
             }
         }
     }
@@ -2362,9 +2380,10 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
 template <int FMR, bool ACC>
 __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ W,
-                                                                        float* __restrict__ D, int M, int N, int K) {
+                                                                        float* __restrict__ D, int M, int N, int K,
+                                                                        const float* __restrict__ G) {
     __shared__ __align__(16) uint8_t lds[Q4sGeom<FMR>::kLds];
-    q4s_wg<FMR, ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds);
+    q4s_wg<FMR, ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, G);
 }
 
 // Column segments on fp16 activations: up to three weight matrices (each
@@ -2538,20 +2557,27 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
 // Q4_K on fp16 activations: 256 x 128 tiles (rf_gemm_q4k_f16a_kernel) where
 // they fill at least three quarters of the CUs, else the eight-wave
 // K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64) or 128.
+// G: when given, D receives fp16 silu(G) * (A W^T) (the up projection of a
+// SwiGLU whose gate product G [M x N] is already computed)
 template <bool ACC>
-static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st) {
+static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
+                              const float* G = nullptr) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
     if (pick == 0) {
-        hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D, M,
-                           N, K);
+        if (G != nullptr)
+            hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<3>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
+                               M, N, K, G);
+        else
+            hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
+                               M, N, K, nullptr);
     } else if (pick == 2) {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(((M + 63) / 64) * (N / kQ4sBN)), dim3(kQ4sThreads),
-                           0, st, A, w, D, M, N, K);
+                           0, st, A, w, D, M, N, K, G);
     } else {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, ACC>), dim3(((M + 127) / 128) * (N / kQ4sBN)),
-                           dim3(kQ4sThreads), 0, st, A, w, D, M, N, K);
+                           dim3(kQ4sThreads), 0, st, A, w, D, M, N, K, G);
     }
     return hipGetLastError();
 }
@@ -2588,11 +2614,29 @@ extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, 
     const uint8_t* wu = static_cast<const uint8_t*>(w_up);
     if (out_f16)
         hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<2>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
-                           static_cast<float*>(out), M, N, K);
+                           static_cast<float*>(out), M, N, K, nullptr);
     else
         hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<1>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
-                           static_cast<float*>(out), M, N, K);
+                           static_cast<float*>(out), M, N, K, nullptr);
     return hipGetLastError();
+}
+
+// The up projection of a SwiGLU on fp16 activations, the gate product
+// already computed: out_f16[M x N] = fp16(silu(gate) * (A Wu^T)), the values
+// of rf_gemm_q4_k_f16_launch on w_up followed by rf_silu_mul_f16_on_stream
+// (same tiles, the SwiGLU in their epilogue).  Shapes as
+// rf_gemm_q4_k_f16_launch; gate [M x N] fp32 must not overlap out_f16.
+extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f16, const void* w_up,
+                                                        const float* gate, uint16_t* out_f16, int M, int N, int K,
+                                                        hipStream_t stream) {
+    if (input_f16 == nullptr || w_up == nullptr || gate == nullptr || out_f16 == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
+        return hipErrorInvalidValue;
+    if (!aligned16(input_f16) || !aligned16(w_up)) return hipErrorInvalidValue;
+    const size_t n = (size_t)M * N;
+    const uintptr_t g0 = reinterpret_cast<uintptr_t>(gate), o0 = reinterpret_cast<uintptr_t>(out_f16);
+    if (g0 < o0 + 2 * n && o0 < g0 + 4 * n) return hipErrorInvalidValue;   // overlapping buffers
+    return gemm_q4_f16<false>(input_f16, w_up, reinterpret_cast<float*>(out_f16), M, N, K, stream, gate);
 }
 
 // Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,

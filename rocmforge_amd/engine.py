@@ -514,13 +514,16 @@ class Engine:
                                                       _p(b["g16"] if self._act16 else b["g"]), int(self._act16), mp,
                                                       c.ff, c.hidden, st), "gemm f16 swiglu")
             elif gu16:
-                # gate and up as two GEMMs on the fp16 norm, then the SwiGLU
-                for mat, out in (("ffn_gate", "g"), ("ffn_up", "u")):
-                    _chk(L.rf_gemm_q4_k_f16_launch(_p(b["xn16"]), _p(m[mat][0]), _p(b[out]), mp, c.ff, c.hidden, st),
-                         "gemm f16")
+                # gate and up as two GEMMs on the fp16 norm; the SwiGLU in the up GEMM's
+                # store when the down projection takes fp16, else its own kernel
+                _chk(L.rf_gemm_q4_k_f16_launch(_p(b["xn16"]), _p(m["ffn_gate"][0]), _p(b["g"]), mp, c.ff, c.hidden,
+                                               st), "gemm f16")
                 if self._act16:
-                    _chk(L.rf_silu_mul_f16_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g16"]), mp * c.ff, st), "swiglu f16")
+                    _chk(L.rf_gemm_q4_k_f16_swiglu_up_launch(_p(b["xn16"]), _p(m["ffn_up"][0]), _p(b["g"]),
+                                                             _p(b["g16"]), mp, c.ff, c.hidden, st), "gemm f16 swiglu up")
                 else:
+                    _chk(L.rf_gemm_q4_k_f16_launch(_p(b["xn16"]), _p(m["ffn_up"][0]), _p(b["u"]), mp, c.ff, c.hidden,
+                                                   st), "gemm f16")
                     _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             elif self._act16:
                 fn = L.rf_gemm_q4_k_swiglu_f16_launch if gt == GgmlType.Q4_K else L.rf_gemm_q6_k_swiglu_f16_launch

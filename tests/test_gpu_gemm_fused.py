@@ -279,6 +279,44 @@ def test_q4k_f16_swiglu(rf, dev, m, n, k, f16):
     assert (err / tol).max() <= 1.0
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 12288, 1024), (256, 12288, 1024), (64, 256, 512), (320, 128, 256)])
+def test_q4k_f16_swiglu_up(rf, dev, m, n, k):
+    # the up GEMM with the SwiGLU in its store (the gate product read back):
+    # bit for bit the plain fp16-activation GEMM and the SwiGLU kernel, on
+    # each tile kind (256 x 128 tiles at 512 x 12288, K-sliced 128- and
+    # 64-row tiles, a partial last tile at M = 320)
+    a = torch.from_numpy(synth.activations(k, seed=m + 3, m=m)).to(torch.bfloat16).float().numpy()
+    da = G.to_dev(a.astype(np.float16).view(np.int16))
+    wu = G.to_dev(synth.weights("q4_k", n, k, seed=43))
+    gate = G.to_dev((np.random.default_rng(m).standard_normal(m * n) * 3).astype(np.float32))
+    out = G.empty(m * n, torch.int16)
+    G.call(rf.rf_gemm_q4_k_f16_swiglu_up_launch, G.ptr(da), G.ptr(wu), G.ptr(gate), G.ptr(out), m, n, k)
+    u = G.empty(m * n, torch.float32)
+    G.call(rf.rf_gemm_q4_k_f16_launch, G.ptr(da), G.ptr(wu), G.ptr(u), m, n, k)
+    ref = G.empty(m * n, torch.int16)
+    G.call(rf.rf_silu_mul_f16_on_stream, G.ptr(gate), G.ptr(u), G.ptr(ref), m * n)
+    np.testing.assert_array_equal(G.host(out), G.host(ref))
+
+
+def test_q4k_f16_swiglu_up_rejections(rf, dev):
+    m, n, k = 64, 128, 256
+    da = G.to_dev(np.zeros(m * k, np.int16))
+    w = G.to_dev(synth.weights("q4_k", n, k, seed=1))
+    g = G.empty(m * n, torch.float32)
+    o = G.empty(m * n, torch.int16)
+    s = G.stream()
+    z = ctypes.c_void_p(0)
+    P = G.ptr
+    f = rf.rf_gemm_q4_k_f16_swiglu_up_launch
+    assert f(P(da), P(w), P(g), P(o), m, n, k, s) == 0
+    torch.cuda.synchronize()
+    assert f(P(da), P(w), z, P(o), m, n, k, s) != 0                              # no gate
+    assert f(P(da), P(w), P(g), ctypes.c_void_p(g.data_ptr() + 64), m, n, k, s) != 0   # output inside the gate
+    assert f(P(da), P(w), P(g), P(o), m, 96, k, s) != 0                          # N % 128
+    assert f(P(da), P(w), P(g), P(o), 32, n, k, s) != 0                          # M % 64
+    assert f(P(da), P(w), P(g), P(o), m, n, 320, s) != 0                         # K % 256
+
+
 def test_q4k_f16_swiglu_rejections(rf, dev):
     m, k = 64, 256
     da = G.to_dev(np.zeros(m * k, np.int16))
