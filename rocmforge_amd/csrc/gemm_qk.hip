@@ -2556,7 +2556,8 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
 
 // Q4_K on fp16 activations: 256 x 128 tiles (rf_gemm_q4k_f16a_kernel) where
 // they fill at least three quarters of the CUs, else the eight-wave
-// K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64) or 128.
+// K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64, or when
+// they come to at most one round of CUs) or 128.
 // G: when given, D receives fp16 silu(G) * (A W^T) (the up projection of a
 // SwiGLU whose gate product G [M x N] is already computed)
 template <bool ACC>
@@ -2565,6 +2566,10 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
+    // 64-row K-sliced tiles also when twice as many of them still fit one
+    // round of CUs (measured on MI355X, N = 4096: M = 256 22.3 against 24.7 us
+    // at K = 4096, 58.4 against 63.1 at K = 12288; M = 512 1-2 % faster)
+    if (pick == 4 && 2L * ((M + 127) / 128) * (N / kQ4sBN) <= (long)device_cu_count()) pick = 2;
     if (pick == 0) {
         if (G != nullptr)
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<3>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
