@@ -12,7 +12,8 @@ Extra objects on the same JSON line: config 0 ("gemv_4096", the single
 Q4_K GEMV), config 3 ("prefill_gemm": TFLOP/s at M = 64..512), config 2
 ("decode_stream"), config 4 ("e2e_qwen3_8b") and the CPU baseline.  Every
 timed region is preceded by an untimed clock ramp of about 0.3 s of the
-same launches.
+same launches, enqueued back to back and still running when the timed
+region is enqueued behind them (the timed launches start on a busy GPU).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -131,8 +132,7 @@ def bench_decode(lib, torch, steps, warmup):
     g_dn = capture([dn_call(i % copies) for i in range(steps)])
 
     def timed(g):
-        ramp(torch, g.replay)
-        torch.cuda.synchronize()
+        ramp(torch, g.replay)      # leaves its last batch in flight
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         g.replay()
@@ -155,14 +155,19 @@ def bench_decode(lib, torch, steps, warmup):
 
 
 def ramp(torch, fn, seconds=0.3):
-    """Untimed clock ramp: repeat fn (a graph replay or a launch loop) for
-    about `seconds` of GPU time before a timed region, so the timed launches
-    run at the clocks a busy GPU settles at (a cold GPU starts lower)."""
+    """Untimed clock ramp: about `seconds` of back-to-back fn calls (a graph
+    replay or a launch loop) before a timed region, so the timed launches run
+    at the clocks a busy GPU settles at.  All calls are enqueued without a
+    wait (a wait between calls leaves the GPU idling, and after an idle spell
+    it runs a K = 20 graph ~5 % slower), and they are still running when the
+    timed region is enqueued behind them."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    fn()
+    torch.cuda.synchronize()
+    one = max(time.perf_counter() - t0, 1e-5)
+    for _ in range(min(4000, max(1, int(seconds / one)))):
         fn()
-        torch.cuda.synchronize()
 
 
 # BASELINE config 0: one Q4_K GEMV 4096x4096 with the Q8_0 quantisation of x
