@@ -2568,7 +2568,7 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
     int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
     // 64-row K-sliced tiles also when twice as many of them still fit one
     // round of CUs (measured on MI355X, N = 4096: M = 256 22.3 against 24.7 us
-    // at K = 4096, 58.4 against 63.1 at K = 12288; M = 512 1-2 % faster)
+    // at K = 4096, 58.4 against 63.1 at K = 12288)
     if (pick == 4 && 2L * ((M + 127) / 128) * (N / kQ4sBN) <= (long)device_cu_count()) pick = 2;
     if (pick == 0) {
         if (G != nullptr)

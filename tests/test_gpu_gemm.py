@@ -129,7 +129,7 @@ def test_gemm_identity_random_weights(rf, dev, fmt, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(512, 14336, 4096), (256, 14336, 4096), (64, 14336, 4096), (128, 4096, 4096),
                                    (576, 6144, 4096), (320, 256, 1024), (128, 14336, 4096), (512, 4096, 4096),
-                                   (512, 4096, 12288), (192, 192, 512), (64, 64, 256)])
+                                   (512, 4096, 12288), (256, 4096, 12288), (192, 192, 512), (64, 64, 256)])
 def test_gemm_q4k_fp16_activations(rf, dev, m, n, k):
     # 256 x 128 tiles at 512 x 14336; elsewhere the K-sliced 64 / 128-row tiles
     # (M <= 64 / above), including partial row tiles and N = 64, 192
@@ -157,7 +157,7 @@ def test_gemm_q6k_fp16_activations(rf, dev, m, n, k):
     _check(G.host(d).reshape(m, n), "q6_k", a, w, m, n, k, f"fp16-A q6_k M={m} {n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (64, 128, 512), (192, 64, 1024)])
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (256, 4096, 12288), (64, 128, 512), (192, 64, 1024)])
 def test_gemm_q4k_fp16_accumulate(rf, dev, m, n, k):
     # inout += product: bit for bit the plain launch's sums plus the old
     # contents (the K-sliced tiles serve both; rows past M stay put)
