@@ -7,17 +7,32 @@
 // rounding is the reference's: A via __float2half (wmma_gemm_q4_k.hip:86),
 // W via __float2half of the fp32 dequant value (:137, q6: :148).
 //
-// Kernels (selected by the launcher from the shape):
+// Routing.  The fp32-activation launchers (the two above, and the segments /
+// accumulate / SwiGLU launchers below) round A to fp16 in a pass of their
+// own into library-owned device memory (the same values the reference's
+// __float2half gives) and run the fp16-activation tiles:
+//  * rf_gemm_q4k_f16a_kernel (Q4_K where 256 x 128 tiles fill at least 3/4
+//    of the CUs): 4 waves, each weight dequantised once per 256 rows of A,
+//    A and the weight ring by LDS DMA.
+//  * rf_gemm_q4k_f16s_kernel (Q4_K otherwise) and rf_gemm_q6k_f16a_kernel
+//    (Q6_K, K % 2048 == 0): 8 waves over 64- or 128-row x 64-column tiles, K
+//    sliced over waves and added through LDS; when the tiles leave at least
+//    half the CUs idle, K is also split over workgroups whose partial tiles
+//    rf_gemm_split_reduce_kernel adds in split order.
+// Every output is one fixed-order sum: no float atomics, the same bits on
+// every run.  When no staging memory is free for the stream (or Q6_K rows are
+// not 16-byte aligned) the fp32-activation kernels run, one workgroup per
+// tile:
 //  * rf_gemm_qk_sq_kernel (N % 256 == 0, K % 512 == 0, and 256 x 256 or
-//    128 x 128 tiles that come to about one workgroup per CU unsplit): 2 x 2
-//    waves, each weight dequantised once per workgroup into an LDS B tile
-//    shared by the two waves that use it.
+//    128 x 128 tiles that come to about one workgroup per CU): 2 x 2 waves,
+//    each weight dequantised once per workgroup into an LDS B tile shared by
+//    the two waves that use it.
 //  * rf_gemm_qk_v7_kernel (otherwise when N % 256 == 0, K % 512 == 0 and,
 //    for Q6_K, K % 2048 == 0): 256-thread workgroups, one wave per SIMD,
 //    over a BM x 256 tile; weights stage through an LDS ring with coalesced
 //    loads, each wave dequantises its own B operands (the next chunk's,
 //    double buffered) in hand-scheduled slots between its MFMAs; XCD-aware
-//    tile order; split-K with float atomics when the tiles leave CUs idle.
+//    tile order.
 //  * rf_gemm_qk_v4_kernel: 8 waves, weights loaded per lane (Q6_K with
 //    K % 2048 != 0, whose rows are not 16-byte aligned for the ring).
 //  * rf_gemm_qk_kernel (any M % 64 == 0, N % 64 == 0, K % 256 == 0): the
@@ -25,10 +40,12 @@
 //    blocks of v_mfma_f32_32x32x16_f16; each 64-wide K chunk of A (fp32 ->
 //    fp16) and of W (dequantised in registers, 2 threads per weight row)
 //    lands in LDS as [row][k] fp16 with a padded stride, double buffered.
-// The v7 kernel also serves two launchers with no reference counterpart:
-// several weight matrices over one input as column segments of a single
-// launch (rf_gemm_q*_k_segments_launch), and D += product
-// (rf_gemm_q*_k_accumulate_launch, also served by sq).
+// Launchers with no reference counterpart: several weight matrices over one
+// input as column segments of a single launch (rf_gemm_q*_k_segments_launch,
+// rf_gemm_qk_f16_segments_launch), D += product (*_accumulate_launch) and
+// gate/up pairs with SwiGLU in the epilogue (*_swiglu_launch).
+#include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "qk_common.h"
@@ -455,9 +472,9 @@ constexpr int kV4LdsBytes = 65536;
 // chunk parity (A staging, quant bytes) and super-block parity (headers); the
 // loop is unrolled over 8 chunks so every index is static.  Loads past c_last
 // re-read the chunk four back (same position in its super-block).
-// SPLIT: the grid is tiles x splits; split s covers an equal run of chunks
-// and adds its partial tile into D (zeroed beforehand) with float atomics.
-template <typename T, int FM, bool SPLIT>
+// The grid is tiles x splits, split s covering an equal run of chunks; the
+// launchers use one split (chunks_per_split = K / 64).
+template <typename T, int FM>
 __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     float* __restrict__ D, int M, int N, int K,
@@ -590,10 +607,7 @@ __global__ __launch_bounds__(kV4Threads) void rf_gemm_qk_v4_kernel(const float* 
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            if constexpr (SPLIT)
-                unsafeAtomicAdd(&D[(size_t)row * N + col], v[e]);
-            else
-                D[(size_t)row * N + col] = v[e];
+            D[(size_t)row * N + col] = v[e];
         }
     };
 #pragma unroll
@@ -703,7 +717,7 @@ struct GemmSegs {
     int pair;
 };
 
-template <typename T, bool IS_Q6, int FM, bool SPLIT>
+template <typename T, bool IS_Q6, int FM>
 __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* __restrict__ A,
                                                                     const uint8_t* __restrict__ W,
                                                                     float* __restrict__ D, int M, int N, int K,
@@ -1122,10 +1136,7 @@ __global__ __launch_bounds__(kV7Threads) void rf_gemm_qk_v7_kernel(const float* 
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 float* o = dseg + (size_t)row * ldd + col;
-                if constexpr (SPLIT)
-                    unsafeAtomicAdd(o, acc[i][j][e]);
-                else
-                    *o = segs.accum ? *o + acc[i][j][e] : acc[i][j][e];
+                *o = segs.accum ? *o + acc[i][j][e] : acc[i][j][e];
             }
         }
 }
@@ -1887,9 +1898,21 @@ __device__ __forceinline__ u32x2 q6a_dq4(uint32_t qb, float S24, float nO) {
 }
 
 // Tile v of the launch (after the XCD remap); lds: the kLds-byte LDS block.
+// K split of the fp16-activation tiles (q6a_wg, q4s_wg): with S > 1 the
+// launch holds S x tiles workgroups, tile v of split s at s * tiles + v (the
+// workgroups of one split neighbours, so one XCD mostly reads one K range of
+// A), split s covers super-blocks [s nsb / S, (s + 1) nsb / S) of every row
+// and stores its partial tile to part + s * M * N (row-major M x N, plain
+// stores); rf_gemm_split_reduce_kernel adds the S partials in split order.
+struct KSplit {
+    int S;
+    float* part;
+};
+
 template <bool ACC>
 __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds) {
+                                       float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds,
+                                       KSplit sp = KSplit{1, nullptr}) {
     uint8_t* ring = lds;
     uint8_t* abuf0 = lds + kQ6aRS * kQ6aStage;
     const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
@@ -1901,11 +1924,20 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     const int ks = wave & 3, cg = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
     const int mtiles = (M + kQ6aBM - 1) / kQ6aBM;
+    const int nsb_row = K / kQK;
+    int sb0 = 0, nsb = nsb_row;                // this workgroup's super-blocks [sb0, sb0 + nsb) of each row
+    if (sp.S > 1) {
+        const int per = mtiles * (N / kQ6aBN);
+        const int s = v / per;
+        v -= s * per;
+        sb0 = s * nsb_row / sp.S;
+        nsb = (s + 1) * nsb_row / sp.S - sb0;
+        D = sp.part + (size_t)s * M * N;
+    }
     const int m0 = (v % mtiles) * kQ6aBM;      // the M tiles of one column tile are neighbours
     const int n0 = (v / mtiles) * kQ6aBN;
-    const int nchunks = K / kKC;
-    const int nsb = K / kQK;
-    const uint32_t row_bytes = (uint32_t)nsb * kQ6KBytes;
+    const int nchunks = 4 * nsb;
+    const uint32_t row_bytes = (uint32_t)nsb_row * kQ6KBytes;
 
     // ---- weight ring: DMA instruction ii = wave + 8 t moves the 16-byte
     // pieces [64 ii, 64 ii + 64) of the stage (row i / 15, piece i % 15 of the
@@ -1921,14 +1953,14 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
         roff[t] = (uint32_t)r * row_bytes + 16u * (uint32_t)pc;
     }
     auto w_dma1 = [&](int t, int sb, int slot) {
-        const int s = min(sb, nsb - 1);
+        const int s = sb0 + min(sb, nsb - 1);
         lds_dma16(ring_lds0 + (uint32_t)slot * kQ6aStage + 1024u * (uint32_t)(wave + 8 * t), roff[t],
                   w_tile + (size_t)((s * kQ6KBytes) & ~15));
     };
 
     // ---- A: instruction gi = 2 wave + g covers rows 8 gi + L / 8 of the chunk,
     // position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row M - 1 --
-    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + ((size_t)m0 * K + (size_t)sb0 * kQK) * 2;
     uint32_t dma_voff[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -1949,13 +1981,13 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     const int brow = 32 * cg + col;
     uint32_t rql[2], rqh[2];
     auto raw_read = [&](int n, int sb) {
-        const int off = (2 * sb) & 15;
+        const int off = (2 * (sb0 + sb)) & 15;
         const uint8_t* rowp = ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB;
         const int oql = off + 64 * n + 16 * ks + 8 * h;
         const int oqh = off + 128 + 32 * n + 16 * (ks & 1) + 8 * h;
         const uint32_t* pl = reinterpret_cast<const uint32_t*>(rowp + (oql & ~3));
         const uint32_t* ph = reinterpret_cast<const uint32_t*>(rowp + (oqh & ~3));
-        if (sb & 1) {
+        if ((sb0 + sb) & 1) {
             const uint32_t l0 = pl[0], l1 = pl[1], l2 = pl[2];
             const uint32_t h0 = ph[0], h1 = ph[1], h2 = ph[2];
             rql[0] = __builtin_amdgcn_alignbit(l1, l0, 16);
@@ -1972,14 +2004,14 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     float d24 = 0.0f, dm32 = 0.0f;
     int scb = 0;
     auto d_read = [&](int sb) {
-        const int off = (2 * sb) & 15;
+        const int off = (2 * (sb0 + sb)) & 15;
         const float d = half_bits_to_float(
             *reinterpret_cast<const uint16_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 208));
         d24 = d * 16777216.0f;
         dm32 = -32.0f * d;
     };
     auto sc_read = [&](int cq, int sb) {
-        const int off = (2 * sb) & 15;
+        const int off = (2 * (sb0 + sb)) & 15;
         scb = *reinterpret_cast<const int8_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 192 +
                                                4 * cq + ks);
     };
@@ -2135,9 +2167,10 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
 template <bool ACC>
 __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ W,
-                                                                        float* __restrict__ D, int M, int N, int K) {
+                                                                        float* __restrict__ D, int M, int N, int K,
+                                                                        KSplit sp) {
     __shared__ __align__(16) uint8_t lds[kQ6aLds];
-    q6a_wg<ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds);
+    q6a_wg<ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, sp);
 }
 
 // ── q4s: Q4_K GEMM on fp16 activations, 32 FMR x 64 tiles, K slices on waves
@@ -2176,7 +2209,7 @@ struct Q4sGeom {
 template <int FMR, bool ACC>
 __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
                                        float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds,
-                                       const float* __restrict__ gate = nullptr) {
+                                       const float* __restrict__ gate = nullptr, KSplit sp = KSplit{1, nullptr}) {
     using G = Q4sGeom<FMR>;
     uint8_t* ring = lds;
     uint8_t* abuf0 = lds + kQ4sRS * kQ4sStage;
@@ -2189,16 +2222,26 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
     const int ks = wave & 3, cg = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
     const int mtiles = (M + G::kBM - 1) / G::kBM;
+    const int nsb_row = K / kQK;
+    int sb0 = 0, nsb = nsb_row;                // this workgroup's super-blocks [sb0, sb0 + nsb) of each row
+    if (sp.S > 1) {
+        const int per = mtiles * (N / kQ4sBN);
+        const int s = v / per;
+        v -= s * per;
+        sb0 = s * nsb_row / sp.S;
+        nsb = (s + 1) * nsb_row / sp.S - sb0;
+        D = sp.part + (size_t)s * M * N;
+        gate = nullptr;
+    }
     const int m0 = (v % mtiles) * G::kBM;      // the M tiles of one column tile are neighbours
     const int n0 = (v / mtiles) * kQ4sBN;
-    const int nchunks = K / kKC;
-    const int nsb = K / kQK;
-    const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+    const int nchunks = 4 * nsb;
+    const uint32_t row_bytes = (uint32_t)nsb_row * kQ4KBytes;
 
     // ---- weight ring: DMA instruction ii = wave + 8 t moves 16-byte pieces
     // [64 ii, 64 ii + 64) of the stage (row i / 9, piece i % 9; pieces past
     // the 576 of the stage repeat the last one) ------------------------------
-    const uint8_t* w_tile = W + (size_t)n0 * row_bytes;
+    const uint8_t* w_tile = W + (size_t)n0 * row_bytes + (size_t)sb0 * kQ4KBytes;
     uint32_t roff[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -2213,7 +2256,7 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
     // ---- A: instruction gi = kAPW wave + g covers rows 8 gi + L / 8 of the
     // chunk, position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row
     // M - 1 ---------------------------------------------------------------------
-    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + ((size_t)m0 * K + (size_t)sb0 * kQK) * 2;
     uint32_t dma_voff[G::kAPW];
 #pragma unroll
     for (int g = 0; g < G::kAPW; ++g) {
@@ -2381,9 +2424,9 @@ template <int FMR, bool ACC>
 __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_q4k_f16s_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ W,
                                                                         float* __restrict__ D, int M, int N, int K,
-                                                                        const float* __restrict__ G) {
+                                                                        const float* __restrict__ G, KSplit sp) {
     __shared__ __align__(16) uint8_t lds[Q4sGeom<FMR>::kLds];
-    q4s_wg<FMR, ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, G);
+    q4s_wg<FMR, ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, G, sp);
 }
 
 // Column segments on fp16 activations: up to three weight matrices (each
@@ -2419,35 +2462,14 @@ __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uin
         q4s_wg<4, false>(A, w, d, M, n, K, v, lds);
 }
 
-// Split count: the largest S with S | (K/64)/8 (each split a whole number of
-// 8-chunk groups) and tiles * S <= CUs (one workgroup per CU; the kernel
-// runs one 512-thread workgroup per CU).  Measured on MI355X at the
-// Llama-3.1-8B FFN shapes this is the best split for M = 64 .. 512.
-static int gemm_splits(int tiles, int nchunks, int cus) {
-    const int groups = nchunks / 8;
-    int best = 1;
-    for (int s = 2; s <= groups && s <= 32; ++s)
-        if (groups % s == 0 && (long)tiles * s <= cus) best = s;
-    return best;
-}
-
-// Zeroes the outputs of the column segments of a split-K launch: segment i
-// is m * widths[i] floats at its own pointer.
-__global__ void rf_fill_zero_segs_kernel(float4* __restrict__ p0, size_t n0, float4* __restrict__ p1, size_t n1,
-                                         float4* __restrict__ p2, size_t n2) {
-    const size_t total = n0 + n1 + n2;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-        float4* p = i < n0 ? p0 + i : (i < n0 + n1 ? p1 + (i - n0) : p2 + (i - n0 - n1));
-        *p = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-}
-
 static GemmSegs single_seg(int N) {
     GemmSegs g{};
     g.n1 = g.n2 = N;
     return g;
 }
 
+// The fp32-activation ring / register-weight kernels, one workgroup per
+// tile and no K split: every output is written once, after its whole sum.
 template <bool IS_Q6, int FM>
 static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
                       const GemmSegs& sg) {
@@ -2456,33 +2478,14 @@ static void launch_v4(const float* A, const uint8_t* w, float* D, int M, int N, 
     using T = typename std::conditional<IS_Q6, Q6Ops, Q4Ops>::type;
     const int tiles = (M / (32 * FM)) * (N / 256);
     const int nchunks = K / kKC;
-    int s = gemm_splits(tiles, nchunks, device_cu_count());
-    if (sg.pair) s = 1;                              // silu(gate) * up needs the whole sums
     // v7 (LDS weight ring); Q6_K needs 16-byte aligned rows (K % 2048 == 0) for the ring
     const bool v7 = !plain || !IS_Q6 || K % 2048 == 0;
-    if (s > 1) {
-        if (!sg.accum) {
-            const size_t a4 = (size_t)M * sg.n1 / 4, b4 = (size_t)M * (sg.n2 - sg.n1) / 4,
-                         c4 = (size_t)M * (N - sg.n2) / 4;
-            hipLaunchKernelGGL(rf_fill_zero_segs_kernel,
-                               dim3((unsigned)std::min<size_t>((a4 + b4 + c4 + 255) / 256, 2048)), dim3(256), 0, st,
-                               reinterpret_cast<float4*>(D), a4, reinterpret_cast<float4*>(sg.d1), b4,
-                               reinterpret_cast<float4*>(sg.d2), c4);
-        }
-        if (v7)
-            hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, true>), dim3(tiles * s), dim3(kV7Threads), 0, st, A,
-                               w, D, M, N, K, tiles, nchunks / s, kGemmBand, sg);
-        else
-            hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, true>), dim3(tiles * s), dim3(kV4Threads), 0, st, A, w, D,
-                               M, N, K, tiles, nchunks / s);
-    } else {
-        if (v7)
-            hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM, false>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
-                               D, M, N, K, tiles, nchunks, kGemmBand, sg);
-        else
-            hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM, false>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M,
-                               N, K, tiles, nchunks);
-    }
+    if (v7)
+        hipLaunchKernelGGL((rf_gemm_qk_v7_kernel<T, IS_Q6, FM>), dim3(tiles), dim3(kV7Threads), 0, st, A, w,
+                           D, M, N, K, tiles, nchunks, kGemmBand, sg);
+    else
+        hipLaunchKernelGGL((rf_gemm_qk_v4_kernel<T, FM>), dim3(tiles), dim3(kV4Threads), 0, st, A, w, D, M,
+                           N, K, tiles, nchunks);
 }
 
 // Shared-dequantisation tiles without a K split; the caller checks that
@@ -2516,12 +2519,11 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
             launch_sq<IS_Q6, 256, 256>(A, w, D, M, N, K, st, sg.accum);
         else if (sq_ok && M % 128 == 0 && 8 * sq128_tiles >= 7 * cus && 8 * sq128_tiles <= 9 * cus)
             launch_sq<IS_Q6, 128, 128>(A, w, D, M, N, K, st, sg.accum);
-        // 128-row tiles, except for Q4_K when they would need a K split
-        // (M = 128, 256 at N = 14336): 64-row tiles halve the split and
-        // its float atomics (measured 3-5 % faster; Q6_K's heavier
-        // dequantisation makes them slower there).  Also 128-row tiles when
-        // they fit in one round of CUs but 64-row tiles would take two
-        // (M = 512 at N = 12288: 192 vs 384 tiles on 256 CUs)
+        // 128-row tiles where they come to at least 7/8 of the CUs, or fit
+        // in one round of CUs where 64-row tiles would take two (M = 512 at
+        // N = 12288: 192 vs 384 tiles on 256 CUs), and always for Q6_K
+        // (its heavier dequantisation favours fewer, taller tiles); else
+        // 64-row tiles
         else if (M % 128 == 0 && (IS_Q6 || 8L * (M / 128) * (N / 256) >= 7L * cus ||
                                   (2L * (M / 128) * (N / 256) > cus && (long)(M / 128) * (N / 256) <= cus)))
             launch_v4<IS_Q6, 4>(A, w, D, M, N, K, st, sg);
@@ -2539,30 +2541,157 @@ static hipError_t launch_gemm(const float* A, const void* W, float* D, int M, in
     return hipGetLastError();
 }
 
-}  // namespace rf
+// ── fp16 staging of fp32 activations, deterministic K split ──────────────
+// The fp32-activation launchers round A to fp16 exactly as the reference
+// does (__float2half, wmma_gemm_q4_k.hip:86) in a pass of their own, into
+// library-owned device memory, and then run the fp16-activation tiles: the
+// operand values are the same, and the tiles read half the bytes of A.  Small
+// launches split K over workgroups; the partial tiles land in the same
+// memory and one more pass adds them in split order, so every output is the
+// same sum on every run (no float atomics anywhere).
 
-using namespace rf;
+// Adds the S partial tiles (part + s * n, s = 0 .. S - 1, n = n4 * 4 floats)
+// in split order and stores the sum (MODE 0), adds it to D (MODE 1: D + sum),
+// or stores fp16 silu(gate) * sum into D read as halves (MODE 2), the
+// epilogues of the unsplit tiles.  All pointers 16-byte aligned.
+template <int MODE>
+__global__ __launch_bounds__(256) void rf_gemm_split_reduce_kernel(const float4* __restrict__ part, int S, size_t n4,
+                                                                    float* __restrict__ D,
+                                                                    const float4* __restrict__ gate) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        float4 t = part[i];
+        for (int k = 1; k < S; ++k) {
+            const float4 p = part[(size_t)k * n4 + i];
+            t.x += p.x;
+            t.y += p.y;
+            t.z += p.z;
+            t.w += p.w;
+        }
+        if constexpr (MODE == 0) {
+            reinterpret_cast<float4*>(D)[i] = t;
+        } else if constexpr (MODE == 1) {
+            float4 d = reinterpret_cast<float4*>(D)[i];
+            d.x = d.x + t.x;
+            d.y = d.y + t.y;
+            d.z = d.z + t.z;
+            d.w = d.w + t.w;
+            reinterpret_cast<float4*>(D)[i] = d;
+        } else {
+            const float4 g = gate[i];
+            const float r0 = g.x / (1.0f + expf(-g.x)) * t.x, r1 = g.y / (1.0f + expf(-g.y)) * t.y;
+            const float r2 = g.z / (1.0f + expf(-g.z)) * t.z, r3 = g.w / (1.0f + expf(-g.w)) * t.w;
+            reinterpret_cast<uint2*>(D)[i] =
+                make_uint2((uint32_t)f16_bits_rn(r0) | ((uint32_t)f16_bits_rn(r1) << 16),
+                           (uint32_t)f16_bits_rn(r2) | ((uint32_t)f16_bits_rn(r3) << 16));
+        }
+    }
+}
 
-// Validation as wmma_gemm_q4_k.hip:207-210 / wmma_gemm_q6_k.hip:220-223,
-// plus 16-byte alignment of A (read as float4) and of Q4_K weights.
-extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, float* output, int M, int N,
-                                            int K, hipStream_t stream) {
-    if (M <= 0 || N <= 0 || K <= 0) return hipErrorInvalidValue;
-    if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(input) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
-        return hipErrorInvalidValue;
-    return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
+// out[i] = fp16(a[i]) (round to nearest even, the value of __float2half) for
+// n4 * 4 elements; both 16-byte aligned.
+__global__ __launch_bounds__(256) void rf_f32_to_f16_kernel(const float4* __restrict__ a, uint2* __restrict__ out,
+                                                             size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        const float4 v = a[i];
+        out[i] = make_uint2(cvt_pk_f16(v.x, v.y), cvt_pk_f16(v.z, v.w));
+    }
+}
+
+static unsigned stream_grid(size_t n4) { return (unsigned)std::min<size_t>((n4 + 255) / 256, 4096); }
+
+// Library-owned scratch: kGemmSlots slots per GPU in a file-scope device
+// array (allocated when the library's code object loads on that GPU, held
+// until the process ends; the launchers never allocate).  A slot serves one
+// stream: its first kSlotABytes hold the fp16 copy of A, the rest the K-split
+// partials.  Launches on one stream are ordered, so they share its slot
+// safely; each further stream (up to kGemmSlots per GPU) gets a slot of its
+// own, and launches on streams past that take the unstaged fp32 kernels.  A
+// captured graph keeps the slot address of the stream it was captured on:
+// replaying it concurrently with other work of that stream races.  In host
+// code the array's name is only a stand-in; its device address is taken once
+// per GPU with hipGetSymbolAddress.
+constexpr int kGemmSlots = 4;
+constexpr size_t kSlotABytes = (size_t)32 << 20;
+constexpr size_t kSlotPartBytes = (size_t)8 << 20;
+constexpr size_t kSlotBytes = kSlotABytes + kSlotPartBytes;
+static __device__ __align__(256) uint8_t gemm_scratch[kGemmSlots * kSlotBytes];
+constexpr int kGemmMaxDevices = 64;
+
+struct GemmSlot {
+    uint16_t* a;        // kSlotABytes
+    float* part;        // kSlotPartBytes
+};
+
+static std::mutex g_slot_mutex;
+static uint8_t* g_slot_base[kGemmMaxDevices];
+static hipStream_t g_slot_owner[kGemmMaxDevices][kGemmSlots];
+static bool g_slot_taken[kGemmMaxDevices][kGemmSlots];
+
+// The slot of `st` on the current device (claimed on its first use); false
+// when every slot belongs to another stream or the array is unavailable.
+static bool gemm_slot(hipStream_t st, GemmSlot* out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kGemmMaxDevices) return false;
+    std::lock_guard<std::mutex> lock(g_slot_mutex);
+    if (g_slot_base[dev] == nullptr) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(gemm_scratch)) != hipSuccess || p == nullptr) return false;
+        g_slot_base[dev] = static_cast<uint8_t*>(p);
+    }
+    int k = -1;
+    for (int i = 0; i < kGemmSlots && k < 0; ++i)
+        if (g_slot_taken[dev][i] && g_slot_owner[dev][i] == st) k = i;
+    for (int i = 0; i < kGemmSlots && k < 0; ++i)
+        if (!g_slot_taken[dev][i]) {
+            g_slot_taken[dev][i] = true;
+            g_slot_owner[dev][i] = st;
+            k = i;
+        }
+    if (k < 0) return false;
+    uint8_t* b = g_slot_base[dev] + (size_t)k * kSlotBytes;
+    out->a = reinterpret_cast<uint16_t*>(b);
+    out->part = reinterpret_cast<float*>(b + kSlotABytes);
+    return true;
+}
+
+// K split for `tiles` one-per-CU workgroups over nsb super-blocks per row:
+// the largest S <= 8 with tiles * S <= CUs whose M x N partials fit the
+// slot, when at least two splits fit (part == nullptr: no split).
+static int ksplit_count(long tiles, int nsb, int M, int N, const float* part) {
+    if (part == nullptr) return 1;
+    const long cus = device_cu_count();
+    int S = 1;
+    for (int s = 2; s <= 8 && s <= nsb; ++s)
+        if (tiles * s <= cus && (size_t)s * M * N * sizeof(float) <= kSlotPartBytes) S = s;
+    return S;
+}
+
+template <int MODE>
+static void launch_reduce(const float* part, int S, int M, int N, float* D, const float* G, hipStream_t st) {
+    const size_t n4 = (size_t)M * N / 4;
+    hipLaunchKernelGGL(rf_gemm_split_reduce_kernel<MODE>, dim3(stream_grid(n4)), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(part), S, n4, D, reinterpret_cast<const float4*>(G));
+}
+
+static void reduce_for(bool acc, const float* G, const float* part, int S, int M, int N, float* D, hipStream_t st) {
+    if (acc)
+        launch_reduce<1>(part, S, M, N, D, nullptr, st);
+    else if (G != nullptr)
+        launch_reduce<2>(part, S, M, N, D, G, st);
+    else
+        launch_reduce<0>(part, S, M, N, D, nullptr, st);
 }
 
 // Q4_K on fp16 activations: 256 x 128 tiles (rf_gemm_q4k_f16a_kernel) where
 // they fill at least three quarters of the CUs, else the eight-wave
 // K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64, or when
-// they come to at most one round of CUs) or 128.
+// they come to at most one round of CUs) or 128, split over K when they
+// leave at least half the CUs idle and `part` (kSlotPartBytes) is given.
 // G: when given, D receives fp16 silu(G) * (A W^T) (the up projection of a
 // SwiGLU whose gate product G [M x N] is already computed)
 template <bool ACC>
 static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
-                              const float* G = nullptr) {
+                              const float* G, float* part) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
@@ -2577,31 +2706,148 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
         else
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
                                M, N, K, nullptr);
+        return hipGetLastError();
+    }
+    const long tiles = (long)((M + 32 * pick - 1) / (32 * pick)) * (N / kQ4sBN);
+    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
+    const KSplit sp{S, S > 1 ? part : nullptr};
+    const unsigned grid = (unsigned)(tiles * S);
+    if (S > 1) {
+        if (pick == 2)
+            hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, false>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w,
+                               nullptr, M, N, K, nullptr, sp);
+        else
+            hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, false>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w,
+                               nullptr, M, N, K, nullptr, sp);
+        reduce_for(ACC, G, part, S, M, N, D, st);
     } else if (pick == 2) {
-        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(((M + 63) / 64) * (N / kQ4sBN)), dim3(kQ4sThreads),
-                           0, st, A, w, D, M, N, K, G);
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w, D, M, N,
+                           K, G, sp);
     } else {
-        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, ACC>), dim3(((M + 127) / 128) * (N / kQ4sBN)),
-                           dim3(kQ4sThreads), 0, st, A, w, D, M, N, K, G);
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, ACC>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w, D, M, N,
+                           K, G, sp);
     }
     return hipGetLastError();
 }
 
+// Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel, 128 x 64 tiles), split
+// over K as gemm_q4_f16 does.  The caller has checked M % 64, N % 64,
+// K % 2048 and 16-byte alignment of A and W.
+template <bool ACC>
+static hipError_t gemm_q6_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
+                              float* part) {
+    const long tiles = (long)((M + kQ6aBM - 1) / kQ6aBM) * (N / kQ6aBN);
+    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    if (S > 1) {
+        hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<false>, dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0, st, A,
+                           w, nullptr, M, N, K, KSplit{S, part});
+        reduce_for(ACC, nullptr, part, S, M, N, D, st);
+    } else {
+        hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<ACC>, dim3((unsigned)tiles), dim3(kQ6aThreads), 0, st, A, w, D, M,
+                           N, K, KSplit{1, nullptr});
+    }
+    return hipGetLastError();
+}
+
+// Stages A (fp32, M x K, 16-byte aligned) as fp16 in the slot, in runs of
+// whole 64-row blocks that fit kSlotABytes, and calls fn(a16, m0, rows) for
+// each run in order (stream-ordered: a run's conversion waits for the
+// previous run's GEMM).  The caller has checked that 64 rows fit.
+template <class F>
+static hipError_t staged_rows(const float* A, int M, int K, const GemmSlot& slot, hipStream_t st, F&& fn) {
+    const int run = (int)std::min<size_t>((size_t)M, kSlotABytes / ((size_t)K * 2) / 64 * 64);
+    for (int m0 = 0; m0 < M; m0 += run) {
+        const int rows = std::min(run, M - m0);
+        const size_t n4 = (size_t)rows * K / 4;
+        hipLaunchKernelGGL(rf_f32_to_f16_kernel, dim3(stream_grid(n4)), dim3(256), 0, st,
+                           reinterpret_cast<const float4*>(A + (size_t)m0 * K), reinterpret_cast<uint2*>(slot.a), n4);
+        const hipError_t e = fn(slot.a, m0, rows);
+        if (e != hipSuccess) return e;
+    }
+    return hipGetLastError();
+}
+
+// The stream's slot when A (K fp16 per row) can be staged in runs of 64 rows.
+static bool staging_slot(hipStream_t st, int K, GemmSlot* slot) {
+    return (size_t)K * 2 * 64 <= kSlotABytes && gemm_slot(st, slot);
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Column segments on fp16 activations (rf_gemm_f16_segs_kernel): up to three
+// weight matrices over one input, each Q4_K or Q6_K with its own output.
+// The caller has checked the shapes and alignment.
+static hipError_t f16_segments(const uint16_t* A, const void* const ws[3], const int q6[3], float* const ds[3],
+                               const int ns[3], int M, int K, hipStream_t st) {
+    F16Segs sg{};
+    const int mtiles = (M + 127) / 128;
+    long total = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (ns[i] == 0) continue;
+        sg.w[i] = static_cast<const uint8_t*>(ws[i]);
+        sg.d[i] = ds[i];
+        sg.n[i] = ns[i];
+        sg.q6[i] = q6[i];
+        sg.tiles[i] = mtiles * (ns[i] / kQ4sBN);
+        total += sg.tiles[i];
+    }
+    if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rf_gemm_f16_segs_kernel, dim3((unsigned)total), dim3(kQ4sThreads), 0, st, A, M, K, sg);
+    return hipGetLastError();
+}
+
+}  // namespace rf
+
+using namespace rf;
+
+// Validation as wmma_gemm_q4_k.hip:207-210 / wmma_gemm_q6_k.hip:220-223,
+// plus 16-byte alignment of A (read as float4) and of Q4_K weights.  A is
+// staged as fp16 (the reference's own rounding of it) and the fp16 tiles
+// run; with no slot for the stream, the fp32 tiles (no K split).
+extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, float* output, int M, int N,
+                                            int K, hipStream_t stream) {
+    if (M <= 0 || N <= 0 || K <= 0) return hipErrorInvalidValue;
+    if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(input) || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    if (staging_slot(stream, K, &slot))
+        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows) {
+            return gemm_q4_f16<false>(a16, weights_q4_k, output + (size_t)m0 * N, rows, N, K, stream, nullptr,
+                                      slot.part);
+        });
+    return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
+}
+
+extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,
+                                            int K, hipStream_t stream) {
+    if (M <= 0 || N <= 0 || K <= 0) return hipErrorInvalidValue;
+    if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(input) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 1u)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    // the fp16 tiles read 16-byte aligned weight rows (K % 2048)
+    if (K % 2048 == 0 && aligned16(weights_q6_k) && staging_slot(stream, K, &slot))
+        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows) {
+            return gemm_q6_f16<false>(a16, weights_q6_k, output + (size_t)m0 * N, rows, N, K, stream, slot.part);
+        });
+    return launch_gemm<true>(input, weights_q6_k, output, M, N, K, stream, single_seg(N));
+}
+
 // fp16 activations (the caller's rounding of A, e.g. in the kernel that
 // produced them): the same operand values as wmma_gemm_q4_k_launch on fp32
-// A, read at half the bytes and without the per-tile conversion.  M % 64,
-// N % 128, K % 256; M need not fill the 256-row tiles.
+// A, read at half the bytes and without the conversion pass.  M % 64,
+// N % 64, K % 256 (the 256 x 128 tiles only when N % 128 == 0); M need not
+// fill the 256-row tiles.
 extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output,
                                               int M, int N, int K, hipStream_t stream) {
     if (input_f16 == nullptr || weights_q4_k == nullptr || output == nullptr) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
         return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
-        return hipErrorInvalidValue;
-    return gemm_q4_f16<false>(input_f16, weights_q4_k, output, M, N, K, stream);
+    if (!aligned16(input_f16) || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    return gemm_q4_f16<false>(input_f16, weights_q4_k, output, M, N, K, stream, nullptr, part);
 }
-
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Gate and up on fp16 activations in one launch, SwiGLU in the epilogue
 // (rf_gemm_q4k_f16a_kernel<1 or 2>: 256 x 128 tiles of 64 gate and the same
@@ -2609,11 +2855,8 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // (out_f16), the values of rf_gemm_q4_k_f16_launch twice and
 // rf_silu_mul(_f16)_on_stream.  M % 64, N % 64, K % 256; input and weights
 // 16-byte aligned.
-extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void* w_gate, const void* w_up,
-                                                     void* out, int out_f16, int M, int N, int K, hipStream_t stream) {
-    if (input_f16 == nullptr || w_gate == nullptr || w_up == nullptr || out == nullptr) return hipErrorInvalidValue;
-    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
-    if (!aligned16(input_f16) || !aligned16(w_gate) || !aligned16(w_up)) return hipErrorInvalidValue;
+static hipError_t q4_f16_swiglu(const uint16_t* input_f16, const void* w_gate, const void* w_up, void* out,
+                                int out_f16, int M, int N, int K, hipStream_t stream) {
     const unsigned tiles = (unsigned)(((M + kF16aBM - 1) / kF16aBM) * (N / 64));
     const uint8_t* wg = static_cast<const uint8_t*>(w_gate);
     const uint8_t* wu = static_cast<const uint8_t*>(w_up);
@@ -2626,50 +2869,60 @@ extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, 
     return hipGetLastError();
 }
 
+extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void* w_gate, const void* w_up,
+                                                     void* out, int out_f16, int M, int N, int K, hipStream_t stream) {
+    if (input_f16 == nullptr || w_gate == nullptr || w_up == nullptr || out == nullptr) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
+    if (!aligned16(input_f16) || !aligned16(w_gate) || !aligned16(w_up)) return hipErrorInvalidValue;
+    return q4_f16_swiglu(input_f16, w_gate, w_up, out, out_f16, M, N, K, stream);
+}
+
 // The up projection of a SwiGLU on fp16 activations, the gate product
 // already computed: out_f16[M x N] = fp16(silu(gate) * (A Wu^T)), the values
 // of rf_gemm_q4_k_f16_launch on w_up followed by rf_silu_mul_f16_on_stream
-// (same tiles, the SwiGLU in their epilogue).  Shapes as
-// rf_gemm_q4_k_f16_launch; gate [M x N] fp32 must not overlap out_f16.
+// (same tiles, the SwiGLU in their epilogue or in the split reduction).
+// Shapes as rf_gemm_q4_k_f16_launch; gate [M x N] fp32, 16-byte aligned,
+// must not overlap out_f16.
 extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f16, const void* w_up,
                                                         const float* gate, uint16_t* out_f16, int M, int N, int K,
                                                         hipStream_t stream) {
     if (input_f16 == nullptr || w_up == nullptr || gate == nullptr || out_f16 == nullptr) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
         return hipErrorInvalidValue;
-    if (!aligned16(input_f16) || !aligned16(w_up)) return hipErrorInvalidValue;
+    if (!aligned16(input_f16) || !aligned16(w_up) || !aligned16(gate) || !aligned16(out_f16))
+        return hipErrorInvalidValue;
     const size_t n = (size_t)M * N;
     const uintptr_t g0 = reinterpret_cast<uintptr_t>(gate), o0 = reinterpret_cast<uintptr_t>(out_f16);
     if (g0 < o0 + 2 * n && o0 < g0 + 4 * n) return hipErrorInvalidValue;   // overlapping buffers
-    return gemm_q4_f16<false>(input_f16, w_up, reinterpret_cast<float*>(out_f16), M, N, K, stream, gate);
+    GemmSlot slot;
+    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    return gemm_q4_f16<false>(input_f16, w_up, reinterpret_cast<float*>(out_f16), M, N, K, stream, gate, part);
 }
 
 // Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): M % 64, N % 64,
 // K % 2048 (weight rows 16-byte aligned); A and the weights 16-byte aligned.
 template <bool ACC>
-static hipError_t gemm_q6_f16(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
-                              int K, hipStream_t stream) {
+static hipError_t q6_f16_checked(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
+                                 int K, hipStream_t stream) {
     if (input_f16 == nullptr || weights_q6_k == nullptr || output == nullptr) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ6aBN) != 0 || (K % 2048) != 0)
         return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 15u))
-        return hipErrorInvalidValue;
-    const int tiles = ((M + kQ6aBM - 1) / kQ6aBM) * (N / kQ6aBN);
-    hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<ACC>, dim3(tiles), dim3(kQ6aThreads), 0, stream, input_f16,
-                       static_cast<const uint8_t*>(weights_q6_k), output, M, N, K);
-    return hipGetLastError();
+    if (!aligned16(input_f16) || !aligned16(weights_q6_k) || !aligned16(output)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    return gemm_q6_f16<ACC>(input_f16, weights_q6_k, output, M, N, K, stream, part);
 }
 
 extern "C" hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output,
                                               int M, int N, int K, hipStream_t stream) {
-    return gemm_q6_f16<false>(input_f16, weights_q6_k, output, M, N, K, stream);
+    return q6_f16_checked<false>(input_f16, weights_q6_k, output, M, N, K, stream);
 }
 
 // inout[M x N] += fp16(A) * fp16(dequant W)^T: each output read and written
-// once, after its fp32 sum (no K split: reproducible bit for bit).
+// once, after its fp32 sum (reproducible bit for bit).
 extern "C" hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k,
                                                          float* inout, int M, int N, int K, hipStream_t stream) {
-    return gemm_q6_f16<true>(input_f16, weights_q6_k, inout, M, N, K, stream);
+    return q6_f16_checked<true>(input_f16, weights_q6_k, inout, M, N, K, stream);
 }
 
 // inout[M x N] += the product of rf_gemm_q4_k_f16_launch, on the K-sliced
@@ -2679,18 +2932,10 @@ extern "C" hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f
     if (input_f16 == nullptr || weights_q4_k == nullptr || inout == nullptr) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % kQ4sBN) != 0 || (K % kQK) != 0)
         return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(input_f16) & 15u) || (reinterpret_cast<uintptr_t>(weights_q4_k) & 15u))
-        return hipErrorInvalidValue;
-    return gemm_q4_f16<true>(input_f16, weights_q4_k, inout, M, N, K, stream);
-}
-
-extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N,
-                                            int K, hipStream_t stream) {
-    if (M <= 0 || N <= 0 || K <= 0) return hipErrorInvalidValue;
-    if ((M % 64) != 0 || (N % 64) != 0 || (K % kQK) != 0) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(input) & 15u) || (reinterpret_cast<uintptr_t>(weights_q6_k) & 1u))
-        return hipErrorInvalidValue;
-    return launch_gemm<true>(input, weights_q6_k, output, M, N, K, stream, single_seg(N));
+    if (!aligned16(input_f16) || !aligned16(weights_q4_k) || !aligned16(inout)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    return gemm_q4_f16<true>(input_f16, weights_q4_k, inout, M, N, K, stream, nullptr, part);
 }
 
 // Shapes the segmented / accumulating launches take: whole 256-column tiles,
@@ -2699,9 +2944,11 @@ extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weig
 template <bool IS_Q6>
 static bool seg_shape_ok(const float* A, int M, int K) {
     if (M <= 0 || K <= 0 || M % 64 || K % (IS_Q6 ? 2048 : 512)) return false;
-    return (reinterpret_cast<uintptr_t>(A) & 15u) == 0;
+    return aligned16(A);
 }
 
+// Staged fp16 column segments; the fp32 v7 segments when the stream has
+// no slot (or a Q6_K weight matrix is only 2-byte aligned).
 template <bool IS_Q6>
 static hipError_t gemm_segments(const float* A, const void* w0, const void* w1, const void* w2, float* d0,
                                 float* d1, float* d2, int M, int n0, int n1, int n2, int K, hipStream_t st) {
@@ -2709,10 +2956,24 @@ static hipError_t gemm_segments(const float* A, const void* w0, const void* w1, 
     if (n0 % 256 || n1 % 256 || n2 % 256 || (n1 == 0 && n2 > 0)) return hipErrorInvalidValue;
     if ((n1 && (!w1 || !d1)) || (n2 && (!w2 || !d2))) return hipErrorInvalidValue;
     const uintptr_t wal = IS_Q6 ? 1u : 15u;
-    for (const void* w : {w0, w1, w2})
+    bool w_al16 = true;
+    for (const void* w : {w0, w1, w2}) {
         if (w && (reinterpret_cast<uintptr_t>(w) & wal)) return hipErrorInvalidValue;
+        if (w && !aligned16(w)) w_al16 = false;
+    }
     for (const float* d : {d0, d1, d2})
         if (d && !aligned16(d)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    if (w_al16 && staging_slot(st, K, &slot)) {
+        const void* ws[3] = {w0, n1 ? w1 : nullptr, n2 ? w2 : nullptr};
+        const int q6[3] = {IS_Q6, IS_Q6, IS_Q6};
+        const int ns[3] = {n0, n1, n2};
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+            float* ds[3] = {d0 + (size_t)m0 * n0, n1 ? d1 + (size_t)m0 * n1 : nullptr,
+                            n2 ? d2 + (size_t)m0 * n2 : nullptr};
+            return f16_segments(a16, ws, q6, ds, ns, rows, K, st);
+        });
+    }
     GemmSegs sg{};
     sg.w1 = static_cast<const uint8_t*>(w1);
     sg.w2 = static_cast<const uint8_t*>(w2);
@@ -2727,6 +2988,13 @@ template <bool IS_Q6>
 static hipError_t gemm_accumulate(const float* A, const void* w, float* D, int M, int N, int K, hipStream_t st) {
     if (!seg_shape_ok<IS_Q6>(A, M, K) || !w || !D || N <= 0 || N % 256 || !aligned16(D)) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(w) & (IS_Q6 ? 1u : 15u)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    if (aligned16(w) && staging_slot(st, K, &slot))
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+            float* d = D + (size_t)m0 * N;
+            return IS_Q6 ? gemm_q6_f16<true>(a16, w, d, rows, N, K, st, slot.part)
+                         : gemm_q4_f16<true>(a16, w, d, rows, N, K, st, nullptr, slot.part);
+        });
     GemmSegs sg = single_seg(N);
     sg.accum = 1;
     return launch_gemm<IS_Q6>(A, w, D, M, N, K, st, sg);
@@ -2759,29 +3027,19 @@ extern "C" hipError_t rf_gemm_qk_f16_segments_launch(const uint16_t* input_f16, 
     if (input_f16 == nullptr || !aligned16(input_f16) || M <= 0 || M % 64 || K <= 0 || K % kQK)
         return hipErrorInvalidValue;
     if (n0 <= 0 || n1 < 0 || n2 < 0 || (n1 == 0 && n2 > 0)) return hipErrorInvalidValue;
-    F16Segs sg{};
     const void* ws[3] = {w0, w1, w2};
     float* ds[3] = {out0, out1, out2};
     const int ns[3] = {n0, n1, n2}, ts[3] = {type0, type1, type2};
-    const int mtiles = (M + 127) / 128;
-    long total = 0;
+    int q6[3] = {0, 0, 0};
     for (int i = 0; i < 3; ++i) {
         if (ns[i] == 0) continue;
         if (ns[i] % kQ4sBN || ws[i] == nullptr || ds[i] == nullptr || !aligned16(ws[i]) || !aligned16(ds[i]))
             return hipErrorInvalidValue;
         if (ts[i] != kQ4KType && ts[i] != kQ6KType) return hipErrorInvalidValue;
         if (ts[i] == kQ6KType && K % 2048) return hipErrorInvalidValue;
-        sg.w[i] = static_cast<const uint8_t*>(ws[i]);
-        sg.d[i] = ds[i];
-        sg.n[i] = ns[i];
-        sg.q6[i] = ts[i] == kQ6KType;
-        sg.tiles[i] = mtiles * (ns[i] / kQ4sBN);
-        total += sg.tiles[i];
+        q6[i] = ts[i] == kQ6KType;
     }
-    if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rf_gemm_f16_segs_kernel, dim3((unsigned)total), dim3(kQ4sThreads), 0, stream, input_f16, M, K,
-                       sg);
-    return hipGetLastError();
+    return f16_segments(input_f16, ws, q6, ds, ns, M, K, stream);
 }
 
 extern "C" hipError_t rf_gemm_q4_k_accumulate_launch(const float* input, const void* weights_q4_k, float* inout,
@@ -2794,6 +3052,9 @@ extern "C" hipError_t rf_gemm_q6_k_accumulate_launch(const float* input, const v
     return gemm_accumulate<true>(input, weights_q6_k, inout, M, N, K, stream);
 }
 
+// Gate/up pairs with SwiGLU in the epilogue: Q4_K staged as fp16 through the
+// paired 256 x 128 tiles (rf_gemm_q4k_f16a_kernel<1, 2>); Q6_K (and Q4_K
+// without a slot) on the fp32 v7 pair tiles.
 template <bool IS_Q6>
 static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, void* D, int M, int N, int K,
                               hipStream_t st, bool f16_out) {
@@ -2801,6 +3062,14 @@ static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, vo
         return hipErrorInvalidValue;
     const uintptr_t wal = IS_Q6 ? 1u : 15u;
     if ((reinterpret_cast<uintptr_t>(wg) & wal) || (reinterpret_cast<uintptr_t>(wu) & wal)) return hipErrorInvalidValue;
+    GemmSlot slot;
+    if (!IS_Q6 && staging_slot(st, K, &slot)) {
+        const size_t esz = f16_out ? 2 : 4;
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+            return q4_f16_swiglu(a16, wg, wu, static_cast<uint8_t*>(D) + (size_t)m0 * N * esz, f16_out, rows, N, K,
+                                 st);
+        });
+    }
     GemmSegs sg = single_seg(2 * N);
     sg.w1 = static_cast<const uint8_t*>(wu);
     sg.pair = f16_out ? 2 : 1;

@@ -1,14 +1,16 @@
-"""GPU parity of the two prefill GEMM launchers that have no reference
+"""GPU parity of the prefill GEMM launchers that have no reference
 counterpart: several weight matrices as column segments of one launch
-(rf_gemm_q*_k_segments_launch), D += product (rf_gemm_q*_k_accumulate_launch)
-and gate/up with SwiGLU in the epilogue (rf_gemm_q*_k_swiglu_launch).
+(rf_gemm_q*_k_segments_launch, rf_gemm_qk_f16_segments_launch), D += product
+(rf_gemm_q*_k_accumulate_launch) and gate/up with SwiGLU in the epilogue
+(rf_gemm_q*_k_swiglu_launch).
 
 Each segment / accumulated product is checked against the oracle's float64
 product of the fp16-rounded operands at the GEMM bar
   |D - D_ref| <= 2e-3 * |D_ref| + 1e-5 * max|D_ref|   (plus 1e-6 * |R| for D = R + product),
-and, where the launch takes no K split, bit for bit against the single-GEMM
-launcher (the per-element arithmetic is the same: one fp32 add of R for the
-accumulating form).
+and bit for bit against the launch that runs the same tiles: a segment
+against its matrix alone on fp16 activations rounded on the host (the fp32
+launchers stage A as fp16 first), an accumulated product against R plus the
+single-GEMM launcher (the same tiles and K split; one fp32 add of R).
 """
 import ctypes
 
@@ -51,33 +53,45 @@ def _segments(rf, fmt, a_dev, ws, m, ns, k):
     return [G.host(d).reshape(m, n) for d, n in zip(ds, ns)]
 
 
-# (fmt, M, segment widths, K, K split taken by the fused launch)
-@pytest.mark.parametrize("fmt,m,ns,k,split", [
-    ("q4_k", 512, (1024, 256, 256), 512, False),    # 64-row tiles, one K pass (Q/K/V shape, narrowed)
-    ("q4_k", 64, (512, 256, 256), 1024, True),      # split-K: every segment zeroed, then atomics
-    ("q4_k", 128, (768, 256), 512, False),          # two segments (V in another type)
-    ("q6_k", 128, (512, 256), 2048, True),
-    ("q6_k", 256, (256, 256, 512), 2048, True),
+def _f16_alone(rf, fmt, a16_dev, w, m, n, k):
+    # one matrix through the fp16-activation segments launcher
+    dw = G.to_dev(w)
+    d = G.empty(m * n, torch.float32)
+    z = ctypes.c_void_p(0)
+    t = 12 if fmt == "q4_k" else 14
+    G.call(rf.rf_gemm_qk_f16_segments_launch, G.ptr(a16_dev), G.ptr(dw), z, z, t, 12, 12, G.ptr(d), z, z, m, n, 0, 0,
+           k)
+    return G.host(d).reshape(m, n)
+
+
+@pytest.mark.parametrize("fmt,m,ns,k", [
+    ("q4_k", 512, (1024, 256, 256), 512),     # Q/K/V shape, narrowed
+    ("q4_k", 64, (512, 256, 256), 1024),      # one 64-row M tile
+    ("q4_k", 128, (768, 256), 512),           # two segments (V in another type)
+    ("q6_k", 128, (512, 256), 2048),
+    ("q6_k", 256, (256, 256, 512), 2048),
 ])
-def test_segments_match_oracle_and_single(rf, dev, fmt, m, ns, k, split):
+def test_segments_match_oracle_and_single(rf, dev, fmt, m, ns, k):
     a = synth.activations(k, seed=m + k, m=m)
     ws = [synth.weights(fmt, n, k, seed=10 + i) for i, n in enumerate(ns)]
     da = G.to_dev(a)
+    a16 = G.to_dev(a.astype(np.float16).view(np.int16))
     got = _segments(rf, fmt, da, ws, m, ns, k)
-    for i, (g, w, n) in enumerate(zip(got, ws, ns)):
+    again = _segments(rf, fmt, da, ws, m, ns, k)
+    for i, (g, g2, w, n) in enumerate(zip(got, again, ws, ns)):
         _check(g, O.gemm(fmt, a, w, m, n, k), f"{fmt} segment {i} {m}x{n}x{k}")
-        if not split:
-            np.testing.assert_array_equal(g, _single(rf, fmt, da, w, m, n, k))
+        np.testing.assert_array_equal(g, g2)                               # the same bits on every run
+        np.testing.assert_array_equal(g, _f16_alone(rf, fmt, a16, w, m, n, k))
 
 
-@pytest.mark.parametrize("fmt,m,n,k,split", [
-    ("q4_k", 64, 256, 512, False),       # v7, 64-row tiles
-    ("q4_k", 256, 14336, 512, False),    # 128 x 128 shared-dequantisation tiles
-    ("q4_k", 128, 512, 2048, True),      # split-K adds onto the caller's values
-    ("q6_k", 256, 512, 4096, True),
-    ("q6_k", 512, 1024, 2048, True),
+@pytest.mark.parametrize("fmt,m,n,k", [
+    ("q4_k", 64, 256, 512),       # 64-row K-sliced tiles, K split over 2 workgroups
+    ("q4_k", 256, 14336, 512),    # 128-row tiles, no K split
+    ("q4_k", 128, 512, 2048),     # K split over 8 workgroups, added onto the caller's values
+    ("q6_k", 256, 512, 4096),
+    ("q6_k", 512, 1024, 2048),
 ])
-def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k, split):
+def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k):
     a = synth.activations(k, seed=3 * m + n, m=m)
     w = synth.weights(fmt, n, k, seed=k + 2)
     r = np.random.default_rng(m + n).standard_normal((m, n)).astype(np.float32) * 4.0
@@ -86,8 +100,7 @@ def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k, split):
     G.call(fn, G.ptr(da), G.ptr(dw), G.ptr(dr), m, n, k)
     got = G.host(dr).reshape(m, n)
     _check(got, O.gemm(fmt, a, w, m, n, k), f"{fmt} accumulate {m}x{n}x{k}", base=r)
-    if not split:
-        np.testing.assert_array_equal(got, r + _single(rf, fmt, da, w, m, n, k))
+    np.testing.assert_array_equal(got, r + _single(rf, fmt, da, w, m, n, k))
 
 
 @pytest.mark.parametrize("fmt,m,n,k", [
@@ -199,10 +212,9 @@ def test_rejections(rf, dev):
     (64, [("q6_k", 192), ("q4_k", 64)], 2048),                        # two segments, one 64-row M tile
 ])
 def test_f16_segments_mixed_types(rf, dev, m, segs, k):
-    # each segment bit for bit its own fp16-activation launcher on the same
-    # 128 x 64 tiles (Q4_K: the accumulating launcher onto zeros, whose
-    # K-sliced tiles add the same partials in the same order; Q6_K: the plain
-    # launcher), and within the GEMM bar of the oracle
+    # each segment bit for bit its matrix alone through the same launcher
+    # (the same 128 x 64 tiles: segment routing moves no bits), and within
+    # the GEMM bar of the oracle
     a = torch.from_numpy(synth.activations(k, seed=m + 3, m=m)).to(torch.bfloat16).float().numpy()
     da = G.to_dev(a.astype(np.float16).view(np.int16))
     ws = [synth.weights(f, n, k, seed=30 + i) for i, (f, n) in enumerate(segs)]
@@ -214,13 +226,7 @@ def test_f16_segments_mixed_types(rf, dev, m, segs, k):
            *([G.ptr(t) for t in ds] + [z] * (3 - len(segs))), m, *([n for _, n in segs] + [0] * (3 - len(segs))), k)
     for i, ((f, n), w, dw, d) in enumerate(zip(segs, ws, dws, ds)):
         got = G.host(d).reshape(m, n)
-        if f == "q4_k":
-            ref = G.empty(m * n, torch.float32).zero_()
-            G.call(rf.rf_gemm_q4_k_f16_accumulate_launch, G.ptr(da), G.ptr(dw), G.ptr(ref), m, n, k)
-        else:
-            ref = G.empty(m * n, torch.float32)
-            G.call(rf.rf_gemm_q6_k_f16_launch, G.ptr(da), G.ptr(dw), G.ptr(ref), m, n, k)
-        np.testing.assert_array_equal(got, G.host(ref).reshape(m, n))
+        np.testing.assert_array_equal(got, _f16_alone(rf, f, da, w, m, n, k))
         _check(got, O.gemm(f, a, w, m, n, k), f"f16 segment {i} {f} {m}x{n}x{k}")
 
 
@@ -296,6 +302,33 @@ def test_q4k_f16_swiglu_up(rf, dev, m, n, k):
     ref = G.empty(m * n, torch.int16)
     G.call(rf.rf_silu_mul_f16_on_stream, G.ptr(gate), G.ptr(u), G.ptr(ref), m * n)
     np.testing.assert_array_equal(G.host(out), G.host(ref))
+
+
+def test_q4k_f16_swiglu_up_full_k_oracle(rf, dev):
+    # the up GEMM the Qwen3-8B prefill runs at 512 tokens (M = 512, N = 12288,
+    # K = 4096: 256 x 128 tiles, 64 chunks of K) against the oracle:
+    # out = fp16(silu(g) * u), u the float64 product of the fp16 operands.
+    # Bar per element: the GEMM bar on u (2e-3 |u| + 2e-5 S, S the sum of the
+    # product magnitudes u adds up) carried through the factor |silu(g)|, plus
+    # one fp16 rounding of the output (half an ulp: 2^-11 |out| relative,
+    # 2^-25 absolute below the normal range)
+    m, n, k = 512, 12288, 4096
+    a = torch.from_numpy(synth.activations(k, seed=51, m=m)).to(torch.bfloat16).float().numpy()
+    wu = synth.weights("q4_k", n, k, seed=52)
+    g = (np.random.default_rng(53).standard_normal(m * n) * 3).astype(np.float32)
+    da, dwu, dg = G.to_dev(a.astype(np.float16).view(np.int16)), G.to_dev(wu), G.to_dev(g)
+    out = G.empty(m * n, torch.int16)
+    G.call(rf.rf_gemm_q4_k_f16_swiglu_up_launch, G.ptr(da), G.ptr(dwu), G.ptr(dg), G.ptr(out), m, n, k)
+    got = G.host(out).view(np.float16).astype(np.float64).reshape(m, n)
+    u = O.gemm("q4_k", a, wu, m, n, k)
+    S = O.gemm_abs("q4_k", a, wu, m, n, k)
+    g64 = g.astype(np.float64).reshape(m, n)
+    silu = g64 / (1.0 + np.exp(-g64))
+    ref = silu * u
+    tol = np.abs(silu) * (2e-3 * np.abs(u) + 2e-5 * S) + 2.0 ** -11 * np.abs(ref) + 2.0 ** -25
+    worst = (np.abs(got - ref) / tol).max()
+    print(f"q4_k f16 swiglu_up {m}x{n}x{k}: worst={worst:.3f}", flush=True)
+    assert worst <= 1.0
 
 
 def test_q4k_f16_swiglu_up_rejections(rf, dev):

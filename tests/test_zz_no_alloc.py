@@ -47,7 +47,7 @@ def test_noalloc_attention_matches_workspace_entry_point(rf, dev):
 
 
 def test_noalloc_attention_rejects_sizes_beyond_the_array(rf, dev):
-    dq = G.empty(128 * 256, torch.float32)
+    dq = G.to_dev(np.zeros(128 * 256, np.float32))      # finite q (fresh memory may hold anything)
     dkc = G.empty(16 * 256, torch.int16)
     dlen = G.to_dev(np.array([4], np.int32))
     # 128 heads x (256 + 4) = 33280 > 16640
