@@ -386,6 +386,44 @@ def bench_gemm(lib, torch):
     return res
 
 
+def bench_mfma_peak(lib, torch):
+    """Sustained v_mfma_f32_32x32x16_f16 rate on this MI355X: one 256-thread
+    workgroup per CU, every wave issuing 8 independent MFMA chains, on fp16
+    operands drawn N(0,1) (the prefill GEMMs' activation distribution) and
+    on zeros (least switching activity), each timed over ~3 ms with HIP events
+    after an untimed ramp.  Reported beside the 2.5 PFLOP/s dense fp16 figure
+    the GEMM fractions are priced against."""
+    dev = torch.device("cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = torch.empty(cus * 256, device=dev)
+    res = {"instruction": "v_mfma_f32_32x32x16_f16", "workgroups": cus, "waves_per_simd": 1,
+           "published_dense_fp16_tflops": FP16_MFMA_PEAK_TFLOPS}
+    g = torch.Generator(device="cpu")
+    g.manual_seed(0)
+    for name, a in (("normal", torch.randn(4096, generator=g).half()), ("zeros", torch.zeros(4096).half())):
+        a = a.to(dev)
+        iters = 20000
+
+        def run():
+            rc = lib.rf_mfma_peak_launch(vp(a), vp(out), cus, iters, st)
+            if rc:
+                raise RuntimeError(f"mfma peak launch failed {rc}")
+
+        ramp(torch, run)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        s = e0.elapsed_time(e1) / 1000 / 3
+        flops = cus * 4 * iters * 8 * 32768
+        res[f"{name}_operands_tflops"] = round(flops / s / 1e12, 1)
+        res[f"{name}_frac_published"] = round(flops / s / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)
+    return res
+
+
 def gemm_pmc(lib, torch):
     """Ten untimed launches of each M = 512 prefill GEMM (Q4_K 14336x4096 and
     Q6_K 4096x14336, each on fp32 and on fp16 activations), for counter collection
@@ -578,6 +616,7 @@ def main():
     out["gemv_4096"] = bench_gemv_cfg0(lib, torch, max(args.steps, 100))
     if not args.no_gemm:
         out["prefill_gemm"] = bench_gemm(lib, torch)
+        out["mfma_peak"] = bench_mfma_peak(lib, torch)
     if not args.no_stream:
         out["decode_stream"] = bench_decode_stream(lib, torch, args.stream_tokens)
     if not args.no_e2e:

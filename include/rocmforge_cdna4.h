@@ -95,7 +95,16 @@ hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* 
  * hip_kernels/wmma/wmma_gemm_q4_k.hip:201 and wmma_gemm_q6_k.hip:212 (Rust
  * decl src/gpu/kernels/wmma.rs:65-83).  NOTE the argument order: input
  * first.  D[M x N] = fp16(A[M x K]) * fp16(dequant W[N x K])^T, fp32 out.
- * M % 64 == 0, N % 64 == 0, K % 256 == 0 (callers pad M to 64 rows). */
+ * M % 64 == 0, N % 64 == 0, K % 256 == 0 (callers pad M to 64 rows).
+ * A is rounded to fp16 (__float2half's value) by a pass of its own into
+ * library-owned device memory (a file-scope array: 4 slots of 40 MB per GPU,
+ * one per stream, claimed on a stream's first launch) and the fp16
+ * tiles of rf_gemm_q*_k_f16_launch run on it; small launches split K over
+ * workgroups and add the partial tiles in a fixed order, so every output is
+ * the same sum on every run.  Launches on one stream share its slot (stream
+ * order); a fifth stream on a GPU gets the fp32-activation tiles instead
+ * (same values up to summation order).  Q6_K takes the fp16 tiles when
+ * K % 2048 == 0 and the weights are 16-byte aligned. */
 hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, float* output, int M, int N, int K,
                                  hipStream_t stream);
 hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, float* output, int M, int N, int K,
@@ -106,9 +115,11 @@ hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weights_q6_k, f
  * caller whose producing kernel already rounded A to fp16 (bit patterns as
  * uint16_t, row-major [M][K]).  Same operand values as
  * wmma_gemm_q4_k_launch(fp32 A), so the same products; A is read at half
- * the bytes and not converted per tile.  256 x 128 tiles where they fill
- * three quarters of the CUs (M = 512 at N = 14336), else 64- or 128-row x
- * 64-column tiles with K split over the waves of a workgroup.  M % 64 == 0,
+ * the bytes and not converted.  256 x 128 tiles where they fill three
+ * quarters of the CUs (M = 512 at N = 14336; they need N % 128 == 0), else
+ * 64- or 128-row x 64-column tiles with K split over the waves of a
+ * workgroup, and over workgroups (partials in the stream's slot, added in
+ * split order) when the tiles leave half the CUs idle.  M % 64 == 0,
  * N % 64 == 0, K % 256 == 0, input and weights 16-byte aligned. */
 hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weights_q4_k, float* output, int M, int N,
                                    int K, hipStream_t stream);
@@ -117,16 +128,12 @@ hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const void* weight
  * GEMM, wmma_gemm_q6_k.hip:93-100): the Q6_K GEMM on fp16 activations, same
  * contract as rf_gemm_q4_k_f16_launch -- the operand values of
  * wmma_gemm_q6_k_launch(fp32 A).  128 x 64 tiles with K split over the
- * waves of a workgroup: meant for M >= 256 at N = 4096 (one tile per CU at
- * M = 512).  M % 64 == 0, N % 64 == 0, K % 2048 == 0, input and weights
+ * waves of a workgroup (one tile per CU at M = 512, N = 4096), and over
+ * workgroups as rf_gemm_q4_k_f16_launch when the tiles leave half the CUs
+ * idle.  M % 64 == 0, N % 64 == 0, K % 2048 == 0, input, weights and output
  * 16-byte aligned. */
 hipError_t rf_gemm_q6_k_f16_launch(const uint16_t* input_f16, const void* weights_q6_k, float* output, int M, int N,
                                    int K, hipStream_t stream);
-/* No counterpart: inout[M x N] += the product of rf_gemm_q6_k_f16_launch (the
- * reference's prefill adds residuals with gpu_add).  Each output is read and
- * written once after its fp32 sum, so the result is inout + that launch's
- * output bit for bit.  Same shape rules.  Used for the FFN down projection of
- * a prefill, into the residual stream. */
 /* No counterpart: inout[M x N] += the product of rf_gemm_q4_k_f16_launch, each
  * output read and written once after its fp32 sum (inout + that product bit
  * for bit).  M % 64 == 0, N % 64 == 0, K % 256 == 0, input and weights 16-byte
@@ -157,9 +164,15 @@ hipError_t rf_gemm_q4_k_f16_swiglu_launch(const uint16_t* input_f16, const void*
  * values of rf_gemm_q4_k_f16_launch on w_up followed by
  * rf_silu_mul_f16_on_stream, with the SwiGLU in the GEMM's store (the
  * reference runs the GEMM and a SwiGLU kernel, src/gpu/forward.rs:2327).
- * Shapes as rf_gemm_q4_k_f16_launch; gate must not overlap out_f16. */
+ * Shapes as rf_gemm_q4_k_f16_launch; gate and out_f16 16-byte aligned and
+ * not overlapping. */
 hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f16, const void* w_up, const float* gate,
                                              uint16_t* out_f16, int M, int N, int K, hipStream_t stream);
+/* No counterpart: inout[M x N] += the product of rf_gemm_q6_k_f16_launch (the
+ * reference's prefill adds residuals with gpu_add).  Each output is read and
+ * written once after its fp32 sum, so the result is inout + that launch's
+ * output bit for bit.  Same shape rules.  Used for the FFN down projection of
+ * a prefill, into the residual stream. */
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
 
@@ -169,7 +182,9 @@ hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const v
  * for i = 0..2, each output row-major with width n_i (n1 = 0 and n2 = 0
  * drop segments; all n_i % 256 == 0).  The per-element arithmetic is the
  * single GEMM's.  K % 512 == 0 (Q6_K: K % 2048 == 0), M % 64 == 0, A and
- * outputs 16-byte aligned.  Used for the Q/K/V projections of a prefill. */
+ * outputs 16-byte aligned.  A is staged as fp16 as for wmma_gemm_q4_k_launch
+ * and rf_gemm_qk_f16_segments_launch runs on it.  Used for the Q/K/V
+ * projections of a prefill. */
 hipError_t rf_gemm_q4_k_segments_launch(const float* input, const void* w0, const void* w1, const void* w2,
                                         float* out0, float* out1, float* out2, int M, int n0, int n1, int n2, int K,
                                         hipStream_t stream);
@@ -485,6 +500,30 @@ hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const float* d_q, con
                                              float* d_workspace,
                                              const size_t workspace_bytes, hipStream_t stream);
 
+/* No counterpart (the reference's decode attention,
+ * hip_kernels/attention.hip:950, has no bound on the sequence): the two
+ * launchers above for a caller that bounds it, seq <= max_seq (e.g. the KV
+ * cache length).  With max_seq <= 2048 one workgroup per query head runs
+ * (16 waves split the positions and merge their partials through LDS in wave
+ * order): no workspace (d_workspace may then be null), one launch instead of
+ * the split kernel and its merge, any GQA group.  Beyond 2048 the split path
+ * with the workspace as above.  Results within fp32 rounding of the
+ * unbounded launchers (another summation order). */
+hipError_t rf_flash_attn_decode_state_bounded(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                              const uint16_t* d_v_cache, const int* d_seq_len, const int num_heads,
+                                              const int num_kv_heads, const int head_dim, const float scale,
+                                              const int max_seq, float* d_workspace, const size_t workspace_bytes,
+                                              hipStream_t stream);
+hipError_t rf_attn_decode_qk_norm_rope_state_bounded(float* d_out, const float* d_q, const float* d_k,
+                                                     const float* d_v, const float* d_q_norm, const float* d_k_norm,
+                                                     uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_state,
+                                                     const int num_heads, const int num_kv_heads, const int head_dim,
+                                                     const float eps, const float theta_base, const int neox,
+                                                     const float* d_freq_scale, const float* d_theta,
+                                                     const float* d_cos_sin, const float scale, const int max_seq,
+                                                     float* d_workspace, const size_t workspace_bytes,
+                                                     hipStream_t stream);
+
 /* hip_kernels/elementwise.hip:615, :651 -- index of the maximum of d_input[n]
  * (ties: the larger index; NaN never wins); partial buffers hold ceil(n / 1024). */
 hipError_t gpu_argmax_f32_on_stream(const float* d_input, float* d_partial_values, int* d_partial_indices,
@@ -576,6 +615,14 @@ hipError_t rf_q8_0_quantize_launch(const float* input, uint16_t* d_out, int8_t* 
  * output row n and 32-element sub-block j. */
 hipError_t rf_q4_k_q8_int_dots_launch(const void* weights_q4_k, const float* input, int32_t* int_dot, int n_rows,
                                       int ncols_dst, hipStream_t stream);
+
+/* ---- Measurement (no reference counterpart) -----------------------------
+ * MFMA peak microbenchmark: grid workgroups of 256 threads, each wave issuing
+ * iters x 8 independent v_mfma_f32_32x32x16_f16 on operands read from
+ * a[0 .. 4096) (fp16 bit patterns: the data decides the switching activity
+ * and with it the clock); out[block * 256 + thread] receives a checksum of
+ * the accumulators.  FLOPs = grid * 4 * iters * 8 * 32768. */
+hipError_t rf_mfma_peak_launch(const uint16_t* a, float* out, int grid, int iters, hipStream_t stream);
 
 /* Library identification string. */
 const char* rf_library_version(void);

@@ -76,6 +76,9 @@ SIGNATURES = {
     "gpu_flash_attn_decode_strided_multi_head_state": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "rf_flash_attn_decode_ws": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp],
     "rf_flash_attn_decode_state_ws": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp],
+    "rf_flash_attn_decode_state_bounded": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _sz, _vp],
+    "rf_attn_decode_qk_norm_rope_state_bounded": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _f,
+                                                  _i, _vp, _vp, _vp, _f, _i, _vp, _sz, _vp],
     "rf_flash_attn_decode_state_noalloc": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp],
     "gpu_argmax_f32_on_stream": [_vp, _vp, _vp, _vp, _i, _vp],
     "gpu_argmax_f32": [_vp, _vp, _vp, _vp, _i],
@@ -95,6 +98,7 @@ SIGNATURES = {
     "rf_attention_prefill_gqa_causal_f16_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "rf_q8_0_quantize_launch": [_vp, _vp, _vp, _vp, _i, _vp],
     "rf_q4_k_q8_int_dots_launch": [_vp, _vp, _vp, _i, _i, _vp],
+    "rf_mfma_peak_launch": [_vp, _vp, _i, _i, _vp],
 }
 
 _LIB = None

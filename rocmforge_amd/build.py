@@ -18,7 +18,8 @@ LIB = PKG / "librocmforge_cdna4.so"
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-SOURCES = ["runtime.hip", "gemv_q4k.hip", "gemv_q6k.hip", "gemm_qk.hip", "model_ops.hip", "dispatch.cpp"]
+SOURCES = ["runtime.hip", "gemv_q4k.hip", "gemv_q6k.hip", "gemm_qk.hip", "model_ops.hip", "mfma_peak.hip",
+           "dispatch.cpp"]
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -101,7 +101,7 @@ __global__ void rf_rope_cos_sin_kernel(float2* __restrict__ cs, int positions, i
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long)positions * half) return;
     const int pos = (int)(idx / half), i = (int)(idx % half);
-    const float a = (float)pos * rope_theta(i, d, base, nullptr, freq_scale);
+    const float a = (float)pos * rope_theta(i, d, base, tab, freq_scale);
     cs[idx] = make_float2(cosf(a), sinf(a));
 }
 
@@ -812,6 +812,185 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
     }
 }
 
+// One workgroup per query head (the path for caches of up to
+// kHeadPathMaxSeq positions): kHeadWaves waves split the positions, each
+// keeping an online (m, l, acc) over its own slots, and the workgroup merges
+// the wave partials through LDS in wave order -- no workspace, no second
+// launch.  Slot s = positions [PPW s, PPW s + PPW) (one load instruction of
+// K and one of V) goes to wave s mod kHeadWaves; a wave issues the K and V
+// loads of kHeadBatch slots before the first use.  The query heads of a KV
+// group read the same K/V rows (L2 hits after the first).
+// QK: the decode step folded in, as in rf_attn_split_kernel: every wave
+// normalises and rotates its query head in registers; the wave whose slot
+// holds the new position (seq - 1) normalises and rotates the new K row
+// itself and uses it (and the new V row) from registers in place of the
+// cache, and in the workgroup of the group's first query head it writes
+// both rows to the caches (no workgroup reads them from memory here).
+constexpr int kHeadWaves = 16;
+constexpr int kHeadBatch = 4;       // 16 waves of 1024 threads: <= 128 VGPRs, no spills at 4 slots per batch
+constexpr int kHeadPathMaxSeq = 2048;
+
+// The arithmetic is spelled out (__fmaf_rn, __fmul_rn) so that the QK and
+// plain instantiations, and every kernel built from this code, contract
+// the same way and give the same bits.
+template <int LPP, bool QK>
+__global__ __launch_bounds__(64 * kHeadWaves) void rf_attn_head_kernel(const float* __restrict__ q,
+                                                                       const __half* kc, const __half* vc,
+                                                                       const int* __restrict__ len_ptr, int len0,
+                                                                       int nh, int nkv, float scale, QkStep qk,
+                                                                       float* __restrict__ out) {
+    constexpr int D = LPP * 8;
+    constexpr int PPW = 64 / LPP;
+    __shared__ __align__(16) float2 lcs[QK ? kHeadWaves : 1][QK ? D / 2 : 2];
+    __shared__ __align__(16) float wacc[kHeadWaves][D];
+    __shared__ float wm[kHeadWaves], wl[kHeadWaves];
+    const int seq = len_ptr ? *len_ptr : len0;
+    const int group = nh / nkv;
+    // workgroup b runs on XCD b % 8: the query heads of one KV head go to one
+    // XCD (its L2 then serves their common K/V rows) when nkv % 8 == 0
+    const int b = blockIdx.x;
+    const int head = nkv % 8 == 0 ? ((b % 8) + 8 * ((b / 8) / group)) * group + (b / 8) % group : b;
+    const int kvh = head / group;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPP, grp = lane / LPP;
+    const size_t row = (size_t)nkv * D;
+    const __half* kh = kc + (size_t)kvh * D + 8 * sub;
+    const __half* vh = vc + (size_t)kvh * D + 8 * sub;
+    const int nslots = (seq + PPW - 1) / PPW;
+    const int pos = seq - 1;
+    const bool pos_wave = QK && (pos / PPW) % kHeadWaves == wave;      // wave-uniform
+    float qv[8], kx[8], vx[8], gq[8], gk[8];
+    float2 cv[8];
+    load8(q + (size_t)head * D + 8 * sub, qv);
+    if constexpr (QK) {
+        if (qk.q_norm != nullptr) load8(qk.q_norm + 8 * sub, gq);
+        if (pos_wave) {
+            load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
+            load8(qk.v + (size_t)kvh * D + 8 * sub, vx);
+            if (qk.k_norm != nullptr) load8(qk.k_norm + 8 * sub, gk);
+        }
+        wave_cos_sin<LPP>(lcs[wave], qk.cs != nullptr ? qk.cs + (size_t)pos * (D / 2) : nullptr, qk.tab, qk.base,
+                          qk.freq_scale, pos, lane);
+        cs8<LPP>(lcs[wave], sub, qk.neox, cv);
+    }
+    float m = kNegMax, l = 0.0f, acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    u32x4 knew{0, 0, 0, 0}, vnew{0, 0, 0, 0};
+    bool first = true;
+    for (int b0 = wave; b0 < nslots; b0 += kHeadWaves * kHeadBatch) {
+        u32x4 kk[kHeadBatch], vv[kHeadBatch];
+#pragma unroll
+        for (int i = 0; i < kHeadBatch; ++i) {
+            const int p = (b0 + kHeadWaves * i) * PPW + grp;
+            const bool ok = p < seq;
+            kk[i] = ok ? *reinterpret_cast<const u32x4*>(kh + (size_t)p * row) : u32x4{0, 0, 0, 0};
+            vv[i] = ok ? *reinterpret_cast<const u32x4*>(vh + (size_t)p * row) : u32x4{0, 0, 0, 0};
+        }
+        if constexpr (QK) {
+            if (first) {      // the per-head step while the first loads fly
+                head_norm_rope<LPP>(qv, sub, qk.q_norm != nullptr, gq, qk.eps, cv, qk.neox);
+                if (pos_wave) {
+                    head_norm_rope<LPP>(kx, sub, qk.k_norm != nullptr, gk, qk.eps, cv, qk.neox);
+                    typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+                    hv8 hk, hvv;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        hk[i] = (_Float16)kx[i];
+                        hvv[i] = (_Float16)vx[i];
+                    }
+                    knew = __builtin_bit_cast(u32x4, hk);
+                    vnew = __builtin_bit_cast(u32x4, hvv);
+                    if (head % group == 0 && grp == 0) {
+                        const size_t c = (size_t)pos * row + (size_t)kvh * D + 8 * sub;
+                        *reinterpret_cast<u32x4*>(qk.kc + c) = knew;
+                        *reinterpret_cast<u32x4*>(qk.vc + c) = vnew;
+                    }
+                }
+                first = false;
+            }
+            if (pos_wave) {
+#pragma unroll
+                for (int i = 0; i < kHeadBatch; ++i)
+                    if ((b0 + kHeadWaves * i) * PPW + grp == pos) {
+                        kk[i] = knew;
+                        vv[i] = vnew;
+                    }
+            }
+        }
+        float sc[kHeadBatch];
+        float cm = kNegMax;
+#pragma unroll
+        for (int i = 0; i < kHeadBatch; ++i) {
+            const uint32_t w4[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+            float t = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 f = __half22float2(__builtin_bit_cast(__half2, w4[u]));
+                t = __fmaf_rn(qv[2 * u], f.x, t);
+                t = __fmaf_rn(qv[2 * u + 1], f.y, t);
+            }
+#pragma unroll
+            for (int o = LPP / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            sc[i] = ((b0 + kHeadWaves * i) * PPW + grp < seq) ? __fmul_rn(t, scale) : kNegMax;
+            cm = fmaxf(cm, sc[i]);
+        }
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+        const float m_new = fmaxf(m, cm);
+        const float alpha = expf(m - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __fmul_rn(acc[j], alpha);
+#pragma unroll
+        for (int i = 0; i < kHeadBatch; ++i) {
+            const float e = ((b0 + kHeadWaves * i) * PPW + grp < seq) ? expf(sc[i] - m_new) : 0.0f;
+            ls += e;
+            const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float2 f = __half22float2(__builtin_bit_cast(__half2, w4[u]));
+                acc[2 * u] = __fmaf_rn(e, f.x, acc[2 * u]);
+                acc[2 * u + 1] = __fmaf_rn(e, f.y, acc[2 * u + 1]);
+            }
+        }
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) ls += __shfl_xor(ls, o);
+        l = __fmaf_rn(l, alpha, ls);
+        m = m_new;
+    }
+    // (the wave holding the new position always has that slot, so the step
+    // above ran; waves without positions leave m = kNegMax, l = 0)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) acc[j] += __shfl_xor(acc[j], o);
+    if (grp == 0) {
+        *reinterpret_cast<float4*>(&wacc[wave][8 * sub]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4*>(&wacc[wave][8 * sub + 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
+    __syncthreads();
+    // out = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) l_w in wave order
+    // (waves without positions have l = 0 and count 0)
+    for (int d = threadIdx.x; d < D; d += 64 * kHeadWaves) {
+        float M = kNegMax;
+#pragma unroll
+        for (int w = 0; w < kHeadWaves; ++w) M = fmaxf(M, wm[w]);
+        float lt = 0.0f, a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kHeadWaves; ++w) {
+            const float f = wl[w] > 0.0f ? expf(wm[w] - M) : 0.0f;
+            lt = __fmaf_rn(f, wl[w], lt);
+            a = __fmaf_rn(f, wacc[w][d], a);
+        }
+        out[(size_t)head * D + d] = a * (1.0f / lt);
+    }
+}
+
 // Workspace of the split path: the (m, l, acc) partials of every head and
 // split, (D + 4) floats each, for at most kMaxSplits splits.  It is the
 // caller's memory (rf_flash_attn_decode_workspace_bytes gives the size);
@@ -821,11 +1000,29 @@ static size_t attn_ws_bytes(int nh, int d) { return (size_t)nh * kMaxSplits * (d
 
 static hipError_t attn_decode(float* out, const float* q, const __half* kc, const __half* vc, const int* len_ptr,
                               int len, int nh, int nkv, int d, float scale, float* ws, size_t ws_bytes,
-                              hipStream_t st, const QkStep* qk = nullptr) {
+                              hipStream_t st, const QkStep* qk = nullptr, int max_seq = 0) {
     if (out == nullptr || q == nullptr || kc == nullptr || vc == nullptr) return hipErrorInvalidValue;
     if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || (len_ptr == nullptr && len <= 0)) return hipErrorInvalidValue;
     if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
     const int group = nh / nkv;
+    if (max_seq > 0 && max_seq <= kHeadPathMaxSeq) {
+        // one workgroup per query head (the sequence is at most max_seq long)
+        const QkStep a = qk ? *qk : QkStep{};
+#define RF_HEAD(LPP)                                                                                                   \
+    if (qk)                                                                                                            \
+        hipLaunchKernelGGL((rf_attn_head_kernel<LPP, true>), dim3(nh), dim3(64 * kHeadWaves), 0, st, q, kc, vc,        \
+                           len_ptr, len, nh, nkv, scale, a, out);                                                      \
+    else                                                                                                               \
+        hipLaunchKernelGGL((rf_attn_head_kernel<LPP, false>), dim3(nh), dim3(64 * kHeadWaves), 0, st, q, kc, vc,       \
+                           len_ptr, len, nh, nkv, scale, a, out)
+        switch (d) {
+        case 64: RF_HEAD(8); break;
+        case 128: RF_HEAD(16); break;
+        default: RF_HEAD(32); break;
+        }
+#undef RF_HEAD
+        return hipGetLastError();
+    }
     if (ws != nullptr && ws_bytes < attn_ws_bytes(nh, d)) return hipErrorInvalidValue;
     if (ws != nullptr && group <= 8) {
         int S = (2 * device_cu_count() + nkv - 1) / nkv;
@@ -1245,6 +1442,40 @@ extern "C" hipError_t rf_attn_decode_qk_norm_rope_state(float* d_out, const floa
     return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
                        reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
                        scale, d_workspace, workspace_bytes, stream, &qk);
+}
+
+// The same two launches for a caller that bounds the sequence: with
+// max_seq <= kHeadPathMaxSeq (the caller guarantees seq <= max_seq) one
+// workgroup per query head runs instead of the split kernel and its merge
+// (rf_attn_head_kernel: no workspace, which may then be null); beyond it the
+// split path and its workspace as above.
+extern "C" hipError_t rf_flash_attn_decode_state_bounded(float* d_out, const float* d_q, const uint16_t* d_k_cache,
+                                                         const uint16_t* d_v_cache, const int* d_seq_len,
+                                                         const int num_heads, const int num_kv_heads,
+                                                         const int head_dim, const float scale, const int max_seq,
+                                                         float* d_workspace, const size_t workspace_bytes,
+                                                         hipStream_t stream) {
+    if (d_seq_len == nullptr || max_seq <= 0) return hipErrorInvalidValue;
+    if (max_seq > kHeadPathMaxSeq && d_workspace == nullptr) return hipErrorInvalidValue;
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_seq_len, 0, num_heads, num_kv_heads, head_dim,
+                       scale, d_workspace, workspace_bytes, stream, nullptr, max_seq);
+}
+
+extern "C" hipError_t rf_attn_decode_qk_norm_rope_state_bounded(
+    float* d_out, const float* d_q, const float* d_k, const float* d_v, const float* d_q_norm, const float* d_k_norm,
+    uint16_t* d_k_cache, uint16_t* d_v_cache, const int* d_state, const int num_heads, const int num_kv_heads,
+    const int head_dim, const float eps, const float theta_base, const int neox, const float* d_freq_scale,
+    const float* d_theta, const float* d_cos_sin, const float scale, const int max_seq, float* d_workspace,
+    const size_t workspace_bytes, hipStream_t stream) {
+    if (d_k == nullptr || d_v == nullptr || d_state == nullptr || max_seq <= 0) return hipErrorInvalidValue;
+    if (max_seq > kHeadPathMaxSeq && d_workspace == nullptr) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(d_cos_sin) & 15u) return hipErrorInvalidValue;
+    QkStep qk{d_k, d_v, d_q_norm, d_k_norm, reinterpret_cast<__half*>(d_k_cache), reinterpret_cast<__half*>(d_v_cache),
+              eps, d_theta, theta_base, neox, d_freq_scale, reinterpret_cast<const float2*>(d_cos_sin)};
+    return attn_decode(d_out, d_q, reinterpret_cast<const __half*>(d_k_cache),
+                       reinterpret_cast<const __half*>(d_v_cache), d_state + 1, 0, num_heads, num_kv_heads, head_dim,
+                       scale, d_workspace, workspace_bytes, stream, &qk, max_seq);
 }
 
 // ---- decode attention without any allocation ----

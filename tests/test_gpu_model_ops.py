@@ -217,6 +217,48 @@ def test_attn_decode(rf, dev, seq, nh, nkv, d):
                                       None, wsb, G.stream()) != 0
 
 
+@pytest.mark.parametrize("seq,nh,nkv,d", [(1, 32, 8, 128), (3, 32, 8, 128), (64, 32, 8, 128), (65, 32, 8, 128),
+                                          (640, 32, 8, 128), (2048, 32, 8, 128), (300, 16, 16, 64),
+                                          (257, 8, 2, 256), (100, 32, 2, 128)])
+def test_attn_decode_bounded(rf, dev, seq, nh, nkv, d):
+    # one workgroup per query head (max_seq <= 2048; GQA groups of any size,
+    # here up to 16): the oracle's attention within 1e-5, no workspace needed;
+    # past 2048 the split path with its workspace, the same bits as
+    # rf_flash_attn_decode_state_ws
+    rng = np.random.default_rng(seq + 3 * d + nkv)
+    max_seq = seq + 3
+    q = rng.standard_normal(nh * d).astype(np.float32)
+    kc = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.uint16)
+    scale = 1.0 / math.sqrt(d)
+    ref = O.attn_decode(q, kc, vc, seq, nh, nkv, d, scale)
+    dq, dkc, dvc = G.to_dev(q), G.to_dev(kc.view(np.int16)), G.to_dev(vc.view(np.int16))
+    dlen = G.to_dev(np.array([seq], np.int32))
+    bound = min(max_seq, 2048)
+    out = G.empty(nh * d, torch.float32).fill_(float("nan"))
+    G.call(rf.rf_flash_attn_decode_state_bounded, G.ptr(out), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh, nkv,
+           d, scale, bound, None, 0)
+    _close(G.host(out), ref, f"head-path attn decode seq {seq} d {d} group {nh // nkv}")
+    again = G.empty(nh * d, torch.float32)
+    G.call(rf.rf_flash_attn_decode_state_bounded, G.ptr(again), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh,
+           nkv, d, scale, bound, None, 0)
+    np.testing.assert_array_equal(G.host(again), G.host(out))
+    if nh // nkv <= 8:
+        wsb = int(rf.rf_flash_attn_decode_workspace_bytes(nh, d))
+        ws = G.empty(wsb // 4, torch.float32)
+        o_split, o_big = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
+        G.call(rf.rf_flash_attn_decode_state_ws, G.ptr(o_split), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh,
+               nkv, d, scale, G.ptr(ws), wsb)
+        G.call(rf.rf_flash_attn_decode_state_bounded, G.ptr(o_big), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen),
+               nh, nkv, d, scale, 4096, G.ptr(ws), wsb)
+        np.testing.assert_array_equal(G.host(o_big), G.host(o_split))
+    s = G.stream()
+    assert rf.rf_flash_attn_decode_state_bounded(G.ptr(out), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh, nkv,
+                                                 d, scale, 0, None, 0, s) != 0           # no bound
+    assert rf.rf_flash_attn_decode_state_bounded(G.ptr(out), G.ptr(dq), G.ptr(dkc), G.ptr(dvc), G.ptr(dlen), nh, nkv,
+                                                 d, scale, 4096, None, 0, s) != 0        # split path needs a workspace
+
+
 @pytest.mark.parametrize("n", [1, 1000, 1024, 1025, 151936])
 def test_argmax(rf, dev, n):
     rng = np.random.default_rng(n)
@@ -348,6 +390,77 @@ def test_attention_with_folded_qk_step(rf, dev, seq, nh, nkv, d):
     ref = O.attn_decode(qr.astype(np.float32), G.host(kc1).view(np.uint16), G.host(vc1).view(np.uint16), seq, nh,
                         nkv, d, scale)
     _close(G.host(out1), ref, f"attention with qk step seq {seq}")
+
+
+@pytest.mark.parametrize("seq,nh,nkv,d", [(1, 32, 8, 128), (2, 32, 8, 128), (641, 32, 8, 128), (100, 8, 8, 64),
+                                          (70, 8, 2, 256), (200, 32, 2, 128)])
+def test_attention_with_folded_qk_step_bounded(rf, dev, seq, nh, nkv, d):
+    # the bounded launch (one workgroup per query head) = the standalone Q/K
+    # step + the bounded attention, bit for bit (caches too: the new K/V row
+    # written once, by the workgroup of the group's first query head, and read
+    # by every head from registers), and the oracle within 1e-5
+    rng = np.random.default_rng(seq + nh + 1)
+    max_seq = seq + 5
+    q = (rng.standard_normal(nh * d) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * d) * 3).astype(np.float32)
+    v = rng.standard_normal(nkv * d).astype(np.float32)
+    qn, kn = ((1 + 0.1 * rng.standard_normal(d)).astype(np.float32) for _ in range(2))
+    cache = rng.standard_normal(max_seq * nkv * d).astype(np.float16).view(np.int16)
+    dq, dk, dv, dqn, dkn = (G.to_dev(a) for a in (q, k, v, qn, kn))
+    st = G.to_dev(np.array([seq - 1, seq], np.int32))
+    kc1, vc1, kc2, vc2 = (G.to_dev(cache) for _ in range(4))
+    out1, out2 = G.empty(nh * d, torch.float32), G.empty(nh * d, torch.float32)
+    scale = 1.0 / math.sqrt(d)
+    G.call(rf.rf_attn_decode_qk_norm_rope_state_bounded, G.ptr(out1), G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn),
+           G.ptr(dkn), G.ptr(kc1), G.ptr(vc1), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, None, scale, max_seq,
+           None, 0)
+    np.testing.assert_array_equal(G.host(dq), q)        # the raw q is left as it was
+    G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(dqn), G.ptr(dkn), G.ptr(kc2),
+           G.ptr(vc2), G.ptr(st), nh, nkv, d, 1e-6, 1e6, 1, None, None, None)
+    dlen = G.to_dev(np.array([seq], np.int32))
+    G.call(rf.rf_flash_attn_decode_state_bounded, G.ptr(out2), G.ptr(dq), G.ptr(kc2), G.ptr(vc2), G.ptr(dlen), nh,
+           nkv, d, scale, max_seq, None, 0)
+    np.testing.assert_array_equal(G.host(out1), G.host(out2))
+    np.testing.assert_array_equal(G.host(kc1), G.host(kc2))
+    np.testing.assert_array_equal(G.host(vc1), G.host(vc2))
+    qr = O.rope(O.rms_norm(q, qn, 1e-6, nh), 1, nh, d, seq - 1, 1e6, True)
+    ref = O.attn_decode(qr.astype(np.float32), G.host(kc1).view(np.uint16), G.host(vc1).view(np.uint16), seq, nh,
+                        nkv, d, scale)
+    _close(G.host(out1), ref, f"bounded attention with qk step seq {seq}")
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+def test_rope_cos_sin_table_follows_theta_table(rf, dev, scaled):
+    # a caller's theta table that is not the standard one (a scaled RoPE
+    # expressed through d_theta): the cos / sin table built from it rotates
+    # like the trig path given the same d_theta, bit for bit
+    nh, nkv, d, max_seq, base, pos = 8, 2, 128, 64, 1e6, 61
+    rng = np.random.default_rng(7)
+    std = G.empty(d // 2, torch.float32)
+    G.call(rf.rf_rope_theta_table, G.ptr(std), d, base)
+    theta = G.to_dev((G.host(std) * (1 + 0.05 * rng.random(d // 2))).astype(np.float32))
+    fs = G.to_dev((1 + rng.random(d // 2)).astype(np.float32)) if scaled else None
+    fsp = G.ptr(fs) if scaled else None
+    cs = G.empty(max_seq * d, torch.float32)
+    G.call(rf.rf_rope_cos_sin_table, G.ptr(cs), max_seq, d, base, G.ptr(theta), fsp)
+    th = G.host(theta) / (G.host(fs) if scaled else 1.0)
+    ang = (np.float32(pos) * th.astype(np.float32)).astype(np.float64)
+    row = G.host(cs).reshape(max_seq, d // 2, 2)[pos]
+    assert np.abs(row[:, 0] - np.cos(ang)).max() <= 4e-7
+    qn, kn = G.to_dev(np.ones(d, np.float32)), G.to_dev(np.ones(d, np.float32))
+    q = (rng.standard_normal(nh * d) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * d) * 3).astype(np.float32)
+    dk, dv = G.to_dev(k), G.to_dev(k)
+    st = G.to_dev(np.array([pos, pos + 1], np.int32))
+    outs = []
+    for table in (None, G.ptr(cs)):
+        dq = G.to_dev(q)
+        kc, vc = G.empty(max_seq * nkv * d, torch.int16).zero_(), G.empty(max_seq * nkv * d, torch.int16).zero_()
+        G.call(rf.rf_qk_norm_rope_kv_write_state, G.ptr(dq), G.ptr(dk), G.ptr(dv), G.ptr(qn), G.ptr(kn), G.ptr(kc),
+               G.ptr(vc), G.ptr(st), nh, nkv, d, 1e-6, base, 1, fsp, G.ptr(theta), table)
+        outs.append((G.host(dq), G.host(kc)))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
 
 
 @pytest.mark.parametrize("d,neox,scaled", [(128, 1, False), (128, 0, False), (64, 1, True), (256, 0, True),
