@@ -97,7 +97,7 @@ hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* 
  * first.  D[M x N] = fp16(A[M x K]) * fp16(dequant W[N x K])^T, fp32 out.
  * M % 64 == 0, N % 64 == 0, K % 256 == 0 (callers pad M to 64 rows).
  * A is rounded to fp16 (__float2half's value) by a pass of its own into
- * library-owned device memory (a file-scope array: 4 slots of 40 MB per GPU,
+ * library-owned device memory (a file-scope array: 4 slots of 56 MB per GPU,
  * one per stream, claimed on a stream's first launch) and the fp16
  * tiles of rf_gemm_q*_k_f16_launch run on it; small launches split K over
  * workgroups and add the partial tiles in a fixed order, so every output is

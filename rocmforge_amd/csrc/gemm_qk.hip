@@ -1871,18 +1871,32 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
 // s * 2^24, -32 s) = s (q - 32) is exact in fp32 (s = d sc has at most 19
 // significant bits), so its fp16 rounding in the same instruction is the
 // reference's value __float2half(d * sc * (q - 32)).
+//
+// Tall tiles (FMR = 8: 256 x 64, Q6aGeom<8>): each wave takes 8 row blocks
+// (8 MFMAs per chunk against the same dequantised B operand, so each weight
+// is dequantised once per 256 rows of A: half the dequantisation per MFMA of
+// the 128-row tiles).  LDS then holds four 32 KB A buffers (a DMA lands
+// within one chunk of slack) and two ring stages; the K-slice partials are
+// exchanged in two rounds of four row blocks.
 constexpr int kQ6aThreads = 512;
 constexpr int kQ6aBM = 128, kQ6aBN = 64;
 constexpr int kQ6aRowB = 240;                         // ring bytes per weight row (14 pieces + 1 padding)
 constexpr int kQ6aRingInstr = 16;                     // 16-byte DMAs per stage
 constexpr int kQ6aStage = kQ6aRingInstr * 1024;       // 16384 B
-constexpr int kQ6aRS = 3;                             // ring stages
-constexpr int kQ6aABufs = 7;                          // DMA of chunk c + 6 issued in chunk c
-constexpr int kQ6aLag = kQ6aABufs - 3;                // chunks a DMA may stay in flight
-constexpr int kQ6aABuf = kQ6aBM * kKC * 2;            // 16 KB
-constexpr int kQ6aLdsLoop = kQ6aRS * kQ6aStage + kQ6aABufs * kQ6aABuf;   // 163,840 B
 constexpr int kQ6aLdsXch = 8 * 3 * 4096;              // 98,304 B: three row blocks of each wave's partial
-constexpr int kQ6aLds = kQ6aLdsLoop > kQ6aLdsXch ? kQ6aLdsLoop : kQ6aLdsXch;
+
+template <int FMR>
+struct Q6aGeom {
+    static constexpr int kBM = 32 * FMR;
+    static constexpr int kRS = FMR == 4 ? 3 : 2;      // ring stages: super-block sb + kRS - 1 loads while sb is used
+    static constexpr int kABufs = FMR == 4 ? 7 : 4;   // DMA of chunk c + kABufs - 1 issued in chunk c
+    static constexpr int kLag = kABufs - 3;           // chunks a DMA may stay in flight
+    static constexpr int kABuf = kBM * kKC * 2;       // 16 or 32 KB
+    static constexpr int kAPW = FMR / 2;              // A DMAs per wave per chunk (1 KB each)
+    static constexpr int kLdsLoop = kRS * kQ6aStage + kABufs * kABuf;   // 163,840 B for both
+    static constexpr int kLds = kLdsLoop > kQ6aLdsXch ? kLdsLoop : kQ6aLdsXch;
+};
+constexpr int kQ6aLds = Q6aGeom<4>::kLds;
 
 // The 4 fp16 weights s (q - 32) of the 6-bit values in the bytes of qb, in
 // byte order, as two packed words.
@@ -1909,12 +1923,13 @@ struct KSplit {
     float* part;
 };
 
-template <bool ACC>
+template <bool ACC, int FMR = 4>
 __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
                                        float* __restrict__ D, int M, int N, int K, int v, uint8_t* lds,
                                        KSplit sp = KSplit{1, nullptr}) {
+    using G = Q6aGeom<FMR>;
     uint8_t* ring = lds;
-    uint8_t* abuf0 = lds + kQ6aRS * kQ6aStage;
+    uint8_t* abuf0 = lds + G::kRS * kQ6aStage;
     const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
     const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
 
@@ -1923,7 +1938,7 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ks = wave & 3, cg = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
-    const int mtiles = (M + kQ6aBM - 1) / kQ6aBM;
+    const int mtiles = (M + G::kBM - 1) / G::kBM;
     const int nsb_row = K / kQK;
     int sb0 = 0, nsb = nsb_row;                // this workgroup's super-blocks [sb0, sb0 + nsb) of each row
     if (sp.S > 1) {
@@ -1934,7 +1949,7 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
         nsb = (s + 1) * nsb_row / sp.S - sb0;
         D = sp.part + (size_t)s * M * N;
     }
-    const int m0 = (v % mtiles) * kQ6aBM;      // the M tiles of one column tile are neighbours
+    const int m0 = (v % mtiles) * G::kBM;      // the M tiles of one column tile are neighbours
     const int n0 = (v / mtiles) * kQ6aBN;
     const int nchunks = 4 * nsb;
     const uint32_t row_bytes = (uint32_t)nsb_row * kQ6KBytes;
@@ -1958,18 +1973,19 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
                   w_tile + (size_t)((s * kQ6KBytes) & ~15));
     };
 
-    // ---- A: instruction gi = 2 wave + g covers rows 8 gi + L / 8 of the chunk,
-    // position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row M - 1 --
+    // ---- A: instruction gi = kAPW wave + g covers rows 8 gi + L / 8 of the
+    // chunk, position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row
+    // M - 1 --------------------------------------------------------------------
     const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + ((size_t)m0 * K + (size_t)sb0 * kQK) * 2;
-    uint32_t dma_voff[2];
+    uint32_t dma_voff[G::kAPW];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const int r = 8 * (2 * wave + g) + (lane >> 3);
+    for (int g = 0; g < G::kAPW; ++g) {
+        const int r = 8 * (G::kAPW * wave + g) + (lane >> 3);
         const int rc = min(r, M - 1 - m0);
         dma_voff[g] = (uint32_t)(rc * K + 8 * ((lane & 7) ^ (r & 7) ^ ((r >> 3) & 1))) * 2u;
     }
     auto a_dma1 = [&](int g, int c, int buf) {
-        lds_dma16(a_lds0 + (uint32_t)(buf * kQ6aABuf + (2 * wave + g) * 1024), dma_voff[g],
+        lds_dma16(a_lds0 + (uint32_t)(buf * G::kABuf + (G::kAPW * wave + g) * 1024), dma_voff[g],
                   a_tile + (size_t)min(c, nchunks - 1) * kKC * 2);
     };
 
@@ -1982,7 +1998,7 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     uint32_t rql[2], rqh[2];
     auto raw_read = [&](int n, int sb) {
         const int off = (2 * (sb0 + sb)) & 15;
-        const uint8_t* rowp = ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB;
+        const uint8_t* rowp = ring + (sb % G::kRS) * kQ6aStage + brow * kQ6aRowB;
         const int oql = off + 64 * n + 16 * ks + 8 * h;
         const int oqh = off + 128 + 32 * n + 16 * (ks & 1) + 8 * h;
         const uint32_t* pl = reinterpret_cast<const uint32_t*>(rowp + (oql & ~3));
@@ -2006,13 +2022,13 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     auto d_read = [&](int sb) {
         const int off = (2 * (sb0 + sb)) & 15;
         const float d = half_bits_to_float(
-            *reinterpret_cast<const uint16_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 208));
+            *reinterpret_cast<const uint16_t*>(ring + (sb % G::kRS) * kQ6aStage + brow * kQ6aRowB + off + 208));
         d24 = d * 16777216.0f;
         dm32 = -32.0f * d;
     };
     auto sc_read = [&](int cq, int sb) {
         const int off = (2 * (sb0 + sb)) & 15;
-        scb = *reinterpret_cast<const int8_t*>(ring + (sb % kQ6aRS) * kQ6aStage + brow * kQ6aRowB + off + 192 +
+        scb = *reinterpret_cast<const int8_t*>(ring + (sb % G::kRS) * kQ6aStage + brow * kQ6aRowB + off + 192 +
                                                4 * cq + ks);
     };
     // qh field 2q of each byte to bits 4-5: rotate right by (2q - 4) mod 32
@@ -2033,30 +2049,31 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
         bq[P] = u32x4{r[0].x, r[0].y, r[1].x, r[1].y};
     };
 
-    f32x16 acc[4];
+    f32x16 acc[FMR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FMR; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
 
     // fragment of row block i: row 32 i + col, k piece 2 ks + h at position
     // (2 ks + h) ^ g(col) of its row
     const int gcol = (col & 7) ^ ((col >> 3) & 1);
-    f16x8 af[2][4];
+    f16x8 af[2][FMR];
     auto frag_ld = [&](int set, int buf, int i) {
-        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * kQ6aABuf + (32 * i + col) * 128 +
+        af[set][i] = *reinterpret_cast<const f16x8*>(abuf0 + buf * G::kABuf + (32 * i + col) * 128 +
                                                      16 * ((2 * ks + h) ^ gcol));
     };
 
-    // ---- prologue: ring stages 0, 1; A chunks 0 .. 5; chunk 0's operands ----
+    // ---- prologue: ring stages 0 .. kRS - 2; A chunks 0 .. kABufs - 2; chunk
+    // 0's operands -------------------------------------------------------------
 #pragma unroll
-    for (int t = 0; t < kRPW; ++t) w_dma1(t, 0, 0);
+    for (int st = 0; st < G::kRS - 1; ++st)
 #pragma unroll
-    for (int t = 0; t < kRPW; ++t) w_dma1(t, 1, 1);
+        for (int t = 0; t < kRPW; ++t) w_dma1(t, st, st);
 #pragma unroll
-    for (int c = 0; c < kQ6aABufs - 1; ++c)
+    for (int c = 0; c < G::kABufs - 1; ++c)
 #pragma unroll
-        for (int g = 0; g < 2; ++g) a_dma1(g, c, c);
+        for (int g = 0; g < G::kAPW; ++g) a_dma1(g, c, c);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
     raw_read(0, 0);
@@ -2064,28 +2081,34 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     sc_read(0, 0);
     b_dequant(0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) frag_ld(0, 0, i);
+    for (int i = 0; i < FMR; ++i) frag_ld(0, 0, i);
 
-    // Chunk c = 4 sb + CQ uses A buffer c % 7 and ring stage sb % 3.  Its 4
-    // MFMA slots carry: the A fragments of chunk c + 1, the A DMA of chunk
-    // c + 6 (into the buffer chunk c - 1 used), in CQ 0 the ring DMA of
-    // super-block sb + 2 (into the stage sb - 1 used), and the B operands of
-    // chunk c + 1 (raw bytes of half n read in the chunk before 2 n).  At the
-    // end every DMA issued up to chunk c - 4 is complete (vmcnt = the 4 x 2 A
-    // and 2 ring DMAs of the last four chunks), then one barrier: a ring DMA
-    // lands by the end of chunk 4 sb + 4, before the stage's first read in
-    // chunk 4 sb + 7.
-    int ab = 0;                                     // c % 7
+    // Chunk c = 4 sb + CQ uses A buffer c % kABufs and ring stage sb % kRS.
+    // Its FMR MFMA slots carry: the A fragments of chunk c + 1, the A DMA of
+    // chunk c + kABufs - 1 (into the buffer chunk c - 1 used), in CQ 0 the
+    // ring DMA of super-block sb + kRS - 1 (into the stage sb - 1 used), and
+    // the B operands of chunk c + 1 (raw bytes of half n read in the chunk
+    // before 2 n).  At the end every DMA issued up to chunk c - kLag is
+    // complete (vmcnt = the A DMAs of the last kLag chunks and the ring DMAs
+    // among them), then one barrier.  A ring stage is first read in the last
+    // chunk of the super-block before it: kRS = 3 (128-row tiles): the DMA
+    // issued in chunk 4 sb lands by the end of chunk 4 sb + 4, before the
+    // read in chunk 4 sb + 7; kRS = 2 (256 rows): it lands by the end of
+    // chunk 4 sb + 1, before the read in chunk 4 sb + 3.
+    int ab = 0;                                     // c % kABufs
     auto iteration = [&](auto cqc, int sb) {
         constexpr int CQ = decltype(cqc)::value;
         constexpr int P = CQ & 1;
         constexpr int NQ = (CQ + 1) & 3;            // chunk c + 1 within its super-block
+        // ring DMAs (issued in CQ 0) among the DMAs of the last kLag chunks
+        constexpr int kRingOut = G::kLag >= 4 ? 1 : (CQ < G::kLag ? 1 : 0);
+        constexpr int kOut = G::kAPW * G::kLag + kRPW * kRingOut;
         const int c = 4 * sb + CQ;
         const int sbn = CQ == 3 ? sb + 1 : sb;
-        const int abn = ab == kQ6aABufs - 1 ? 0 : ab + 1;       // chunk c + 1
-        const int abp = ab == 0 ? kQ6aABufs - 1 : ab - 1;       // chunk c - 1 (= c + 6)
+        const int abn = ab == G::kABufs - 1 ? 0 : ab + 1;       // chunk c + 1
+        const int abp = ab == 0 ? G::kABufs - 1 : ab - 1;       // chunk c - 1 (= c + kABufs - 1)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < FMR; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[P][i], __builtin_bit_cast(f16x8, bq[P]), acc[i], 0, 0,
                                                             0);
             if (i == 0) {
@@ -2094,16 +2117,16 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
                 if constexpr (NQ == 0) d_read(sbn);
                 sc_read(NQ, sbn);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) frag_ld(P ^ 1, abn, r);
+                for (int r = 0; r < FMR; ++r) frag_ld(P ^ 1, abn, r);
             }
-            if (i < 2) a_dma1(i, c + kQ6aABufs - 1, abp);
+            if (i < G::kAPW) a_dma1(i, c + G::kABufs - 1, abp);
             if constexpr (CQ == 0) {
-                if (i < kRPW) w_dma1(i, sb + 2, (sb + 2) % kQ6aRS);
+                if (i < kRPW) w_dma1(i, sb + G::kRS - 1, (sb + G::kRS - 1) % G::kRS);
             }
-            if (i == 3) b_dequant(NQ & 1, P ^ 1);
+            if (i == FMR - 1) b_dequant(NQ & 1, P ^ 1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kQ6aLag + kRPW) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kOut) : "memory");
         lds_barrier();
         ab = abn;
     };
@@ -2115,62 +2138,68 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- K slices: wave (ks, cg) keeps row block ks and hands the other three
-    // to the waves of its column group; [src wave][slot 0..2][e / 4][lane] of
-    // float4 (each access one contiguous 1 KB per wave) -----------------------
-    __syncthreads();
+    // ---- K slices, in rounds of four row blocks: wave (ks, cg) keeps row
+    // block 4 rd + ks and hands the other three of the round to the waves of
+    // its column group; [src wave][slot 0..2][e / 4][lane] of float4 (each
+    // access one contiguous 1 KB per wave).  acc is indexed by compile-time
+    // constants only (the round loop is unrolled) ------------------------------
     float4* xch = reinterpret_cast<float4*>(lds);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (i == ks) continue;
-        const int slot = i < ks ? i : i - 1;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            xch[((wave * 3 + slot) * 4 + q) * 64 + lane] =
-                make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
-    }
-    __syncthreads();
-    // block ks of the column group: partials of ks' = 0..3 added in that order
-    f32x16 own = acc[0];
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (i == ks) own = acc[i];
     const int ncol = n0 + 32 * cg + col;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int rd = 0; rd < FMR / 4; ++rd) {
+        __syncthreads();
 #pragma unroll
-        for (int src = 0; src < 4; ++src) {
-            float4 p;
-            if (src == ks) {
-                p = make_float4(own[4 * q], own[4 * q + 1], own[4 * q + 2], own[4 * q + 3]);
-            } else {
-                const int slot = ks < src ? ks : ks - 1;
-                p = xch[(((4 * cg + src) * 3 + slot) * 4 + q) * 64 + lane];
-            }
-            s[0] += p.x;
-            s[1] += p.y;
-            s[2] += p.z;
-            s[3] += p.w;
+        for (int i = 0; i < 4; ++i) {
+            if (i == ks) continue;
+            const int slot = i < ks ? i : i - 1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                xch[((wave * 3 + slot) * 4 + q) * 64 + lane] =
+                    make_float4(acc[4 * rd + i][4 * q], acc[4 * rd + i][4 * q + 1], acc[4 * rd + i][4 * q + 2],
+                                acc[4 * rd + i][4 * q + 3]);
         }
+        __syncthreads();
+        // block 4 rd + ks of the column group: partials of ks' = 0..3 added in that order
+        f32x16 own = acc[4 * rd];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
-            if (row < M) {
-                float* o = D + (size_t)row * N + ncol;
-                *o = ACC ? *o + s[u] : s[u];
+        for (int i = 1; i < 4; ++i)
+            if (i == ks) own = acc[4 * rd + i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int src = 0; src < 4; ++src) {
+                float4 p;
+                if (src == ks) {
+                    p = make_float4(own[4 * q], own[4 * q + 1], own[4 * q + 2], own[4 * q + 3]);
+                } else {
+                    const int slot = ks < src ? ks : ks - 1;
+                    p = xch[(((4 * cg + src) * 3 + slot) * 4 + q) * 64 + lane];
+                }
+                s4[0] += p.x;
+                s4[1] += p.y;
+                s4[2] += p.z;
+                s4[3] += p.w;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int row = m0 + 32 * (4 * rd + ks) + 8 * q + 4 * h + u;
+                if (row < M) {
+                    float* o = D + (size_t)row * N + ncol;
+                    *o = ACC ? *o + s4[u] : s4[u];
+                }
             }
         }
     }
 }
 
-template <bool ACC>
+template <bool ACC, int FMR>
 __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ W,
                                                                         float* __restrict__ D, int M, int N, int K,
                                                                         KSplit sp) {
-    __shared__ __align__(16) uint8_t lds[kQ6aLds];
-    q6a_wg<ACC>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, sp);
+    __shared__ __align__(16) uint8_t lds[Q6aGeom<FMR>::kLds];
+    q6a_wg<ACC, FMR>(A, W, D, M, N, K, xcd_remap((int)blockIdx.x, (int)gridDim.x), lds, sp);
 }
 
 // ── q4s: Q4_K GEMM on fp16 activations, 32 FMR x 64 tiles, K slices on waves
@@ -2612,7 +2641,7 @@ static unsigned stream_grid(size_t n4) { return (unsigned)std::min<size_t>((n4 +
 // per GPU with hipGetSymbolAddress.
 constexpr int kGemmSlots = 4;
 constexpr size_t kSlotABytes = (size_t)32 << 20;
-constexpr size_t kSlotPartBytes = (size_t)8 << 20;
+constexpr size_t kSlotPartBytes = (size_t)24 << 20;
 constexpr size_t kSlotBytes = kSlotABytes + kSlotPartBytes;
 static __device__ __align__(256) uint8_t gemm_scratch[kGemmSlots * kSlotBytes];
 constexpr int kGemmMaxDevices = 64;
@@ -2730,23 +2759,38 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
     return hipGetLastError();
 }
 
-// Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel, 128 x 64 tiles), split
-// over K as gemm_q4_f16 does.  The caller has checked M % 64, N % 64,
-// K % 2048 and 16-byte alignment of A and W.
+// Q6_K on fp16 activations (rf_gemm_q6k_f16a_kernel): 256 x 64 tiles from
+// M = kQ6TallMinM rows (each weight dequantised once per 256 rows), else
+// 128 x 64, split over K as gemm_q4_f16 does.  The caller has checked
+// M % 64, N % 64, K % 2048 and 16-byte alignment of A and W.
+#ifndef RF_Q6_TALL_MIN_M
+#define RF_Q6_TALL_MIN_M 256
+#endif
+constexpr int kQ6TallMinM = RF_Q6_TALL_MIN_M;
+
+template <bool ACC, int FMR>
+static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
+                         float* part) {
+    const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ6aBN);
+    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
+    if (S > 1) {
+        hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<false, FMR>), dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0,
+                           st, A, w, nullptr, M, N, K, KSplit{S, part});
+        reduce_for(ACC, nullptr, part, S, M, N, D, st);
+    } else {
+        hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<ACC, FMR>), dim3((unsigned)tiles), dim3(kQ6aThreads), 0, st, A, w,
+                           D, M, N, K, KSplit{1, nullptr});
+    }
+}
+
 template <bool ACC>
 static hipError_t gemm_q6_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
                               float* part) {
-    const long tiles = (long)((M + kQ6aBM - 1) / kQ6aBM) * (N / kQ6aBN);
-    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    if (S > 1) {
-        hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<false>, dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0, st, A,
-                           w, nullptr, M, N, K, KSplit{S, part});
-        reduce_for(ACC, nullptr, part, S, M, N, D, st);
-    } else {
-        hipLaunchKernelGGL(rf_gemm_q6k_f16a_kernel<ACC>, dim3((unsigned)tiles), dim3(kQ6aThreads), 0, st, A, w, D, M,
-                           N, K, KSplit{1, nullptr});
-    }
+    if (M >= kQ6TallMinM)
+        q6_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, part);
+    else
+        q6_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, part);
     return hipGetLastError();
 }
 
