@@ -2220,17 +2220,23 @@ __global__ __launch_bounds__(kQ6aThreads) void rf_gemm_q6k_f16a_kernel(const uin
 constexpr int kQ4sThreads = 512;
 constexpr int kQ4sBN = 64;
 constexpr int kQ4sStage = 16 * 1024;                  // 64 rows x 144 B (+ padding DMAs)
-constexpr int kQ4sRS = 3;
-constexpr int kQ4sABufs = 7;
-constexpr int kQ4sLag = kQ4sABufs - 3;
 
+// FMR = 8 (256 x 64 tiles): each weight dequantised once per 256 rows of A;
+// LDS then holds two ring stages and four 32 KB A buffers (one chunk of DMA
+// slack), as in the tall Q6_K tiles, and the K-slice partials go through
+// LDS in rounds of four row blocks.
 template <int FMR>
 struct Q4sGeom {
     static constexpr int kBM = 32 * FMR;
+    static constexpr int kRS = FMR == 8 ? 2 : 3;      // ring stages
+    static constexpr int kABufs = FMR == 8 ? 4 : 7;   // DMA of chunk c + kABufs - 1 issued in chunk c
+    static constexpr int kLag = kABufs - 3;           // chunks a DMA may stay in flight
     static constexpr int kABuf = kBM * kKC * 2;       // FMR x 4 KB
     static constexpr int kAPW = FMR / 2;              // A DMAs per wave per chunk (1 KB each)
-    static constexpr int kLdsLoop = kQ4sRS * kQ4sStage + kQ4sABufs * kABuf;
-    static constexpr int kLdsXch = 8 * FMR * 4096;    // every wave's partial tile
+    static constexpr int kRounds = FMR == 8 ? 2 : 1;  // exchange rounds of the K-slice partials
+    static constexpr int kXB = FMR / kRounds;         // row blocks per round
+    static constexpr int kLdsLoop = kRS * kQ4sStage + kABufs * kABuf;
+    static constexpr int kLdsXch = 8 * kXB * 4096;    // every wave's partial blocks of one round
     static constexpr int kLds = kLdsLoop > kLdsXch ? kLdsLoop : kLdsXch;
 };
 
@@ -2241,7 +2247,7 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
                                        const float* __restrict__ gate = nullptr, KSplit sp = KSplit{1, nullptr}) {
     using G = Q4sGeom<FMR>;
     uint8_t* ring = lds;
-    uint8_t* abuf0 = lds + kQ4sRS * kQ4sStage;
+    uint8_t* abuf0 = lds + G::kRS * kQ4sStage;
     const uint32_t ring_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(ring);
     const uint32_t a_lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) uint8_t*)(abuf0);
 
@@ -2305,7 +2311,7 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
     const float nfac = hf ? 1048576.0f : 16777216.0f;
     float sD[4], sM[4];                         // per chunk p of the super-block: (d sc 2^x, -dmin m)
     auto hdr_read = [&](int sb) {
-        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + (sb % kQ4sRS) * kQ4sStage + brow * kQ4KBytes);
+        const u32x4 hd = *reinterpret_cast<const u32x4*>(ring + (sb % G::kRS) * kQ4sStage + brow * kQ4KBytes);
         const float d = half_bits_to_float(hd.x) * nfac, dmin = half_bits_to_float(hd.x >> 16);
         // get_scale_min_k4 for sub-blocks hf, 2 + hf (bytes of the low words)
         // and 4 + hf, 6 + hf (high words), word-wide without branches
@@ -2322,7 +2328,7 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
     };
     u32x2 rqs;
     auto qs_read = [&](int p, int sb) {
-        rqs = *reinterpret_cast<const u32x2*>(ring + (sb % kQ4sRS) * kQ4sStage + brow * kQ4KBytes + 16 + 32 * p +
+        rqs = *reinterpret_cast<const u32x2*>(ring + (sb % G::kRS) * kQ4sStage + brow * kQ4KBytes + 16 + 32 * p +
                                                16 * (ks & 1) + 8 * h);
     };
     u32x4 bq[2];                          // [chunk parity]
@@ -2346,13 +2352,14 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
                                                      16 * ((2 * ks + h) ^ gcol));
     };
 
-    // ---- prologue: ring stages 0, 1; A chunks 0 .. 5; chunk 0's operands ----
+    // ---- prologue: ring stages 0 .. kRS - 2; A chunks 0 .. kABufs - 2;
+    // chunk 0's operands --------------------------------------------------------
 #pragma unroll
-    for (int t = 0; t < 2; ++t) w_dma1(t, 0, 0);
+    for (int st = 0; st < G::kRS - 1; ++st)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) w_dma1(t, 1, 1);
+        for (int t = 0; t < 2; ++t) w_dma1(t, st, st);
 #pragma unroll
-    for (int c = 0; c < kQ4sABufs - 1; ++c)
+    for (int c = 0; c < G::kABufs - 1; ++c)
 #pragma unroll
         for (int g = 0; g < G::kAPW; ++g) a_dma1(g, c, c);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -2363,21 +2370,28 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
 #pragma unroll
     for (int i = 0; i < FMR; ++i) frag_ld(0, 0, i);
 
-    // Chunk c = 4 sb + CQ: A buffer c % 7, ring stage sb % 3.  After the
-    // first MFMA every LDS read of chunk c + 1 (its fragments, qs bytes and,
-    // entering a new super-block, its header); the A DMA of chunk c + 6;
-    // in CQ 0 the ring DMA of super-block sb + 2; the B operands of chunk
-    // c + 1 after the last MFMA.  At the end every DMA issued up to chunk
-    // c - 4 is complete, then one barrier.
+    // Chunk c = 4 sb + CQ: A buffer c % kABufs, ring stage sb % kRS.  After
+    // the first MFMA every LDS read of chunk c + 1 (its fragments, qs bytes
+    // and, entering a new super-block, its header); the A DMA of chunk
+    // c + kABufs - 1; in CQ 0 the ring DMA of super-block sb + kRS - 1; the B
+    // operands of chunk c + 1 after the last MFMA.  At the end every DMA
+    // issued up to chunk c - kLag is complete (the ring DMA of chunk 4 sb
+    // counted among the last kLag chunks' DMAs), then one barrier.  A ring
+    // stage is first read in the last chunk of the super-block before it:
+    // with kRS = 3 its DMA (chunk 4 sb) lands by the end of 4 sb + 4, before
+    // the read in 4 sb + 7; with kRS = 2 by the end of 4 sb + 1, before the
+    // read in 4 sb + 3.
     int ab = 0;
     auto iteration = [&](auto cqc, int sb) {
         constexpr int CQ = decltype(cqc)::value;
         constexpr int P = CQ & 1;
         constexpr int NQ = (CQ + 1) & 3;
+        constexpr int kRingOut = G::kLag >= 4 ? 1 : (CQ < G::kLag ? 1 : 0);
+        constexpr int kOut = G::kAPW * G::kLag + 2 * kRingOut;
         const int c = 4 * sb + CQ;
         const int sbn = CQ == 3 ? sb + 1 : sb;
-        const int abn = ab == kQ4sABufs - 1 ? 0 : ab + 1;
-        const int abp = ab == 0 ? kQ4sABufs - 1 : ab - 1;
+        const int abn = ab == G::kABufs - 1 ? 0 : ab + 1;
+        const int abp = ab == 0 ? G::kABufs - 1 : ab - 1;
 #pragma unroll
         for (int i = 0; i < FMR; ++i) {
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[P][i], __builtin_bit_cast(f16x8, bq[P]), acc[i], 0, 0,
@@ -2388,14 +2402,14 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
 #pragma unroll
                 for (int r = 0; r < FMR; ++r) frag_ld(P ^ 1, abn, r);
             }
-            if (i < G::kAPW) a_dma1(i, c + kQ4sABufs - 1, abp);
+            if (i < G::kAPW) a_dma1(i, c + G::kABufs - 1, abp);
             if constexpr (CQ == 0) {
-                if (i < 2) w_dma1(i, sb + 2, (sb + 2) % kQ4sRS);
+                if (i < 2) w_dma1(i, sb + G::kRS - 1, (sb + G::kRS - 1) % G::kRS);
             }
             if (i == FMR - 1) b_dequant(NQ, P ^ 1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(G::kAPW * kQ4sLag + 2) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kOut) : "memory");
         lds_barrier();
         ab = abn;
     };
@@ -2407,42 +2421,49 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- K slices: every wave parks its FMR row blocks in LDS
-    // ([wave][row block][e / 4][lane] of float4); wave (ks, cg), ks < FMR, adds
-    // row block ks of column group cg over ks' = 0..3 in that order ----------
-    __syncthreads();
+    // ---- K slices, in rounds of kXB row blocks: every wave parks the round's
+    // blocks in LDS ([wave][block][e / 4][lane] of float4); wave (ks, cg),
+    // ks < kXB, adds block kXB rd + ks of column group cg over ks' = 0..3 in
+    // that order (acc indexed by compile-time constants: the round loop is
+    // unrolled) --------------------------------------------------------------
     float4* xch = reinterpret_cast<float4*>(lds);
-#pragma unroll
-    for (int i = 0; i < FMR; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            xch[((wave * FMR + i) * 4 + q) * 64 + lane] =
-                make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
-    __syncthreads();
-    if (ks >= FMR) return;
     const int ncol = n0 + 32 * cg + col;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int rd = 0; rd < G::kRounds; ++rd) {
+        __syncthreads();
 #pragma unroll
-        for (int src = 0; src < 4; ++src) {
-            const float4 p = xch[(((4 * cg + src) * FMR + ks) * 4 + q) * 64 + lane];
-            s[0] += p.x;
-            s[1] += p.y;
-            s[2] += p.z;
-            s[3] += p.w;
-        }
+        for (int i = 0; i < G::kXB; ++i)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int row = m0 + 32 * ks + 8 * q + 4 * h + u;
-            if (row < M) {
-                const size_t e = (size_t)row * N + ncol;
-                if (!ACC && gate != nullptr) {   // up projection of a SwiGLU: fp16 silu(gate) * up
-                    const float gg = gate[e];
-                    reinterpret_cast<uint16_t*>(D)[e] = f16_bits_rn(gg / (1.0f + expf(-gg)) * s[u]);
-                } else {
-                    float* o = D + e;
-                    *o = ACC ? *o + s[u] : s[u];
+            for (int q = 0; q < 4; ++q)
+                xch[((wave * G::kXB + i) * 4 + q) * 64 + lane] =
+                    make_float4(acc[G::kXB * rd + i][4 * q], acc[G::kXB * rd + i][4 * q + 1],
+                                acc[G::kXB * rd + i][4 * q + 2], acc[G::kXB * rd + i][4 * q + 3]);
+        __syncthreads();
+        if (ks < G::kXB) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int src = 0; src < 4; ++src) {
+                    const float4 p = xch[(((4 * cg + src) * G::kXB + ks) * 4 + q) * 64 + lane];
+                    s4[0] += p.x;
+                    s4[1] += p.y;
+                    s4[2] += p.z;
+                    s4[3] += p.w;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int row = m0 + 32 * (G::kXB * rd + ks) + 8 * q + 4 * h + u;
+                    if (row < M) {
+                        const size_t e = (size_t)row * N + ncol;
+                        if (!ACC && gate != nullptr) {   // up projection of a SwiGLU: fp16 silu(gate) * up
+                            const float gg = gate[e];
+                            reinterpret_cast<uint16_t*>(D)[e] = f16_bits_rn(gg / (1.0f + expf(-gg)) * s4[u]);
+                        } else {
+                            float* o = D + e;
+                            *o = ACC ? *o + s4[u] : s4[u];
+                        }
+                    }
                 }
             }
         }
@@ -2713,22 +2734,38 @@ static void reduce_for(bool acc, const float* G, const float* part, int S, int M
 
 // Q4_K on fp16 activations: 256 x 128 tiles (rf_gemm_q4k_f16a_kernel) where
 // they fill at least three quarters of the CUs, else the eight-wave
-// K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 64 rows (M <= 64, or when
-// they come to at most one round of CUs) or 128, split over K when they
-// leave at least half the CUs idle and `part` (kSlotPartBytes) is given.
+// K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 256 rows (from M =
+// kQ4TallMinM: each weight dequantised once per 256 rows), 64 rows (M <= 64,
+// or when they come to at most one round of CUs) or 128, split over K when
+// they leave at least half the CUs idle and `part` (kSlotPartBytes) is given.
 // G: when given, D receives fp16 silu(G) * (A W^T) (the up projection of a
 // SwiGLU whose gate product G [M x N] is already computed)
+#ifndef RF_Q4_TALL_MIN_M
+#define RF_Q4_TALL_MIN_M 256
+#endif
+constexpr int kQ4TallMinM = RF_Q4_TALL_MIN_M;
+
+template <bool ACC, int FMR>
+static void q4_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
+                         const float* G, float* part) {
+    const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ4sBN);
+    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
+    if (S > 1) {
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, false>), dim3((unsigned)(tiles * S)), dim3(kQ4sThreads), 0,
+                           st, A, w, nullptr, M, N, K, nullptr, KSplit{S, part});
+        reduce_for(ACC, G, part, S, M, N, D, st);
+    } else {
+        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, ACC>), dim3((unsigned)tiles), dim3(kQ4sThreads), 0, st, A, w,
+                           D, M, N, K, G, KSplit{1, nullptr});
+    }
+}
+
 template <bool ACC>
 static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
                               const float* G, float* part) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
-    int pick = !ACC && 4 * big >= 3L * device_cu_count() ? 0 : (M <= 64 ? 2 : 4);
-    // 64-row K-sliced tiles also when twice as many of them still fit one
-    // round of CUs (measured on MI355X, N = 4096: M = 256 22.3 against 24.7 us
-    // at K = 4096, 58.4 against 63.1 at K = 12288)
-    if (pick == 4 && 2L * ((M + 127) / 128) * (N / kQ4sBN) <= (long)device_cu_count()) pick = 2;
-    if (pick == 0) {
+    if (!ACC && 4 * big >= 3L * device_cu_count()) {
         if (G != nullptr)
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<3>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
                                M, N, K, G);
@@ -2737,25 +2774,28 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
                                M, N, K, nullptr);
         return hipGetLastError();
     }
-    const long tiles = (long)((M + 32 * pick - 1) / (32 * pick)) * (N / kQ4sBN);
-    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
-    const KSplit sp{S, S > 1 ? part : nullptr};
-    const unsigned grid = (unsigned)(tiles * S);
-    if (S > 1) {
-        if (pick == 2)
-            hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, false>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w,
-                               nullptr, M, N, K, nullptr, sp);
-        else
-            hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, false>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w,
-                               nullptr, M, N, K, nullptr, sp);
-        reduce_for(ACC, G, part, S, M, N, D, st);
-    } else if (pick == 2) {
-        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<2, ACC>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w, D, M, N,
-                           K, G, sp);
-    } else {
-        hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<4, ACC>), dim3(grid), dim3(kQ4sThreads), 0, st, A, w, D, M, N,
-                           K, G, sp);
+    if (M >= kQ4TallMinM) {
+        // 256-row tiles where they fill 3/4 of the CUs unsplit, or where their
+        // K split leaves each workgroup at least 24 super-blocks (measured on
+        // MI355X: 14336 x 4096 at M = 256 43.3 against 53.1 us, 4096 x 12288
+        // at M = 512 68.3 against 72.2; but 4096 x 4096 at M = 512, split in
+        // two, 33.2 against 27.9 for 128-row tiles)
+        const long cus = device_cu_count();
+        const long t8 = (long)((M + 255) / 256) * (N / kQ4sBN);
+        const int s8 = 2 * t8 <= cus ? ksplit_count(t8, K / kQK, M, N, part) : 1;
+        if (4 * t8 >= 3 * cus || (s8 > 1 && (K / kQK) / s8 >= 24)) {
+            q4_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, G, part);
+            return hipGetLastError();
+        }
     }
+    // 64-row K-sliced tiles also when twice as many of them still fit one
+    // round of CUs (measured on MI355X, N = 4096: M = 256 22.3 against 24.7 us
+    // at K = 4096, 58.4 against 63.1 at K = 12288)
+    const bool rows64 = M <= 64 || 2L * ((M + 127) / 128) * (N / kQ4sBN) <= (long)device_cu_count();
+    if (rows64)
+        q4_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, G, part);
+    else
+        q4_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, G, part);
     return hipGetLastError();
 }
 

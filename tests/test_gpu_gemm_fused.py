@@ -90,6 +90,7 @@ def test_segments_match_oracle_and_single(rf, dev, fmt, m, ns, k):
     ("q4_k", 128, 512, 2048),     # K split over 8 workgroups, added onto the caller's values
     ("q6_k", 256, 512, 4096),
     ("q6_k", 512, 1024, 2048),
+    ("q4_k", 512, 4096, 12288),   # 256-row tiles, K split in two, the sum added in the reduction
 ])
 def test_accumulate_adds_to_contents(rf, dev, fmt, m, n, k):
     a = synth.activations(k, seed=3 * m + n, m=m)
@@ -285,12 +286,15 @@ def test_q4k_f16_swiglu(rf, dev, m, n, k, f16):
     assert (err / tol).max() <= 1.0
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 12288, 1024), (256, 12288, 1024), (64, 256, 512), (320, 128, 256)])
+@pytest.mark.parametrize("m,n,k", [(512, 12288, 1024), (256, 12288, 1024), (64, 256, 512), (320, 128, 256),
+                                   (512, 4096, 12288)])
 def test_q4k_f16_swiglu_up(rf, dev, m, n, k):
     # the up GEMM with the SwiGLU in its store (the gate product read back):
     # bit for bit the plain fp16-activation GEMM and the SwiGLU kernel, on
-    # each tile kind (256 x 128 tiles at 512 x 12288, K-sliced 128- and
-    # 64-row tiles, a partial last tile at M = 320)
+    # each tile kind (256 x 128 tiles at 512 x 12288, K-sliced 256-row tiles
+    # unsplit at 256 x 12288 and split over K at 512 x 4096 x 12288 -- the
+    # SwiGLU then in the split reduction --, 128- and 64-row tiles, a partial
+    # last tile at M = 320)
     a = torch.from_numpy(synth.activations(k, seed=m + 3, m=m)).to(torch.bfloat16).float().numpy()
     da = G.to_dev(a.astype(np.float16).view(np.int16))
     wu = G.to_dev(synth.weights("q4_k", n, k, seed=43))
