@@ -1885,16 +1885,38 @@ constexpr int kQ6aRingInstr = 16;                     // 16-byte DMAs per stage
 constexpr int kQ6aStage = kQ6aRingInstr * 1024;       // 16384 B
 constexpr int kQ6aLdsXch = 8 * 3 * 4096;              // 98,304 B: three row blocks of each wave's partial
 
+// DMAs a wave may leave in flight at the end of chunk c = 4 sb + CQ of the
+// K-sliced tiles (q6a_wg, q4s_wg), whose waves issue apw A DMAs per chunk
+// and, in CQ 0, rpw ring DMAs for super-block sb + rs - 1.  In flight: the
+// DMAs of the last `lag` chunks (an A DMA issued in chunk c lands by the end
+// of chunk c + lag, before its buffer's first read in c + lag + 1); with two
+// ring stages the stage loaded in chunk 4 sb is read in chunk 4 sb + 3, so
+// at the end of CQ 2 the window starts after chunk 4 sb.  vmcnt counts in
+// issue order, so completing the oldest DMA completes every older one.
+constexpr int ksplit_dma_out(int cq, int apw, int rpw, int lag, int rs) {
+    const int win = (rs == 2 && cq >= 2 && cq < lag) ? cq : lag;    // chunks in the window, ending at c
+    const int ring_in = win >= 4 ? 1 : (cq < win ? 1 : 0);         // the window holds a CQ 0 chunk
+    return apw * win + rpw * ring_in;
+}
+
+// Tile geometry: FMR = 2 (64 rows, M <= 64) is lean -- two ring stages and
+// six A buffers, 80 KB of LDS, so two workgroups share a CU -- and its K
+// split spreads over twice the CUs (measured on MI355X, 4096 x 14336 at
+// M = 64: 27.3 us against 31.0 for 128-row tiles one per CU; the same
+// geometry for the Q4_K 64-row tiles was slower, 24.0 against 21.0).
 template <int FMR>
 struct Q6aGeom {
     static constexpr int kBM = 32 * FMR;
     static constexpr int kRS = FMR == 4 ? 3 : 2;      // ring stages: super-block sb + kRS - 1 loads while sb is used
-    static constexpr int kABufs = FMR == 4 ? 7 : 4;   // DMA of chunk c + kABufs - 1 issued in chunk c
+    static constexpr int kABufs = FMR == 4 ? 7 : (FMR == 2 ? 6 : 4);   // DMA of chunk c + kABufs - 1 in chunk c
     static constexpr int kLag = kABufs - 3;           // chunks a DMA may stay in flight
-    static constexpr int kABuf = kBM * kKC * 2;       // 16 or 32 KB
+    static constexpr int kABuf = kBM * kKC * 2;       // 8, 16 or 32 KB
     static constexpr int kAPW = FMR / 2;              // A DMAs per wave per chunk (1 KB each)
-    static constexpr int kLdsLoop = kRS * kQ6aStage + kABufs * kABuf;   // 163,840 B for both
-    static constexpr int kLds = kLdsLoop > kQ6aLdsXch ? kLdsLoop : kQ6aLdsXch;
+    static constexpr int kXB = FMR < 4 ? FMR : 4;     // row blocks per exchange round of the K-slice partials
+    static constexpr int kRounds = FMR / kXB;
+    static constexpr int kLdsLoop = kRS * kQ6aStage + kABufs * kABuf;   // 81,920 B (FMR 2) or 163,840 B
+    static constexpr int kLdsXch = 8 * kXB * 4096;    // every wave's partial blocks of one round
+    static constexpr int kLds = kLdsLoop > kLdsXch ? kLdsLoop : kLdsXch;
 };
 constexpr int kQ6aLds = Q6aGeom<4>::kLds;
 
@@ -2101,8 +2123,7 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
         constexpr int P = CQ & 1;
         constexpr int NQ = (CQ + 1) & 3;            // chunk c + 1 within its super-block
         // ring DMAs (issued in CQ 0) among the DMAs of the last kLag chunks
-        constexpr int kRingOut = G::kLag >= 4 ? 1 : (CQ < G::kLag ? 1 : 0);
-        constexpr int kOut = G::kAPW * G::kLag + kRPW * kRingOut;
+        constexpr int kOut = ksplit_dma_out(CQ, G::kAPW, kRPW, G::kLag, G::kRS);
         const int c = 4 * sb + CQ;
         const int sbn = CQ == 3 ? sb + 1 : sb;
         const int abn = ab == G::kABufs - 1 ? 0 : ab + 1;       // chunk c + 1
@@ -2138,55 +2159,43 @@ __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uin
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- K slices, in rounds of four row blocks: wave (ks, cg) keeps row
-    // block 4 rd + ks and hands the other three of the round to the waves of
-    // its column group; [src wave][slot 0..2][e / 4][lane] of float4 (each
-    // access one contiguous 1 KB per wave).  acc is indexed by compile-time
-    // constants only (the round loop is unrolled) ------------------------------
+    // ---- K slices, in rounds of kXB row blocks: every wave parks the round's
+    // blocks in LDS ([wave][block][e / 4][lane] of float4: each access one
+    // contiguous 1 KB per wave); wave (ks, cg), ks < kXB, adds block
+    // kXB rd + ks of column group cg over ks' = 0..3 in that order (acc
+    // indexed by compile-time constants: the round loop is unrolled) ---------
     float4* xch = reinterpret_cast<float4*>(lds);
     const int ncol = n0 + 32 * cg + col;
 #pragma unroll
-    for (int rd = 0; rd < FMR / 4; ++rd) {
+    for (int rd = 0; rd < G::kRounds; ++rd) {
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (i == ks) continue;
-            const int slot = i < ks ? i : i - 1;
+        for (int i = 0; i < G::kXB; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                xch[((wave * 3 + slot) * 4 + q) * 64 + lane] =
-                    make_float4(acc[4 * rd + i][4 * q], acc[4 * rd + i][4 * q + 1], acc[4 * rd + i][4 * q + 2],
-                                acc[4 * rd + i][4 * q + 3]);
-        }
+                xch[((wave * G::kXB + i) * 4 + q) * 64 + lane] =
+                    make_float4(acc[G::kXB * rd + i][4 * q], acc[G::kXB * rd + i][4 * q + 1],
+                                acc[G::kXB * rd + i][4 * q + 2], acc[G::kXB * rd + i][4 * q + 3]);
         __syncthreads();
-        // block 4 rd + ks of the column group: partials of ks' = 0..3 added in that order
-        f32x16 own = acc[4 * rd];
+        if (ks < G::kXB) {
 #pragma unroll
-        for (int i = 1; i < 4; ++i)
-            if (i == ks) own = acc[4 * rd + i];
+            for (int q = 0; q < 4; ++q) {
+                float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int src = 0; src < 4; ++src) {
-                float4 p;
-                if (src == ks) {
-                    p = make_float4(own[4 * q], own[4 * q + 1], own[4 * q + 2], own[4 * q + 3]);
-                } else {
-                    const int slot = ks < src ? ks : ks - 1;
-                    p = xch[(((4 * cg + src) * 3 + slot) * 4 + q) * 64 + lane];
+                for (int src = 0; src < 4; ++src) {
+                    const float4 p = xch[(((4 * cg + src) * G::kXB + ks) * 4 + q) * 64 + lane];
+                    s4[0] += p.x;
+                    s4[1] += p.y;
+                    s4[2] += p.z;
+                    s4[3] += p.w;
                 }
-                s4[0] += p.x;
-                s4[1] += p.y;
-                s4[2] += p.z;
-                s4[3] += p.w;
-            }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int row = m0 + 32 * (4 * rd + ks) + 8 * q + 4 * h + u;
-                if (row < M) {
-                    float* o = D + (size_t)row * N + ncol;
-                    *o = ACC ? *o + s4[u] : s4[u];
+                for (int u = 0; u < 4; ++u) {
+                    const int row = m0 + 32 * (G::kXB * rd + ks) + 8 * q + 4 * h + u;
+                    if (row < M) {
+                        float* o = D + (size_t)row * N + ncol;
+                        *o = ACC ? *o + s4[u] : s4[u];
+                    }
                 }
             }
         }
@@ -2386,8 +2395,7 @@ __device__ __forceinline__ void q4s_wg(const uint16_t* __restrict__ A, const uin
         constexpr int CQ = decltype(cqc)::value;
         constexpr int P = CQ & 1;
         constexpr int NQ = (CQ + 1) & 3;
-        constexpr int kRingOut = G::kLag >= 4 ? 1 : (CQ < G::kLag ? 1 : 0);
-        constexpr int kOut = G::kAPW * G::kLag + 2 * kRingOut;
+        constexpr int kOut = ksplit_dma_out(CQ, G::kAPW, 2, G::kLag, G::kRS);
         const int c = 4 * sb + CQ;
         const int sbn = CQ == 3 ? sb + 1 : sb;
         const int abn = ab == G::kABufs - 1 ? 0 : ab + 1;
@@ -2704,15 +2712,15 @@ static bool gemm_slot(hipStream_t st, GemmSlot* out) {
     return true;
 }
 
-// K split for `tiles` one-per-CU workgroups over nsb super-blocks per row:
-// the largest S <= 8 with tiles * S <= CUs whose M x N partials fit the
-// slot, when at least two splits fit (part == nullptr: no split).
-static int ksplit_count(long tiles, int nsb, int M, int N, const float* part) {
+// K split for `tiles` workgroups over nsb super-blocks per row, `per_cu`
+// of which fit a CU at once: the largest S <= 8 with tiles * S <= per_cu
+// CUs whose M x N partials fit the slot (part == nullptr: no split).
+static int ksplit_count(long tiles, int nsb, int M, int N, const float* part, int per_cu = 1) {
     if (part == nullptr) return 1;
-    const long cus = device_cu_count();
+    const long cap = (long)per_cu * device_cu_count();
     int S = 1;
     for (int s = 2; s <= 8 && s <= nsb; ++s)
-        if (tiles * s <= cus && (size_t)s * M * N * sizeof(float) <= kSlotPartBytes) S = s;
+        if (tiles * s <= cap && (size_t)s * M * N * sizeof(float) <= kSlotPartBytes) S = s;
     return S;
 }
 
@@ -2744,6 +2752,7 @@ static void reduce_for(bool acc, const float* G, const float* part, int S, int M
 #define RF_Q4_TALL_MIN_M 256
 #endif
 constexpr int kQ4TallMinM = RF_Q4_TALL_MIN_M;
+
 
 template <bool ACC, int FMR>
 static void q4_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
@@ -2807,12 +2816,15 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
 #define RF_Q6_TALL_MIN_M 256
 #endif
 constexpr int kQ6TallMinM = RF_Q6_TALL_MIN_M;
+constexpr int kQ6LeanMaxM = 64;      // 64-row tiles up to this M (at M = 128: 40.0 against 33.0 us)
 
 template <bool ACC, int FMR>
 static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
                          float* part) {
     const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ6aBN);
-    const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
+    const int per_cu = FMR == 2 ? 2 : 1;      // the lean 64-row tiles: two workgroups per CU
+    const int S = 2 * tiles <= (long)per_cu * device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part, per_cu)
+                                                                  : 1;
     if (S > 1) {
         hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<false, FMR>), dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0,
                            st, A, w, nullptr, M, N, K, KSplit{S, part});
@@ -2829,6 +2841,8 @@ static hipError_t gemm_q6_f16(const uint16_t* A, const void* W, float* D, int M,
     const uint8_t* w = static_cast<const uint8_t*>(W);
     if (M >= kQ6TallMinM)
         q6_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, part);
+    else if (M <= kQ6LeanMaxM)
+        q6_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, part);
     else
         q6_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, part);
     return hipGetLastError();

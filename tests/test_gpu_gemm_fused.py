@@ -161,11 +161,13 @@ def test_swiglu_pairs_f16_out(rf, dev, fmt, m, n, k):
     np.testing.assert_array_equal(got.view(np.int16), want.view(np.int16))
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 4096, 12288), (192, 128, 2048)])
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 12288), (192, 128, 2048), (64, 256, 4096)])
 def test_q6k_f16_accumulate(rf, dev, m, n, k):
     # inout += product: bit for bit the plain fp16-activation launch plus the
     # old contents (one fp32 add per output), and within the GEMM bar of the
-    # oracle; M = 192 leaves a partial 128-row tile whose rows past M stay put
+    # oracle; M = 192 leaves a partial 128-row tile whose rows past M stay put;
+    # M = 512 (256-row tiles) and M = 64 (64-row tiles, two per CU) split K,
+    # the product then added in the reduction
     a = torch.from_numpy(synth.activations(k, seed=m + 17, m=m)).to(torch.bfloat16).float().numpy()
     w = synth.weights("q6_k", n, k, seed=k + 3)
     da, dw = G.to_dev(a.astype(np.float16).view(np.int16)), G.to_dev(w)
