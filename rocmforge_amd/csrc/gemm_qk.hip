@@ -2500,12 +2500,18 @@ struct F16Segs {
     int q6[3];
     int tiles[3];      // M tiles x column tiles of each segment
 };
-static_assert(kQ6aBM == 128 && kQ6aBN == kQ4sBN && kQ6aThreads == kQ4sThreads, "q6a and q4s tiles differ");
-constexpr int kF16SegLds = kQ6aLds > Q4sGeom<4>::kLds ? kQ6aLds : Q4sGeom<4>::kLds;
+static_assert(kQ6aBN == kQ4sBN && kQ6aThreads == kQ4sThreads, "q6a and q4s tiles differ");
+template <int FMR>
+struct F16SegGeom {
+    static constexpr int kLds = Q6aGeom<FMR>::kLds > Q4sGeom<FMR>::kLds ? Q6aGeom<FMR>::kLds : Q4sGeom<FMR>::kLds;
+};
 
+// FMR = 4 (128-row tiles) or 8 (256-row tiles, each weight dequantised once
+// per 256 rows of A)
+template <int FMR>
 __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uint16_t* __restrict__ A, int M, int K,
                                                                         F16Segs sg) {
-    __shared__ __align__(16) uint8_t lds[kF16SegLds];
+    __shared__ __align__(16) uint8_t lds[F16SegGeom<FMR>::kLds];
     int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     // segment selection by selects (no runtime index into the argument)
     const int s = v < sg.tiles[0] ? 0 : (v < sg.tiles[0] + sg.tiles[1] ? 1 : 2);
@@ -2515,9 +2521,9 @@ __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uin
     const int n = s == 0 ? sg.n[0] : (s == 1 ? sg.n[1] : sg.n[2]);
     const int q6 = s == 0 ? sg.q6[0] : (s == 1 ? sg.q6[1] : sg.q6[2]);
     if (q6)
-        q6a_wg<false>(A, w, d, M, n, K, v, lds);
+        q6a_wg<false, FMR>(A, w, d, M, n, K, v, lds);
     else
-        q4s_wg<4, false>(A, w, d, M, n, K, v, lds);
+        q4s_wg<FMR, false>(A, w, d, M, n, K, v, lds);
 }
 
 static GemmSegs single_seg(int N) {
@@ -2876,10 +2882,17 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Column segments on fp16 activations (rf_gemm_f16_segs_kernel): up to three
 // weight matrices over one input, each Q4_K or Q6_K with its own output.
 // The caller has checked the shapes and alignment.
+#ifndef RF_SEG_TALL_MIN_M
+#define RF_SEG_TALL_MIN_M 256
+#endif
 static hipError_t f16_segments(const uint16_t* A, const void* const ws[3], const int q6[3], float* const ds[3],
                                const int ns[3], int M, int K, hipStream_t st) {
     F16Segs sg{};
-    const int mtiles = (M + 127) / 128;
+    // 256-row tiles from M = RF_SEG_TALL_MIN_M, else 128-row tiles (measured on
+    // MI355X: the Qwen3-8B prefill of 512 tokens, Q/K/V of 4096 + 1024 + 1024
+    // rows: 11.38 against 11.78 ms -- 192 tiles, one round of CUs, against 384)
+    const bool tall = M >= RF_SEG_TALL_MIN_M;
+    const int mtiles = tall ? (M + 255) / 256 : (M + 127) / 128;
     long total = 0;
     for (int i = 0; i < 3; ++i) {
         if (ns[i] == 0) continue;
@@ -2891,7 +2904,10 @@ static hipError_t f16_segments(const uint16_t* A, const void* const ws[3], const
         total += sg.tiles[i];
     }
     if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rf_gemm_f16_segs_kernel, dim3((unsigned)total), dim3(kQ4sThreads), 0, st, A, M, K, sg);
+    if (tall)
+        hipLaunchKernelGGL(rf_gemm_f16_segs_kernel<8>, dim3((unsigned)total), dim3(kQ4sThreads), 0, st, A, M, K, sg);
+    else
+        hipLaunchKernelGGL(rf_gemm_f16_segs_kernel<4>, dim3((unsigned)total), dim3(kQ4sThreads), 0, st, A, M, K, sg);
     return hipGetLastError();
 }
 
