@@ -1461,11 +1461,6 @@ __device__ __forceinline__ uint2 f16a_dq4(uint32_t w, uint32_t m, float D, float
     return make_uint2(cvt_pk_f16(v0, v1), cvt_pk_f16(v2, v3));
 }
 
-// 16 bytes a lane from global memory straight into LDS at m0 + 16 lane
-__device__ __forceinline__ void lds_dma16(uint32_t lds_dst, uint32_t voff, const uint8_t* sbase) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                 :: "s"(lds_dst), "v"(voff), "s"(sbase) : "memory", "m0");
-}
 
 // PAIR (gate and up in one tile, SwiGLU in the epilogue): the tile's 128
 // weight rows are gate rows [n0, n0 + 64) of W (waves 0-1) and the same up

@@ -449,6 +449,12 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Device CU count, cached per device (host side).
+// 16 bytes a lane from global memory straight into LDS at m0 + 16 lane
+__device__ __forceinline__ void lds_dma16(uint32_t lds_dst, uint32_t voff, const uint8_t* sbase) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(lds_dst), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+
 int device_cu_count();
 
 }  // namespace rf
