@@ -102,8 +102,11 @@ hipError_t gemv_q6_k_f32_residual_launch(const void* weights_q6_k, const float* 
  * tiles of rf_gemm_q*_k_f16_launch run on it; small launches split K over
  * workgroups and add the partial tiles in a fixed order, so every output is
  * the same sum on every run.  Launches on one stream share its slot (stream
- * order); a fifth stream on a GPU gets the fp32-activation tiles instead
- * (same values up to summation order).  Q6_K takes the fp16 tiles when
+ * order); a stream without one takes a free slot or, outside stream
+ * capture, the slot of an idle stream (hipStreamQuery), else the
+ * fp32-activation tiles run (same values up to summation order).  A stream
+ * that will be captured should launch a GEMM once before its capture, so
+ * that it holds a slot.  Q6_K takes the fp16 tiles when
  * K % 2048 == 0 and the weights are 16-byte aligned. */
 hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weights_q4_k, float* output, int M, int N, int K,
                                  hipStream_t stream);

@@ -2661,14 +2661,19 @@ static unsigned stream_grid(size_t n4) { return (unsigned)std::min<size_t>((n4 +
 // Library-owned scratch: kGemmSlots slots per GPU in a file-scope device
 // array (allocated when the library's code object loads on that GPU, held
 // until the process ends; the launchers never allocate).  A slot serves one
-// stream: its first kSlotABytes hold the fp16 copy of A, the rest the K-split
-// partials.  Launches on one stream are ordered, so they share its slot
-// safely; each further stream (up to kGemmSlots per GPU) gets a slot of its
-// own, and launches on streams past that take the unstaged fp32 kernels.  A
-// captured graph keeps the slot address of the stream it was captured on:
-// replaying it concurrently with other work of that stream races.  In host
-// code the array's name is only a stand-in; its device address is taken once
-// per GPU with hipGetSymbolAddress.
+// stream at a time: its first kSlotABytes hold the fp16 copy of A, the rest
+// the K-split partials.  Launches on one stream are ordered, so they share
+// its slot safely.  A stream without a slot takes a free one, else (outside
+// stream capture) one whose stream is idle (hipStreamQuery: a host-side
+// query, nothing enqueued), else runs the unstaged fp32 kernels.  A slot
+// claimed under stream capture stays with the capturing stream (the graph
+// holds its address; replaying that graph concurrently with other GEMM work
+// of the same stream races), and so does the slot of a stream that has been
+// destroyed.  The hand-over assumes one host thread launching on a GPU at a
+// time (the reference's contract): a slot taken from an idle stream whose
+// own thread is between claiming and enqueuing would be shared.  In host
+// code the array's name is only a stand-in; its device address is taken
+// once per GPU with hipGetSymbolAddress.
 constexpr int kGemmSlots = 4;
 constexpr size_t kSlotABytes = (size_t)32 << 20;
 constexpr size_t kSlotPartBytes = (size_t)24 << 20;
@@ -2681,32 +2686,41 @@ struct GemmSlot {
     float* part;        // kSlotPartBytes
 };
 
+struct SlotState {
+    hipStream_t owner;
+    bool taken;
+    bool captured;      // claimed under stream capture: never handed on
+};
 static std::mutex g_slot_mutex;
 static uint8_t* g_slot_base[kGemmMaxDevices];
-static hipStream_t g_slot_owner[kGemmMaxDevices][kGemmSlots];
-static bool g_slot_taken[kGemmMaxDevices][kGemmSlots];
+static SlotState g_slots[kGemmMaxDevices][kGemmSlots];
 
-// The slot of `st` on the current device (claimed on its first use); false
-// when every slot belongs to another stream or the array is unavailable.
+// The slot of `st` on the current device: its own, a free one, or (outside
+// stream capture, where stream queries are not allowed) one whose stream is
+// idle; false when none is available.
 static bool gemm_slot(hipStream_t st, GemmSlot* out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kGemmMaxDevices) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> lock(g_slot_mutex);
     if (g_slot_base[dev] == nullptr) {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(gemm_scratch)) != hipSuccess || p == nullptr) return false;
         g_slot_base[dev] = static_cast<uint8_t*>(p);
     }
+    SlotState* sl = g_slots[dev];
     int k = -1;
     for (int i = 0; i < kGemmSlots && k < 0; ++i)
-        if (g_slot_taken[dev][i] && g_slot_owner[dev][i] == st) k = i;
+        if (sl[i].taken && sl[i].owner == st) k = i;
     for (int i = 0; i < kGemmSlots && k < 0; ++i)
-        if (!g_slot_taken[dev][i]) {
-            g_slot_taken[dev][i] = true;
-            g_slot_owner[dev][i] = st;
-            k = i;
-        }
+        if (!sl[i].taken) k = i;
+    for (int i = 0; i < kGemmSlots && k < 0 && !capturing; ++i)
+        if (!sl[i].captured && hipStreamQuery(sl[i].owner) == hipSuccess) k = i;
     if (k < 0) return false;
+    sl[k].taken = true;
+    sl[k].owner = st;
+    sl[k].captured = sl[k].captured || capturing;
     uint8_t* b = g_slot_base[dev] + (size_t)k * kSlotBytes;
     out->a = reinterpret_cast<uint16_t*>(b);
     out->part = reinterpret_cast<float*>(b + kSlotABytes);

@@ -247,3 +247,91 @@ def test_gemm_zero_padded_rows(rf, dev):
     got = _run(rf, "q4_k", a, w, m, n, k)
     assert np.all(got[77:] == 0.0)
     _check(got, "q4_k", a, w, m, n, k, "padded")
+
+
+def test_gemm_staging_slots_across_streams(rf, dev):
+    # The fp32-activation entry points stage A in a per-stream slot of the
+    # library (4 per GPU).  Six streams launching at once: every result
+    # within the GEMM bar of the oracle (streams without a slot take the fp32
+    # kernels); once they have finished, their slots pass to new streams, and
+    # every stream then gives the bits of the staged path.
+    m, n, k = 64, 512, 1024
+    cases = []
+    for i in range(6):
+        a = synth.activations(k, seed=100 + i, m=m)
+        w = synth.weights("q4_k", n, k, seed=200 + i)
+        cases.append((a, w, G.to_dev(a), G.to_dev(w)))
+    ref_bits = []
+    for a, w, da, dw in cases:                      # the current stream: staged path
+        d = G.empty(m * n, torch.float32)
+        G.call(rf.wmma_gemm_q4_k_launch, G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k)
+        ref_bits.append(G.host(d))
+    for rnd in range(2):
+        streams = [torch.cuda.Stream() for _ in range(6)]
+        outs = [G.empty(m * n, torch.float32) for _ in range(6)]
+        torch.cuda.synchronize()
+        for (a, w, da, dw), s, d in zip(cases, streams, outs):
+            rc = rf.wmma_gemm_q4_k_launch(G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k, ctypes.c_void_p(s.cuda_stream))
+            assert rc == 0
+        torch.cuda.synchronize()
+        for i, ((a, w, da, dw), d) in enumerate(zip(cases, outs)):
+            _check(G.host(d).reshape(m, n), "q4_k", a, w, m, n, k, f"stream {i} round {rnd}")
+        # one stream at a time, each after the last finished: every one gets a slot
+        for (a, w, da, dw), s, d, rb in zip(cases, streams, outs, ref_bits):
+            rc = rf.wmma_gemm_q4_k_launch(G.ptr(da), G.ptr(dw), G.ptr(d), m, n, k, ctypes.c_void_p(s.cuda_stream))
+            assert rc == 0
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(G.host(d), rb)
+        del streams
+
+
+@pytest.mark.parametrize("warm", [True, False])
+def test_gemm_reference_entry_points_capture(rf, dev, warm):
+    # wmma_gemm_q4_k_launch / wmma_gemm_q6_k_launch captured into a HIP graph
+    # (staging pass, K-split GEMM and reduction).  A stream that has launched
+    # a GEMM before holds a staging slot, so its capture runs the staged path:
+    # every replay, with eager GEMM work in between, gives the eager result bit
+    # for bit.  A stream whose first GEMM is captured can only take a free
+    # slot (slots are not handed over during capture), else the fp32 kernels:
+    # every replay the same bits, within the GEMM bar of the oracle
+    shapes = [("q4_k", 64, 512, 1024), ("q6_k", 64, 256, 2048), ("q6_k", 256, 512, 4096)]
+    bufs = []
+    for fmt, m, n, k in shapes:
+        a = synth.activations(k, seed=m + n, m=m)
+        w = synth.weights(fmt, n, k, seed=k + 5)
+        da, dw = G.to_dev(a), G.to_dev(w)
+        eager, out = G.empty(m * n, torch.float32), G.empty(m * n, torch.float32)
+        fn = rf.wmma_gemm_q4_k_launch if fmt == "q4_k" else rf.wmma_gemm_q6_k_launch
+        G.call(fn, G.ptr(da), G.ptr(dw), G.ptr(eager), m, n, k)
+        bufs.append((fmt, m, n, k, a, w, da, dw, eager, out, fn))
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    if warm:
+        for fmt, m, n, k, a, w, da, dw, eager, out, fn in bufs:
+            assert fn(G.ptr(da), G.ptr(dw), G.ptr(out), m, n, k, ctypes.c_void_p(cs.cuda_stream)) == 0
+        torch.cuda.synchronize()
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(g, stream=cs):
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for fmt, m, n, k, a, w, da, dw, eager, out, fn in bufs:
+                assert fn(G.ptr(da), G.ptr(dw), G.ptr(out), m, n, k, st) == 0
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    first = None
+    for rep in range(3):
+        for *_, out, fn in bufs:
+            out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [G.host(b[9]) for b in bufs]
+        first = first or got
+        for (fmt, m, n, k, a, w, da, dw, eager, out, fn), o, f in zip(bufs, got, first):
+            np.testing.assert_array_equal(o, f)                 # every replay the same bits
+            if warm:
+                np.testing.assert_array_equal(o, G.host(eager))
+            # eager work on the current stream between replays
+            G.call(fn, G.ptr(da), G.ptr(dw), G.ptr(eager), m, n, k)
+    for (fmt, m, n, k, a, w, *_), o in zip(bufs, first):
+        _check(o.reshape(m, n), fmt, a, w, m, n, k, f"captured {fmt} {m}x{n}x{k}")
