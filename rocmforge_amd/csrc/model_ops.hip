@@ -280,27 +280,53 @@ __global__ void rf_kv_write_batched_kernel(__half* kc, __half* vc, const float* 
 // rope_pair takes (theta_i from the caller's table when given, divided by
 // freq_scale[i] when given), or the same values from a rf_rope_cos_sin_kernel
 // table row: the rotations match the per-element RoPE launchers bit for bit.
+// In two halves for a caller that issues other loads in between: the lane's
+// (cos, sin) values (from the table row, or evaluated), then their LDS
+// store.  N = pairs per lane (D / 2 over 64 lanes, at least 1).
 template <int LPP>
-__device__ __forceinline__ void wave_cos_sin(float2* w, const float2* __restrict__ cs_row,
-                                             const float* __restrict__ tab, float base,
-                                             const float* __restrict__ freq_scale, int pos, int lane) {
+struct CsLane {
+    static constexpr int N = (4 * LPP + 63) / 64;
+    float2 c[N];
+};
+template <int LPP>
+__device__ __forceinline__ CsLane<LPP> wave_cos_sin_get(const float2* __restrict__ cs_row,
+                                                       const float* __restrict__ tab, float base,
+                                                       const float* __restrict__ freq_scale, int pos, int lane) {
     constexpr int H = 4 * LPP;   // D / 2
+    CsLane<LPP> r;
 #pragma unroll
-    for (int i = lane; i < H; i += 64) {
-        float2 c;
+    for (int k = 0; k < CsLane<LPP>::N; ++k) {
+        const int i = lane + 64 * k;
+        if (i >= H) break;
         if (cs_row != nullptr) {
-            c = cs_row[i];
+            r.c[k] = cs_row[i];
         } else {
             const float a = (float)pos * rope_theta(i, 8 * LPP, base, tab, freq_scale);
-            c = make_float2(cosf(a), sinf(a));
+            r.c[k] = make_float2(cosf(a), sinf(a));
         }
-        w[i] = c;
+    }
+    return r;
+}
+template <int LPP>
+__device__ __forceinline__ void wave_cos_sin_put(float2* w, const CsLane<LPP>& r, int lane) {
+    constexpr int H = 4 * LPP;
+#pragma unroll
+    for (int k = 0; k < CsLane<LPP>::N; ++k) {
+        const int i = lane + 64 * k;
+        if (i >= H) break;
+        w[i] = r.c[k];
     }
     // the slice is the wave's own: a wave-scope fence orders the writes
     // before the other lanes' reads
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+template <int LPP>
+__device__ __forceinline__ void wave_cos_sin(float2* w, const float2* __restrict__ cs_row,
+                                             const float* __restrict__ tab, float base,
+                                             const float* __restrict__ freq_scale, int pos, int lane) {
+    wave_cos_sin_put<LPP>(w, wave_cos_sin_get<LPP>(cs_row, tab, base, freq_scale, pos, lane), lane);
 }
 
 // The lane's (cos, sin) pairs from a wave_cos_sin slice: NeoX pairs (i,
@@ -636,12 +662,14 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
     // loads in the order they are needed: q, (owner) the raw k / v, then the first chunk
     float qv[8], kx[8], vx[8], gq[8], gk[8];
     float2 cv[8];
+    CsLane<LPP> csl;
     load8(q + (size_t)head * D + 8 * sub, qv);
     if constexpr (QK) {
         if (qk.q_norm != nullptr) load8(qk.q_norm + 8 * sub, gq);
-        wave_cos_sin<LPP>(lcs[wave], qk.cs != nullptr ? qk.cs + (size_t)pos * (D / 2) : nullptr, qk.tab, qk.base,
-                          qk.freq_scale, pos, lane);
-        cs8<LPP>(lcs[wave], sub, qk.neox, cv);
+        // the cos / sin values now, their LDS slice after the first chunk's
+        // K / V loads are issued (the slice waits for this load only)
+        csl = wave_cos_sin_get<LPP>(qk.cs != nullptr ? qk.cs + (size_t)pos * (D / 2) : nullptr, qk.tab, qk.base,
+                                    qk.freq_scale, pos, lane);
     }
     if (owner && wave == 0) {
         load8(qk.k + (size_t)kvh * D + 8 * sub, kx);
@@ -662,6 +690,8 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
         }
         if constexpr (QK) {
             if (c0 == split * kSplitChunk) {     // first chunk: the per-head step, while the loads fly
+                wave_cos_sin_put<LPP>(lcs[wave], csl, lane);
+                cs8<LPP>(lcs[wave], sub, qk.neox, cv);
                 head_norm_rope<LPP>(qv, sub, qk.q_norm != nullptr, gq, qk.eps, cv, qk.neox);
                 if (owner) {
                     if (wave == 0) {
@@ -750,8 +780,12 @@ __global__ __launch_bounds__(512) void rf_attn_split_kernel(const float* __restr
 }
 
 // One workgroup per head: thread t takes float4 dim-chunk t % (D / 4) of
-// the splits congruent to t / (D / 4), all its loads issued together; the
+// the splits congruent to t / (D / 4); the first wave takes the (m, l) of
+// split = lane.  Every load is issued before the first use (one round trip):
+// the accumulators of empty splits are loaded too (their slots hold
+// whatever the workspace held) and weighted by 0 through a select.  The
 // split groups are added in LDS.
+constexpr int kMergeSplitsPerThread = 8;    // kMaxSplits / (256 / (D / 4)) for D = 128
 __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restrict__ ws, float* __restrict__ out,
                                                             int nh, int D, int S) {
     __shared__ float fs[64];
@@ -760,12 +794,39 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
     const int head = blockIdx.x;
     const int t = threadIdx.x;
     const float* base = ws + (size_t)head * S * (D + 4);
-    if (t < 64) {
-        float mv = kNegMax, lv = 0.0f;
-        if (t < S) {
-            mv = base[(size_t)t * (D + 4) + D];
-            lv = base[(size_t)t * (D + 4) + D + 1];
+    const int nch = D / 4;                  // 16, 32 or 64 dim-chunks
+    const int ngr = 256 / nch;              // split groups
+    const int ch = t % nch, gr = t / nch;
+    float mv = kNegMax, lv = 0.0f;
+    if (t < 64 && t < S) {
+        mv = base[(size_t)t * (D + 4) + D];
+        lv = base[(size_t)t * (D + 4) + D + 1];
+    }
+    constexpr int U = kMergeSplitsPerThread;
+    float4 v[U];
+    auto load = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u * ngr;
+            v[u] = s < S ? *reinterpret_cast<const float4*>(base + (size_t)s * (D + 4) + 4 * ch)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    };
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u * ngr;
+            const float f = s < S ? fs[s] : 0.0f;
+            const bool use = f > 0.0f;
+            a.x += use ? f * v[u].x : 0.0f;
+            a.y += use ? f * v[u].y : 0.0f;
+            a.z += use ? f * v[u].z : 0.0f;
+            a.w += use ? f * v[u].w : 0.0f;
+        }
+    };
+    load(gr);                               // in flight with the (m, l) loads
+    if (t < 64) {
         float M = mv;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
@@ -777,26 +838,10 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
         if (t == 0) lt_s = lt;
     }
     __syncthreads();
-    const int nch = D / 4;                  // 16, 32 or 64 dim-chunks
-    const int ngr = 256 / nch;              // split groups
-    const int ch = t % nch, gr = t / nch;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = gr; s0 < S; s0 += 4 * ngr) {
-        float4 v[4];
-        float f[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int s = s0 + u * ngr;
-            f[u] = s < S ? fs[s] : 0.0f;
-            // an empty split wrote no acc: its slots hold whatever the
-            // workspace held before, so they are never read
-            v[u] = f[u] > 0.0f ? *reinterpret_cast<const float4*>(base + (size_t)s * (D + 4) + 4 * ch)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            a.x += f[u] * v[u].x; a.y += f[u] * v[u].y; a.z += f[u] * v[u].z; a.w += f[u] * v[u].w;
-        }
+    add(gr);
+    for (int s0 = gr + U * ngr; s0 < S; s0 += U * ngr) {   // D = 256 with more than 32 splits
+        load(s0);
+        add(s0);
     }
     part[t] = a;
     __syncthreads();
