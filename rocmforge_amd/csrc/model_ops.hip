@@ -818,11 +818,13 @@ __global__ __launch_bounds__(256) void rf_attn_merge_kernel(const float* __restr
         for (int u = 0; u < U; ++u) {
             const int s = s0 + u * ngr;
             const float f = s < S ? fs[s] : 0.0f;
-            const bool use = f > 0.0f;
-            a.x += use ? f * v[u].x : 0.0f;
-            a.y += use ? f * v[u].y : 0.0f;
-            a.z += use ? f * v[u].z : 0.0f;
-            a.w += use ? f * v[u].w : 0.0f;
+            // an empty split's slots are zeroed by a select (they may hold
+            // anything), then one fma per element
+            const float4 w = f > 0.0f ? v[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+            a.x = __builtin_fmaf(f, w.x, a.x);
+            a.y = __builtin_fmaf(f, w.y, a.y);
+            a.z = __builtin_fmaf(f, w.z, a.z);
+            a.w = __builtin_fmaf(f, w.w, a.w);
         }
     };
     load(gr);                               // in flight with the (m, l) loads
