@@ -1462,6 +1462,17 @@ __device__ __forceinline__ uint2 f16a_dq4(uint32_t w, uint32_t m, float D, float
 }
 
 
+// K split of the fp16-activation tiles (rf_gemm_q4k_f16a_kernel, q6a_wg, q4s_wg): with S > 1 the
+// launch holds S x tiles workgroups, tile v of split s at s * tiles + v (the
+// workgroups of one split neighbours, so one XCD mostly reads one K range of
+// A), split s covers super-blocks [s nsb / S, (s + 1) nsb / S) of every row
+// and stores its partial tile to part + s * M * N (row-major M x N, plain
+// stores); rf_gemm_split_reduce_kernel adds the S partials in split order.
+struct KSplit {
+    int S;
+    float* part;
+};
+
 // PAIR (gate and up in one tile, SwiGLU in the epilogue): the tile's 128
 // weight rows are gate rows [n0, n0 + 64) of W (waves 0-1) and the same up
 // rows of W1 (waves 2-3), n0 = 64 per column tile; after the K halves are
@@ -1469,13 +1480,14 @@ __device__ __forceinline__ uint2 f16a_dq4(uint32_t w, uint32_t m, float D, float
 // store silu(gate) * up into D[M x N] (N = the gate/up row count) as fp32
 // (PAIR 1) or rounded to fp16 (PAIR 2, D read as halves).  PAIR 3: a plain
 // tile whose store is the up projection of a SwiGLU, fp16 silu(G) * sum
-// with the gate product G [M x N] read back.
+// with the gate product G [M x N] read back.  sp: K split (plain tiles,
+// PAIR_ARG 0, only).
 template <int PAIR_ARG>
 __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const uint16_t* __restrict__ A,
                                                                          const uint8_t* __restrict__ W,
                                                                          const uint8_t* __restrict__ W1,
                                                                          float* __restrict__ D, int M, int N, int K,
-                                                                         const float* __restrict__ G) {
+                                                                         const float* __restrict__ G, KSplit sp) {
     constexpr int PAIR = PAIR_ARG == 3 ? 0 : PAIR_ARG;      // 3: a plain tile, gated store
     // one LDS block: ring (2 stages), A (3 buffers), scale tables (2); after
     // the loop its first 128 KB carry the K-half exchange
@@ -1492,12 +1504,21 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
     const int kh = wave & 1, wn = wave >> 1;
     const int h = lane >> 5, col = lane & 31;
     const int mtiles = (M + kF16aBM - 1) / kF16aBM;
-    const int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int m0 = (v % mtiles) * kF16aBM;      // the M tiles of one column tile are neighbours
-    const int n0 = (v / mtiles) * (PAIR ? kF16aBN / 2 : kF16aBN);
-    const int nchunks = K / kKC;
-    const int nsb = K / kQK;
-    const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+    int v = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int nsb_row = K / kQK;
+    int sb0 = 0, nsb = nsb_row;                // this workgroup's super-blocks [sb0, sb0 + nsb) of each row
+    if (PAIR_ARG == 0 && sp.S > 1) {
+        const int per = mtiles * (N / kF16aBN);
+        const int s = v / per;
+        v -= s * per;
+        sb0 = __builtin_amdgcn_readfirstlane(s * nsb_row / sp.S);
+        nsb = __builtin_amdgcn_readfirstlane((s + 1) * nsb_row / sp.S - sb0);
+        D = sp.part + (size_t)s * M * N;
+    }
+    const int m0 = __builtin_amdgcn_readfirstlane((v % mtiles) * kF16aBM);   // the M tiles of one column tile are neighbours
+    const int n0 = __builtin_amdgcn_readfirstlane((v / mtiles) * (PAIR ? kF16aBN / 2 : kF16aBN));
+    const int nchunks = 4 * nsb;
+    const uint32_t row_bytes = (uint32_t)nsb_row * kQ4KBytes;
 
     // ---- weight ring: stage = super-block sb of the tile's 128 rows; group
     // g of 64 lanes moves 16-byte pieces [64 g, 64 g + 64) (row pc / 9; with
@@ -1516,12 +1537,12 @@ __global__ __launch_bounds__(kF16aThreads) void rf_gemm_q4k_f16a_kernel(const ui
     }
     auto w_dma1 = [&](int t, int sb, int slot) {
         lds_dma16(__builtin_amdgcn_readfirstlane(ring_lds0 + (uint32_t)slot * kF16aStage + gdst[t]), goff[t],
-                  (gup[t] ? w1_tile : w_tile) + (size_t)min(sb, nsb - 1) * kQ4KBytes);
+                  (gup[t] ? w1_tile : w_tile) + (size_t)(sb0 + min(sb, nsb - 1)) * kQ4KBytes);
     };
 
     // ---- A: instruction gi = 8 wave + g covers rows 8 gi + L / 8 of the chunk,
     // position L % 8 (k piece (L % 8) ^ g(row)); rows past M read row M - 1 --
-    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + (size_t)m0 * K * 2;
+    const uint8_t* a_tile = reinterpret_cast<const uint8_t*>(A) + ((size_t)m0 * K + (size_t)sb0 * kQK) * 2;
     uint32_t dma_voff[kF16aANI];
 #pragma unroll
     for (int g = 0; g < kF16aANI; ++g) {
@@ -1929,16 +1950,6 @@ __device__ __forceinline__ u32x2 q6a_dq4(uint32_t qb, float S24, float nO) {
 }
 
 // Tile v of the launch (after the XCD remap); lds: the kLds-byte LDS block.
-// K split of the fp16-activation tiles (q6a_wg, q4s_wg): with S > 1 the
-// launch holds S x tiles workgroups, tile v of split s at s * tiles + v (the
-// workgroups of one split neighbours, so one XCD mostly reads one K range of
-// A), split s covers super-blocks [s nsb / S, (s + 1) nsb / S) of every row
-// and stores its partial tile to part + s * M * N (row-major M x N, plain
-// stores); rf_gemm_split_reduce_kernel adds the S partials in split order.
-struct KSplit {
-    int S;
-    float* part;
-};
 
 template <bool ACC, int FMR = 4>
 __device__ __forceinline__ void q6a_wg(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
@@ -2661,8 +2672,9 @@ static unsigned stream_grid(size_t n4) { return (unsigned)std::min<size_t>((n4 +
 // Library-owned scratch: kGemmSlots slots per GPU in a file-scope device
 // array (allocated when the library's code object loads on that GPU, held
 // until the process ends; the launchers never allocate).  A slot serves one
-// stream at a time: its first kSlotABytes hold the fp16 copy of A, the rest
-// the K-split partials.  Launches on one stream are ordered, so they share
+// stream at a time: on the fp32-activation launchers its first bytes hold
+// the fp16 copy of A (up to kSlotABytes) and the K-split partials follow it;
+// on the fp16-activation launchers the whole slot takes partials.  Launches on one stream are ordered, so they share
 // its slot safely.  A stream without a slot takes a free one, else (outside
 // stream capture) one whose stream is idle (hipStreamQuery: a host-side
 // query, nothing enqueued), else runs the unstaged fp32 kernels.  A slot
@@ -2682,9 +2694,20 @@ static __device__ __align__(256) uint8_t gemm_scratch[kGemmSlots * kSlotBytes];
 constexpr int kGemmMaxDevices = 64;
 
 struct GemmSlot {
-    uint16_t* a;        // kSlotABytes
-    float* part;        // kSlotPartBytes
+    uint16_t* a;        // the slot's kSlotBytes
 };
+
+// Room for K-split partials: the whole slot on the fp16-activation
+// launchers, the part after the staged rows of A on the fp32 ones (at least
+// kSlotPartBytes).
+struct PartBuf {
+    float* p;
+    size_t bytes;
+};
+static PartBuf slot_parts(const GemmSlot& slot, size_t a_bytes) {
+    const size_t off = (a_bytes + 255) & ~(size_t)255;
+    return PartBuf{reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(slot.a) + off), kSlotBytes - off};
+}
 
 struct SlotState {
     hipStream_t owner;
@@ -2723,19 +2746,18 @@ static bool gemm_slot(hipStream_t st, GemmSlot* out) {
     sl[k].captured = sl[k].captured || capturing;
     uint8_t* b = g_slot_base[dev] + (size_t)k * kSlotBytes;
     out->a = reinterpret_cast<uint16_t*>(b);
-    out->part = reinterpret_cast<float*>(b + kSlotABytes);
     return true;
 }
 
 // K split for `tiles` workgroups over nsb super-blocks per row, `per_cu`
 // of which fit a CU at once: the largest S <= 8 with tiles * S <= per_cu
-// CUs whose M x N partials fit the slot (part == nullptr: no split).
-static int ksplit_count(long tiles, int nsb, int M, int N, const float* part, int per_cu = 1) {
-    if (part == nullptr) return 1;
+// CUs whose M x N partials fit part (part.p == nullptr: no split).
+static int ksplit_count(long tiles, int nsb, int M, int N, const PartBuf& part, int per_cu = 1) {
+    if (part.p == nullptr) return 1;
     const long cap = (long)per_cu * device_cu_count();
     int S = 1;
     for (int s = 2; s <= 8 && s <= nsb; ++s)
-        if (tiles * s <= cap && (size_t)s * M * N * sizeof(float) <= kSlotPartBytes) S = s;
+        if (tiles * s <= cap && (size_t)s * M * N * sizeof(float) <= part.bytes) S = s;
     return S;
 }
 
@@ -2760,7 +2782,7 @@ static void reduce_for(bool acc, const float* G, const float* part, int S, int M
 // K-sliced tiles (rf_gemm_q4k_f16s_kernel) of 256 rows (from M =
 // kQ4TallMinM: each weight dequantised once per 256 rows), 64 rows (M <= 64,
 // or when they come to at most one round of CUs) or 128, split over K when
-// they leave at least half the CUs idle and `part` (kSlotPartBytes) is given.
+// they leave at least half the CUs idle and `part` is given.
 // G: when given, D receives fp16 silu(G) * (A W^T) (the up projection of a
 // SwiGLU whose gate product G [M x N] is already computed)
 #ifndef RF_Q4_TALL_MIN_M
@@ -2771,13 +2793,13 @@ constexpr int kQ4TallMinM = RF_Q4_TALL_MIN_M;
 
 template <bool ACC, int FMR>
 static void q4_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
-                         const float* G, float* part) {
+                         const float* G, const PartBuf& part) {
     const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ4sBN);
     const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
     if (S > 1) {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, false>), dim3((unsigned)(tiles * S)), dim3(kQ4sThreads), 0,
-                           st, A, w, nullptr, M, N, K, nullptr, KSplit{S, part});
-        reduce_for(ACC, G, part, S, M, N, D, st);
+                           st, A, w, nullptr, M, N, K, nullptr, KSplit{S, part.p});
+        reduce_for(ACC, G, part.p, S, M, N, D, st);
     } else {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, ACC>), dim3((unsigned)tiles), dim3(kQ4sThreads), 0, st, A, w,
                            D, M, N, K, G, KSplit{1, nullptr});
@@ -2786,17 +2808,34 @@ static void q4_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, i
 
 template <bool ACC>
 static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
-                              const float* G, float* part) {
+                              const float* G, const PartBuf& part) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     if (!ACC && 4 * big >= 3L * device_cu_count()) {
         if (G != nullptr)
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<3>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
-                               M, N, K, G);
+                               M, N, K, G, KSplit{1, nullptr});
         else
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)big), dim3(kF16aThreads), 0, st, A, w, w, D,
-                               M, N, K, nullptr);
+                               M, N, K, nullptr, KSplit{1, nullptr});
         return hipGetLastError();
+    }
+    if (M >= kQ4TallMinM && big > 0) {
+        // 256 x 128 tiles split over K where the split brings them to at
+        // least three quarters of the CUs and leaves each split >= 12
+        // super-blocks (measured on MI355X, fp16 A: 4096 x 12288 at M = 512
+        // split in 4, 60.9 against 68.3 us for the 256 x 64 tiles split in
+        // 2; with 8 super-blocks per split, 14336 x 4096 at M = 256, 45.0
+        // against 43.5; with 4, 4096 x 4096 at M = 512, 34.8 against 27.9)
+        const long cus = device_cu_count();
+        const int nsb = K / kQK;
+        const int S = ksplit_count(big, nsb, M, N, part);
+        if (S > 1 && 4 * big * S >= 3 * cus && nsb / S >= 12) {
+            hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)(big * S)), dim3(kF16aThreads), 0, st, A, w,
+                               w, nullptr, M, N, K, nullptr, KSplit{S, part.p});
+            reduce_for(ACC, G, part.p, S, M, N, D, st);
+            return hipGetLastError();
+        }
     }
     if (M >= kQ4TallMinM) {
         // 256-row tiles where they fill 3/4 of the CUs unsplit, or where their
@@ -2835,15 +2874,15 @@ constexpr int kQ6LeanMaxM = 64;      // 64-row tiles up to this M (at M = 128: 4
 
 template <bool ACC, int FMR>
 static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
-                         float* part) {
+                         const PartBuf& part) {
     const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ6aBN);
     const int per_cu = FMR == 2 ? 2 : 1;      // the lean 64-row tiles: two workgroups per CU
     const int S = 2 * tiles <= (long)per_cu * device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part, per_cu)
                                                                   : 1;
     if (S > 1) {
         hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<false, FMR>), dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0,
-                           st, A, w, nullptr, M, N, K, KSplit{S, part});
-        reduce_for(ACC, nullptr, part, S, M, N, D, st);
+                           st, A, w, nullptr, M, N, K, KSplit{S, part.p});
+        reduce_for(ACC, nullptr, part.p, S, M, N, D, st);
     } else {
         hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<ACC, FMR>), dim3((unsigned)tiles), dim3(kQ6aThreads), 0, st, A, w,
                            D, M, N, K, KSplit{1, nullptr});
@@ -2852,7 +2891,7 @@ static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, i
 
 template <bool ACC>
 static hipError_t gemm_q6_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
-                              float* part) {
+                              const PartBuf& part) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     if (M >= kQ6TallMinM)
         q6_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, part);
@@ -2875,7 +2914,7 @@ static hipError_t staged_rows(const float* A, int M, int K, const GemmSlot& slot
         const size_t n4 = (size_t)rows * K / 4;
         hipLaunchKernelGGL(rf_f32_to_f16_kernel, dim3(stream_grid(n4)), dim3(256), 0, st,
                            reinterpret_cast<const float4*>(A + (size_t)m0 * K), reinterpret_cast<uint2*>(slot.a), n4);
-        const hipError_t e = fn(slot.a, m0, rows);
+        const hipError_t e = fn(slot.a, m0, rows, slot_parts(slot, (size_t)rows * K * 2));
         if (e != hipSuccess) return e;
     }
     return hipGetLastError();
@@ -2935,9 +2974,9 @@ extern "C" hipError_t wmma_gemm_q4_k_launch(const float* input, const void* weig
     if (!aligned16(input) || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
     GemmSlot slot;
     if (staging_slot(stream, K, &slot))
-        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows) {
+        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows, const PartBuf& pb) {
             return gemm_q4_f16<false>(a16, weights_q4_k, output + (size_t)m0 * N, rows, N, K, stream, nullptr,
-                                      slot.part);
+                                      pb);
         });
     return launch_gemm<false>(input, weights_q4_k, output, M, N, K, stream, single_seg(N));
 }
@@ -2950,8 +2989,8 @@ extern "C" hipError_t wmma_gemm_q6_k_launch(const float* input, const void* weig
     GemmSlot slot;
     // the fp16 tiles read 16-byte aligned weight rows (K % 2048)
     if (K % 2048 == 0 && aligned16(weights_q6_k) && staging_slot(stream, K, &slot))
-        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows) {
-            return gemm_q6_f16<false>(a16, weights_q6_k, output + (size_t)m0 * N, rows, N, K, stream, slot.part);
+        return staged_rows(input, M, K, slot, stream, [&](const uint16_t* a16, int m0, int rows, const PartBuf& pb) {
+            return gemm_q6_f16<false>(a16, weights_q6_k, output + (size_t)m0 * N, rows, N, K, stream, pb);
         });
     return launch_gemm<true>(input, weights_q6_k, output, M, N, K, stream, single_seg(N));
 }
@@ -2968,7 +3007,7 @@ extern "C" hipError_t rf_gemm_q4_k_f16_launch(const uint16_t* input_f16, const v
         return hipErrorInvalidValue;
     if (!aligned16(input_f16) || !aligned16(weights_q4_k)) return hipErrorInvalidValue;
     GemmSlot slot;
-    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
     return gemm_q4_f16<false>(input_f16, weights_q4_k, output, M, N, K, stream, nullptr, part);
 }
 
@@ -2985,10 +3024,10 @@ static hipError_t q4_f16_swiglu(const uint16_t* input_f16, const void* w_gate, c
     const uint8_t* wu = static_cast<const uint8_t*>(w_up);
     if (out_f16)
         hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<2>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
-                           static_cast<float*>(out), M, N, K, nullptr);
+                           static_cast<float*>(out), M, N, K, nullptr, KSplit{1, nullptr});
     else
         hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<1>, dim3(tiles), dim3(kF16aThreads), 0, stream, input_f16, wg, wu,
-                           static_cast<float*>(out), M, N, K, nullptr);
+                           static_cast<float*>(out), M, N, K, nullptr, KSplit{1, nullptr});
     return hipGetLastError();
 }
 
@@ -3018,7 +3057,7 @@ extern "C" hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f1
     const uintptr_t g0 = reinterpret_cast<uintptr_t>(gate), o0 = reinterpret_cast<uintptr_t>(out_f16);
     if (g0 < o0 + 2 * n && o0 < g0 + 4 * n) return hipErrorInvalidValue;   // overlapping buffers
     GemmSlot slot;
-    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
     return gemm_q4_f16<false>(input_f16, w_up, reinterpret_cast<float*>(out_f16), M, N, K, stream, gate, part);
 }
 
@@ -3032,7 +3071,7 @@ static hipError_t q6_f16_checked(const uint16_t* input_f16, const void* weights_
         return hipErrorInvalidValue;
     if (!aligned16(input_f16) || !aligned16(weights_q6_k) || !aligned16(output)) return hipErrorInvalidValue;
     GemmSlot slot;
-    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
     return gemm_q6_f16<ACC>(input_f16, weights_q6_k, output, M, N, K, stream, part);
 }
 
@@ -3057,7 +3096,7 @@ extern "C" hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f
         return hipErrorInvalidValue;
     if (!aligned16(input_f16) || !aligned16(weights_q4_k) || !aligned16(inout)) return hipErrorInvalidValue;
     GemmSlot slot;
-    float* part = gemm_slot(stream, &slot) ? slot.part : nullptr;
+    const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
     return gemm_q4_f16<true>(input_f16, weights_q4_k, inout, M, N, K, stream, nullptr, part);
 }
 
@@ -3091,7 +3130,7 @@ static hipError_t gemm_segments(const float* A, const void* w0, const void* w1, 
         const void* ws[3] = {w0, n1 ? w1 : nullptr, n2 ? w2 : nullptr};
         const int q6[3] = {IS_Q6, IS_Q6, IS_Q6};
         const int ns[3] = {n0, n1, n2};
-        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows, const PartBuf& pb) {
             float* ds[3] = {d0 + (size_t)m0 * n0, n1 ? d1 + (size_t)m0 * n1 : nullptr,
                             n2 ? d2 + (size_t)m0 * n2 : nullptr};
             return f16_segments(a16, ws, q6, ds, ns, rows, K, st);
@@ -3113,10 +3152,10 @@ static hipError_t gemm_accumulate(const float* A, const void* w, float* D, int M
     if (reinterpret_cast<uintptr_t>(w) & (IS_Q6 ? 1u : 15u)) return hipErrorInvalidValue;
     GemmSlot slot;
     if (aligned16(w) && staging_slot(st, K, &slot))
-        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows, const PartBuf& pb) {
             float* d = D + (size_t)m0 * N;
-            return IS_Q6 ? gemm_q6_f16<true>(a16, w, d, rows, N, K, st, slot.part)
-                         : gemm_q4_f16<true>(a16, w, d, rows, N, K, st, nullptr, slot.part);
+            return IS_Q6 ? gemm_q6_f16<true>(a16, w, d, rows, N, K, st, pb)
+                         : gemm_q4_f16<true>(a16, w, d, rows, N, K, st, nullptr, pb);
         });
     GemmSegs sg = single_seg(N);
     sg.accum = 1;
@@ -3188,7 +3227,7 @@ static hipError_t gemm_swiglu(const float* A, const void* wg, const void* wu, vo
     GemmSlot slot;
     if (!IS_Q6 && staging_slot(st, K, &slot)) {
         const size_t esz = f16_out ? 2 : 4;
-        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows) {
+        return staged_rows(A, M, K, slot, st, [&](const uint16_t* a16, int m0, int rows, const PartBuf& pb) {
             return q4_f16_swiglu(a16, wg, wu, static_cast<uint8_t*>(D) + (size_t)m0 * N * esz, f16_out, rows, N, K,
                                  st);
         });
