@@ -100,10 +100,12 @@ def test_gemm_tiled_kernel_branches(rf, dev, fmt, m, n, k):
     _check(_run(rf, fmt, a, w, m, n, k), fmt, a, w, m, n, k, f"{fmt} {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("fmt,n,k", [("q4_k", 14336, 4096), ("q6_k", 4096, 14336)])
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 14336, 4096), ("q6_k", 4096, 14336), ("q4_k", 4096, 12288)])
 @pytest.mark.parametrize("m", [64, 128, 256, 512])
 def test_gemm_llama_ffn_shapes(rf, dev, fmt, n, k, m):
-    # BASELINE config 3 at full size; A is bf16-valued N(0,1)
+    # BASELINE config 3 at full size, and the Qwen3-8B Q4_K down projection
+    # (4096 x 12288: at M = 512 the 256 x 128 tiles split over K in four);
+    # A is bf16-valued N(0,1)
     a = torch.from_numpy(synth.activations(k, seed=7, m=m)).to(torch.bfloat16).float().numpy()
     w = synth.weights(fmt, n, k, seed=8)
     _check(_run(rf, fmt, a, w, m, n, k), fmt, a, w, m, n, k, f"{fmt} M={m} {n}x{k}")
@@ -131,8 +133,9 @@ def test_gemm_identity_random_weights(rf, dev, fmt, m, n, k):
                                    (576, 6144, 4096), (320, 256, 1024), (128, 14336, 4096), (512, 4096, 4096),
                                    (512, 4096, 12288), (256, 4096, 12288), (192, 192, 512), (64, 64, 256)])
 def test_gemm_q4k_fp16_activations(rf, dev, m, n, k):
-    # 256 x 128 tiles at 512 x 14336; elsewhere the K-sliced 64 / 128-row tiles
-    # (M <= 64 / above), including partial row tiles and N = 64, 192
+    # 256 x 128 tiles at 512 x 14336 (and split over K at 512 x 4096 x 12288);
+    # elsewhere the K-sliced 64 / 128 / 256-row tiles, including partial row
+    # tiles and N = 64, 192
     # rf_gemm_q4_k_f16_launch on A rounded to fp16 by the caller: the operands
     # of wmma_gemm_q4_k_launch on fp32 A, so the same oracle and bar
     a = torch.from_numpy(synth.activations(k, seed=m + 11, m=m)).to(torch.bfloat16).float().numpy()
