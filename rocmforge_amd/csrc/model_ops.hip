@@ -1715,11 +1715,13 @@ extern "C" hipError_t gpu_increment_decode_state_on_stream(int* d_state, hipStre
 // v_exp_f32; within a few fp32 ulps of expf, P is rounded to fp16 anyway),
 // the causal mask is applied only on the tiles that reach past a wave's
 // first query, and O is rescaled only when some lane's maximum moved.  The
-// V^T tile's key index is XOR-swizzled by 4 (dim / 8): the 16 threads that
-// write one key's dims (rows 8 apart) then hit different banks, and every
-// group of 4 keys an operand read takes stays contiguous.  The kernel is
-// compiled with MFMA results in VGPRs (the rescale touches every
-// accumulator each tile).
+// next K / V tile is loaded into registers while the current one is used;
+// V is written transposed as 32-bit key pairs, its keys permuted (bits 2
+// and 3 swapped) so that the 8 keys of an operand are one 16-byte read, and
+// XOR-swizzled by 8 ((dim / 8) % 8) so that the 16 threads writing one key
+// pair (rows 8 apart) hit different banks.  Measured at 512 positions, 32
+// heads, fp32 output: 26.5 us before these changes (and one wave per SIMD,
+// the mask on diagonal tiles only), 17.4 after, the same bits.
 namespace rf {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -1731,8 +1733,11 @@ constexpr int kVStr = 64 + 8;        // V^T tile row stride (halves)
 
 // OUT = float, or uint16_t: fp16 bits of the fp32 output (round to nearest
 // even), the operand a GEMM on fp16 activations reads
+// One wave per SIMD (waves_per_eu 1): the whole register file for the
+// accumulators and the prefetched tile (measured 22.8 against 26.5 us at 512
+// positions, 32 heads).
 template <int NWQ, typename OUT>
-__global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
+__global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(1, 1))) void rf_attn_prefill_kernel(const _Float16* __restrict__ Q,
                                                               const _Float16* __restrict__ K,
                                                               const _Float16* __restrict__ V, OUT* __restrict__ O,
                                                               int seq, int nq, int nkv, int causal, float scale) {
@@ -1769,23 +1774,52 @@ __global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float1
     const int wg_last_q = min(qb + 32 * NWQ - 1, seq - 1);
     const int ntiles = causal ? wg_last_q / 64 + 1 : seq / 64;
     const int wave_tiles = causal ? (q0 + 31) / 64 + 1 : seq / 64;
+    // K / V tiles: thread chunk i = key c >> 4, dims (c & 15) * 8, c = tid +
+    // 64 NWQ i; tile t + 1 is loaded into registers while tile t is used
+    // (V: chunks 2 p, 2 p + 1 are keys 2 (tid / 16 + 4 NWQ p) and the next, so
+    // the transposed tile takes them as one 32-bit key pair per dim)
+    constexpr int NCH = 16 / NWQ;
+    auto vkey = [&](int i) { return 2 * ((tid >> 4) + 4 * NWQ * (i >> 1)) + (i & 1); };
+    auto vpos = [](int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); };
+    h8 kr[NCH], vr[NCH];
+    auto tile_load = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = tid + 64 * NWQ * i;
+            const int key = c >> 4, d8 = (c & 15) * 8;
+            kr[i] = *reinterpret_cast<const h8*>(K + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
+            vr[i] = *reinterpret_cast<const h8*>(V + (size_t)(t0 + vkey(i)) * kvrow + (size_t)kvh * kAttD + d8);
+        }
+    };
+    if (ntiles > 0) tile_load(0);
     for (int t = 0; t < ntiles; ++t) {
         const int t0 = 64 * t;
         __syncthreads();   // previous tile's reads done
         // K tile: 64 keys x 128 dims, 16-byte chunks; V tile transposed
 #pragma unroll
-        for (int i = 0; i < 16 / NWQ; ++i) {
+        for (int i = 0; i < NCH; ++i) {
             const int c = tid + 64 * NWQ * i;     // 0..1023
             const int key = c >> 4, d8 = (c & 15) * 8;
-            const h8 kv = *reinterpret_cast<const h8*>(K + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
+            const h8 kv = kr[i];
             *reinterpret_cast<h8*>(&ks[key * kKStr + d8]) = kv;
-            const h8 vv = *reinterpret_cast<const h8*>(V + (size_t)(t0 + key) * kvrow + (size_t)kvh * kAttD + d8);
-            // transposed, keys XOR-swizzled by 4 (d / 8): the 16 threads of a key
-            // write rows 8 apart, which the swizzle spreads over the banks
-            const int sw = 4 * (c & 15);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vt[(d8 + j) * kVStr + (key ^ sw)] = vv[j];
         }
+        // V transposed: key k of a row at position vpos(k) ^ 8 ((d / 8) % 8),
+        // vpos swapping bits 2 and 3 of the key (so the 8 keys an MFMA operand
+        // takes, k .. k + 3 and k + 8 .. k + 11 for k % 8 = 0 or 4, are one
+        // aligned 16-byte run), the XOR spreading the 16 threads of a key pair,
+        // whose rows are 8 apart, over the banks
+#pragma unroll
+        for (int pi = 0; pi < NCH / 2; ++pi) {
+            const int d8 = (tid & 15) * 8, k0 = vkey(2 * pi);
+            const int sw = 8 * (tid & 7);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 pr = {vr[2 * pi][j], vr[2 * pi + 1][j]};
+                *reinterpret_cast<h2*>(&vt[(d8 + j) * kVStr + (vpos(k0) ^ sw)]) = pr;
+            }
+        }
+        if (t + 1 < ntiles) tile_load(t0 + 64);
         __syncthreads();
         if (!active || t >= wave_tiles) continue;
 
@@ -1803,21 +1837,31 @@ __global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float1
         }
         // scale (in the log2 domain: exp(x - m) = 2^(x log2 e - m log2 e), one
         // v_exp_f32 each), mask (only a tile that reaches past the wave's first
-        // query holds keys to mask), tile max
+        // query holds keys to mask: a branch of its own, so the other tiles
+        // carry no compare and select per element), tile max
         float tmax = kNegMax;
         const bool diag = causal && t0 + 63 > q0;
+        if (diag) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float v = s[b][e] * scale2;
-                if (diag) {
+                for (int e = 0; e < 16; ++e) {
+                    float v = s[b][e] * scale2;
                     const int key = t0 + 32 * b + 8 * (e >> 2) + 4 * hi + (e & 3);
                     if (key > query) v = kNegMax;
+                    s[b][e] = v;
+                    tmax = fmaxf(tmax, v);
                 }
-                s[b][e] = v;
-                tmax = fmaxf(tmax, v);
-            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float v = s[b][e] * scale2;
+                    s[b][e] = v;
+                    tmax = fmaxf(tmax, v);
+                }
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float m_new = fmaxf(m, tmax);
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
@@ -1849,14 +1893,11 @@ __global__ __launch_bounds__(64 * NWQ) void rf_attn_prefill_kernel(const _Float1
             const int kb = 32 * (j >> 1) + 16 * (j & 1) + 4 * hi;
 #pragma unroll
             for (int bd = 0; bd < 4; ++bd) {
-                // row d = 32 bd + col, keys kb .. kb + 3 and kb + 8 .. kb + 11 under
-                // the row's swizzle 4 (d / 8) (a multiple of 4: groups stay whole)
-                const int sw = 4 * ((4 * bd + (col >> 3)) & 15);
+                // row d = 32 bd + col, keys kb .. kb + 3 and kb + 8 .. kb + 11: the
+                // 16-byte run at vpos(kb) under the row's swizzle 8 ((d / 8) % 8)
+                const int sw = 8 * ((4 * bd + (col >> 3)) & 7);
                 const _Float16* vrow = &vt[(32 * bd + col) * kVStr];
-                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                const h4 lo = *reinterpret_cast<const h4*>(vrow + (kb ^ sw));
-                const h4 hi4 = *reinterpret_cast<const h4*>(vrow + ((kb + 8) ^ sw));
-                const h8 a = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                const h8 a = *reinterpret_cast<const h8*>(vrow + (vpos(kb) ^ sw));
                 o[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[j], o[bd], 0, 0, 0);
             }
         }
