@@ -19,6 +19,10 @@
 //    difference to the reference is the fp32 summation order.
 //  * Workgroups stride over row groups; the grid is capped at a multiple of
 //    the CU count so a large N re-uses each workgroup's quantised vector.
+//  * Long rows (K a multiple of 4096 from 8192: the Qwen3-8B ffn_down) take
+//    a K-split kernel instead (rf_q4k_q8_lin_kernel): each wave of a team
+//    keeps its K slice's Q8 x in registers and streams every row of its
+//    workgroup.
 #include <type_traits>
 
 #include "q6k_lin.h"
@@ -379,6 +383,103 @@ __global__ __launch_bounds__(kThreads) void rf_q4k_f32_gemv_kernel(const uint8_t
     }
 }
 
+// ── K-split Q4_K Q8-inline GEMV for long rows (K >= 8192, K / 256 % 16 == 0) ──
+// A team of nwk = K / 4096 waves per workgroup; team wave tw takes
+// super-blocks [16 tw, 16 tw + 16) of every row (lane 4 s + p: super-block
+// 16 tw + s, nibble pair p, as in the one-row-per-step kernel) for the rows
+// g, g + G, .. (< N) of workgroup g of G.  Each lane owns the 64 elements of
+// x its nibble pair meets -- two whole Q8_0 blocks -- and quantises them in
+// registers (the quantiser's arithmetic, with no cross-lane step), so the
+// weight stream runs with no LDS traffic and no barrier in front of it.  A
+// row's sum is the team's 4 nwk 16-lane partial sums added in team-wave
+// order after the loop, the same whatever the grid.  norm_w (optional):
+// x -> (x * inv) * norm_w first, inv in the canonical order of the
+// standalone norm (same bits as gpu_rms_norm then the plain launch).
+template <int NB>
+__global__ __launch_bounds__(512) void rf_q4k_q8_lin_kernel(const uint8_t* __restrict__ w,
+                                                             const float* __restrict__ x, const float* residual,
+                                                             float* y, int K, int N,
+                                                             const float* __restrict__ norm_w, float eps) {
+    extern __shared__ __align__(16) float part[];   // [rows of this workgroup][nwk][4]
+    __shared__ float red[4];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int tw = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nwk = blockDim.x / kWave;
+    const int nsb = K / kQK;
+    const size_t row_bytes = (size_t)nsb * kQ4KBytes;
+    const int s = lane >> 2, p = lane & 3;
+    const int sb = 16 * tw + s;
+    const int g = blockIdx.x, G = gridDim.x;
+    const int nrows = g < N ? (N - 1 - g) / G + 1 : 0;
+    const float inv_rms = norm_w ? rms_inv_canonical(x, K, eps, red) : 1.0f;
+
+    // x: elements sb * 256 + 64 p .. + 63 = Q8_0 blocks 8 sb + 2 p, + 1
+    u32x4 xlo[2], xhi[2];
+    float xd[2];
+    int xq[2];
+    {
+        const float4* xv = reinterpret_cast<const float4*>(x + (size_t)sb * kQK + 64 * p);
+        float4 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = xv[i];
+        if (norm_w) {
+            const float4* gv = reinterpret_cast<const float4*>(norm_w + (size_t)sb * kQK + 64 * p);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 gg = gv[i];
+                v[i] = make_float4((v[i].x * inv_rms) * gg.x, (v[i].y * inv_rms) * gg.y, (v[i].z * inv_rms) * gg.z,
+                                   (v[i].w * inv_rms) * gg.w);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            float e[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                e[4 * i] = v[8 * b + i].x; e[4 * i + 1] = v[8 * b + i].y;
+                e[4 * i + 2] = v[8 * b + i].z; e[4 * i + 3] = v[8 * b + i].w;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(e[i]));
+            const float scale = fmaxf(amax / 127.0f, 1e-30f);
+            const float sf = __half2float(__float2half(scale));
+            const float inv = 1.0f / sf;
+            uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+            int sum = 0;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int q = (int)fminf(fmaxf(e[i] * inv, -127.0f), 127.0f);
+                sum += q;
+                packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+            }
+            u32x4* dst = b ? xhi : xlo;
+            dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+            dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            xd[b] = sf;
+            xq[b] = sum;
+        }
+    }
+    const uint8_t* wl = w + (size_t)sb * kQ4KBytes;
+    auto load = [&](Q4KUnit& u, int j) {
+        const int row = nrows ? g + min(j, nrows - 1) * G : 0;
+        u = q4k_load_unit(wl + (size_t)row * row_bytes, p);
+    };
+    auto process = [&](const Q4KUnit& u, int j) {
+        const float acc = q4k_q8_unit_dot(u, p, xlo, xhi, xd[0], xd[1], xq[0], xq[1], 0.0f);
+        const float r16 = row16_sum(acc);
+        if ((lane & 15) == 0) part[(j * nwk + tw) * 4 + (lane >> 4)] = r16;
+    };
+    Q4KUnit ring[NB];
+    ring_pipeline<NB>(nrows, ring, load, process, [&]() {});
+    __syncthreads();
+    for (int j = tw * kWave + lane; j < nrows; j += nwk * kWave) {
+        float t = 0.0f;
+        for (int k = 0; k < 4 * nwk; ++k) t += part[j * nwk * 4 + k];
+        y[g + j * G] = t + (residual ? residual[g + j * G] : 0.0f);
+    }
+}
+
 // ── launch helpers ────────────────────────────────────────────────────────
 // Grid: a fixed number of workgroups per CU (every wave then streams an
 // equal contiguous share of the rows), fewer when N is too small to give each
@@ -510,12 +611,35 @@ static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t
 // 525-526, 556-557).  Additionally the weights must be 16-byte aligned: the
 // kernels stream them with 16-byte loads (GGUF tensors are uploaded into
 // their own hipMalloc buffers, which are 256-byte aligned).
+// The K-split kernel for long rows: K a multiple of 4096 from 8192 (the
+// launchers' Q8 LDS rule caps K at 30720), 16-byte aligned weights and x.
+// One workgroup per CU, three rows in flight per wave (measured on MI355X,
+// 4096 x 12288 + residual: 8.4-8.5 us against 9.1-9.4 for the one-row-per-step
+// kernel; two workgroups per CU 10.1, two rows in flight 11.1).
+constexpr int kQ4LinRing = 4;
+static bool q4_lin_ok(const void* w, const float* x, int K) {
+    return K >= 8192 && K % 4096 == 0 && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+}
+static hipError_t launch_q4_lin(const void* w, const float* x, const float* res, float* y, int K, int N,
+                                hipStream_t st, const float* norm_w = nullptr, float eps = 0.0f) {
+    const int nwk = K / 4096;
+    const int cap = device_cu_count();
+    const int grid = N < cap ? N : cap;
+    const size_t lds = (size_t)((N + grid - 1) / grid) * nwk * 4 * sizeof(float);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((rf_q4k_q8_lin_kernel<kQ4LinRing>), dim3(grid), dim3(nwk * 64), lds, st,
+                       static_cast<const uint8_t*>(w), x, res, y, K, N, norm_w, eps);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t gemv_q4_k_f32_q8_inline_launch(const void* weights_q4_k, const float* input, float* output,
                                                      int n_rows, int ncols_dst, hipStream_t stream) {
     if (n_rows <= 0 || ncols_dst <= 0) return hipErrorInvalidValue;
     if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
     if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
     if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    if (q4_lin_ok(weights_q4_k, input, n_rows))
+        return launch_q4_lin(weights_q4_k, input, nullptr, output, n_rows, ncols_dst, stream);
     return launch_q8<kPlain>(weights_q4_k, nullptr, input, nullptr, output, n_rows, ncols_dst, stream);
 }
 
@@ -526,6 +650,8 @@ extern "C" hipError_t gemv_q4_k_f32_q8_inline_residual_launch(const void* weight
     if ((n_rows % kQK) != 0) return hipErrorInvalidValue;
     if (!q8_inline_fits(n_rows)) return hipErrorInvalidValue;
     if (!aligned16(weights_q4_k)) return hipErrorInvalidValue;
+    if (q4_lin_ok(weights_q4_k, input, n_rows))
+        return launch_q4_lin(weights_q4_k, input, residual, output, n_rows, ncols_dst, stream);
     return launch_q8<kResidual>(weights_q4_k, nullptr, input, residual, output, n_rows, ncols_dst, stream);
 }
 
@@ -587,6 +713,8 @@ extern "C" hipError_t rf_gemv_q4_k_q8_rmsnorm_launch(const void* weights_q4_k, c
                                                      int ncols_dst, hipStream_t stream) {
     if (n_rows <= 0 || ncols_dst <= 0 || (n_rows % kQK) != 0 || !q8_inline_fits(n_rows)) return hipErrorInvalidValue;
     if (!aligned16(weights_q4_k) || !norm_args_ok(input, norm_w)) return hipErrorInvalidValue;
+    if (q4_lin_ok(weights_q4_k, input, n_rows))
+        return launch_q4_lin(weights_q4_k, input, nullptr, output, n_rows, ncols_dst, stream, norm_w, eps);
     QkvArgs a{};
     a.norm_w = norm_w;
     a.eps = eps;

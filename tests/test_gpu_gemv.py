@@ -27,7 +27,9 @@ pytestmark = pytest.mark.gpu
 REL_TOL = 1e-5
 ELEM_TOL = 1.0
 
-SHAPES = [(256, 1), (256, 64), (512, 100), (4096, 4096), (1024, 6144 + 13), (14336, 96), (30720, 40)]
+# (12288 / 8192 rows: the K-split kernel for long rows, N not a multiple of the grid)
+SHAPES = [(256, 1), (256, 64), (512, 100), (4096, 4096), (1024, 6144 + 13), (14336, 96), (30720, 40), (12288, 4096),
+          (8192, 1000)]
 
 
 def _check(y, ref, what):
@@ -74,7 +76,7 @@ def test_q4k_q8_inline_gemv(rf, dev, k, n):
     _check(G.host(y), O.gemv_q4k_q8(w, x, k, n), f"q8 gemv {n}x{k}")
 
 
-@pytest.mark.parametrize("k,n", [(4096, 4096), (512, 77)])
+@pytest.mark.parametrize("k,n", [(4096, 4096), (512, 77), (12288, 4096)])
 def test_q4k_q8_inline_residual_in_place(rf, dev, k, n):
     w = synth.q4_k_weights(n, k, seed=7)
     x = synth.activations(k, seed=8)
