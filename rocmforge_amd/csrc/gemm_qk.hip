@@ -2250,6 +2250,9 @@ struct Q4sGeom {
     static constexpr int kAPW = FMR / 2;              // A DMAs per wave per chunk (1 KB each)
     static constexpr int kRounds = FMR == 8 ? 2 : 1;  // exchange rounds of the K-slice partials
     static constexpr int kXB = FMR / kRounds;         // row blocks per round
+    // a ring stage DMA'd in chunk 4 sb (super-block sb + kRS - 1) is first
+    // read in chunk 4 (sb + kRS - 1) - 1, so it must land within kLag chunks
+    static_assert(FMR == 8 || kLag <= 4 * (kRS - 1) - 2, "ring stage read before its DMA lands");
     static constexpr int kLdsLoop = kRS * kQ4sStage + kABufs * kABuf;
     static constexpr int kLdsXch = 8 * kXB * 4096;    // every wave's partial blocks of one round
     static constexpr int kLds = kLdsLoop > kLdsXch ? kLdsLoop : kLdsXch;
