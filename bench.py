@@ -569,7 +569,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the sharding design is described in DESIGN.md)"}))
+                                   "(sharding over several GPUs is not implemented)"}))
         sys.exit(2)
     import torch
 
