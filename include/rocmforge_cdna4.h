@@ -146,7 +146,8 @@ hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f16, const v
 /* Up to three weight matrices over one fp16 input as column segments of one
  * launch, each Q4_K (type 12) or Q6_K (type 14, GGML type ids):
  * out_s[M x n_s] = the product of rf_gemm_q4_k_f16_launch /
- * rf_gemm_q6_k_f16_launch on 128 x 64 tiles (each output written once).  The
+ * rf_gemm_q6_k_f16_launch on K-sliced 64-column tiles of 128 or 256 rows
+ * (each output written once, the bits of those launchers).  The
  * prefill Q/K/V of a layer of any type mix (the reference runs three GEMMs,
  * src/gpu/forward.rs:2327).  M % 64, n_s % 64 (n1, n2 may be 0), K % 256
  * (K % 2048 with a Q6_K segment); input, weights and outputs 16-byte aligned. */

@@ -2506,7 +2506,7 @@ struct F16Segs {
     const uint8_t* w[3];
     float* d[3];
     int n[3];
-    int q6[3];
+    int q6[3];         // 1: Q6_K on the launch's tiles; 2: Q6_K on 128-row tiles in a 256-row launch
     int tiles[3];      // M tiles x column tiles of each segment
 };
 static_assert(kQ6aBN == kQ4sBN && kQ6aThreads == kQ4sThreads, "q6a and q4s tiles differ");
@@ -2516,7 +2516,7 @@ struct F16SegGeom {
 };
 
 // FMR = 4 (128-row tiles) or 8 (256-row tiles, each weight dequantised once
-// per 256 rows of A)
+// per 256 rows of A; a Q6_K segment of such a launch runs 128-row tiles)
 template <int FMR>
 __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uint16_t* __restrict__ A, int M, int K,
                                                                         F16Segs sg) {
@@ -2529,7 +2529,10 @@ __global__ __launch_bounds__(kQ4sThreads) void rf_gemm_f16_segs_kernel(const uin
     float* d = s == 0 ? sg.d[0] : (s == 1 ? sg.d[1] : sg.d[2]);
     const int n = s == 0 ? sg.n[0] : (s == 1 ? sg.n[1] : sg.n[2]);
     const int q6 = s == 0 ? sg.q6[0] : (s == 1 ? sg.q6[1] : sg.q6[2]);
-    if (q6)
+    static_assert(Q6aGeom<4>::kLds <= F16SegGeom<8>::kLds, "128-row Q6_K tiles fit the 256-row launch's LDS");
+    if (FMR == 8 && q6 == 2)
+        q6a_wg<false, 4>(A, w, d, M, n, K, v, lds);
+    else if (q6)
         q6a_wg<false, FMR>(A, w, d, M, n, K, v, lds);
     else
         q4s_wg<FMR, false>(A, w, d, M, n, K, v, lds);
@@ -2952,6 +2955,14 @@ static hipError_t f16_segments(const uint16_t* A, const void* const ws[3], const
         sg.n[i] = ns[i];
         sg.q6[i] = q6[i];
         sg.tiles[i] = mtiles * (ns[i] / kQ4sBN);
+        if (tall && q6[i]) {
+            // a Q6_K segment on 128-row tiles: the 256-row Q6_K tiles take
+            // longer than the Q4_K ones and set the launch's time (measured on
+            // MI355X, Qwen3-8B Q/K/V with a Q6_K V: M = 512 42.5-44.8 against
+            // 45.8-50.5 us, M = 256 36.8-37.7 against 41.7-42.2; same bits)
+            sg.q6[i] = 2;
+            sg.tiles[i] = ((M + 127) / 128) * (ns[i] / kQ4sBN);
+        }
         total += sg.tiles[i];
     }
     if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
@@ -3180,7 +3191,8 @@ extern "C" hipError_t rf_gemm_q6_k_segments_launch(const float* input, const voi
 // Up to three weight matrices over one fp16 input as column segments of one
 // launch (rf_gemm_f16_segs_kernel), each Q4_K (type 12) or Q6_K (type 14):
 // out_s[M x n_s] = fp16(A) * fp16(dequant W_s)^T, the products of
-// rf_gemm_q4_k_f16_launch / rf_gemm_q6_k_f16_launch on 128 x 64 tiles.  The
+// rf_gemm_q4_k_f16_launch / rf_gemm_q6_k_f16_launch on K-sliced 64-column
+// tiles of 128 or 256 rows.  The
 // prefill Q/K/V of a layer whatever its type mix.  M % 64, n_s % 64 (n1, n2
 // may be 0: fewer segments), K % 256 (K % 2048 with a Q6_K segment); input,
 // weights and outputs 16-byte aligned.

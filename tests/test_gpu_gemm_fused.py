@@ -212,6 +212,7 @@ def test_rejections(rf, dev):
 @pytest.mark.parametrize("m,segs,k", [
     (512, [("q4_k", 4096), ("q4_k", 1024), ("q6_k", 1024)], 4096),    # Qwen3-8B layer with a Q6_K V
     (320, [("q4_k", 512), ("q4_k", 128), ("q4_k", 128)], 2048),       # all Q4_K, partial 128-row tile
+    (320, [("q4_k", 512), ("q6_k", 128), ("q4_k", 192)], 2048),       # Q6_K on 128-row tiles beside 256-row Q4_K
     (64, [("q6_k", 192), ("q4_k", 64)], 2048),                        # two segments, one 64-row M tile
 ])
 def test_f16_segments_mixed_types(rf, dev, m, segs, k):
