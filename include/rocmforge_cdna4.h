@@ -179,6 +179,21 @@ hipError_t rf_gemm_q4_k_f16_swiglu_up_launch(const uint16_t* input_f16, const vo
  * a prefill, into the residual stream. */
 hipError_t rf_gemm_q6_k_f16_accumulate_launch(const uint16_t* input_f16, const void* weights_q6_k, float* inout,
                                               int M, int N, int K, hipStream_t stream);
+/* No counterpart (the reference's prefill adds the residual with gpu_add and
+ * normalises the next layer's input in its own kernel).  The accumulate
+ * launchers above, then rf_rms_norm_batched_f16_on_stream of inout (rows of
+ * N, weights norm_w, eps) into out_f16 [M x N]: inout and out_f16 have the
+ * bits of those two calls.  When the GEMM splits over K the norm is taken in
+ * the split reduction's pass over the rows (N % 2048 == 0, N <= 8192).  Same
+ * shape rules as the accumulate launchers; norm_w and out_f16 16-byte aligned,
+ * out_f16 not overlapping inout.  Used for the FFN down projection of a
+ * prefill layer followed by the next layer's attention norm. */
+hipError_t rf_gemm_q4_k_f16_accumulate_rmsnorm_launch(const uint16_t* input_f16, const void* weights_q4_k,
+                                                      float* inout, const float* norm_w, float eps, uint16_t* out_f16,
+                                                      int M, int N, int K, hipStream_t stream);
+hipError_t rf_gemm_q6_k_f16_accumulate_rmsnorm_launch(const uint16_t* input_f16, const void* weights_q6_k,
+                                                      float* inout, const float* norm_w, float eps, uint16_t* out_f16,
+                                                      int M, int N, int K, hipStream_t stream);
 
 /* No counterpart in the reference (its prefill issues one GEMM per weight
  * and adds residuals with gpu_add).  Several weight matrices that share the

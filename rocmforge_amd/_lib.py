@@ -33,6 +33,8 @@ SIGNATURES = {
     "rf_gemm_q6_k_f16_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q6_k_f16_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
     "rf_gemm_q4_k_f16_accumulate_launch": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q4_k_f16_accumulate_rmsnorm_launch": [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp],
+    "rf_gemm_q6_k_f16_accumulate_rmsnorm_launch": [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _vp],
     "rf_gemm_qk_f16_segments_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "rf_gemm_q4_k_f16_swiglu_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "rf_gemm_q4_k_f16_swiglu_up_launch": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp],

@@ -2767,6 +2767,75 @@ static int ksplit_count(long tiles, int nsb, int M, int N, const PartBuf& part, 
     return S;
 }
 
+// The split reduction into the residual stream with the RMSNorm of the
+// result in the same pass (the next layer's input norm of a prefill): one
+// workgroup per row of N = 2048 NG.  Row r: h = D + (p_0 + .. + p_{S-1}) in
+// rf_gemm_split_reduce_kernel<1>'s order, stored to D; thread t holds the
+// elements 8 t + 2048 g .. + 7 (g < NG) and takes their squares in
+// rms_inv_canonical's order, so out = fp16((h * inv) * w) has the bits of
+// rf_rms_norm_batched_f16_on_stream run on the stored h.
+template <int NG>
+__global__ __launch_bounds__(256) void rf_split_reduce_rmsnorm_kernel(const float* __restrict__ part, int S, int M,
+                                                                      int N, float* __restrict__ D,
+                                                                      const float* __restrict__ w, float eps,
+                                                                      uint16_t* __restrict__ out) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const size_t mn = (size_t)M * N;
+    const size_t row = (size_t)r * N;
+    float4 h[NG][2];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const size_t e = row + 8 * threadIdx.x + 2048 * g + 4 * q;
+            float4 t = *reinterpret_cast<const float4*>(part + e);
+            for (int k = 1; k < S; ++k) {
+                const float4 p = *reinterpret_cast<const float4*>(part + (size_t)k * mn + e);
+                t.x += p.x;
+                t.y += p.y;
+                t.z += p.z;
+                t.w += p.w;
+            }
+            float4 d = *reinterpret_cast<const float4*>(D + e);
+            d.x = d.x + t.x;
+            d.y = d.y + t.y;
+            d.z = d.z + t.z;
+            d.w = d.w + t.w;
+            *reinterpret_cast<float4*>(D + e) = d;
+            h[g][q] = d;
+        }
+    float ss = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) ss += sq8(h[g][0], h[g][1]);
+    ss = xor_sum64(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    const float inv = rms_inv_finish(red, N, eps);
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = 8 * threadIdx.x + 2048 * g + 4 * q;
+            const float4 a = h[g][q];
+            const float4 gw = *reinterpret_cast<const float4*>(w + c);
+            const uint32_t lo =
+                (uint32_t)f16_bits_rn((a.x * inv) * gw.x) | ((uint32_t)f16_bits_rn((a.y * inv) * gw.y) << 16);
+            const uint32_t hi =
+                (uint32_t)f16_bits_rn((a.z * inv) * gw.z) | ((uint32_t)f16_bits_rn((a.w * inv) * gw.w) << 16);
+            *reinterpret_cast<uint2*>(out + row + c) = make_uint2(lo, hi);
+        }
+}
+
+// An RMSNorm of the accumulated rows (weights w, fp16 output) that a split
+// reduction may fold in; fused is set when it did.
+struct RowNorm {
+    const float* w;
+    float eps;
+    uint16_t* out;
+    bool* fused;
+    bool fits(int N) const { return N % 2048 == 0 && N <= 8192; }
+};
+
 template <int MODE>
 static void launch_reduce(const float* part, int S, int M, int N, float* D, const float* G, hipStream_t st) {
     const size_t n4 = (size_t)M * N / 4;
@@ -2774,8 +2843,21 @@ static void launch_reduce(const float* part, int S, int M, int N, float* D, cons
                        reinterpret_cast<const float4*>(part), S, n4, D, reinterpret_cast<const float4*>(G));
 }
 
-static void reduce_for(bool acc, const float* G, const float* part, int S, int M, int N, float* D, hipStream_t st) {
-    if (acc)
+static void reduce_for(bool acc, const float* G, const float* part, int S, int M, int N, float* D, hipStream_t st,
+                       const RowNorm* rn = nullptr) {
+    if (acc && rn != nullptr && rn->fits(N)) {
+        auto go = [&](auto ngc) {
+            hipLaunchKernelGGL((rf_split_reduce_rmsnorm_kernel<decltype(ngc)::value>), dim3((unsigned)M), dim3(256), 0,
+                               st, part, S, M, N, D, rn->w, rn->eps, rn->out);
+        };
+        switch (N / 2048) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        default: go(std::integral_constant<int, 4>{}); break;
+        }
+        *rn->fused = true;
+    } else if (acc)
         launch_reduce<1>(part, S, M, N, D, nullptr, st);
     else if (G != nullptr)
         launch_reduce<2>(part, S, M, N, D, G, st);
@@ -2799,22 +2881,24 @@ constexpr int kQ4TallMinM = RF_Q4_TALL_MIN_M;
 
 template <bool ACC, int FMR>
 static void q4_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
-                         const float* G, const PartBuf& part) {
+                         const float* G, const PartBuf& part, const RowNorm* rn = nullptr) {
     const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ4sBN);
     const int S = 2 * tiles <= (long)device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part) : 1;
     if (S > 1) {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, false>), dim3((unsigned)(tiles * S)), dim3(kQ4sThreads), 0,
                            st, A, w, nullptr, M, N, K, nullptr, KSplit{S, part.p});
-        reduce_for(ACC, G, part.p, S, M, N, D, st);
+        reduce_for(ACC, G, part.p, S, M, N, D, st, rn);
     } else {
         hipLaunchKernelGGL((rf_gemm_q4k_f16s_kernel<FMR, ACC>), dim3((unsigned)tiles), dim3(kQ4sThreads), 0, st, A, w,
                            D, M, N, K, G, KSplit{1, nullptr});
     }
 }
 
+// rn (ACC only): an RMSNorm of the accumulated rows the split reduction
+// may fold in (the caller runs it itself when rn->fused stays false).
 template <bool ACC>
 static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
-                              const float* G, const PartBuf& part) {
+                              const float* G, const PartBuf& part, const RowNorm* rn = nullptr) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const long big = (long)((M + kF16aBM - 1) / kF16aBM) * (N % kF16aBN == 0 ? N / kF16aBN : 0);
     if (!ACC && 4 * big >= 3L * device_cu_count()) {
@@ -2839,7 +2923,7 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
         if (S > 1 && 4 * big * S >= 3 * cus && nsb / S >= 12) {
             hipLaunchKernelGGL(rf_gemm_q4k_f16a_kernel<0>, dim3((unsigned)(big * S)), dim3(kF16aThreads), 0, st, A, w,
                                w, nullptr, M, N, K, nullptr, KSplit{S, part.p});
-            reduce_for(ACC, G, part.p, S, M, N, D, st);
+            reduce_for(ACC, G, part.p, S, M, N, D, st, rn);
             return hipGetLastError();
         }
     }
@@ -2853,7 +2937,7 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
         const long t8 = (long)((M + 255) / 256) * (N / kQ4sBN);
         const int s8 = 2 * t8 <= cus ? ksplit_count(t8, K / kQK, M, N, part) : 1;
         if (4 * t8 >= 3 * cus || (s8 > 1 && (K / kQK) / s8 >= 24)) {
-            q4_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, G, part);
+            q4_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, G, part, rn);
             return hipGetLastError();
         }
     }
@@ -2862,9 +2946,9 @@ static hipError_t gemm_q4_f16(const uint16_t* A, const void* W, float* D, int M,
     // at K = 4096, 58.4 against 63.1 at K = 12288)
     const bool rows64 = M <= 64 || 2L * ((M + 127) / 128) * (N / kQ4sBN) <= (long)device_cu_count();
     if (rows64)
-        q4_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, G, part);
+        q4_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, G, part, rn);
     else
-        q4_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, G, part);
+        q4_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, G, part, rn);
     return hipGetLastError();
 }
 
@@ -2880,7 +2964,7 @@ constexpr int kQ6LeanMaxM = 64;      // 64-row tiles up to this M (at M = 128: 4
 
 template <bool ACC, int FMR>
 static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, int N, int K, hipStream_t st,
-                         const PartBuf& part) {
+                         const PartBuf& part, const RowNorm* rn = nullptr) {
     const long tiles = (long)((M + 32 * FMR - 1) / (32 * FMR)) * (N / kQ6aBN);
     const int per_cu = FMR == 2 ? 2 : 1;      // the lean 64-row tiles: two workgroups per CU
     const int S = 2 * tiles <= (long)per_cu * device_cu_count() ? ksplit_count(tiles, K / kQK, M, N, part, per_cu)
@@ -2888,7 +2972,7 @@ static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, i
     if (S > 1) {
         hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<false, FMR>), dim3((unsigned)(tiles * S)), dim3(kQ6aThreads), 0,
                            st, A, w, nullptr, M, N, K, KSplit{S, part.p});
-        reduce_for(ACC, nullptr, part.p, S, M, N, D, st);
+        reduce_for(ACC, nullptr, part.p, S, M, N, D, st, rn);
     } else {
         hipLaunchKernelGGL((rf_gemm_q6k_f16a_kernel<ACC, FMR>), dim3((unsigned)tiles), dim3(kQ6aThreads), 0, st, A, w,
                            D, M, N, K, KSplit{1, nullptr});
@@ -2897,14 +2981,14 @@ static void q6_f16_tiles(const uint16_t* A, const uint8_t* w, float* D, int M, i
 
 template <bool ACC>
 static hipError_t gemm_q6_f16(const uint16_t* A, const void* W, float* D, int M, int N, int K, hipStream_t st,
-                              const PartBuf& part) {
+                              const PartBuf& part, const RowNorm* rn = nullptr) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     if (M >= kQ6TallMinM)
-        q6_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, part);
+        q6_f16_tiles<ACC, 8>(A, w, D, M, N, K, st, part, rn);
     else if (M <= kQ6LeanMaxM)
-        q6_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, part);
+        q6_f16_tiles<ACC, 2>(A, w, D, M, N, K, st, part, rn);
     else
-        q6_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, part);
+        q6_f16_tiles<ACC, 4>(A, w, D, M, N, K, st, part, rn);
     return hipGetLastError();
 }
 
@@ -3112,6 +3196,52 @@ extern "C" hipError_t rf_gemm_q4_k_f16_accumulate_launch(const uint16_t* input_f
     GemmSlot slot;
     const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
     return gemm_q4_f16<true>(input_f16, weights_q4_k, inout, M, N, K, stream, nullptr, part);
+}
+
+extern "C" hipError_t rf_rms_norm_batched_f16_on_stream(const float* d_x, const float* d_weight, uint16_t* d_out_f16,
+                                                        const int n, const float eps, const int seq_len,
+                                                        hipStream_t stream);
+
+// The accumulate launchers above followed by rf_rms_norm_batched_f16_on_stream
+// of inout (rows of N, weights norm_w) into out_f16, with the norm folded into
+// the split-K reduction when the GEMM splits (N % 2048 == 0, N <= 8192);
+// both outputs have the bits of the two calls.  norm_w and out_f16 16-byte
+// aligned; out_f16 must not overlap inout or the input.
+template <bool IS_Q6>
+static hipError_t accumulate_rmsnorm(const uint16_t* input_f16, const void* weights, float* inout,
+                                     const float* norm_w, float eps, uint16_t* out_f16, int M, int N, int K,
+                                     hipStream_t stream) {
+    if (input_f16 == nullptr || weights == nullptr || inout == nullptr || norm_w == nullptr || out_f16 == nullptr)
+        return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || (M % 64) != 0 || (N % 64) != 0 || (K % (IS_Q6 ? 2048 : kQK)) != 0)
+        return hipErrorInvalidValue;
+    if (!aligned16(input_f16) || !aligned16(weights) || !aligned16(inout) || !aligned16(norm_w) || !aligned16(out_f16))
+        return hipErrorInvalidValue;
+    const size_t n = (size_t)M * N;
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(inout), o0 = reinterpret_cast<uintptr_t>(out_f16);
+    if (d0 < o0 + 2 * n && o0 < d0 + 4 * n) return hipErrorInvalidValue;   // overlapping buffers
+    GemmSlot slot;
+    const PartBuf part = gemm_slot(stream, &slot) ? slot_parts(slot, 0) : PartBuf{nullptr, 0};
+    bool fused = false;
+    const RowNorm rn{norm_w, eps, out_f16, &fused};
+    const hipError_t e = IS_Q6 ? gemm_q6_f16<true>(input_f16, weights, inout, M, N, K, stream, part, &rn)
+                               : gemm_q4_f16<true>(input_f16, weights, inout, M, N, K, stream, nullptr, part, &rn);
+    if (e != hipSuccess || fused) return e;
+    return rf_rms_norm_batched_f16_on_stream(inout, norm_w, out_f16, N, eps, M, stream);
+}
+
+extern "C" hipError_t rf_gemm_q4_k_f16_accumulate_rmsnorm_launch(const uint16_t* input_f16, const void* weights_q4_k,
+                                                                 float* inout, const float* norm_w, float eps,
+                                                                 uint16_t* out_f16, int M, int N, int K,
+                                                                 hipStream_t stream) {
+    return accumulate_rmsnorm<false>(input_f16, weights_q4_k, inout, norm_w, eps, out_f16, M, N, K, stream);
+}
+
+extern "C" hipError_t rf_gemm_q6_k_f16_accumulate_rmsnorm_launch(const uint16_t* input_f16, const void* weights_q6_k,
+                                                                 float* inout, const float* norm_w, float eps,
+                                                                 uint16_t* out_f16, int M, int N, int K,
+                                                                 hipStream_t stream) {
+    return accumulate_rmsnorm<true>(input_f16, weights_q6_k, inout, norm_w, eps, out_f16, M, N, K, stream);
 }
 
 // Shapes the segmented / accumulating launches take: whole 256-column tiles,

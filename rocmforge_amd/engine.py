@@ -155,7 +155,7 @@ class Engine:
 
     def __init__(self, cfg: ModelConfig, weights: Weights, max_seq: int = 1024, device="cuda:0",
                  fuse_norm: bool = True, fold_qk: bool = True, fuse_gemm: bool = True, ffn_f16: bool = True,
-                 rope_table: bool = True, attn_bounded: bool = False):
+                 rope_table: bool = True, attn_bounded: bool = False, norm_in_down: bool = True):
         """fuse_norm: decode with the RMSNorms folded into the GEMVs that
         consume them, the per-head Q/K step into the attention and the state
         advance into the argmax (same bits as the separate launches);
@@ -178,7 +178,11 @@ class Engine:
         merged inside it, instead of the split kernel and its merge launch
         (the same attention within fp32 rounding; measured on MI355X at the
         Qwen3-8B shape 1.843 ms/token against 1.816 for the split path, so
-        off by default)."""
+        off by default);
+        norm_in_down: (with the fp16 prefill path) the next layer's attention
+        norm taken by the FFN-down launch that adds into the residual stream
+        (rf_gemm_q*_k_f16_accumulate_rmsnorm_launch: in the split-K
+        reduction's pass over the rows; the same bits as the separate norm)."""
         import torch
         self.cfg, self.w, self.max_seq, self.dev = cfg, weights, max_seq, device
         self.fuse_norm = fuse_norm
@@ -186,6 +190,7 @@ class Engine:
         self.fuse_gemm = fuse_gemm
         self.rope_table = rope_table
         self.attn_bounded = attn_bounded
+        self.norm_in_down = norm_in_down
         self.lib = _lib.load()
         ops._lib()
         f32, i16 = torch.float32, torch.int16
@@ -421,6 +426,15 @@ class Engine:
                     "ids": z(mp, torch.int32)}
         return self._pf
 
+    def _qkv16_ok(self, lw) -> bool:
+        """Whether a prefill layer runs Q/K/V as fp16 segments on its attention
+        norm rounded to fp16."""
+        c = self.cfg
+        types = [lw.mats[n][1].wtype for n in ("attn_q", "attn_k", "attn_v")]
+        return (self.fuse_gemm and self.ffn_f16 and all(ty in (GgmlType.Q4_K, GgmlType.Q6_K) for ty in types)
+                and c.q_size % 64 == 0 and c.kv_size % 64 == 0
+                and c.hidden % (2048 if GgmlType.Q6_K in types else 256) == 0)
+
     def prefill(self, tokens, trace=None) -> int:
         """Runs the prompt (positions 0..M-1), fills the KV caches, sets the
         state to {M, M + 1} and self.token to the greedy next token, which
@@ -441,19 +455,19 @@ class Engine:
         _chk(L.gpu_embed_q4_k_batch(_p(self.w.token_emb[0]), _p(b["ids"]), _p(b["x"]), c.hidden, c.vocab, M, st),
              "embed")
         t("embed", -1)
+        normed_ahead = False     # this layer's fp16 attention norm was written by the last FFN-down launch
         for i, lw in enumerate(self.w.layers):
             m = lw.mats
             qkv = [(m["attn_q"], b["q"], c.q_size), (m["attn_k"], b["k"], c.kv_size),
                    (m["attn_v"], b["v"], c.kv_size)]
             types = [wm[1].wtype for wm, _, _ in qkv]
             # Q/K/V on the attention norm rounded to fp16 (the operand values the fp32
-            # launchers round it to): one launch of 128 x 64 tiles whatever the type mix
-            self._qkv16 = (self.fuse_gemm and self.ffn_f16 and all(ty in (GgmlType.Q4_K, GgmlType.Q6_K) for ty in types)
-                           and c.q_size % 64 == 0 and c.kv_size % 64 == 0
-                           and c.hidden % (2048 if GgmlType.Q6_K in types else 256) == 0)
+            # launchers round it to): one launch of K-sliced tiles whatever the type mix
+            self._qkv16 = self._qkv16_ok(lw)
             if self._qkv16:
-                _chk(L.rf_rms_norm_batched_f16_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn16"]), c.hidden, c.eps,
-                                                         mp, st), "norm f16")
+                if not normed_ahead:
+                    _chk(L.rf_rms_norm_batched_f16_on_stream(_p(b["x"]), _p(lw.attn_norm), _p(b["xn16"]), c.hidden,
+                                                             c.eps, mp, st), "norm f16")
                 _chk(L.rf_gemm_qk_f16_segments_launch(_p(b["xn16"]), *[_p(wm[0]) for wm, _, _ in qkv],
                                                       *[int(ty) for ty in types], *[_p(o) for _, o, _ in qkv], mp,
                                                       c.q_size, c.kv_size, c.kv_size, c.hidden, st), "qkv f16")
@@ -562,7 +576,17 @@ class Engine:
                 self._gemm(m["ffn_up"], b["xn"], b["u"], c.ff, c.hidden, M, st)
                 _chk(L.rf_silu_mul_on_stream(_p(b["g"]), _p(b["u"]), _p(b["g"]), mp * c.ff, st), "swiglu")
             t("gate_up", i)
-            if self._act16:
+            nxt = self.w.layers[i + 1] if i + 1 < len(self.w.layers) else None
+            normed_ahead = False
+            if self._act16 and self.norm_in_down and nxt is not None and self._qkv16_ok(nxt):
+                # the next layer's fp16 attention norm taken with the residual add
+                q6 = m["ffn_down"][1].wtype == GgmlType.Q6_K
+                fn = (L.rf_gemm_q6_k_f16_accumulate_rmsnorm_launch if q6
+                      else L.rf_gemm_q4_k_f16_accumulate_rmsnorm_launch)
+                _chk(fn(_p(b["g16"]), _p(m["ffn_down"][0]), _p(b["x"]), _p(nxt.attn_norm), c.eps, _p(b["xn16"]), mp,
+                        c.hidden, c.ff, st), "gemm f16 accumulate + norm")
+                normed_ahead = True
+            elif self._act16:
                 fn = (L.rf_gemm_q6_k_f16_accumulate_launch if m["ffn_down"][1].wtype == GgmlType.Q6_K
                       else L.rf_gemm_q4_k_f16_accumulate_launch)
                 _chk(fn(_p(b["g16"]), _p(m["ffn_down"][0]), _p(b["x"]), mp, c.hidden, c.ff, st),

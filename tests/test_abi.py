@@ -81,3 +81,18 @@ def test_qkv_q6v_rejects_pointers(rf):
     assert f(P, P, ctypes.c_void_p(0x100002), NUL, NUL, NUL, P, P, 1e-6, P, P, P, 4096, 64, 16,
              NUL) == HIP_ERROR_INVALID_VALUE
     assert f(P, P, P, NUL, NUL, NUL, P, P, 1e-6, P, P, P, 4096, 0, 16, NUL) == HIP_ERROR_INVALID_VALUE
+
+
+def test_accumulate_rmsnorm_rejections(rf):
+    # validation before any HIP call: null pointers, shapes, alignment, overlap
+    f4, f6 = rf.rf_gemm_q4_k_f16_accumulate_rmsnorm_launch, rf.rf_gemm_q6_k_f16_accumulate_rmsnorm_launch
+    eps = ctypes.c_float(1e-6)
+    o = ctypes.c_void_p(0x200000)
+    for f in (f4, f6):
+        assert f(P, P, P, NUL, eps, o, 64, 4096, 4096, NUL) == HIP_ERROR_INVALID_VALUE     # no norm weights
+        assert f(P, P, P, P, eps, NUL, 64, 4096, 4096, NUL) == HIP_ERROR_INVALID_VALUE     # no output
+        assert f(P, P, P, P, eps, o, 96, 4096, 4096, NUL) == HIP_ERROR_INVALID_VALUE       # M % 64
+        assert f(P, P, P, P, eps, o, 64, 4000, 4096, NUL) == HIP_ERROR_INVALID_VALUE       # N % 64
+        assert f(P, P, P, P, eps, ctypes.c_void_p(0x200002), 64, 4096, 4096, NUL) == HIP_ERROR_INVALID_VALUE
+        assert f(P, P, P, P, eps, ctypes.c_void_p(0x100000 + 4096), 64, 4096, 4096, NUL) == HIP_ERROR_INVALID_VALUE
+    assert f6(P, P, P, P, eps, o, 64, 4096, 1024, NUL) == HIP_ERROR_INVALID_VALUE           # Q6_K K % 2048

@@ -179,6 +179,28 @@ def test_prefill_512_qwen3_8b_shape(qwen3):
     assert seen["qkv16"] and seen["ffn16"] and seen["act16"] and seen["att16"]
 
 
+def test_prefill_norm_in_down_same_bits(qwen3):
+    # the next layer's attention norm taken by the FFN-down launch (in its
+    # split-K reduction at the Qwen3-8B shape: Q4_K down split in four, Q6_K
+    # down in two at M = 512; 64-row tiles split at M = 64) against the
+    # separate norm launch: the same token, logits, residual stream and caches
+    e, _, _ = qwen3
+    for n in (512, 9):
+        prompt = [int(t) for t in np.random.default_rng(n).integers(0, e.cfg.vocab, n)]
+        runs = []
+        for fold in (True, False):
+            e.norm_in_down = fold
+            tok = e.prefill(prompt)
+            torch.cuda.synchronize()
+            runs.append((tok, _h(e.logits).copy(), _h(e._pf["x"]).copy(),
+                         [_h(t).reshape(-1, e.cfg.kv_size)[:n].copy() for t in e.kc + e.vc]))
+        e.norm_in_down = True
+        (ta, la, xa, ca), (tb, lb, xb, cb) = runs
+        assert ta == tb and np.array_equal(la, lb) and np.array_equal(xa, xb), n
+        for x, y in zip(ca, cb):
+            assert np.array_equal(x, y)
+
+
 def _snapshot(eng):
     return [t.clone() for t in [eng.token, eng.state, *eng.kc, *eng.vc]]
 

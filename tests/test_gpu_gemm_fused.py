@@ -372,3 +372,41 @@ def test_q4k_f16_swiglu_rejections(rf, dev):
     assert f(P(da), P(w), P(w), P(d), 0, m, 96, k, s) != 0       # N % 64
     assert f(P(da), P(w), P(w), P(d), 0, 32, 64, k, s) != 0      # M % 64
     assert f(P(da), P(w), P(w), P(d), 0, m, 64, 320, s) != 0     # K % 256
+
+
+# (format, M, N, K): the down projection of a prefill layer into the residual
+# stream with the next layer's attention norm -- split over K (the norm taken
+# in the reduction: N = 2048, 4096, 6144) and unsplit (the separate norm)
+@pytest.mark.parametrize("fmt,m,n,k", [
+    ("q4_k", 512, 4096, 12288),    # 256 x 128 tiles split over K in four
+    ("q6_k", 512, 4096, 12288),    # 256 x 64 tiles split over K
+    ("q4_k", 64, 2048, 4096),      # 64-row tiles split over K, one 2048 group per row
+    ("q6_k", 128, 6144, 2048),     # three 2048 groups per row
+    ("q4_k", 512, 4096, 4096),     # 128-row tiles, no split: the separate norm
+])
+def test_accumulate_rmsnorm_bits(rf, dev, fmt, m, n, k):
+    # inout and the fp16 norm bit for bit the accumulate launcher followed by
+    # rf_rms_norm_batched_f16_on_stream; the norm within its own bar of the
+    # float64 RMSNorm of the accumulated rows
+    a = torch.from_numpy(synth.activations(k, seed=m + n, m=m)).to(torch.bfloat16).float().numpy()
+    da = G.to_dev(a.astype(np.float16).view(np.int16))
+    dw = G.to_dev(synth.weights(fmt, n, k, seed=k + 5))
+    r0 = np.random.default_rng(n).standard_normal((m, n)).astype(np.float32)
+    gw = (np.random.default_rng(k).random(n) + 0.5).astype(np.float32)
+    dg = G.to_dev(gw)
+    eps = ctypes.c_float(1e-6)
+    ref_io, got_io = G.to_dev(r0), G.to_dev(r0)
+    ref_o = G.empty(m * n, torch.int16).fill_(-1)
+    got_o = G.empty(m * n, torch.int16).fill_(-1)
+    acc = rf.rf_gemm_q4_k_f16_accumulate_launch if fmt == "q4_k" else rf.rf_gemm_q6_k_f16_accumulate_launch
+    G.call(acc, G.ptr(da), G.ptr(dw), G.ptr(ref_io), m, n, k)
+    G.call(rf.rf_rms_norm_batched_f16_on_stream, G.ptr(ref_io), G.ptr(dg), G.ptr(ref_o), n, eps, m)
+    fused = (rf.rf_gemm_q4_k_f16_accumulate_rmsnorm_launch if fmt == "q4_k"
+             else rf.rf_gemm_q6_k_f16_accumulate_rmsnorm_launch)
+    G.call(fused, G.ptr(da), G.ptr(dw), G.ptr(got_io), G.ptr(dg), eps, G.ptr(got_o), m, n, k)
+    np.testing.assert_array_equal(G.host(got_io), G.host(ref_io))
+    np.testing.assert_array_equal(G.host(got_o), G.host(ref_o))
+    h = G.host(got_io).reshape(m, n).astype(np.float64)
+    want = h / np.sqrt((h * h).mean(axis=1, keepdims=True) + 1e-6) * gw
+    got = G.host(got_o).view(np.float16).reshape(m, n).astype(np.float64)
+    assert (np.abs(got - want) <= 1e-3 * np.abs(want) + 1e-4).all(), f"{fmt} {m}x{n}x{k} norm"
