@@ -162,9 +162,24 @@ __device__ __forceinline__ float sq8(const float4& a, const float4& b) {
     return t;
 }
 
+// The xor butterfly v += v[lane ^ o], o = 32, 16, .., 1, every lane ending
+// with the same sum, on VALU exchanges: v_permlane32_swap / _16_swap for 32
+// and 16, DPP row_ror:8 for 8, row_shl:4 / row_shr:4 selected by lane bit 2
+// for 4, quad permutes for 2 and 1 -- the sums of the __shfl_xor form bit for
+// bit (each step adds the same partner), without its LDS round trips.
 __device__ __forceinline__ float xor_sum64(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int lane = threadIdx.x & 63;
+    const uint32_t b32 = __float_as_uint(v);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(b32, b32, false, false);
+    v += __uint_as_float(lane >= 32 ? r32[0] : r32[1]);
+    const uint32_t b16 = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(b16, b16, false, false);
+    v += __uint_as_float(((lane >> 4) & 1) ? r16[0] : r16[1]);
+    v += dpp_f<0x128>(v);                     // row_ror:8
+    const float up = dpp_f<0x104>(v), dn = dpp_f<0x114>(v);   // row_shl:4, row_shr:4
+    v += (lane & 4) ? dn : up;
+    v += dpp_f<kQuadXor2>(v);
+    v += dpp_f<kQuadXor1>(v);
     return v;
 }
 
